@@ -1,0 +1,162 @@
+/*
+ * q4mi.h -- C ABI of the MI355X (gfx950) Q4_1 dequant-matmul kernels.
+ *
+ * Plain C: device pointers, sizes and an opaque HIP stream (`void*`, a
+ * hipStream_t; NULL = the default stream). No HIP or torch types appear in
+ * these signatures, so ctypes / cgo / JNI bind them without HIP headers.
+ *
+ * Every function returns Q4MI_OK (0) or a negative Q4MI_E* code. All device
+ * memory belongs to the caller; the library never allocates. Work is enqueued
+ * on `stream` and is asynchronous to the host; the functions are re-entrant
+ * and keep no global state apart from the counters inside a caller-owned
+ * workspace (calls that share one workspace must be ordered on one stream).
+ *
+ * Weights live in the "mx" layout (see q4_packed_bytes): an [N, K] matrix,
+ * N % 64 == 0, K % 32 == 0, cut into tiles of 64 rows x 32 K (one GGUF block
+ * column) of 1280 bytes: 1024 B of 4-bit codes laid out as the B operand of a
+ * 16x16x32 bf16 MFMA, then 256 B of (bf16 d << 16 | bf16 m) scale words.
+ * Tiles of one 64-row group are contiguous along K.
+ *
+ * Reference interfaces replaced (paths under the reference repository):
+ *   pack_q4_1_pool / pool layout  open_kernels/q4_1_pack.py:124-142
+ *   dequant_pool / dq_chunks_q4_1 open_kernels/q4_1_pack.py:173-180,
+ *                                 open_kernels/model/q4nx.py:105-126
+ *   gemv_q4 design + kernel       open_kernels/designs/gemv_q4/gemv_q4.py:118-194,
+ *                                 designs/gemv_q4/gemv_q4.h:320-341
+ *   gemm_q4 (batched decode)      open_kernels/designs/gemm_q4/gemm_q4.py:164-197,
+ *                                 designs/gemm_q4/gemm_q4.h:208-226
+ *   gemm_q4_prefill               open_kernels/designs/gemm_q4_prefill/gemm_q4_prefill.py:171-177
+ *   moe_batch / moe_experts       open_kernels/designs/moe_batch/moe_batch.py:145-146,
+ *                                 open_kernels/designs/moe_experts/moe_experts.py:1-43
+ */
+#ifndef Q4MI_H
+#define Q4MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define Q4MI_OK            0
+#define Q4MI_E_SHAPE      -1   /* a dimension is not a multiple the layout needs, or <= 0 */
+#define Q4MI_E_ARG        -2   /* NULL pointer, bad enum, bad block width */
+#define Q4MI_E_WORKSPACE  -3   /* workspace missing or too small */
+#define Q4MI_E_LAUNCH     -4   /* the HIP launch itself failed */
+#define Q4MI_E_RANGE      -5   /* M or another count out of the supported range */
+
+/* activation dtypes */
+#define Q4MI_F32   0
+#define Q4MI_BF16  1
+
+/* Library version, e.g. 100 for 0.1.0. */
+int q4mi_version(void);
+
+/* Human-readable text for a status code (static storage). */
+const char* q4mi_strerror(int status);
+
+/* Bytes of the mx layout for an [N, K] matrix (N % 64 == 0, K % 32 == 0),
+ * or Q4MI_E_SHAPE. Same 0.625 B/weight as GGUF Q4_1 (1280 B per 2048 weights).
+ * Replaces the size rule of pack_q4_1_pool (q4_1_pack.py:112-121, 5120 B per
+ * 32x256 chunk). */
+int64_t q4_packed_bytes(int64_t N, int64_t K);
+
+/* GGUF blocks -> mx layout, on the device.
+ * `gguf_blocks`: uint8[N][K/32][block_bytes], block_bytes 20 (Q4_1: fp16 d,
+ * fp16 m, 16 code bytes) or 18 (Q4_0: fp16 d, codes; its min is -8 d).
+ * scale_mode 0: d and m narrowed fp16 -> bf16 round-to-nearest-even, the
+ * reference's pool semantics (q4_1_pack.py:104-109, :129-130). No other mode.
+ * Replaces pack_q4_1_pool (q4_1_pack.py:124-142) as the packer. */
+int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* packed,
+              int64_t N, int64_t K, int scale_mode, void* stream);
+
+/* Reference pool chunks -> mx layout, on the device: the 5120-byte
+ * 32-row x 256-K chunks in band order with row split `rs`
+ * (q4_1_pack.py:16-34, :112-121; K % 256 == 0, N % (32*rs) == 0). The bytes
+ * carry over exactly (bf16 scales, same codes). */
+int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed,
+                   int64_t N, int64_t K, void* stream);
+
+/* mx layout -> f32 W[N][K] row-major, w = fl32(q * d + m), bit-exact with
+ * dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:155-180, q4nx.py:105-126). */
+int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
+
+/* Workspace bytes q4_gemv needs for (M, N, K); 0 when it needs none. The
+ * workspace starts with a fixed 16 KB region of arrival counters: zero-fill
+ * the buffer once before its first use; every q4_gemv call leaves those
+ * counters at zero again, whatever its shape. Do not hand the same buffer to
+ * another function in between (it would overwrite the counters). */
+size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K);
+
+/* Decode GEMV / skinny GEMM: Y[M][N] = X[M][K] . W[N][K]^T, fp32 accumulate,
+ * fp32 out. 1 <= M <= 16. x_dtype Q4MI_F32 or Q4MI_BF16, X row-major [M][K].
+ * Replaces gemv_q4 (M = 1; gemv_q4.py:118-123: pool in, bf16 x in, f32 y out)
+ * and gemm_q4 (M = 1..24; gemm_q4.py:164-197); Y is the logical [M][N] order
+ * (the reference's device order is core-interleaved, check.py:59-79). */
+int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
+            int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+            void* stream);
+
+/* One matrix of a grouped GEMV launch (device-resident array of these). */
+typedef struct q4_gemv_desc {
+    const uint8_t* packed;   /* mx layout, [N, K] */
+    const void* x;           /* [M][K] activations (dtype of the launch) */
+    float* y;                /* [M][N] output */
+    int64_t N;
+    int64_t K;
+    int64_t item_begin;      /* sum of N/64 over the descriptors before this one */
+} q4_gemv_desc;
+
+/* Many independent GEMVs in ONE launch: descriptor i covers work items
+ * [item_begin_i, item_begin_i + N_i/64). `descs` is a DEVICE pointer to
+ * `count` descriptors sorted by item_begin; total_items = sum of N_i/64.
+ * Same M and x dtype for all. The counterpart of the reference's fused
+ * multi-projection dispatches (one xclbin running several gemv_q4 bands,
+ * gemv_q4.py:46-53 YOFF/YTOT; designs/dense, designs/moe_experts). */
+int q4_gemv_grouped(const q4_gemv_desc* descs, int count, int64_t total_items,
+                    int M, int x_dtype, void* stream);
+
+/* Workspace bytes q4_gemm_prefill needs (0 if none). */
+size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K);
+
+/* Prefill GEMM: Y[T][N] = X[T][K] . W[N][K]^T with W dequantized into LDS
+ * tiles feeding MFMA, fp32 accumulate, fp32 out. Any T >= 0, N % 64 == 0,
+ * K % 32 == 0. precision 0 (default): each weight is rounded once to fp16
+ * (11-bit significand; X bf16 -> fp16 exactly for |x| in fp16's range) and
+ * fed to the fp16 MFMA, whose dense peak equals bf16's on CDNA4.
+ * precision 1: the reference's own tile, RNE_bf16(fl32(q*d+m)), into the
+ * bf16 MFMA (gemm_q4_dequant.h:283-286; its rel_fro bar is 5e-3).
+ * Replaces gemm_q4_prefill (gemm_q4_prefill.py:171-177: pool W, bf16 X,
+ * f32 Y[N][T]); Y here is token-major [T][N], the engine's order after
+ * host::transpose (core.cpp:2955-2963). */
+int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype, float* y,
+                    int T, int64_t N, int64_t K, int precision,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes q4_moe_gemv needs. */
+size_t q4_moe_workspace_bytes(int T, int E, int topk, int H, int F);
+
+/* Routed MoE expert block for T decode tokens:
+ *   out[t] = sum_j topk_w[t][j] * down_e( silu(gate_e . x_t) * (up_e . x_t) ),
+ *   e = topk_ids[t][j],
+ * fp32 h, fp32 accumulate, fp32 out[T][H].
+ * gate_up: E experts, each an mx matrix [2F, H] whose row groups alternate
+ *   gate / up (64 gate rows, then the same 64 rows of up, ...);
+ * down: E experts, each an mx matrix [H, F];
+ * x: [T][H] in x_dtype; topk_ids int32 [T][topk] in [0, E); topk_w f32.
+ * H % 64 == 0, F % 64 == 0, 1 <= T*topk <= 4096, topk <= 16.
+ * Replaces moe_batch (moe_batch.py:145-281, per-slot
+ * y = down(silu(gate x) * (up x))) with the host gather/scatter of
+ * Core::moe_block (core.cpp:5150-5245) moved onto the device. */
+int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype,
+                const int32_t* topk_ids, const float* topk_w, float* out,
+                int T, int E, int topk, int64_t H, int64_t F,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4MI_H */

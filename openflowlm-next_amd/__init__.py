@@ -1,0 +1,24 @@
+"""openflowlm-next_amd -- MI355X (gfx950) Q4_1 dequant-matmul kernels.
+
+The hot path of OpenFlowLM (the q4_1 dequantize-and-multiply behind every
+projection and FFN matmul) as hand-written HIP kernels behind a C ABI
+(``include/q4mi.h``, ``libq4mi.so``), with the reference's Python-facing
+operator surface on top (packed Q4_1 in, bf16/fp32 activations in, fp32 out).
+
+Import with ``importlib.import_module("openflowlm-next_amd")`` (the directory
+name is not a Python identifier).
+"""
+from . import _lib
+from .q4 import (GemvGroup, PackedExperts, PackedQ4, dequant, gemm_q4, gemm_q4_prefill, gemv_q4,
+                 moe_batch, pack_moe_experts, pack_q4_1, pack_q4_1_pool, packed_bytes)
+
+__all__ = [
+    "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "dequant",
+    "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
+    "load_library",
+]
+
+
+def load_library():
+    """Load libq4mi.so (raises ImportError when it was never built)."""
+    return _lib.load()

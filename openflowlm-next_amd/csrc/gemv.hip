@@ -1,0 +1,218 @@
+// gemv.hip -- decode GEMV / skinny GEMM on the mx layout: Y[M][N] = X[M][K] . W^T,
+// 1 <= M <= 16, fp32 accumulate (inner loop in gemv_core.h).
+//
+// Work item = one 64-row group over a K range, one 256-thread workgroup.
+// K splits (S > 1, for matrices too short to fill 256 CUs): each workgroup
+// writes its partial sums to the workspace; the last of the S workgroups of a
+// row group (counted with a device-scope atomic) adds the S partials in split
+// order, so the result does not depend on arrival order.
+#include <stdlib.h>
+
+#include "gemv_core.h"
+#include "q4mi_internal.h"
+
+using namespace q4mi;
+
+namespace {
+
+struct GemvParams {
+    const uint8_t* packed;
+    const void* x;
+    float* y;
+    int M;
+    int S;
+    int64_t N, K;
+    float* part;      // [S][M][N] partial sums (S > 1)
+    uint32_t* cnt;    // [N/64] arrival counters (S > 1)
+};
+
+
+// Store the row group's result, or hand it to the split reduction.
+template <int NTL>
+__device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4][NTL][64], const GemvParams& P,
+                                            float* __restrict__ y, int64_t N, int64_t g, int s, int S) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
+    const int64_t n = g * 64 + r * 16 + i16;
+    const int M = P.M;
+    float v[NTL];
+    wave_sum<NTL>(acc, red, v);
+    if (S == 1) {
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) {
+            const int tok = kg * 4 + j;
+            if (tok < M) y[(int64_t)tok * N + n] = v[j];
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < NTL; ++j) {
+        const int tok = kg * 4 + j;
+        if (tok < M) __hip_atomic_store(&P.part[((int64_t)s * M + tok) * N + n], v[j], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __shared__ int last;
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = (atomicAdd(&P.cnt[g], 1u) == (unsigned)(S - 1));
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+#pragma unroll
+    for (int j = 0; j < NTL; ++j) {
+        const int tok = kg * 4 + j;
+        if (tok < M) {
+            float acc_s = 0.f;
+            for (int q = 0; q < S; ++q)
+                acc_s += __hip_atomic_load(&P.part[((int64_t)q * M + tok) * N + n], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            y[(int64_t)tok * N + n] = acc_s;
+        }
+    }
+    if (tid == 0) __hip_atomic_store(&P.cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NTL, bool XF32>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
+    __shared__ float red[kWaves][4][NTL][64];
+    const int64_t item = blockIdx.x;
+    const int S = P.S;
+    const int64_t g = item / S;
+    const int s = (int)(item % S);
+    const int KB = (int)(P.K >> 5);
+    const int kb0 = (int)((int64_t)s * KB / S), kb1 = (int)((int64_t)(s + 1) * KB / S);
+    float acc[4][NTL];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
+    gemv_rows<NTL, XF32>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
+    gemv_finish<NTL>(acc, red, P, P.y, P.N, g, s, S);
+}
+
+template <int NTL, bool XF32>
+__global__ __launch_bounds__(256) void gemv_grouped_kernel(const q4_gemv_desc* __restrict__ descs, int count, int M) {
+    __shared__ float red[kWaves][4][NTL][64];
+    const int64_t item = blockIdx.x;
+    int lo = 0, hi = count - 1;
+    while (lo < hi) {               // last descriptor with item_begin <= item
+        const int mid = (lo + hi + 1) >> 1;
+        if (descs[mid].item_begin <= item) lo = mid;
+        else hi = mid - 1;
+    }
+    const q4_gemv_desc D = descs[lo];
+    const int64_t g = item - D.item_begin;
+    if (g < 0 || g >= (D.N >> 6)) return;   // inconsistent total_items: the whole workgroup leaves
+    float acc[4][NTL];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
+    gemv_rows<NTL, XF32>(D.packed, D.x, DenseRows{M}, D.K, g, 0, (int)(D.K >> 5), acc);
+    GemvParams P{};
+    P.M = M;
+    gemv_finish<NTL>(acc, red, P, D.y, D.N, g, 0, 1);
+}
+
+// Workgroups to aim for when a matrix has few row groups.
+int64_t target_workgroups() {
+    static int64_t t = [] {
+        const char* e = getenv("Q4MI_GEMV_TARGET_WGS");
+        const long v = e ? atol(e) : 0;
+        return (int64_t)(v > 0 ? v : 1024);
+    }();
+    return t;
+}
+
+// The workspace starts with a fixed region of arrival counters (one per row
+// group), so a call of any shape finds its counters at the same place, left
+// at zero by the previous call; partial sums follow it.
+constexpr int64_t kMaxSplitGroups = 4096;                 // row groups a split call may have
+constexpr size_t kCounterBytes = kMaxSplitGroups * 4;     // 16 KB
+
+int choose_splits(int64_t N, int64_t K) {
+    const int64_t G = N / 64, KB = K / 32;
+    const int64_t target = target_workgroups();
+    if (G >= target || G > kMaxSplitGroups) return 1;
+    int64_t S = ceil_div(target, G);
+    const int64_t max_s = KB / 8;           // keep >= 8 blocks (2 tiles per wave) per split
+    if (S > max_s) S = max_s;
+    return (int)(S < 1 ? 1 : S);
+}
+
+size_t workspace_for(int M, int64_t N, int64_t K, int S) {
+    (void)K;
+    if (S <= 1) return 0;
+    return kCounterBytes + (size_t)S * M * N * sizeof(float);
+}
+
+template <int NTL>
+void launch_gemv(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
+    else hipLaunchKernelGGL((gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
+}
+
+template <int NTL>
+void launch_grouped(bool xf32, dim3 grid, hipStream_t st, const q4_gemv_desc* d, int count, int M) {
+    if (xf32) hipLaunchKernelGGL((gemv_grouped_kernel<NTL, true>), grid, dim3(256), 0, st, d, count, M);
+    else hipLaunchKernelGGL((gemv_grouped_kernel<NTL, false>), grid, dim3(256), 0, st, d, count, M);
+}
+
+}  // namespace
+
+extern "C" size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K) {
+    if (M < 1 || M > 16 || N <= 0 || K <= 0 || N % 64 || K % 32) return 0;
+    return workspace_for(M, N, K, choose_splits(N, K));
+}
+
+extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y, int M, int64_t N, int64_t K,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (M < 0 || M > 16) return Q4MI_E_RANGE;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
+    if (!packed || !x || !y) return Q4MI_E_ARG;
+    const int S = choose_splits(N, K);
+    GemvParams P{};
+    P.packed = packed;
+    P.x = x;
+    P.y = y;
+    P.M = M;
+    P.S = S;
+    P.N = N;
+    P.K = K;
+    if (S > 1) {
+        const size_t need = workspace_for(M, N, K, S);
+        if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
+        P.cnt = (uint32_t*)workspace;
+        P.part = (float*)((char*)workspace + kCounterBytes);
+    }
+    const dim3 grid((unsigned)((N / 64) * S));
+    const hipStream_t st = (hipStream_t)stream;
+    const bool xf32 = x_dtype == Q4MI_F32;
+    switch (M < 4 ? M : 4) {
+        case 1: launch_gemv<1>(xf32, grid, st, P); break;
+        case 2: launch_gemv<2>(xf32, grid, st, P); break;
+        case 3: launch_gemv<3>(xf32, grid, st, P); break;
+        default: launch_gemv<4>(xf32, grid, st, P); break;
+    }
+    return launch_status();
+}
+
+extern "C" int q4_gemv_grouped(const q4_gemv_desc* descs, int count, int64_t total_items, int M, int x_dtype,
+                               void* stream) {
+    if (!descs || count <= 0 || total_items <= 0) return Q4MI_E_ARG;
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (M < 1 || M > 16) return Q4MI_E_RANGE;
+    if (total_items > 0x7FFFFFFF) return Q4MI_E_RANGE;
+    const dim3 grid((unsigned)total_items);
+    const hipStream_t st = (hipStream_t)stream;
+    const bool xf32 = x_dtype == Q4MI_F32;
+    switch (M < 4 ? M : 4) {
+        case 1: launch_grouped<1>(xf32, grid, st, descs, count, M); break;
+        case 2: launch_grouped<2>(xf32, grid, st, descs, count, M); break;
+        case 3: launch_grouped<3>(xf32, grid, st, descs, count, M); break;
+        default: launch_grouped<4>(xf32, grid, st, descs, count, M); break;
+    }
+    return launch_status();
+}

@@ -1,0 +1,139 @@
+// gemv_core.h -- the decode GEMV inner loop on the mx layout, shared by the
+// dense GEMV (gemv.hip) and the routed-expert kernels (moe.hip).
+//
+// A 256-thread workgroup works on one 64-row group; its four waves take every
+// fourth 32-K tile of a K range. Per tile (64 rows x 32 K, 1280 B) a wave
+// issues two 128-bit loads per lane (codes, scales) and the activation
+// fragment, then:
+//   ns  = MFMA(X, -128)             -> -128 * sum_k x, per token (the C input)
+//   P_r = MFMA(X, 128 + q_r, ns)    -> sum_k q x, rows 16r..16r+15
+//   acc_r += d_r * P_r + m_r * sum_k x
+// which is the Q4_1 factorisation the reference GEMV uses,
+//   y[r] = sum_kb { d[kb][r] * sum_k q x + m[kb][r] * sum_k x }
+// (open_kernels/designs/gemv_q4/gemv_q4.h:33-34), here with the exact 4-bit
+// codes and bf16 activations on the bf16 MFMA and the scales applied in fp32.
+// The MFMA's A operand is the activation (tokens as rows), so each lane's
+// 4 outputs are 4 tokens of one weight row: one d and one m per lane per row
+// tile. f32 activations are split x = hi + lo (two bf16s, |residual| <=
+// 2^-18 |x|) and both halves go through the MFMA.
+#pragma once
+
+#include "q4mi_device.h"
+
+namespace q4mi {
+
+constexpr int kWaves = 4;      // waves per workgroup
+constexpr int kUnroll = 4;     // tiles in flight per wave
+
+
+// Token slot -> activation row. Slots at or past M map to the last real
+// token: MFMA rows (tokens) are independent and those rows of the result are
+// never stored, so no lane needs a branch or a zero fill.
+struct DenseRows {
+    int M;
+    __device__ __forceinline__ int64_t operator()(int tok) const { return tok < M ? tok : M - 1; }
+};
+struct GatherRows {            // rows listed in LDS (routed tokens of one expert)
+    const int* rows;
+    int M;
+    __device__ __forceinline__ int64_t operator()(int tok) const { return rows[tok < M ? tok : M - 1]; }
+};
+
+// Activation fragment of one tile: the 8 x of activation row `row` at k0.
+template <bool XF32>
+__device__ __forceinline__ void load_xfrag(const void* __restrict__ x, int64_t K, int64_t row, int64_t k0,
+                                           bf16x8& hi, bf16x8& lo) {
+    if constexpr (XF32) {
+        const f32x4* p = (const f32x4*)((const float*)x + row * K + k0);
+        const f32x4 a = p[0], b = p[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const __bf16 ha = (__bf16)a[e], hb = (__bf16)b[e];
+            hi[e] = ha;
+            hi[e + 4] = hb;
+            lo[e] = (__bf16)(a[e] - (float)ha);
+            lo[e + 4] = (__bf16)(b[e] - (float)hb);
+        }
+    } else {
+        hi = *(const bf16x8*)((const __bf16*)x + row * K + k0);
+    }
+}
+
+// Accumulate this wave's share of tiles [kb0, kb1) of row group g.
+// Loads are unconditional (a tile index past kb1 is clamped to kb1 - 1 and
+// its data skipped) so the compiler can count them statically and wait for
+// each tile's loads only, keeping kUnroll tiles in flight per wave.
+template <int NTL, bool XF32, class Rows>
+__device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, const void* __restrict__ x, Rows rows,
+                                          int64_t K, int64_t g, int kb0, int kb1, float (&acc)[4][NTL]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
+    kb0 = __builtin_amdgcn_readfirstlane(kb0);
+    kb1 = __builtin_amdgcn_readfirstlane(kb1);
+    const int i16 = lane & 15, kg = lane >> 4;
+    const int64_t KB = K >> 5;
+    const uint8_t* gbase = packed + g * KB * kTileBytes;
+    const int coff = lane * 16, soff = kCodeBytes + i16 * 16;   // per-lane byte offsets in a tile
+    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const CodeConsts kc = code_consts();
+    const int64_t xrow = rows(i16);
+
+    for (int kb = kb0 + wave; kb < kb1; kb += kWaves * kUnroll) {
+        u32x4 c[kUnroll], s[kUnroll];
+        bf16x8 xh[kUnroll], xl[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int t = min(kb + kWaves * u, kb1 - 1);
+            const uint8_t* tp = gbase + (int64_t)t * kTileBytes;      // wave-uniform tile base
+            c[u] = load_nt_u32x4(tp + coff);
+            s[u] = load_nt_u32x4(tp + soff);
+            load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (kb + kWaves * u < kb1) {
+                f32x4 ns = mfma_bf16(xh[u], neg128, zero4);
+                if constexpr (XF32) ns = mfma_bf16(xl[u], neg128, ns);
+                f32x4 p[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bf16x8 b = codes_to_bf16(c[u][r], kc);
+                    p[r] = mfma_bf16(xh[u], b, ns);
+                    if constexpr (XF32) p[r] = mfma_bf16(xl[u], b, p[r]);
+                }
+                float sx[NTL];
+#pragma unroll
+                for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float d = bf16_hi_to_f32(s[u][r]), m = bf16_lo_to_f32(s[u][r]);
+#pragma unroll
+                    for (int j = 0; j < NTL; ++j) {
+                        acc[r][j] = __builtin_fmaf(d, p[r][j], acc[r][j]);
+                        acc[r][j] = __builtin_fmaf(m, sx[j], acc[r][j]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Sum the four waves' accumulators through LDS. Afterwards thread t owns
+// row 16 r + lane % 16 of the row group (r = t >> 6, lane = t & 63) for the
+// tokens 4 (lane / 16) + j, j < NTL: v[j].
+template <int NTL>
+__device__ __forceinline__ void wave_sum(float (&acc)[4][NTL], float (*red)[4][NTL][64], float (&v)[NTL]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) red[wave][r][j][lane] = acc[r][j];
+    __syncthreads();
+    const int r = wave;
+#pragma unroll
+    for (int j = 0; j < NTL; ++j)
+        v[j] = (red[0][r][j][lane] + red[1][r][j][lane]) + (red[2][r][j][lane] + red[3][r][j][lane]);
+}
+
+}  // namespace q4mi

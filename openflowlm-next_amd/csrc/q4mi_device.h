@@ -1,0 +1,93 @@
+// q4mi_device.h -- device helpers shared by the gfx950 Q4_1 kernels.
+//
+// The mx weight layout (an [N, K] matrix, N % 64 == 0, K % 32 == 0):
+//   tile (g, kb) = 64 rows x 32 K, 1280 B, at byte (g * K/32 + kb) * 1280.
+//   codes  [0, 1024): dword (lane, r) at lane*16 + r*4 (lane 0..63, r 0..3)
+//            row n = 64 g + 16 r + lane % 16, k = 32 kb + 8 (lane / 16) + e,
+//            code e (0..7) at bit 16 * (e & 1) + 4 * (e >> 1).
+//   scales [1024, 1280): dword at 1024 + (lane % 16)*16 + r*4 for the same
+//            row: (bf16 d << 16) | bf16 m.
+// One codes dword is the B operand of a v_mfma_f32_16x16x32_bf16 for the
+// eight k of row lane%16 in k-group lane/16: codes_to_bf16 turns it into
+// eight bf16 values 128 + q with two ALU ops per pair (mask, or a magic
+// exponent) and the MFMA folds the 128 offset back out through its C input.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q4mi {
+
+constexpr int kRows = 64;        // rows per tile / row group
+constexpr int kBlk = 32;         // K per tile (one GGUF block)
+constexpr int kTileBytes = 1280;
+constexpr int kCodeBytes = 1024;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 128.0 in both halves: OR-ing a code q (0..15) into the low mantissa
+// bits gives exactly the bf16 value 128 + q (exponent 2^7, unit mantissa step 1).
+constexpr uint32_t kMagic128 = 0x43004300u;
+constexpr uint32_t kNib2 = 0x000F000Fu;
+
+// A constant held in a VGPR the optimizer cannot see through. gfx9 VOP3
+// encodings take no literal and read at most one SGPR, so v_and_or_b32 with
+// the mask and the magic needs both in VGPRs; hoisted out of loops by the
+// caller, this keeps the conversion at one op per pair (plus a shift).
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+    uint32_t v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(c));
+    return v;
+}
+
+struct CodeConsts {
+    uint32_t nib2, magic;
+};
+__device__ __forceinline__ CodeConsts code_consts() { return {vgpr_const(kNib2), vgpr_const(kMagic128)}; }
+
+__device__ __forceinline__ bf16x8 codes_to_bf16(uint32_t w, CodeConsts k) {
+    u32x4 v;
+    v[0] = (w & k.nib2) | k.magic;
+    v[1] = ((w >> 4) & k.nib2) | k.magic;
+    v[2] = ((w >> 8) & k.nib2) | k.magic;
+    v[3] = ((w >> 12) & k.nib2) | k.magic;
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ float bf16_hi_to_f32(uint32_t s) {   // d from a scale word
+    return __builtin_bit_cast(float, s & 0xFFFF0000u);
+}
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t s) {   // m from a scale word
+    return __builtin_bit_cast(float, s << 16);
+}
+
+// f32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// fp16 bits -> f32 (exact).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Streaming loads of weight bytes: read once, keep them out of the caches'
+// way (the "nt" bit on the global load).
+__device__ __forceinline__ u32x4 load_nt_u32x4(const void* p) {
+    return __builtin_nontemporal_load((const u32x4*)p);
+}
+__device__ __forceinline__ uint32_t load_nt_u32(const void* p) {
+    return __builtin_nontemporal_load((const uint32_t*)p);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace q4mi

@@ -1,0 +1,160 @@
+// repack.hip -- GGUF blocks / reference pool chunks -> mx layout, and the
+// bit-exact dequant of the mx layout. One thread per (row, 32-K block).
+//
+// Reference semantics followed:
+//   GGUF Q4_1 block: fp16 d | fp16 m | 16 bytes, byte j = value j (low nibble)
+//     and value j+16 (high nibble); Q4_0 has no m and reads as m = -8 d
+//     (open_kernels/q4_1_pack.py:1-9, :84-101).
+//   d, m narrowed fp16 -> bf16 by round-to-nearest-even (q4_1_pack.py:104-109,
+//     :129-130): the only change to the GGUF bytes.
+//   pool chunk: 32 rows x 256 K, d bf16[256] @0 index kb*32 + r, m @512, code
+//     nibble p = (r/16)*4096 + k*16 + r%16 @1024 (even p = low half), chunks
+//     in band order with row split rs (q4_1_pack.py:16-34, :112-142).
+//   dequant: w = fl32(q * d + m) (q4_1_pack.py:155-170, q4nx.py:105-126);
+//     q*d is exact in f32 (4-bit x 8-bit significands), so one fma equals the
+//     reference's multiply-then-add bit for bit.
+#include "q4mi_device.h"
+#include "q4mi_internal.h"
+
+using namespace q4mi;
+
+namespace {
+
+__device__ __forceinline__ void mx_write_block(uint8_t* packed, int64_t KB, int64_t n, int64_t kb,
+                                               const uint8_t code[32], uint32_t scale_word) {
+    const int64_t g = n >> 6;
+    const int i = (int)(n & 63);
+    const int r = i >> 4, i16 = i & 15;
+    uint8_t* tile = packed + (g * KB + kb) * kTileBytes;
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            w |= (uint32_t)code[8 * kg + e] << (16 * (e & 1) + 4 * (e >> 1));
+        *(uint32_t*)(tile + (kg * 16 + i16) * 16 + r * 4) = w;
+    }
+    *(uint32_t*)(tile + kCodeBytes + i16 * 16 + r * 4) = scale_word;
+}
+
+__global__ __launch_bounds__(256) void repack_gguf_kernel(const uint8_t* __restrict__ src, int bw,
+                                                          uint8_t* __restrict__ packed, int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    // idx -> (tile, row): 64 consecutive threads fill one tile
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    const uint8_t* b = src + (n * KB + kb) * bw;
+    uint32_t dbits = (uint32_t)b[0] | ((uint32_t)b[1] << 8);
+    float d = f16_bits_to_f32(dbits), m;
+    const uint8_t* qs;
+    if (bw == 20) {
+        m = f16_bits_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+        qs = b + 4;
+    } else {
+        m = -8.0f * d;   // Q4_0 written the Q4_1 way; exact
+        qs = b + 2;
+    }
+    uint8_t code[32];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        uint8_t v = qs[j];
+        code[j] = v & 0xF;
+        code[j + 16] = v >> 4;
+    }
+    mx_write_block(packed, KB, n, kb, code, (f32_to_bf16_rne(d) << 16) | f32_to_bf16_rne(m));
+}
+
+__global__ __launch_bounds__(256) void repack_pool_kernel(const uint8_t* __restrict__ pool, int rs,
+                                                          uint8_t* __restrict__ packed, int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    const int64_t K = KB * 32;
+    const int64_t per_band = (int64_t)rs * K / 256;
+    const int64_t band = n / (32 * rs);
+    const int64_t ci = (kb / 8) * rs + (n % (32 * rs)) / 32;
+    const uint8_t* ch = pool + (band * per_band + ci) * 5120;
+    const int r = (int)(n & 31);
+    const int kbl = (int)(kb & 7);
+    const uint16_t* sc = (const uint16_t*)ch;
+    const uint32_t d16 = sc[kbl * 32 + r];
+    const uint32_t m16 = sc[256 + kbl * 32 + r];
+    uint8_t code[32];
+    const uint8_t* nib = ch + 1024 + (r >> 4) * 2048 + (r & 15) / 2;
+    const int sh = 4 * (r & 1);
+#pragma unroll
+    for (int v = 0; v < 32; ++v) code[v] = (nib[(32 * kbl + v) * 8] >> sh) & 0xF;
+    mx_write_block(packed, KB, n, kb, code, (d16 << 16) | m16);
+}
+
+// Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats.
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
+                                                      int64_t N, int64_t K) {
+    const int64_t K8 = K >> 3;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * K8) return;
+    const int64_t n = idx / K8, k8 = idx % K8;
+    const int64_t KB = K >> 5;
+    const int64_t g = n >> 6, kb = k8 >> 2;
+    const int i = (int)(n & 63), r = i >> 4, i16 = i & 15, kg = (int)(k8 & 3);
+    const uint8_t* tile = packed + (g * KB + kb) * kTileBytes;
+    const uint32_t c = *(const uint32_t*)(tile + (kg * 16 + i16) * 16 + r * 4);
+    const uint32_t s = *(const uint32_t*)(tile + kCodeBytes + i16 * 16 + r * 4);
+    const float d = bf16_hi_to_f32(s), m = bf16_lo_to_f32(s);
+    f32x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        lo[e] = __builtin_fmaf((float)((c >> (16 * (e & 1) + 4 * (e >> 1))) & 0xF), d, m);
+        hi[e] = __builtin_fmaf((float)((c >> (16 * ((e + 4) & 1) + 4 * ((e + 4) >> 1))) & 0xF), d, m);
+    }
+    f32x4* out = (f32x4*)(w + n * K + k8 * 8);
+    out[0] = lo;
+    out[1] = hi;
+}
+
+}  // namespace
+
+extern "C" int64_t q4_packed_bytes(int64_t N, int64_t K) {
+    if (N == 0 && K > 0 && K % 32 == 0) return 0;
+    if (N <= 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    return (N / 64) * (K / 32) * (int64_t)kTileBytes;
+}
+
+extern "C" int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* packed, int64_t N, int64_t K,
+                         int scale_mode, void* stream) {
+    if (block_bytes != 20 && block_bytes != 18) return Q4MI_E_ARG;
+    if (scale_mode != 0) return Q4MI_E_ARG;
+    if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;   // empty: nothing to touch
+    if (!gguf_blocks || !packed) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(repack_gguf_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, gguf_blocks,
+                       block_bytes, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed, int64_t N, int64_t K, void* stream) {
+    if (rs <= 0) return Q4MI_E_ARG;
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!pool || !packed) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(repack_pool_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, pool, rs, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
+    if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;
+    if (!packed || !w) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    const int64_t total = N * (K / 8);
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(dequant_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, packed, w, N, K);
+    return launch_status();
+}

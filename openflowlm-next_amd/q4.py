@@ -1,0 +1,382 @@
+"""Python operator surface of the MI355X Q4_1 kernels (ctypes over libq4mi.so).
+
+Same semantics as the reference's operators for this path -- packed Q4_1
+weights in, bf16 or fp32 activations in, fp32 out:
+
+* ``pack_q4_1`` / ``pack_q4_1_pool``   weight packing (open_kernels/q4_1_pack.py:124-142)
+* ``dequant``                          dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:173-180,
+                                       model/q4nx.py:105-126), bit-exact
+* ``gemv_q4``                          designs/gemv_q4 (gemv_q4.py:118-123): y[N] = W x
+* ``gemm_q4``                          designs/gemm_q4 (gemm_q4.py:164-197): Y[M,N], M <= 16
+* ``gemm_q4_prefill``                  designs/gemm_q4_prefill (gemm_q4_prefill.py:171-177)
+* ``moe_batch``                        designs/moe_batch + Core::moe_block's gather/scatter
+                                       (moe_batch.py:145-281, core.cpp:5150-5245)
+
+Every call goes to a HIP kernel; nothing here computes on the CPU. Tensors
+may be torch (on the GPU) or numpy (copied to the GPU). Work is enqueued on
+torch's current stream of the tensors' device.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import Q4MI_BF16, Q4MI_F32, Q4GemvDesc, check
+
+__all__ = [
+    "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "dequant",
+    "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
+]
+
+ROWS = 64          # rows per mx tile / row group
+BLK = 32           # K per tile (one GGUF block)
+
+
+def _lib_handle():
+    return _lib.load()
+
+
+def _device(dev=None) -> torch.device:
+    if dev is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    d = torch.device(dev)
+    if d.type != "cuda":
+        raise ValueError(f"device must be a GPU, got {d}")
+    return d if d.index is not None else torch.device("cuda", torch.cuda.current_device())
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _to_dev(a, dev: torch.device, dtype=None) -> torch.Tensor:
+    if isinstance(a, np.ndarray):
+        t = torch.from_numpy(np.ascontiguousarray(a))
+    elif isinstance(a, torch.Tensor):
+        t = a
+    else:
+        raise TypeError(f"expected a numpy array or torch tensor, got {type(a)}")
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t.to(dev, non_blocking=False).contiguous()
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def packed_bytes(n: int, k: int) -> int:
+    """Bytes of the mx layout for an [n, k] matrix (n % 64 == 0, k % 32 == 0)."""
+    b = _lib_handle().q4_packed_bytes(n, k)
+    if b < 0:
+        raise ValueError(f"[{n}, {k}] does not fit the mx layout (n % 64 == 0, k % 32 == 0)")
+    return int(b)
+
+
+@dataclass
+class PackedQ4:
+    """One [n, k] Q4_1 weight matrix in the mx layout, resident on a GPU."""
+    data: torch.Tensor        # uint8, packed_bytes(n, k)
+    n: int
+    k: int
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+
+@dataclass
+class PackedExperts:
+    """E experts' matrices of one shape [n, k], back to back in the mx layout."""
+    data: torch.Tensor
+    experts: int
+    n: int
+    k: int
+
+    @property
+    def expert_bytes(self) -> int:
+        return packed_bytes(self.n, self.k)
+
+
+# --------------------------------------------------------------------------
+# packing and dequant
+# --------------------------------------------------------------------------
+
+def pack_q4_1(blocks, device=None, out: torch.Tensor | None = None) -> PackedQ4:
+    """GGUF Q4_1 (20 B) or Q4_0 (18 B) blocks uint8[N, K/32, w] -> mx layout on the GPU.
+
+    d and m are narrowed fp16 -> bf16 (RNE), exactly the reference pool's
+    semantics (q4_1_pack.py:104-109, :129-130); the block width says which
+    format it is, as in q4_1_pack.py:8-9."""
+    dev = _device(device if device is not None else (blocks.device if isinstance(blocks, torch.Tensor)
+                                                     and blocks.is_cuda else None))
+    src = _to_dev(blocks, dev, torch.uint8)
+    if src.dim() != 3 or src.shape[2] not in (18, 20):
+        raise ValueError(f"blocks must be uint8[N, K/32, 20|18], got {tuple(src.shape)}")
+    n, nb, w = src.shape
+    k = nb * BLK
+    nbytes = packed_bytes(n, k)
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    elif out.numel() < nbytes or out.dtype != torch.uint8:
+        raise ValueError("out is too small or not uint8")
+    with torch.cuda.device(dev):
+        check("q4_repack", _lib_handle().q4_repack(_ptr(src), w, _ptr(out), n, k, 0, _stream(dev)))
+    return PackedQ4(out[:nbytes], n, k)
+
+
+def pack_q4_1_pool(pool, n: int, k: int, rs: int, device=None) -> PackedQ4:
+    """The reference's pool chunk bytes (5120 B chunks, band row split rs;
+    q4_1_pack.py:16-34) -> mx layout on the GPU. Bytes carry over exactly."""
+    dev = _device(device)
+    src = _to_dev(pool, dev, torch.uint8).reshape(-1)
+    if src.numel() != n * k * 5 // 8:
+        raise ValueError(f"pool holds {src.numel()} bytes, [{n}, {k}] needs {n * k * 5 // 8}")
+    nbytes = packed_bytes(n, k)
+    out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_repack_pool", _lib_handle().q4_repack_pool(_ptr(src), rs, _ptr(out), n, k, _stream(dev)))
+    return PackedQ4(out, n, k)
+
+
+def dequant(w: PackedQ4, out: torch.Tensor | None = None) -> torch.Tensor:
+    """mx layout -> f32[n, k], w = fl32(q*d + m), bit-exact with dequant_pool."""
+    dev = w.device
+    if out is None:
+        out = torch.empty((w.n, w.k), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_dequant", _lib_handle().q4_dequant(_ptr(w.data), _ptr(out), w.n, w.k, _stream(dev)))
+    return out
+
+
+# --------------------------------------------------------------------------
+# workspaces (zero-filled once; the kernels leave their counters at zero)
+# --------------------------------------------------------------------------
+
+_WS: dict = {}
+
+
+def _workspace(dev: torch.device, nbytes: int, op: str) -> torch.Tensor | None:
+    """A zero-filled scratch buffer per (operator, device, stream): operators
+    never share one, because q4_gemv keeps its arrival counters (left at zero
+    by every call) at the start of its workspace."""
+    if nbytes == 0:
+        return None
+    key = (op, dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _WS[key] = ws
+    return ws
+
+
+def _x_dtype(x: torch.Tensor) -> int:
+    if x.dtype == torch.bfloat16:
+        return Q4MI_BF16
+    if x.dtype == torch.float32:
+        return Q4MI_F32
+    raise TypeError(f"activations must be bf16 or fp32, got {x.dtype}")
+
+
+def _acts(x, dev: torch.device) -> torch.Tensor:
+    if isinstance(x, np.ndarray):
+        x = torch.from_numpy(np.ascontiguousarray(x))
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.to(torch.float32)
+    return x.to(dev).contiguous()
+
+
+# --------------------------------------------------------------------------
+# decode GEMV / skinny GEMM
+# --------------------------------------------------------------------------
+
+def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None) -> torch.Tensor:
+    """Y[M, N] = X[M, K] @ W^T for 1 <= M <= 16 decode tokens, fp32 out
+    (gemm_q4.py:164-197's operator, logical [M, N] order)."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != w.k:
+        raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q4 takes 1..16 tokens, got {M} (use gemm_q4_prefill)")
+    if y is None:
+        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        nbytes = lib.q4_gemv_workspace_bytes(M, w.n, w.k)
+        ws = _workspace(dev, nbytes, "gemv")
+        check("q4_gemv", lib.q4_gemv(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), M, w.n, w.k,
+                                     _ptr(ws) if ws is not None else None,
+                                     ws.numel() if ws is not None else 0, _stream(dev)))
+    return y
+
+
+def gemv_q4(w: PackedQ4, x, y: torch.Tensor | None = None) -> torch.Tensor:
+    """y[N] = W[N, K] @ x[K], fp32 out (gemv_q4.py:118-123: pool in, bf16 x in, f32 y out)."""
+    xt = _acts(x, w.device)
+    if xt.dim() != 1:
+        raise ValueError("gemv_q4 takes one activation vector x[K]")
+    out = gemm_q4(w, xt.unsqueeze(0), None if y is None else y.view(1, -1))
+    return out.view(-1)
+
+
+class GemvGroup:
+    """Many independent GEMVs (same M, same activation dtype) as ONE launch.
+
+    ``items`` is a list of (PackedQ4, x[M, K], y[M, N]) on one device; the
+    descriptor table is built and uploaded once, so ``run()`` is a single
+    kernel launch -- the counterpart of the reference's fused dispatches that
+    run several projections' bands in one xclbin (gemv_q4.py:46-53)."""
+
+    def __init__(self, items):
+        if not items:
+            raise ValueError("empty group")
+        dev = items[0][0].device
+        descs = (Q4GemvDesc * len(items))()
+        begin = 0
+        m0 = dt = None
+        self._keep = []
+        for i, (w, x, y) in enumerate(items):
+            if x.device != dev or y.device != dev or w.device != dev:
+                raise ValueError("all group members must be on one device")
+            xx = x if x.dim() == 2 else x.view(1, -1)
+            M, K = xx.shape
+            if K != w.k or tuple(y.reshape(M, -1).shape) != (M, w.n) or y.dtype != torch.float32:
+                raise ValueError(f"item {i}: x {tuple(xx.shape)} / y {tuple(y.shape)} do not fit W {w.shape}")
+            if not (xx.is_contiguous() and y.is_contiguous()):
+                raise ValueError(f"item {i}: x and y must be contiguous")
+            m0 = M if m0 is None else m0
+            d = _x_dtype(xx)
+            dt = d if dt is None else dt
+            if M != m0 or d != dt:
+                raise ValueError("all group members need the same M and activation dtype")
+            packed_bytes(w.n, w.k)
+            descs[i] = Q4GemvDesc(_ptr(w.data), _ptr(xx), _ptr(y), w.n, w.k, begin)
+            begin += w.n // ROWS
+            self._keep.append((w, xx, y))
+        if not 1 <= m0 <= 16:
+            raise ValueError("GemvGroup takes 1..16 tokens")
+        raw = np.frombuffer(bytes(descs), dtype=np.uint8)
+        self.table = torch.from_numpy(raw.copy()).to(dev)
+        self.count = len(items)
+        self.total_items = begin
+        self.M = m0
+        self.x_dtype = dt
+        self.device = dev
+        self.weight_bytes = sum(w.nbytes for w, _, _ in self._keep)
+
+    def run(self) -> None:
+        with torch.cuda.device(self.device):
+            check("q4_gemv_grouped", _lib_handle().q4_gemv_grouped(
+                _ptr(self.table), self.count, self.total_items, self.M, self.x_dtype, _stream(self.device)))
+
+    __call__ = run
+
+
+# --------------------------------------------------------------------------
+# prefill GEMM
+# --------------------------------------------------------------------------
+
+_PRECISION = {"fp16": 0, "bf16": 1}
+
+
+def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16") -> torch.Tensor:
+    """Y[T, N] = X[T, K] @ W^T for a prefill block of T tokens, fp32 out.
+
+    precision "fp16": each weight rounded once to fp16 in LDS (fp16 MFMA);
+    "bf16": the reference tile RNE_bf16(fl32(q*d+m)) (gemm_q4_dequant.h:283-286)."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() != 2 or xt.shape[1] != w.k:
+        raise ValueError(f"x must be [T, {w.k}], got {tuple(xt.shape)}")
+    T = xt.shape[0]
+    if y is None:
+        y = torch.empty((T, w.n), dtype=torch.float32, device=dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        nbytes = lib.q4_gemm_prefill_workspace_bytes(T, w.n, w.k)
+        ws = _workspace(dev, nbytes, "prefill")
+        check("q4_gemm_prefill", lib.q4_gemm_prefill(
+            _ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), T, w.n, w.k, _PRECISION[precision],
+            _ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0, _stream(dev)))
+    return y
+
+
+# --------------------------------------------------------------------------
+# routed MoE
+# --------------------------------------------------------------------------
+
+def pack_moe_experts(gate_blocks, up_blocks, down_blocks, device=None):
+    """Per-expert GGUF blocks -> (gate_up, down) PackedExperts.
+
+    gate_up expert e is one [2F, H] mx matrix whose 64-row groups alternate
+    gate rows and the same up rows (the counterpart of the reference pool's
+    interleaved up/gate stripes, moe_batch/make_test.py:35-59); down expert e
+    is [H, F]."""
+    dev = _device(device)
+    E = len(gate_blocks)
+    F, nbh, bw = np.asarray(gate_blocks[0]).shape
+    H = nbh * BLK
+    Hd, nbf, _ = np.asarray(down_blocks[0]).shape
+    if Hd != H or nbf * BLK != F:
+        raise ValueError("down must be [H, F] for gate/up [F, H]")
+    gu_bytes = packed_bytes(2 * F, H)
+    dn_bytes = packed_bytes(H, F)
+    gu = torch.empty(E * gu_bytes, dtype=torch.uint8, device=dev)
+    dn = torch.empty(E * dn_bytes, dtype=torch.uint8, device=dev)
+    for e in range(E):
+        g = np.asarray(gate_blocks[e]).reshape(F // ROWS, ROWS, nbh, bw)
+        u = np.asarray(up_blocks[e]).reshape(F // ROWS, ROWS, nbh, bw)
+        inter = np.stack([g, u], axis=1).reshape(2 * F, nbh, bw)
+        pack_q4_1(inter, dev, out=gu[e * gu_bytes:(e + 1) * gu_bytes])
+        pack_q4_1(np.asarray(down_blocks[e]), dev, out=dn[e * dn_bytes:(e + 1) * dn_bytes])
+    return PackedExperts(gu, E, 2 * F, H), PackedExperts(dn, E, H, F)
+
+
+def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[t] = sum_j w[t,j] * down_e(silu(gate_e x_t) * (up_e x_t)), e = ids[t,j]; fp32 h,
+    fp32 out [T, H] (moe_batch.py's per-slot product plus core.cpp:5150-5245's
+    gather/scatter, done on the device)."""
+    dev = gate_up.data.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    T, H = xt.shape
+    F = gate_up.n // 2
+    E = gate_up.experts
+    if H != gate_up.k or down.n != H or down.k != F or down.experts != E:
+        raise ValueError("expert shapes do not match x")
+    ids = _to_dev(topk_ids, dev, torch.int32)
+    wts = _to_dev(topk_w, dev, torch.float32)
+    if ids.dim() == 1:
+        ids, wts = ids.unsqueeze(0), wts.unsqueeze(0)
+    if ids.shape[0] != T or ids.shape != wts.shape:
+        raise ValueError("topk_ids / topk_w must be [T, topk]")
+    topk = ids.shape[1]
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        nbytes = lib.q4_moe_workspace_bytes(T, E, topk, H, F)
+        ws = _workspace(dev, nbytes, "moe")
+        check("q4_moe_gemv", lib.q4_moe_gemv(
+            _ptr(gate_up.data), _ptr(down.data), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts), _ptr(out),
+            T, E, topk, H, F, _ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0,
+            _stream(dev)))
+    return out

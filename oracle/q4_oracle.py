@@ -1,0 +1,459 @@
+r"""CPU oracle for the Q4_1 dequant-matmul path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
+may import this module, and only as the checker (or the timed CPU baseline).
+The product path (``openflowlm-next_amd``) never calls it.
+
+A numpy restatement, written from scratch, of the reference's CPU path for
+this hot path (``/root/reference`` is read as text, never imported):
+
+* GGUF Q4_1 / Q4_0 blocks        open_kernels/q4_1_pack.py:1-43, :58-101
+* fp16 -> bf16 RNE narrowing      open_kernels/q4_1_pack.py:104-109, :129-130
+* bf16 <-> f32 bit helpers        open_kernels/model/q4nx.py:95-102
+* the 5120 B pool chunk layout    open_kernels/q4_1_pack.py:16-34, :112-142
+* dequant of pool chunks          open_kernels/q4_1_pack.py:155-180,
+                                  open_kernels/model/q4nx.py:105-126,
+                                  utilities/benchmark-q4-decode.py:19-34
+* fp64 GEMV reference             open_kernels/q4_1_pack.py:183-191
+* T-token prefill reference       open_kernels/designs/gemm_q4_prefill/make_test.py:82-94
+* MoE routing + expert reference  open_kernels/model/replica.py:121-140,
+                                  open_kernels/designs/moe_batch/make_test.py:87-98
+* Q4_0 -> Q4_1 transcode          open_kernels/recipes/pack.py:606-622
+
+``ml_dtypes`` (which the reference uses for its bf16 casts) is absent here; the
+bf16 conversions are restated as IEEE round-to-nearest-even on the f32 bits.
+
+Pinning (what fixes each function independently of its own formula) is done in
+``tests/test_oracle.py``: the seed-702 scalar-loop known-answer test of
+``specs/open-engine/tests/test_q4nx_decode_layout.py:8-30``, the pack->dequant
+identity of ``q4_1_pack._selftest`` (:194-209), torch's own fp16->bf16 RNE,
+brute-force scalar loops on tiny shapes, one-hot / all-ones activations, and
+the exact Q4_0 identity m = -8 d.  Functions with no such check are marked
+"parity unpinned" in their docstrings (there are none at present).
+
+The MI355X weight layout (``pack_mx`` / ``unpack_mx``) is this build's own
+format, not the reference's; its oracle is pinned by round trips against the
+GGUF blocks and the reference pool layout.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+CH = 5120            # pool chunk bytes: 32 rows x 256 K  (q4_1_pack.py:52)
+BLK = 32             # values per GGUF block              (q4_1_pack.py:53)
+Q4_1_BYTES = 20      # fp16 d, fp16 m, 16 nibble bytes     (q4_1_pack.py:54)
+Q4_0_BYTES = 18      # fp16 d, 16 nibble bytes, min = -8 d (q4_1_pack.py:55)
+
+# MI355X layout geometry (this build's format; see pack_mx)
+MX_ROWS = 64                 # output rows per tile (a row group)
+MX_TILE = 1280               # bytes per tile: 1024 B codes + 256 B scales
+MX_CODES = 1024
+
+
+# --------------------------------------------------------------------------
+# bf16 helpers (q4nx.py:95-102)
+# --------------------------------------------------------------------------
+
+def bf16_to_f32(u16) -> np.ndarray:
+    """bf16 bit patterns -> f32 (exact widening; q4nx.py:95-96)."""
+    return (np.asarray(u16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f32) -> np.ndarray:
+    """f32 -> bf16 bit patterns, round-to-nearest-even (q4nx.py:99-102).
+
+    Finite inputs only (the path never carries NaN/Inf scales)."""
+    u = np.ascontiguousarray(np.asarray(f32, dtype=np.float32)).view(np.uint32)
+    return ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
+
+def bf16_round(f32) -> np.ndarray:
+    """f32 -> nearest bf16 value, returned as f32."""
+    return bf16_to_f32(f32_to_bf16(f32))
+
+
+# --------------------------------------------------------------------------
+# GGUF blocks (q4_1_pack.py:58-109)
+# --------------------------------------------------------------------------
+
+def random_q4_1_blocks_ref(n: int, k: int, rng: np.random.Generator, scale: float = 0.02) -> np.ndarray:
+    """The reference's synthetic Q4_1 generator, same draws in the same order
+    (q4_1_pack.py:70-81): uint8[n, k//32, 20]."""
+    assert k % BLK == 0
+    nb = k // BLK
+    d = (rng.random((n, nb), np.float32) * scale + 1e-3).astype(np.float16)
+    m = ((rng.random((n, nb), np.float32) - 0.5) * scale * 15).astype(np.float16)
+    q = rng.integers(0, 16, (n, nb, BLK), dtype=np.uint8)
+    return _assemble_q4_1(d, m, q)
+
+
+def random_q4_0_blocks_ref(n: int, k: int, rng: np.random.Generator, scale: float = 0.02) -> np.ndarray:
+    """The reference's synthetic Q4_0 generator (q4_1_pack.py:58-67): uint8[n, k//32, 18]."""
+    assert k % BLK == 0
+    nb = k // BLK
+    d = (rng.random((n, nb), np.float32) * scale + 1e-3).astype(np.float16)
+    q = rng.integers(0, 16, (n, nb, BLK), dtype=np.uint8)
+    blocks = np.empty((n, nb, Q4_0_BYTES), np.uint8)
+    blocks[..., 0:2] = d.view(np.uint8).reshape(n, nb, 2)
+    blocks[..., 2:18] = q[..., :16] | (q[..., 16:] << 4)
+    return blocks
+
+
+def baseline_q4_1_blocks(n: int, k: int, rng: np.random.Generator) -> np.ndarray:
+    """The benchmark distribution: q ~ U{0..15}, d = fp16(|N(0,1)|*0.002 + 1e-4),
+    m = fp16(-8*d*U(0.9,1.1)); uint8[n, k//32, 20].
+
+    Draw order: d, then the U(0.9,1.1) factor, then the codes."""
+    assert k % BLK == 0
+    nb = k // BLK
+    d = (np.abs(rng.standard_normal((n, nb), np.float32)) * np.float32(0.002) + np.float32(1e-4)).astype(np.float16)
+    u = rng.uniform(0.9, 1.1, (n, nb)).astype(np.float32)
+    m = (np.float32(-8.0) * d.astype(np.float32) * u).astype(np.float16)
+    q = rng.integers(0, 16, (n, nb, BLK), dtype=np.uint8)
+    return _assemble_q4_1(d, m, q)
+
+
+def _assemble_q4_1(d16: np.ndarray, m16: np.ndarray, q: np.ndarray) -> np.ndarray:
+    n, nb = d16.shape
+    blocks = np.empty((n, nb, Q4_1_BYTES), np.uint8)
+    blocks[..., 0:2] = np.ascontiguousarray(d16).view(np.uint8).reshape(n, nb, 2)
+    blocks[..., 2:4] = np.ascontiguousarray(m16).view(np.uint8).reshape(n, nb, 2)
+    blocks[..., 4:20] = q[..., :16] | (q[..., 16:] << 4)   # byte j: value j low, j+16 high
+    return blocks
+
+
+def unpack_q4_1_blocks(blocks: np.ndarray):
+    """uint8[n, nb, 20|18] -> (d f32[n,nb], m f32[n,nb], q uint8[n, nb*32]).
+
+    Q4_0 reads as m = -8 d (q4_1_pack.py:84-101)."""
+    n, nb, width = blocks.shape
+    if width not in (Q4_1_BYTES, Q4_0_BYTES):
+        raise ValueError(f"block width {width} is neither Q4_1 (20) nor Q4_0 (18)")
+    d = np.ascontiguousarray(blocks[..., 0:2]).view(np.float16).reshape(n, nb).astype(np.float32)
+    if width == Q4_1_BYTES:
+        m = np.ascontiguousarray(blocks[..., 2:4]).view(np.float16).reshape(n, nb).astype(np.float32)
+        qs = blocks[..., 4:20]
+    else:
+        m = np.float32(-8.0) * d
+        qs = blocks[..., 2:18]
+    q = np.concatenate([qs & 0xF, qs >> 4], axis=-1).reshape(n, nb * BLK)
+    return d, m, q
+
+
+def dequant_q4_1(blocks: np.ndarray, bf16_scales: bool = True) -> np.ndarray:
+    """GGUF blocks -> f32[n, k] = fl32(q*d + m) (q4_1_pack.py:104-109).
+
+    ``bf16_scales=True`` narrows d and m to bf16 first: what the kernels see."""
+    d, m, q = unpack_q4_1_blocks(blocks)
+    if bf16_scales:
+        d, m = bf16_round(d), bf16_round(m)
+    return q.astype(np.float32) * np.repeat(d, BLK, axis=1) + np.repeat(m, BLK, axis=1)
+
+
+def q4_0_to_q4_1(blocks: np.ndarray) -> np.ndarray:
+    """Exact Q4_0 (18 B) -> Q4_1 (20 B) transcode: m = -8 d, same codes
+    (recipes/pack.py:606-622 states it for the signed container form; for GGUF
+    offset-binary codes the nibbles are kept as they are)."""
+    n, nb, width = blocks.shape
+    assert width == Q4_0_BYTES
+    d16 = np.ascontiguousarray(blocks[..., 0:2]).view(np.float16).reshape(n, nb)
+    m16 = (np.float32(-8.0) * d16.astype(np.float32)).astype(np.float16)
+    out = np.empty((n, nb, Q4_1_BYTES), np.uint8)
+    out[..., 0:2] = blocks[..., 0:2]
+    out[..., 2:4] = m16.view(np.uint8).reshape(n, nb, 2)
+    out[..., 4:20] = blocks[..., 2:18]
+    return out
+
+
+# --------------------------------------------------------------------------
+# Reference pool layout (q4_1_pack.py:16-34, :112-191)
+# --------------------------------------------------------------------------
+
+def chunk_geometry(n: int, k: int, rs: int):
+    """(nch, per_band, rows0[nch], cols0[nch]) for the pool order (q4_1_pack.py:112-121)."""
+    assert k % 256 == 0 and n % (32 * rs) == 0
+    per_band = rs * k // 256
+    nch = n * k // (32 * 256)
+    c = np.arange(nch)
+    band, ci = np.divmod(c, per_band)
+    rows0 = 32 * rs * band + 32 * (ci % rs)
+    cols0 = 256 * (ci // rs)
+    return nch, per_band, rows0, cols0
+
+
+def pack_q4_1_pool(blocks: np.ndarray, rs: int) -> np.ndarray:
+    """GGUF blocks -> pool-order chunk bytes uint8[nch*5120] (q4_1_pack.py:124-142).
+
+    Chunk: d bf16[256] @0 (index kb*32+r), m bf16[256] @512, nibbles @1024 with
+    nibble p = (r//16)*4096 + k*16 + r%16, even p in the low half of byte p//2."""
+    n, nb, _ = blocks.shape
+    k = nb * BLK
+    d, m, q = unpack_q4_1_blocks(blocks)
+    d16, m16 = f32_to_bf16(d), f32_to_bf16(m)
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    # gather every chunk's [32 r, 256 k] window at once
+    r_idx = rows0[:, None] + np.arange(32)[None, :]                      # [nch, 32]
+    kb_idx = (cols0 // BLK)[:, None] + np.arange(8)[None, :]              # [nch, 8]
+    dd = d16[r_idx[:, :, None], kb_idx[:, None, :]]                       # [nch, 32 r, 8 kb]
+    mm = m16[r_idx[:, :, None], kb_idx[:, None, :]]
+    k_idx = cols0[:, None] + np.arange(256)[None, :]                      # [nch, 256]
+    qq = q[r_idx[:, :, None], k_idx[:, None, :]]                          # [nch, 32 r, 256 k]
+    qq = qq.reshape(nch, 2, 16, 256).transpose(0, 1, 3, 2).reshape(nch, 8192)  # [rb, k, r16]
+    out = np.empty((nch, CH), np.uint8)
+    out[:, 0:512] = np.ascontiguousarray(dd.transpose(0, 2, 1)).reshape(nch, 256).view(np.uint8)
+    out[:, 512:1024] = np.ascontiguousarray(mm.transpose(0, 2, 1)).reshape(nch, 256).view(np.uint8)
+    out[:, 1024:] = qq[:, 0::2] | (qq[:, 1::2] << 4)
+    return out.reshape(-1)
+
+
+def dequant_chunk(b: np.ndarray) -> np.ndarray:
+    """One 5120 B pool chunk -> f32[32 rows, 256 k] (q4_1_pack.py:155-170)."""
+    d = bf16_to_f32(np.ascontiguousarray(b[0:512]).view(np.uint16))
+    m = bf16_to_f32(np.ascontiguousarray(b[512:1024]).view(np.uint16))
+    qb = b[1024:CH]
+    nib = np.empty(8192, np.uint8)
+    nib[0::2] = qb & 0xF
+    nib[1::2] = qb >> 4
+    n3 = nib.reshape(2, 256, 16)                       # [rb, k, r16]
+    codes = n3.transpose(0, 2, 1).reshape(32, 256).astype(np.float32)   # [r, k]
+    j = (np.arange(256) // BLK)[None, :] * 32 + np.arange(32)[:, None]  # kb*32 + r
+    return codes * d[j] + m[j]
+
+
+def dequant_pool(pool: np.ndarray, n: int, k: int, rs: int) -> np.ndarray:
+    """Pool-order chunk bytes -> f32[n, k] (q4_1_pack.py:173-180)."""
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    chunks = np.asarray(pool, np.uint8).reshape(nch, CH)
+    tiles = dq_chunks_q4_1(chunks).reshape(nch, 32, 256)
+    w = np.empty((n, k), np.float32)
+    for c in range(nch):
+        w[rows0[c]:rows0[c] + 32, cols0[c]:cols0[c] + 256] = tiles[c]
+    return w
+
+
+def dq_chunks_q4_1(chunks: np.ndarray) -> np.ndarray:
+    """[n, 5120] chunk bytes -> [n, 32 row, 8 block, 32 lane] f32 (q4nx.py:105-126).
+
+    Value at (row, block, lane) = nib[p]*d[j] + m[j] with
+    p = (row//16)*4096 + block*512 + lane*16 + row%16 and j = block*32 + row."""
+    chunks = np.asarray(chunks, np.uint8)
+    nch = chunks.shape[0]
+    meta = bf16_to_f32(np.ascontiguousarray(chunks[:, :1024]).view(np.uint16))
+    d, mn = meta[:, :256], meta[:, 256:]
+    q = chunks[:, 1024:]
+    nib = np.empty((nch, 8192), dtype=np.float32)
+    nib[:, 0::2] = q & 0xF
+    nib[:, 1::2] = q >> 4
+    r = np.arange(32)[:, None, None]
+    bc = np.arange(8)[None, :, None]
+    i = np.arange(32)[None, None, :]
+    p = ((r // 16) * 4096 + bc * 512 + i * 16 + (r % 16)).reshape(-1)
+    j = np.broadcast_to(bc * 32 + r, (32, 8, 32)).reshape(-1)
+    shape = (nch, 32, 8, 32)
+    return (np.take(nib, p, axis=1).reshape(shape) * np.take(d, j, axis=1).reshape(shape)
+            + np.take(mn, j, axis=1).reshape(shape))
+
+
+def legacy_decode(chunks: np.ndarray) -> np.ndarray:
+    """The benchmark harness's strided-indexing dequant (benchmark-q4-decode.py:19-34);
+    byte-identical to dq_chunks_q4_1 by construction of the same fp32 operations."""
+    nch = chunks.shape[0]
+    meta = bf16_to_f32(np.ascontiguousarray(chunks[:, :1024]).view(np.uint16))
+    d, mn = meta[:, :256], meta[:, 256:]
+    q = chunks[:, 1024:]
+    n = np.empty((nch, 8192), dtype=np.float32)
+    n[:, 0::2] = q & 0xF
+    n[:, 1::2] = q >> 4
+    r = np.arange(32)[:, None, None]
+    bc = np.arange(8)[None, :, None]
+    i = np.arange(32)[None, None, :]
+    p = ((r // 16) * 4096 + bc * 512 + i * 16 + (r % 16)).reshape(-1)
+    j = (bc * 32 + r + 0 * i).reshape(-1)
+    s = (nch, 32, 8, 32)
+    return n[:, p].reshape(s) * d[:, j].reshape(s) + mn[:, j].reshape(s)
+
+
+def pool_reference(pool: np.ndarray, x: np.ndarray, n: int, k: int, rs: int) -> np.ndarray:
+    """y = W @ x accumulated in fp64 from the pool bytes, returned f32[n]
+    (q4_1_pack.py:183-191)."""
+    w = dequant_pool(pool, n, k, rs).astype(np.float64)
+    return (w @ np.asarray(x, np.float64)).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# References for the kernels' outputs
+# --------------------------------------------------------------------------
+
+def gemv_reference(blocks: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """Y[M, N] = X[M, K] @ W^T in fp64 from the bf16-scale dequant of the blocks
+    (pool_reference semantics, q4_1_pack.py:183-191; batched rows as in
+    designs/gemm_q4/make_test.py: every token row is an independent GEMV)."""
+    w = dequant_q4_1(blocks, bf16_scales=True).astype(np.float64)
+    xx = np.atleast_2d(np.asarray(x, np.float64))
+    return (xx @ w.T).astype(np.float32)
+
+
+def prefill_reference(blocks: np.ndarray, x_tk: np.ndarray) -> np.ndarray:
+    """Y[T, N] for T distinct token activations, fp64 from the same weights
+    (gemm_q4_prefill/make_test.py:82-94, returned token-major: the engine's
+    layout after host::transpose, core.cpp:2960)."""
+    return gemv_reference(blocks, x_tk)
+
+
+def maxrel(got: np.ndarray, ref: np.ndarray) -> float:
+    """max|got-ref| / max|ref| in fp64 (designs/gemv_q4/compare.py:13)."""
+    g = np.asarray(got, np.float64).reshape(-1)
+    r = np.asarray(ref, np.float64).reshape(-1)
+    return float(np.abs(g - r).max() / (np.abs(r).max() + 1e-30)) if r.size else 0.0
+
+
+def rel_fro(got: np.ndarray, ref: np.ndarray) -> float:
+    """||got-ref||_F / ||ref||_F (gemm_q4_prefill/compare.py:33)."""
+    g = np.asarray(got, np.float64).reshape(-1)
+    r = np.asarray(ref, np.float64).reshape(-1)
+    return float(np.linalg.norm(g - r) / (np.linalg.norm(r) + 1e-30))
+
+
+def softmax_topk(logits: np.ndarray, topk: int):
+    """Per token: p = softmax(logits); ids = argsort(-p, stable)[:topk];
+    w = p[ids] / sum(p[ids])  (replica.py:121-128 route, :135 renormalise).
+
+    Returns (ids int32[T, topk], w f32[T, topk])."""
+    lg = np.atleast_2d(np.asarray(logits, np.float64))
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :topk]
+    pw = np.take_along_axis(p, ids, axis=1)
+    w = pw / pw.sum(axis=1, keepdims=True)
+    return ids.astype(np.int32), w.astype(np.float32)
+
+
+def silu(v: np.ndarray) -> np.ndarray:
+    return v / (1.0 + np.exp(-v))
+
+
+def moe_reference(gate_w, up_w, down_w, x: np.ndarray, ids: np.ndarray, wts: np.ndarray,
+                  h_bf16: bool = False) -> np.ndarray:
+    """out[t] = sum_j wts[t,j] * down_e( silu(gate_e x_t) * (up_e x_t) ), e = ids[t,j],
+    in fp64 (replica.py:131-140 moe_decode without the shared expert; the
+    per-expert product is moe_batch/make_test.py:91-98).
+
+    ``gate_w/up_w/down_w`` are callables e -> f32 dequantized [rows, cols]
+    (or arrays indexed by e). ``h_bf16`` rounds h to bf16 as the reference's
+    moe_batch kernel does (make_test.py:96); the default keeps it in fp64 as
+    the replica does."""
+    get = (lambda a: (lambda e: a[e])) if not callable(gate_w) else None
+    g_of = get(gate_w) if get else gate_w
+    u_of = get(up_w) if get else up_w
+    d_of = get(down_w) if get else down_w
+    xx = np.atleast_2d(np.asarray(x, np.float64))
+    T = xx.shape[0]
+    out = np.zeros((T, np.asarray(d_of(int(ids[0, 0]))).shape[0]), np.float64)
+    for e in np.unique(ids):
+        toks, slots = np.nonzero(ids == e)
+        xe = xx[toks]
+        g = xe @ np.asarray(g_of(int(e)), np.float64).T
+        u = xe @ np.asarray(u_of(int(e)), np.float64).T
+        h = silu(g) * u
+        if h_bf16:
+            h = bf16_round(h.astype(np.float32)).astype(np.float64)
+        y = h @ np.asarray(d_of(int(e)), np.float64).T
+        out[toks] += np.asarray(wts, np.float64)[toks, slots][:, None] * y
+    return out.astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# The MI355X layout (this build's own format)
+# --------------------------------------------------------------------------
+#
+# An [N, K] matrix (N % 64 == 0, K % 32 == 0) is a grid of tiles (g, kb):
+# row group g = n // 64, block kb = k // 32; tile (g, kb) sits at byte
+# (g * K/32 + kb) * 1280, so one row group streams contiguously along K.
+#
+#   codes  [0, 1024): dword (lane, r) at byte lane*16 + r*4, lane 0..63, r 0..3:
+#           row n = 64 g + 16 r + lane % 16,  k = 32 kb + 8 (lane // 16) + e,
+#           e = 0..7, nibble e at bit 16*(e % 2) + 4*(e // 2).
+#   scales [1024, 1280): dword at 1024 + (lane % 16)*16 + r*4 for the same row:
+#           bits 31..16 = bf16 d, bits 15..0 = bf16 m.
+#
+# A 16x16x32 bf16 MFMA's B operand is exactly one codes dword per lane (the
+# eight k of row lane%16 in k-group lane//16), so one 128-bit load per lane
+# feeds four MFMAs (r = 0..3) and a wave streams 1 KB per load.
+
+def mx_bytes(n: int, k: int) -> int:
+    assert n % MX_ROWS == 0 and k % BLK == 0
+    return (n // MX_ROWS) * (k // BLK) * MX_TILE
+
+
+_E = np.arange(8)
+_NIB_SHIFT = 16 * (_E % 2) + 4 * (_E // 2)        # bit position of element e
+
+
+def pack_mx(blocks: np.ndarray) -> np.ndarray:
+    """GGUF Q4_1/Q4_0 blocks [N, K/32, 20|18] -> the MI355X layout bytes
+    (d and m narrowed to bf16 by RNE, as q4_1_pack.py:129-130 does)."""
+    d, m, q = unpack_q4_1_blocks(blocks)
+    return pack_mx_from_parts(f32_to_bf16(d), f32_to_bf16(m), q)
+
+
+def unpack_mx(packed: np.ndarray, n: int, k: int):
+    """MI355X layout bytes -> (d16 uint16[n,kb], m16 uint16[n,kb], q uint8[n,k])."""
+    nb = k // BLK
+    G = n // MX_ROWS
+    t = np.asarray(packed, np.uint8).reshape(G, nb, MX_TILE)
+    codes = np.ascontiguousarray(t[:, :, :MX_CODES]).view(np.uint32).reshape(G, nb, 4, 16, 4)  # [G,kb,kg,i,r]
+    sc = np.ascontiguousarray(t[:, :, MX_CODES:]).view(np.uint32).reshape(G, nb, 16, 4)        # [G,kb,i,r]
+    dw = codes.transpose(0, 4, 3, 1, 2).reshape(n, nb, 4)                                       # [n, kb, kg]
+    q = np.empty((n, nb, 4, 8), np.uint8)
+    for e in range(8):
+        q[..., e] = (dw >> np.uint32(_NIB_SHIFT[e])) & np.uint32(0xF)
+    s = sc.transpose(0, 3, 2, 1).reshape(n, nb)
+    return (s >> np.uint32(16)).astype(np.uint16), (s & np.uint32(0xFFFF)).astype(np.uint16), q.reshape(n, k)
+
+
+def dequant_mx(packed: np.ndarray, n: int, k: int) -> np.ndarray:
+    """MI355X layout -> f32[n, k] = fl32(q*d + m) with the stored bf16 d, m."""
+    d16, m16, q = unpack_mx(packed, n, k)
+    d = np.repeat(bf16_to_f32(d16), BLK, axis=1)
+    m = np.repeat(bf16_to_f32(m16), BLK, axis=1)
+    return q.astype(np.float32) * d + m
+
+
+def pool_to_blocks(pool: np.ndarray, n: int, k: int, rs: int):
+    """Invert pack_q4_1_pool to (d16, m16, q): bf16 scales [n, k/32], codes [n, k]."""
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    ch = np.asarray(pool, np.uint8).reshape(nch, CH)
+    d16 = np.empty((n, k // BLK), np.uint16)
+    m16 = np.empty((n, k // BLK), np.uint16)
+    q = np.empty((n, k), np.uint8)
+    dd = np.ascontiguousarray(ch[:, 0:512]).view(np.uint16).reshape(nch, 8, 32)
+    mm = np.ascontiguousarray(ch[:, 512:1024]).view(np.uint16).reshape(nch, 8, 32)
+    nib = np.empty((nch, 8192), np.uint8)
+    nib[:, 0::2] = ch[:, 1024:] & 0xF
+    nib[:, 1::2] = ch[:, 1024:] >> 4
+    qq = nib.reshape(nch, 2, 256, 16).transpose(0, 1, 3, 2).reshape(nch, 32, 256)
+    for c in range(nch):
+        r0, c0 = int(rows0[c]), int(cols0[c])
+        d16[r0:r0 + 32, c0 // BLK:c0 // BLK + 8] = dd[c].T
+        m16[r0:r0 + 32, c0 // BLK:c0 // BLK + 8] = mm[c].T
+        q[r0:r0 + 32, c0:c0 + 256] = qq[c]
+    return d16, m16, q
+
+
+def pack_mx_from_parts(d16: np.ndarray, m16: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """(bf16 d bits [N, K/32], bf16 m bits, codes uint8[N, K]) -> MI355X layout bytes."""
+    n, nb = d16.shape
+    assert n % MX_ROWS == 0 and q.shape == (n, nb * BLK)
+    G = n // MX_ROWS
+    q5 = q.reshape(n, nb, 4, 8).astype(np.uint32)
+    dw = np.zeros((n, nb, 4), np.uint32)                                # [n, kb, kg]
+    for e in range(8):
+        dw |= q5[..., e] << np.uint32(_NIB_SHIFT[e])
+    sc = (d16.astype(np.uint32) << np.uint32(16)) | m16.astype(np.uint32)   # [n, kb]
+    # n = 64 G + 16 r + i;  codes dword index within a tile = (kg*16 + i)*4 + r
+    codes = dw.reshape(G, 4, 16, nb, 4).transpose(0, 3, 4, 2, 1)          # [G, kb, kg, i, r]
+    sc = sc.reshape(G, 4, 16, nb).transpose(0, 3, 2, 1)                   # [G, kb, i, r]
+    out = np.empty((G, nb, MX_TILE), np.uint8)
+    out[:, :, :MX_CODES] = np.ascontiguousarray(codes).reshape(G, nb, 256).view(np.uint8).reshape(G, nb, MX_CODES)
+    out[:, :, MX_CODES:] = np.ascontiguousarray(sc).reshape(G, nb, 64).view(np.uint8).reshape(G, nb, 256)
+    return out.reshape(-1)

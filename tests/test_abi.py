@@ -1,0 +1,90 @@
+"""The C ABI: libq4mi.so loads on a CPU-only host, exports every function
+include/q4mi.h declares, and rejects bad arguments before touching the GPU."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "q4mi.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "defined")))
+
+
+def test_header_declares_the_expected_surface():
+    names = declared_functions()
+    for must in ("q4_packed_bytes", "q4_repack", "q4_repack_pool", "q4_dequant", "q4_gemv",
+                 "q4_gemv_grouped", "q4_gemm_prefill", "q4_moe_gemv"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared in q4mi.h but not exported: {missing}"
+
+
+def test_python_binding_covers_the_header(pkg):
+    from importlib import import_module
+    sigs = import_module("openflowlm-next_amd._lib").SIGNATURES
+    assert set(declared_functions()) <= set(sigs)
+
+
+def test_version_and_strerror(lib):
+    assert lib.q4mi_version() >= 100
+    for code in (0, -1, -2, -3, -4, -5):
+        assert lib.q4mi_strerror(code)
+    assert lib.q4mi_strerror(-99) == b"unknown status"
+
+
+@pytest.mark.parametrize("n,k,want", [(64, 32, 1280), (4096, 4096, 4096 * 4096 * 5 // 8),
+                                      (128256, 4096, 128256 * 4096 * 5 // 8), (0, 32, 0),
+                                      (63, 32, -1), (64, 48, -1), (-64, 32, -1), (64, 0, -1)])
+def test_packed_bytes(lib, n, k, want):
+    assert lib.q4_packed_bytes(n, k) == want
+
+
+def test_argument_errors_before_any_launch(lib):
+    """Every one of these returns before a HIP call (no GPU needed)."""
+    fake = C.c_void_p(0x1000)   # never dereferenced: each call fails validation first
+    assert lib.q4_repack(fake, 19, fake, 64, 32, 0, None) == -2          # block width
+    assert lib.q4_repack(fake, 20, fake, 64, 32, 1, None) == -2          # scale mode
+    assert lib.q4_repack(None, 20, fake, 64, 32, 0, None) == -2          # NULL
+    assert lib.q4_repack(fake, 20, fake, 96, 32, 0, None) == -1          # N % 64
+    assert lib.q4_repack(fake, 20, fake, 64, 40, 0, None) == -1          # K % 32
+    assert lib.q4_repack(None, 20, None, 0, 32, 0, None) == 0            # empty is a no-op
+    assert lib.q4_repack_pool(fake, 2, fake, 64, 128, None) == -1        # K % 256
+    assert lib.q4_repack_pool(fake, 0, fake, 64, 256, None) == -2        # rs
+    assert lib.q4_repack_pool(fake, 4, fake, 64, 256, None) == -1        # N % (32 rs)
+    assert lib.q4_dequant(fake, None, 64, 32, None) == -2
+    assert lib.q4_dequant(None, None, 0, 32, None) == 0
+    assert lib.q4_gemv(fake, fake, 2, fake, 1, 64, 32, None, 0, None) == -2    # dtype
+    assert lib.q4_gemv(fake, fake, 1, fake, 17, 64, 32, None, 0, None) == -5   # M > 16
+    assert lib.q4_gemv(fake, fake, 1, fake, 1, 100, 32, None, 0, None) == -1   # N % 64
+    assert lib.q4_gemv(None, None, 1, None, 0, 64, 32, None, 0, None) == 0     # M = 0
+    # a short matrix is split along K and needs the workspace the query reports
+    need = lib.q4_gemv_workspace_bytes(1, 4096, 4096)
+    assert need > 0
+    assert lib.q4_gemv(fake, fake, 1, fake, 1, 4096, 4096, None, 0, None) == -3
+    assert lib.q4_gemv(fake, fake, 1, fake, 1, 4096, 4096, fake, need - 1, None) == -3
+    assert lib.q4_gemv_grouped(None, 1, 1, 1, 1, None) == -2
+    assert lib.q4_gemv_grouped(fake, 1, 1, 17, 1, None) == -5
+
+
+def test_gemv_workspace_query(lib):
+    assert lib.q4_gemv_workspace_bytes(1, 128256, 4096) == 0     # enough row groups: no split
+    assert lib.q4_gemv_workspace_bytes(16, 4096, 14336) >= 16 * 4096 * 4 * 2
+    assert lib.q4_gemv_workspace_bytes(0, 64, 32) == 0
+
+
+def test_loader_fails_loudly_without_the_library(tmp_path):
+    from importlib import import_module
+    L = import_module("openflowlm-next_amd._lib")
+    with pytest.raises(ImportError):
+        L.load(tmp_path / "libq4mi.so")

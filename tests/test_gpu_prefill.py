@@ -1,0 +1,108 @@
+"""GPU parity of the prefill dequant GEMM against the fp64 oracle.
+
+Bars: precision "fp16" (default) maxrel <= 1e-3 (the north star's bar) against
+Y from the same bytes in fp64 over T distinct token activations
+(gemm_q4_prefill/make_test.py:82-94); precision "bf16" (the reference's own
+bf16 tile, gemm_q4_dequant.h:283-286) is held to the reference's rel_fro <= 5e-3
+gate (gemm_q4_prefill/compare.py:26) and to bit-exact agreement with an fp64
+product over the bf16-rounded weights to fp32 accumulation noise.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _x(rng, T, K):
+    return torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("T,N,K", [(1, 64, 32), (17, 128, 256), (256, 512, 1024), (300, 1024, 2048),
+                                   (512, 2560, 2560), (128, 4096, 14336)])
+def test_prefill_fp16_matches_oracle(gpu, pkg, oracle, T, N, K):
+    say(f"prefill fp16 T={T} N={N} K={K}")
+    rng = np.random.default_rng(T + N + K)
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    X = _x(rng, T, K)
+    assert len({X[t].view(torch.int16).numpy().tobytes() for t in range(T)}) == T
+    w = pkg.pack_q4_1(blocks, gpu)
+    Y = pkg.gemm_q4_prefill(w, X.to(gpu)).cpu().numpy()
+    ref = oracle.prefill_reference(blocks, X.to(torch.float32).numpy())
+    assert Y.shape == (T, N) and np.isfinite(Y).all()
+    mr = oracle.maxrel(Y, ref)
+    assert mr <= 1e-3, mr
+
+
+def test_prefill_reference_generator_weights(gpu, pkg, oracle):
+    """The reference's own fixture recipe: random_q4_1_blocks (seed 0) packed to
+    the pool at rs=2, T distinct tokens, fp64 reference from the pool bytes."""
+    say("prefill reference fixture qkv T=256")
+    rng = np.random.default_rng(0)
+    N, K, T = 2560, 2560, 256
+    blocks = oracle.random_q4_1_blocks_ref(N, K, rng)
+    pool = oracle.pack_q4_1_pool(blocks, 2)
+    X = torch.from_numpy(np.stack([rng.standard_normal(K).astype(np.float32) for _ in range(T)])).to(torch.bfloat16)
+    w = pkg.pack_q4_1_pool(pool, N, K, 2, gpu)
+    Y = pkg.gemm_q4_prefill(w, X.to(gpu)).cpu().numpy()
+    Wd = oracle.dequant_pool(pool, N, K, 2).astype(np.float64)
+    ref = (X.to(torch.float32).numpy().astype(np.float64) @ Wd.T).astype(np.float32)
+    assert oracle.maxrel(Y, ref) <= 1e-3
+    assert oracle.rel_fro(Y, ref) <= 5e-3
+
+
+def test_prefill_bf16_mode_is_the_reference_tile(gpu, pkg, oracle):
+    say("prefill bf16 mode")
+    rng = np.random.default_rng(5)
+    N, K, T = 512, 2048, 256
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    X = _x(rng, T, K)
+    w = pkg.pack_q4_1(blocks, gpu)
+    Y = pkg.gemm_q4_prefill(w, X.to(gpu), precision="bf16").cpu().numpy()
+    Wb = oracle.bf16_round(oracle.dequant_q4_1(blocks)).astype(np.float64)   # RNE_bf16(fl32(q*d+m))
+    exact_tile = (X.to(torch.float32).numpy().astype(np.float64) @ Wb.T)
+    assert oracle.maxrel(Y, exact_tile) < 1e-5            # fp32 accumulation noise only
+    ref = oracle.prefill_reference(blocks, X.to(torch.float32).numpy())
+    assert oracle.rel_fro(Y, ref) <= 5e-3                 # the reference's prefill gate
+
+
+def test_prefill_f32_activations_and_large_values(gpu, pkg, oracle):
+    """fp32 X, and a token whose max |x| is far beyond fp16's range: the row
+    is scaled by a power of two on the way in and back on the way out."""
+    say("prefill f32 + large tokens")
+    rng = np.random.default_rng(6)
+    N, K, T = 256, 1024, 40
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    X[3] *= 1e6
+    X[7, 5] = 3e5
+    w = pkg.pack_q4_1(blocks, gpu)
+    Y = pkg.gemm_q4_prefill(w, torch.from_numpy(X).to(gpu)).cpu().numpy()
+    ref = oracle.prefill_reference(blocks, X)
+    assert np.isfinite(Y).all()
+    for t in range(T):
+        assert oracle.maxrel(Y[t], ref[t]) <= 1e-3, t
+
+
+def test_prefill_agrees_with_decode_gemm(gpu, pkg, oracle):
+    """Both paths compute the same product; the decode path keeps exact codes."""
+    say("prefill vs gemm_q4")
+    rng = np.random.default_rng(8)
+    N, K, T = 1024, 4096, 16
+    w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(N, K, rng), gpu)
+    X = _x(rng, T, K).to(gpu)
+    a = pkg.gemm_q4_prefill(w, X).cpu().numpy()
+    b = pkg.gemm_q4(w, X).cpu().numpy()
+    assert oracle.maxrel(a, b) <= 1e-3
+
+
+def test_prefill_empty(gpu, pkg, oracle):
+    say("prefill empty")
+    rng = np.random.default_rng(9)
+    w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(64, 64, rng), gpu)
+    Y = pkg.gemm_q4_prefill(w, torch.zeros(0, 64, dtype=torch.bfloat16, device=gpu))
+    assert Y.shape == (0, 64)
