@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the Q4_1 dequant-matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--extras 0,2,3,4|none]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--extras 0,2,3,4|none] [--no-cpu]
 
 Headline: the Llama-3-8B decode weight sweep at
 M=1 -- 32 layers of q/k/v/o/gate/up/down plus lm_head, 4.69 GB of Q4_1
@@ -13,9 +13,14 @@ measured time, inputs resident in HBM. The same JSON line carries:
                   duration from HIP events on its stream, against 8 TB/s;
 * cpu_baseline -- the oracle's numpy restatement of the reference CPU path
                   (pool-chunk dequant as q4nx.py:105-126, then an f32 matvec)
-                  timed on this host over one Llama layer (136 MB of Q4_1);
-* extras       -- configs 0 (single GEMV), 2 (M = 4/8/16), 3 (prefill GEMM
-                  TFLOP/s), 4 (routed MoE) and the per-stage decode issue order.
+                  timed on this host over one Llama layer, 15 passes;
+* extras       -- the same sweep issued stage by stage as a decode step would
+                  (fused qkv, o, fused gate/up, down per layer, lm_head: 129
+                  GEMV calls), config 0 (single GEMV), config 2 (M = 4/8/16),
+                  config 3 (prefill GEMM TFLOP/s) and config 4 (routed MoE).
+                  Multi-launch extras are captured in a HIP graph and timed
+                  over replays (after checking a replay against the eager run),
+                  so host launch overhead is not what they measure.
 
 Runs on one GPU only: --gpus above 1 exits with a message.
 """
@@ -34,7 +39,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 / fp16 MFMA, TFLOP/s
+MFMA_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 / fp16 MFMA, TFLOP/s
 
 LLAMA_LAYER = [  # (name, N, K) per layer of Llama-3-8B
     ("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
@@ -42,6 +47,21 @@ LLAMA_LAYER = [  # (name, N, K) per layer of Llama-3-8B
 ]
 LM_HEAD = ("lm_head", 128256, 4096)
 SEED = 1234
+
+
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_grouped_llama3_8b_m1.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (counter runs cannot happen inside this process)."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -66,62 +86,77 @@ def gen_blocks(torch, n: int, k: int, gen, dev):
     return blocks
 
 
-def build_sweep(torch, q4, dev, M: int = 1, layers: int = 32, weights=None):
-    """The Llama-3-8B sweep: (GemvGroup for the whole sweep, staged groups, bytes).
+class Llama:
+    """Packed Llama-3-8B weights. q/k/v live in one [6144, 4096] buffer and
+    gate/up in one [28672, 4096] buffer: mx row groups are contiguous, so the
+    fused matrix and its row slices are the same bytes."""
 
-    x inputs follow the decode dataflow: q/k/v share one x, gate/up share one,
-    o, down and lm_head have their own; every matrix has its own y."""
+    def __init__(self, torch, q4, dev, layers: int = 32):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED)
+        self.layers = []
+        for _ in range(layers):
+            qkv = torch.empty(q4.packed_bytes(6144, 4096), dtype=torch.uint8, device=dev)
+            gu = torch.empty(q4.packed_bytes(28672, 4096), dtype=torch.uint8, device=dev)
+            parts = {}
+            off = {"qkv": 0, "gu": 0}
+            for name, n, k in LLAMA_LAYER:
+                nb = q4.packed_bytes(n, k)
+                if name in ("q", "k", "v", "gate", "up"):
+                    buf = qkv if name in ("q", "k", "v") else gu
+                    key = "qkv" if name in ("q", "k", "v") else "gu"
+                    dst = buf[off[key]:off[key] + nb]
+                    off[key] += nb
+                else:
+                    dst = torch.empty(nb, dtype=torch.uint8, device=dev)
+                parts[name] = q4.pack_q4_1(gen_blocks(torch, n, k, gen, dev), dev, out=dst)
+            parts["qkv"] = q4.PackedQ4(qkv, 6144, 4096)
+            parts["gate_up"] = q4.PackedQ4(gu, 28672, 4096)
+            self.layers.append(parts)
+        self.head = q4.pack_q4_1(gen_blocks(torch, LM_HEAD[1], LM_HEAD[2], gen, dev), dev)
+        torch.cuda.synchronize()
+        self.weight_bytes = sum(p[n].nbytes for p in self.layers for n, _, _ in LLAMA_LAYER) + self.head.nbytes
+        self.matrices = len(self.layers) * len(LLAMA_LAYER) + 1
+
+
+def sweep_inputs(torch, model, dev, M: int):
+    """Activations of one decode step (q/k/v share x, gate/up share x) and outputs."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED + M)
-    if weights is None:
-        weights = []
-        for layer in range(layers):
-            for name, n, k in LLAMA_LAYER:
-                blocks = gen_blocks(torch, n, k, gen, dev)
-                weights.append((f"{name}{layer}", q4.pack_q4_1(blocks, dev)))
-                del blocks
-        blocks = gen_blocks(torch, LM_HEAD[1], LM_HEAD[2], gen, dev)
-        weights.append((LM_HEAD[0], q4.pack_q4_1(blocks, dev)))
-        del blocks
-        torch.cuda.synchronize()
 
     def act(k):
         return torch.randn(M, k, generator=gen, device=dev).to(torch.bfloat16)
+    per_layer = []
+    for _ in model.layers:
+        per_layer.append({"in": act(4096), "o": act(4096), "mlp": act(4096), "dn": act(14336)})
+    return per_layer, act(4096)
 
-    items, stages, nbytes = [], [], 0
-    wi = iter(weights)
-    for layer in range(layers):
-        x_in, x_o, x_mlp, x_dn = act(4096), act(4096), act(4096), act(14336)
-        xs = {"q": x_in, "k": x_in, "v": x_in, "o": x_o, "gate": x_mlp, "up": x_mlp, "down": x_dn}
-        per = {}
+
+def grouped_sweep(torch, q4, model, acts, xhead, M: int):
+    """One GemvGroup over all 225 matrices; returns (group, algorithmic bytes)."""
+    dev = model.head.device
+    items, nbytes = [], 0
+    which = {"q": "in", "k": "in", "v": "in", "o": "o", "gate": "mlp", "up": "mlp", "down": "dn"}
+    for parts, xs in zip(model.layers, acts):
         for name, n, k in LLAMA_LAYER:
-            _, w = next(wi)
             y = torch.empty(M, n, dtype=torch.float32, device=dev)
-            it = (w, xs[name], y)
-            items.append(it)
-            per[name] = it
-            nbytes += w.nbytes + M * k * 2 + M * n * 4
-        stages += [[per["q"], per["k"], per["v"]], [per["o"]], [per["gate"], per["up"]], [per["down"]]]
-    _, w = next(wi)
+            items.append((parts[name], xs[which[name]], y))
+            nbytes += parts[name].nbytes + M * k * 2 + M * n * 4
     y = torch.empty(M, LM_HEAD[1], dtype=torch.float32, device=dev)
-    it = (w, act(4096), y)
-    items.append(it)
-    stages.append([it])
-    nbytes += w.nbytes + M * 4096 * 2 + M * LM_HEAD[1] * 4
-    return q4.GemvGroup(items), [q4.GemvGroup(s) for s in stages], nbytes, weights
+    items.append((model.head, xhead, y))
+    nbytes += model.head.nbytes + M * 4096 * 2 + M * LM_HEAD[1] * 4
+    return q4.GemvGroup(items), nbytes
 
 
 def time_launches(torch, fn, steps: int, warmup: int):
-    """Run fn warmup times, then `steps` timed times bracketed by synchronize;
-    each call is bracketed by HIP events on the current stream.
-    Returns (total_ms_wall_by_events, mean_ms_per_call)."""
+    """warmup calls, then `steps` calls each bracketed by HIP events on the
+    current stream. Returns (total ms between the outer events, mean ms per call)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(st)
     for a, b in ev:
         a.record(st)
@@ -129,9 +164,44 @@ def time_launches(torch, fn, steps: int, warmup: int):
         b.record(st)
     t1.record(st)
     torch.cuda.synchronize()
-    total = t0.elapsed_time(t1)
-    per = sum(a.elapsed_time(b) for a, b in ev) / steps
-    return total, per
+    return t0.elapsed_time(t1), sum(a.elapsed_time(b) for a, b in ev) / steps
+
+
+def graph_time(torch, fn, outputs, replays: int = 20) -> float:
+    """Capture fn() in a HIP graph, check one replay against the eager run
+    (bit for bit: every kernel here is deterministic), then time `replays`
+    replays with events. Returns mean ms per replay."""
+    fn()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outputs]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        fn()
+    torch.cuda.synchronize()
+    for o in outputs:
+        o.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    for o, e in zip(outputs, eager):
+        if not torch.equal(o, e):
+            raise RuntimeError("graph replay differs from the eager run")
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(replays):
+        g.replay()
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / replays
 
 
 # --------------------------------------------------------------------------
@@ -139,45 +209,46 @@ def time_launches(torch, fn, steps: int, warmup: int):
 # process so the BLAS thread count can be set before numpy loads
 # --------------------------------------------------------------------------
 
-def cpu_baseline_child(threads: int) -> dict:
+def cpu_baseline_child(threads: int, passes: int) -> dict:
     import numpy as np
     from oracle import q4_oracle as O
     rng = np.random.default_rng(SEED)
-    total_bytes, secs = 0, 0.0
-    chunk_slice = 2048                       # 10 MB of chunks -> 64 MB of f32 at a time
-    for name, n, k in LLAMA_LAYER:
+    layer = []
+    for name, n, k in LLAMA_LAYER:                       # one layer in pool-chunk form (rs = 1 band order)
         nch = n * k // 8192
         chunks = rng.integers(0, 256, (nch, 5120), dtype=np.uint8)
         d = (np.abs(rng.standard_normal((nch, 256))) * 0.002 + 1e-4).astype(np.float16).astype(np.float32)
-        m = -8 * d * rng.uniform(0.9, 1.1, (nch, 256)).astype(np.float32)
+        m = (-8 * d * rng.uniform(0.9, 1.1, (nch, 256))).astype(np.float16).astype(np.float32)
         chunks[:, 0:512] = O.f32_to_bf16(d).view(np.uint8).reshape(nch, 512)
-        chunks[:, 512:1024] = O.f32_to_bf16(m.astype(np.float16).astype(np.float32)).view(np.uint8).reshape(nch, 512)
-        x = rng.standard_normal(k).astype(np.float32)
-        # rs=1 band order: chunk c covers rows 32*(c // (k/256)), k-tile c % (k/256)
-        per_row = k // 256
-        y = np.zeros(n, np.float32)
-        t = time.perf_counter()
-        for c0 in range(0, nch, chunk_slice):
-            c1 = min(nch, c0 + chunk_slice)
-            w = O.dq_chunks_q4_1(chunks[c0:c1]).reshape(c1 - c0, 32, 256)
+        chunks[:, 512:1024] = O.f32_to_bf16(m).view(np.uint8).reshape(nch, 512)
+        layer.append((n, k, chunks, rng.standard_normal(k).astype(np.float32)))
+    chunk_slice = 2048                                   # 10 MB of chunks -> 64 MB of f32 at a time
+    total_bytes, t = 0, time.perf_counter()
+    for _ in range(passes):
+        for n, k, chunks, x in layer:
+            per_row = k // 256                           # chunk c: rows 32 (c // per_row), k-tile c % per_row
             xs = x.reshape(per_row, 256)
-            kt = np.arange(c0, c1) % per_row
-            part = np.matmul(w, xs[kt][:, :, None])[..., 0]             # [c, 32] f32
-            rows = (np.arange(c0, c1) // per_row)
-            np.add.at(y.reshape(-1, 32), rows, part)
-        secs += time.perf_counter() - t
-        total_bytes += nch * 5120
-    return {"seconds": secs, "bytes": total_bytes, "gbs": total_bytes / secs / 1e9, "threads": threads}
+            y = np.zeros((n // 32, 32), np.float32)
+            for c0 in range(0, chunks.shape[0], chunk_slice):
+                c1 = min(chunks.shape[0], c0 + chunk_slice)
+                w = O.dq_chunks_q4_1(chunks[c0:c1]).reshape(c1 - c0, 32, 256)
+                cc = np.arange(c0, c1)
+                part = np.matmul(w, xs[cc % per_row][:, :, None])[..., 0]
+                np.add.at(y, cc // per_row, part)
+            total_bytes += chunks.nbytes
+    secs = time.perf_counter() - t
+    return {"seconds": secs, "bytes": total_bytes, "gbs": total_bytes / secs / 1e9, "threads": threads,
+            "passes": passes}
 
 
-def cpu_baseline(threads: int) -> dict | None:
+def cpu_baseline(threads: int, passes: int) -> dict | None:
     env = dict(os.environ)
     for v in ("OPENBLAS_NUM_THREADS", "OMP_NUM_THREADS", "MKL_NUM_THREADS"):
         env[v] = str(threads)
     env["HIP_VISIBLE_DEVICES"] = ""      # the CPU leg never touches the GPU
     try:
-        r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-child", str(threads)],
-                           capture_output=True, text=True, env=env, timeout=600)
+        r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-child", str(threads),
+                            "--cpu-passes", str(passes)], capture_output=True, text=True, env=env, timeout=900)
         if r.returncode != 0:
             log(f"cpu baseline failed: {r.stderr[-500:]}")
             return None
@@ -191,37 +262,85 @@ def cpu_baseline(threads: int) -> dict | None:
 # extras
 # --------------------------------------------------------------------------
 
+def extra_staged(torch, q4, model, acts, xhead):
+    """The sweep as a decode step issues it: per layer fused qkv, o, fused
+    gate/up, down (each its own q4_gemv call, split along K where short), then
+    lm_head -- 129 calls, one HIP graph."""
+    dev = model.head.device
+    calls, outs, nbytes = [], [], 0
+    for parts, xs in zip(model.layers, acts):
+        for wname, xname in (("qkv", "in"), ("o", "o"), ("gate_up", "mlp"), ("down", "dn")):
+            w = parts[wname]
+            y = torch.empty(1, w.n, dtype=torch.float32, device=dev)
+            calls.append((w, xs[xname], y))
+            outs.append(y)
+            nbytes += w.nbytes + w.k * 2 + w.n * 4
+    y = torch.empty(1, model.head.n, dtype=torch.float32, device=dev)
+    calls.append((model.head, xhead, y))
+    outs.append(y)
+    nbytes += model.head.nbytes + 4096 * 2 + model.head.n * 4
+    wsz = max(q4.gemv_workspace_bytes(1, w.n, w.k) for w, _, _ in calls)
+    ws = torch.empty(max(wsz, 256), dtype=torch.uint8, device=dev)
+
+    def run():
+        for w, x, y in calls:
+            q4.gemm_q4(w, x, y, workspace=ws)
+    ms = graph_time(torch, run, outs, replays=10)
+    return {"ms": ms, "gbs": nbytes / ms / 1e6, "calls": len(calls), "bytes": nbytes}
+
+
+def extra_peaks(torch, dev):
+    """On-box reference points: HBM read bandwidth of a plain reduction over
+    4 GiB (torch.sum, reads only) and dense bf16 GEMM throughput of the vendor
+    library (torch.matmul, 8192^3, hipBLASLt) -- measured, beside the vendor peaks."""
+    x = torch.ones(1 << 30, dtype=torch.float32, device=dev)
+    _, ms = time_launches(torch, lambda: x.sum(), 10, 3)
+    read_gbs = x.numel() * 4 / ms / 1e6
+    del x
+    a = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
+    b = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
+    _, ms2 = time_launches(torch, lambda: a @ b, 10, 3)
+    return {"hbm_read_gbs_torch_sum": read_gbs, "bf16_gemm_tflops_torch_matmul": 2 * 8192 ** 3 / ms2 / 1e9,
+            "vendor_hbm_gbs": HBM_PEAK_GBS, "vendor_bf16_tflops": MFMA_PEAK_TFLOPS}
+
+
 def extra_config0(torch, q4, dev):
-    """Single GEMV N=K=4096, fp32 x: cache-resident and over 32 rotated copies (335 MB)."""
+    """Single GEMV N=K=4096 with fp32 x: the same weights over and over
+    (cache-resident) and 32 rotating copies (335 MB, beyond the 256 MB MALL)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED)
-    ws = [q4.pack_q4_1(gen_blocks(torch, 4096, 4096, gen, dev), dev) for _ in range(32)]
+    ws_w = [q4.pack_q4_1(gen_blocks(torch, 4096, 4096, gen, dev), dev) for _ in range(32)]
     x = torch.randn(4096, generator=gen, device=dev)
-    y = torch.empty(4096, device=dev)
-    nbytes = ws[0].nbytes + 4096 * 4 + 4096 * 4
-    _, hot = time_launches(torch, lambda: q4.gemv_q4(ws[0], x, y), 50, 10)
-    i = [0]
+    ys = [torch.empty(4096, device=dev) for _ in range(32)]
+    ws = torch.empty(max(q4.gemv_workspace_bytes(1, 4096, 4096), 256), dtype=torch.uint8, device=dev)
+    nbytes = ws_w[0].nbytes + 4096 * 4 + 4096 * 4
+
+    def hot():
+        for i in range(32):
+            q4.gemv_q4(ws_w[0], x, ys[i], workspace=ws)
 
     def rot():
-        q4.gemv_q4(ws[i[0] % 32], x, y)
-        i[0] += 1
-    _, cold = time_launches(torch, rot, 64, 32)
-    return {"cache_resident_us": hot * 1e3, "cache_resident_gbs": nbytes / hot / 1e6,
-            "rotated_us": cold * 1e3, "rotated_gbs": nbytes / cold / 1e6}
+        for i in range(32):
+            q4.gemv_q4(ws_w[i], x, ys[i], workspace=ws)
+    hot_us = graph_time(torch, hot, ys) / 32 * 1e3
+    rot_us = graph_time(torch, rot, ys) / 32 * 1e3
+    return {"cache_resident_us": hot_us, "cache_resident_gbs": nbytes / hot_us / 1e3,
+            "rotated_us": rot_us, "rotated_gbs": nbytes / rot_us / 1e3,
+            "splits": q4.gemv_workspace_bytes(1, 4096, 4096) // (4096 * 4)}
 
 
-def extra_config2(torch, q4, dev, weights, steps):
+def extra_config2(torch, q4, model, steps):
     out = {}
     for M in (4, 8, 16):
-        grp, _, nbytes, _ = build_sweep(torch, q4, dev, M=M, weights=weights)
+        acts, xhead = sweep_inputs(torch, model, model.head.device, M)
+        grp, nbytes = grouped_sweep(torch, q4, model, acts, xhead, M)
         _, per = time_launches(torch, grp.run, steps, 2)
-        out[f"M{M}"] = {"ms": per, "gbs": nbytes / per / 1e6, "tflops": 2 * M * 7.505e9 / per / 1e9}
+        out[f"M{M}"] = {"ms": per, "gbs": nbytes / per / 1e6, "tflops": 2 * M * model.weight_bytes * 1.6 / per / 1e9}
+        del grp, acts
     return out
 
 
 def extra_config3(torch, q4, dev):
-    if not hasattr(q4.load_library(), "q4_gemm_prefill"):
-        return None
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED)
     out = {}
@@ -231,23 +350,27 @@ def extra_config3(torch, q4, dev):
         for name, (n, k) in mats.items():
             x = torch.randn(T, k, generator=gen, device=dev).to(torch.bfloat16)
             y = torch.empty(T, n, device=dev)
-            _, per = time_launches(torch, lambda: q4.gemm_q4_prefill(packed[name], x, y), 10, 3)
-            out[f"T{T}_{name}"] = {"ms": per, "tflops": 2.0 * T * n * k / per / 1e9}
+            ws = torch.empty(q4.prefill_workspace_bytes(T, n, k), dtype=torch.uint8, device=dev)
+
+            def run():
+                for _ in range(3):
+                    q4.gemm_q4_prefill(packed[name], x, y, workspace=ws)
+            ms = graph_time(torch, run, [y], replays=5) / 3
+            tf = 2.0 * T * n * k / ms / 1e9
+            out[f"T{T}_{name}"] = {"ms": ms, "tflops": tf, "frac_of_peak": tf / MFMA_PEAK_TFLOPS}
     return out
 
 
 def extra_config4(torch, q4, dev):
-    if not hasattr(q4.load_library(), "q4_moe_gemv"):
-        return None
     import numpy as np
     E, K8, H, F, T, pools = 128, 8, 2048, 768, 16, 4
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED)
     experts = []
+    gb, db = q4.packed_bytes(2 * F, H), q4.packed_bytes(H, F)
     for _ in range(pools):             # 4 independent expert pools (4 x 377 MB) defeat the 256 MB MALL
-        gu = torch.empty(E * q4.packed_bytes(2 * F, H), dtype=torch.uint8, device=dev)
-        dn = torch.empty(E * q4.packed_bytes(H, F), dtype=torch.uint8, device=dev)
-        gb, db = q4.packed_bytes(2 * F, H), q4.packed_bytes(H, F)
+        gu = torch.empty(E * gb, dtype=torch.uint8, device=dev)
+        dn = torch.empty(E * db, dtype=torch.uint8, device=dev)
         for e in range(E):
             q4.pack_q4_1(gen_blocks(torch, 2 * F, H, gen, dev), dev, out=gu[e * gb:(e + 1) * gb])
             q4.pack_q4_1(gen_blocks(torch, H, F, gen, dev), dev, out=dn[e * db:(e + 1) * db])
@@ -262,18 +385,17 @@ def extra_config4(torch, q4, dev):
     ids_t = torch.from_numpy(ids.astype(np.int32)).to(dev)
     w_t = torch.from_numpy(w.astype(np.float32)).to(dev)
     x = torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16)
-    out = torch.empty(T, H, device=dev)
+    outs = [torch.empty(T, H, device=dev) for _ in range(pools)]
+    ws = torch.empty(q4.moe_workspace_bytes(T, E, K8, H, F), dtype=torch.uint8, device=dev)
     distinct = len(np.unique(ids))
-    nbytes = distinct * (q4.packed_bytes(2 * F, H) + q4.packed_bytes(H, F)) + T * H * 2 + T * H * 4
-    i = [0]
+    nbytes = distinct * (gb + db) + T * H * 2 + T * H * 4
 
     def run():
-        gu, dn = experts[i[0] % pools]
-        q4.moe_batch(gu, dn, x, ids_t, w_t, out)
-        i[0] += 1
-    _, per = time_launches(torch, run, 40, 8)
-    return {"ms": per, "gbs": nbytes / per / 1e6, "distinct_experts": distinct, "bytes": nbytes,
-            "tflops": 2.0 * T * K8 * 3 * H * F / per / 1e9}
+        for i, (gu, dn) in enumerate(experts):
+            q4.moe_batch(gu, dn, x, ids_t, w_t, outs[i], workspace=ws)
+    ms = graph_time(torch, run, outs, replays=10) / pools
+    return {"ms": ms, "gbs": nbytes / ms / 1e6, "distinct_experts": distinct, "bytes": nbytes,
+            "tflops": 2.0 * T * K8 * 3 * H * F / ms / 1e9}
 
 
 # --------------------------------------------------------------------------
@@ -283,13 +405,18 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="0,2,3,4", help="comma list of configs to add, or 'none'")
+    ap.add_argument("--extras", default="staged,0,2,3,4,peaks", help="comma list (staged,0,2,3,4,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-passes", type=int, default=15, help="passes over one layer in the CPU baseline")
     ap.add_argument("--cpu-baseline-child", type=int, default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--only-extras", action="store_true",
+                    help="skip the headline sweep; run the --extras list and print them (profiling runs)")
+    ap.add_argument("--copy-probe", type=int, default=0,
+                    help="only copy this many bytes device-to-device 5 times (calibrates HBM traffic counters)")
     a = ap.parse_args()
 
     if a.cpu_baseline_child is not None:
-        print(json.dumps(cpu_baseline_child(a.cpu_baseline_child)))
+        print(json.dumps(cpu_baseline_child(a.cpu_baseline_child, a.cpu_passes)))
         return 0
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or ws != 1:
@@ -302,59 +429,78 @@ def main() -> int:
     q4.load_library()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if a.copy_probe:
+        src = torch.randint(0, 256, (a.copy_probe,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": a.copy_probe, "copies": 5}))
+        return 0
 
-    log("building the Llama-3-8B sweep (4.69 GB of Q4_1 weights) ...")
-    grp, stages, nbytes, weights = build_sweep(torch, q4, dev, M=1)
-    wbytes = sum(w.nbytes for _, w in weights)
-    log(f"{len(weights)} matrices, {wbytes / 1e9:.3f} GB weights; timing {a.steps} steps")
+    if a.only_extras:
+        out = {}
+        for cfg in [c.strip() for c in a.extras.split(",") if c.strip()]:
+            if cfg == "0":
+                out["config0_gemv_4096_f32x"] = extra_config0(torch, q4, dev)
+            elif cfg == "3":
+                out["config3_prefill"] = extra_config3(torch, q4, dev)
+            elif cfg == "4":
+                out["config4_moe"] = extra_config4(torch, q4, dev)
+            elif cfg == "peaks":
+                out["measured_peaks"] = extra_peaks(torch, dev)
+        print(json.dumps(out), flush=True)
+        return 0
 
-    torch.cuda.synchronize()
+    log("packing the Llama-3-8B weights (4.69 GB of Q4_1) ...")
+    model = Llama(torch, q4, dev)
+    acts, xhead = sweep_inputs(torch, model, dev, 1)
+    grp, nbytes = grouped_sweep(torch, q4, model, acts, xhead, 1)
+    log(f"{model.matrices} matrices, {model.weight_bytes / 1e9:.3f} GB; timing {a.steps} steps")
+
     total_ms, per_launch_ms = time_launches(torch, grp.run, a.steps, a.warmup)
     ms_per_step = total_ms / a.steps
     value = nbytes / (ms_per_step * 1e-3) / 1e9            # GB/s, whole job
-    achieved = nbytes / (per_launch_ms * 1e-3) / 1e9        # one launch == one step here
+    achieved = nbytes / (per_launch_ms * 1e-3) / 1e9        # one launch == one step
 
-    def staged():
-        for s in stages:
-            s.run()
-    _, staged_ms = time_launches(torch, staged, max(3, a.steps // 4), 2)
-    extras = {"config1_staged_129_launches": {"ms": staged_ms, "gbs": nbytes / staged_ms / 1e6}}
-
+    extras = {}
     wanted = [] if a.extras == "none" else [s.strip() for s in a.extras.split(",") if s.strip()]
     for cfg in wanted:
         t = time.perf_counter()
         try:
-            if cfg == "0":
-                extras["config0_gemv_4096"] = extra_config0(torch, q4, dev)
+            if cfg == "peaks":
+                extras["measured_peaks"] = extra_peaks(torch, dev)
+            elif cfg == "staged":
+                extras["config1_staged_decode_order"] = extra_staged(torch, q4, model, acts, xhead)
+            elif cfg == "0":
+                extras["config0_gemv_4096_f32x"] = extra_config0(torch, q4, dev)
             elif cfg == "2":
-                extras["config2_skinny"] = extra_config2(torch, q4, dev, weights, max(3, a.steps // 4))
+                extras["config2_skinny"] = extra_config2(torch, q4, model, max(3, a.steps // 4))
             elif cfg == "3":
-                r = extra_config3(torch, q4, dev)
-                if r:
-                    extras["config3_prefill"] = r
+                extras["config3_prefill"] = extra_config3(torch, q4, dev)
             elif cfg == "4":
-                r = extra_config4(torch, q4, dev)
-                if r:
-                    extras["config4_moe"] = r
+                extras["config4_moe"] = extra_config4(torch, q4, dev)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
-        log(f"extra config {cfg}: {time.perf_counter() - t:.1f}s")
+        log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")
+        torch.cuda.empty_cache()
 
     cpu = None
     if not a.no_cpu:
-        log("CPU baseline (numpy restatement, 1 thread) ...")
-        c1 = cpu_baseline(1)
-        cores = os.cpu_count() or 1
-        log(f"CPU baseline (all {cores} cores) ...")
-        call = cpu_baseline(cores)
+        log(f"CPU baseline: numpy restatement, 1 thread, {a.cpu_passes} passes over one layer ...")
+        c1 = cpu_baseline(1, a.cpu_passes)
+        cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+        log(f"CPU baseline: all {cores} cores ...")
+        call = cpu_baseline(cores, max(3, a.cpu_passes // 3))
         if c1:
-            cpu = {"value": c1["gbs"], "unit": "GB/s", "cores": 1, "kind": "port",
-                   "sample": f"one Llama-3-8B layer (q,k,v,o,gate,up,down; {c1['bytes'] / 1e6:.1f} MB Q4_1): "
-                             "pool-chunk dequant (q4nx.dq_chunks_q4_1 restated) + f32 matvec, "
-                             "OPENBLAS_NUM_THREADS=1",
-                   "seconds": c1["seconds"]}
+            cpu = {"value": round(c1["gbs"], 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                   "sample": f"{c1['passes']} passes over one Llama-3-8B layer (q,k,v,o,gate,up,down; "
+                             f"{c1['bytes'] / c1['passes'] / 1e6:.1f} MB of Q4_1 each): pool-chunk dequant "
+                             "(q4nx.dq_chunks_q4_1 restated) + f32 matvec, OPENBLAS_NUM_THREADS=1",
+                   "seconds": round(c1["seconds"], 2)}
             if call:
-                cpu["all_cores"] = {"value": call["gbs"], "cores": cores, "seconds": call["seconds"]}
+                cpu["all_cores"] = {"value": round(call["gbs"], 4), "cores": cores,
+                                    "seconds": round(call["seconds"], 2), "passes": call["passes"]}
 
     line = {
         "metric": "Q4_1 decode GEMV HBM GB/s (% of peak) at M=1; prefill GEMM TFLOP/s",
@@ -371,11 +517,13 @@ def main() -> int:
         "data": "synthetic (seeded GGUF Q4_1 weights: q~U{0..15}, d=fp16(|N|*0.002+1e-4), m=fp16(-8dU(0.9,1.1)); "
                 "bf16 N(0,1) activations)",
         "config": {"workload": "llama3-8b decode weight sweep, M=1, 32 layers + lm_head, one grouped launch/step",
-                   "matrices": len(weights), "weight_bytes": wbytes, "algorithmic_bytes_per_step": nbytes,
-                   "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
+                   "matrices": model.matrices, "weight_bytes": model.weight_bytes,
+                   "algorithmic_bytes_per_step": nbytes, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_grouped_kernel<1,bf16>", "mean_launch_ms": round(per_launch_ms, 4)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/gemv_grouped_llama3_8b_m1.md (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, "
+                                       "factors from a 1 GiB copy)",
+                     "kernel": "gemv_grouped_kernel<1,false>", "mean_launch_ms": round(per_launch_ms, 4)},
         "cpu_baseline": cpu,
         "extras": extras,
     }

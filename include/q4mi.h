@@ -8,8 +8,8 @@
  * Every function returns Q4MI_OK (0) or a negative Q4MI_E* code. All device
  * memory belongs to the caller; the library never allocates. Work is enqueued
  * on `stream` and is asynchronous to the host; the functions are re-entrant
- * and keep no global state apart from the counters inside a caller-owned
- * workspace (calls that share one workspace must be ordered on one stream).
+ * and keep no global state (calls that share one caller-owned workspace must
+ * be ordered on one stream).
  *
  * Weights live in the "mx" layout (see q4_packed_bytes): an [N, K] matrix,
  * N % 64 == 0, K % 32 == 0, cut into tiles of 64 rows x 32 K (one GGUF block
@@ -83,11 +83,11 @@ int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed,
  * dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:155-180, q4nx.py:105-126). */
 int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
 
-/* Workspace bytes q4_gemv needs for (M, N, K); 0 when it needs none. The
- * workspace starts with a fixed 16 KB region of arrival counters: zero-fill
- * the buffer once before its first use; every q4_gemv call leaves those
- * counters at zero again, whatever its shape. Do not hand the same buffer to
- * another function in between (it would overwrite the counters). */
+/* Workspace bytes q4_gemv needs for (M, N, K); 0 when it needs none (enough
+ * 64-row groups to fill the GPU). A short matrix is split along K: the
+ * workspace holds the per-split partial sums, which a second launch adds in
+ * split order. No initial contents are needed; calls sharing one workspace
+ * must be ordered on one stream. */
 size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K);
 
 /* Decode GEMV / skinny GEMM: Y[M][N] = X[M][K] . W[N][K]^T, fp32 accumulate,

@@ -2,10 +2,12 @@
 // 1 <= M <= 16, fp32 accumulate (inner loop in gemv_core.h).
 //
 // Work item = one 64-row group over a K range, one 256-thread workgroup.
-// K splits (S > 1, for matrices too short to fill 256 CUs): each workgroup
-// writes its partial sums to the workspace; the last of the S workgroups of a
-// row group (counted with a device-scope atomic) adds the S partials in split
-// order, so the result does not depend on arrival order.
+// K splits (S > 1, for matrices too short to fill 256 CUs): the GEMV kernel
+// writes each split's partial sums to the workspace and a second, tiny kernel
+// adds the S partials in split order, so the result does not depend on the
+// order the workgroups ran in. (Finishing in the last-arriving workgroup
+// instead needs device-scope fences, which on gfx950 write back and
+// invalidate the L2 of every XCD -- far slower than the extra launch.)
 #include <stdlib.h>
 
 #include "gemv_core.h"
@@ -23,53 +25,33 @@ struct GemvParams {
     int S;
     int64_t N, K;
     float* part;      // [S][M][N] partial sums (S > 1)
-    uint32_t* cnt;    // [N/64] arrival counters (S > 1)
 };
 
 
-// Store the row group's result, or hand it to the split reduction.
+// Store the row group's result (S == 1) or this split's partial sums.
 template <int NTL>
-__device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4][NTL][64], const GemvParams& P,
-                                            float* __restrict__ y, int64_t N, int64_t g, int s, int S) {
+__device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4][NTL][64], int M,
+                                            float* __restrict__ y, int64_t N, int64_t g) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int64_t n = g * 64 + r * 16 + i16;
-    const int M = P.M;
     float v[NTL];
     wave_sum<NTL>(acc, red, v);
-    if (S == 1) {
-#pragma unroll
-        for (int j = 0; j < NTL; ++j) {
-            const int tok = kg * 4 + j;
-            if (tok < M) y[(int64_t)tok * N + n] = v[j];
-        }
-        return;
-    }
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
         const int tok = kg * 4 + j;
-        if (tok < M) __hip_atomic_store(&P.part[((int64_t)s * M + tok) * N + n], v[j], __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
+        if (tok < M) y[(int64_t)tok * N + n] = v[j];
     }
-    __shared__ int last;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = (atomicAdd(&P.cnt[g], 1u) == (unsigned)(S - 1));
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-#pragma unroll
-    for (int j = 0; j < NTL; ++j) {
-        const int tok = kg * 4 + j;
-        if (tok < M) {
-            float acc_s = 0.f;
-            for (int q = 0; q < S; ++q)
-                acc_s += __hip_atomic_load(&P.part[((int64_t)q * M + tok) * N + n], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-            y[(int64_t)tok * N + n] = acc_s;
-        }
-    }
-    if (tid == 0) __hip_atomic_store(&P.cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// y[t][n] = sum over s = 0..S-1 of part[s][t][n], in split order.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                           int64_t MN, int S) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= MN) return;
+    float s = 0.f;
+    for (int q = 0; q < S; ++q) s += part[(int64_t)q * MN + i];
+    y[i] = s;
 }
 
 template <int NTL, bool XF32>
@@ -87,7 +69,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
     gemv_rows<NTL, XF32>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
-    gemv_finish<NTL>(acc, red, P, P.y, P.N, g, s, S);
+    float* out = S == 1 ? P.y : P.part + (int64_t)s * P.M * P.N;
+    gemv_finish<NTL>(acc, red, P.M, out, P.N, g);
 }
 
 template <int NTL, bool XF32>
@@ -109,9 +92,7 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const q4_gemv_desc* _
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
     gemv_rows<NTL, XF32>(D.packed, D.x, DenseRows{M}, D.K, g, 0, (int)(D.K >> 5), acc);
-    GemvParams P{};
-    P.M = M;
-    gemv_finish<NTL>(acc, red, P, D.y, D.N, g, 0, 1);
+    gemv_finish<NTL>(acc, red, M, D.y, D.N, g);
 }
 
 // Workgroups to aim for when a matrix has few row groups.
@@ -124,11 +105,7 @@ int64_t target_workgroups() {
     return t;
 }
 
-// The workspace starts with a fixed region of arrival counters (one per row
-// group), so a call of any shape finds its counters at the same place, left
-// at zero by the previous call; partial sums follow it.
 constexpr int64_t kMaxSplitGroups = 4096;                 // row groups a split call may have
-constexpr size_t kCounterBytes = kMaxSplitGroups * 4;     // 16 KB
 
 int choose_splits(int64_t N, int64_t K) {
     const int64_t G = N / 64, KB = K / 32;
@@ -143,7 +120,7 @@ int choose_splits(int64_t N, int64_t K) {
 size_t workspace_for(int M, int64_t N, int64_t K, int S) {
     (void)K;
     if (S <= 1) return 0;
-    return kCounterBytes + (size_t)S * M * N * sizeof(float);
+    return (size_t)S * M * N * sizeof(float);
 }
 
 template <int NTL>
@@ -184,8 +161,7 @@ extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float*
     if (S > 1) {
         const size_t need = workspace_for(M, N, K, S);
         if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
-        P.cnt = (uint32_t*)workspace;
-        P.part = (float*)((char*)workspace + kCounterBytes);
+        P.part = (float*)workspace;
     }
     const dim3 grid((unsigned)((N / 64) * S));
     const hipStream_t st = (hipStream_t)stream;
@@ -195,6 +171,12 @@ extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float*
         case 2: launch_gemv<2>(xf32, grid, st, P); break;
         case 3: launch_gemv<3>(xf32, grid, st, P); break;
         default: launch_gemv<4>(xf32, grid, st, P); break;
+    }
+    if (S > 1) {
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        const int64_t MN = (int64_t)M * N;
+        hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)ceil_div(MN, 256)), dim3(256), 0, st, P.part, y, MN,
+                           S);
     }
     return launch_status();
 }

@@ -18,13 +18,17 @@
 // output per block, i.e. twice the MFMA time of the same block at
 // 512 MAC/clk vs 16 FMA/clk per SIMD, so it cannot reach the MFMA roofline.
 //
-// Tiling: a 256-thread workgroup computes BN weight rows x BT tokens, its four
-// waves 2x2 over that tile. Per 32-K step every wave of the group turns the
-// mx codes of its 64-row group into 16-bit weights and stores them to LDS;
-// activations are copied to LDS; both are double buffered so the global loads
-// and the dequant of step k+1 overlap the MFMAs of step k (one barrier per
-// step). LDS rows are 40 halves (80 B) so a 16-lane ds_read_b128 phase hits
-// distinct banks.
+// Tiling: a workgroup computes BN weight rows x BT tokens with WGN x WGT
+// waves. Per LDS stage (KS blocks of 32 K) the waves turn the stage's mx
+// tiles (one 64-row group x 32 K each) into 16-bit weights in LDS and copy
+// the activations to LDS; stages are double buffered so the global loads and
+// the dequant of stage s+1 overlap the MFMAs of stage s, with one barrier per
+// stage. The default variant runs 8 waves (two per SIMD, 128x64 wave tiles),
+// so one wave's dequant and LDS traffic hide behind the other's MFMAs. LDS
+// rows are padded by 8 halves so a 16-lane ds_read_b128 phase hits distinct
+// banks.
+#include <stdlib.h>
+
 #include "q4mi_device.h"
 #include "q4mi_internal.h"
 
@@ -34,7 +38,6 @@ namespace {
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-constexpr int kLdsStride = 40;     // halves per LDS row: 32 k + 8 pad
 constexpr uint32_t kMagic1024 = 0x64006400u;   // fp16 1024.0 in both halves
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
@@ -72,41 +75,60 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, uint32_t s, uint32_t nib2,
     return out;
 }
 
-template <int BN, int BT, int PREC>
-__global__ __launch_bounds__(256) void prefill_kernel(const uint8_t* __restrict__ packed,
-                                                      const uint16_t* __restrict__ x16,
-                                                      const float* __restrict__ tscale, float* __restrict__ y,
-                                                      int T, int N, int K, int tiles_t) {
-    constexpr int WN = BN / 2, WT = BT / 2;          // wave tile
+// BN x BT workgroup tile, WGN x WGT waves (wave tile BN/WGN x BT/WGT), KS
+// 32-K blocks per LDS stage.
+template <int BN, int BT, int WGN, int WGT, int KS, int PREC>
+__global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* __restrict__ packed,
+                                                                 const uint16_t* __restrict__ x16,
+                                                                 const float* __restrict__ tscale,
+                                                                 float* __restrict__ y, int T, int N, int K,
+                                                                 int tiles_t) {
+    constexpr int NT = 64 * WGN * WGT, NW = WGN * WGT;
+    constexpr int WN = BN / WGN, WT = BT / WGT;      // wave tile
     constexpr int FN = WN / 16, FT = WT / 16;        // 16-wide fragments per wave
     constexpr int RG = BN / 64;                      // mx row groups per workgroup tile
-    constexpr int XCH = BT * 4 / 256;                // 16-byte activation chunks per thread
+    constexpr int WTILES = RG * KS;                  // mx tiles per stage
+    constexpr int WPW = (WTILES + NW - 1) / NW;      // mx tiles per wave per stage
+    constexpr int BK = 32 * KS;
+    constexpr int STR = BK + 8;                      // halves per LDS row (pad: conflict-free b128 reads)
+    constexpr int XCH = BT * KS * 4 / NT;            // 16-byte activation chunks per thread per stage
+    static_assert(XCH * NT == BT * KS * 4, "activation chunks must divide evenly");
     typedef typename std::conditional<PREC == 0, f16x8, bf16x8>::type frag_t;
 
-    __shared__ __attribute__((aligned(16))) uint16_t wl[2][BN * kLdsStride];
-    __shared__ __attribute__((aligned(16))) uint16_t xl[2][BT * kLdsStride];
+    __shared__ __attribute__((aligned(16))) uint16_t wl[2][BN * STR];
+    __shared__ __attribute__((aligned(16))) uint16_t xl[2][BT * STR];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 1, wt = wave >> 1;
+    const int wn = wave % WGN, wt = wave / WGN;
     const int bt = blockIdx.x % tiles_t, bn = blockIdx.x / tiles_t;
     const int n0 = bn * BN, t0 = bt * BT;
-    const int KB = K >> 5;
+    const int KB = K >> 5, NSTAGE = KB / KS;
     const int G = N >> 6;
     const int i16 = lane & 15, kg = lane >> 4;
 
-    // this thread's mx row group (waves beyond RG have none) and activation chunks
-    const bool has_w = wave < RG;
-    const int rg = min(n0 / 64 + (has_w ? wave : 0), G - 1);         // clamp ragged N
-    const uint8_t* wbase = packed + (int64_t)rg * KB * kTileBytes;
+    // this wave's mx tiles: tile u = wave + NW*i -> (row group u % RG, block u / RG of the stage)
+    const uint8_t* wbase[WPW];
+    int wrow[WPW], wcol[WPW];
+    bool wown[WPW];
+#pragma unroll
+    for (int i = 0; i < WPW; ++i) {
+        const int u = wave + NW * i;
+        wown[i] = u < WTILES;
+        const int rgl = u % RG, kbl = u / RG;
+        const int rg = min(n0 / 64 + rgl, G - 1);                       // clamp ragged N
+        wbase[i] = packed + ((int64_t)rg * KB + kbl) * kTileBytes;
+        wrow[i] = rgl * 64 + i16;
+        wcol[i] = kbl * 32 + kg * 8;
+    }
     const int coff = lane * 16, soff = kCodeBytes + i16 * 16;
     const uint16_t* xsrc[XCH];
     int xdst[XCH];
 #pragma unroll
     for (int c = 0; c < XCH; ++c) {
-        const int ch = tid + 256 * c, tok = ch >> 2, part = ch & 3;
+        const int ch = tid + NT * c, tok = ch / (KS * 4), part = ch % (KS * 4);
         xsrc[c] = x16 + (int64_t)min(t0 + tok, T - 1) * K + part * 8;
-        xdst[c] = tok * kLdsStride + part * 8;
+        xdst[c] = tok * STR + part * 8;
     }
     const uint32_t nib2 = vgpr_const(kNib2);
     const uint32_t magic = vgpr_const(PREC == 0 ? kMagic1024 : kMagic128);
@@ -117,23 +139,29 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int j = 0; j < FT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 wc = {}, ws = {};
+    u32x4 wc[WPW], wsc[WPW];
     u32x4 xr[XCH];
-    auto gload = [&](int ks) {
-        if (has_w) {
-            const uint8_t* tp = wbase + (int64_t)ks * kTileBytes;
-            wc = load_nt_u32x4(tp + coff);
-            ws = load_nt_u32x4(tp + soff);
+    auto gload = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < WPW; ++i) {
+            if (wown[i]) {
+                const uint8_t* tp = wbase[i] + (int64_t)st * KS * kTileBytes;
+                wc[i] = load_nt_u32x4(tp + coff);
+                wsc[i] = load_nt_u32x4(tp + soff);
+            }
         }
 #pragma unroll
-        for (int c = 0; c < XCH; ++c) xr[c] = *(const u32x4*)(xsrc[c] + ks * 32);
+        for (int c = 0; c < XCH; ++c) xr[c] = *(const u32x4*)(xsrc[c] + st * BK);
     };
     auto lstore = [&](int buf) {
-        if (has_w) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const u32x4 v = dequant8<PREC>(wc[r], ws[r], nib2, magic);
-                *(u32x4*)&wl[buf][(wave * 64 + r * 16 + i16) * kLdsStride + kg * 8] = v;
+        for (int i = 0; i < WPW; ++i) {
+            if (wown[i]) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const u32x4 v = dequant8<PREC>(wc[i][r], wsc[i][r], nib2, magic);
+                    *(u32x4*)&wl[buf][(wrow[i] + r * 16) * STR + wcol[i]] = v;
+                }
             }
         }
 #pragma unroll
@@ -143,21 +171,24 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint8_t* __restrict_
     gload(0);
     lstore(0);
     __syncthreads();
-    for (int ks = 0; ks < KB; ++ks) {
-        const int buf = ks & 1;
-        const bool more = ks + 1 < KB;
-        if (more) gload(ks + 1);
-        frag_t a[FN], b[FT];
+    for (int st = 0; st < NSTAGE; ++st) {
+        const int buf = st & 1;
+        const bool more = st + 1 < NSTAGE;
+        if (more) gload(st + 1);
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
-            a[i] = *(const frag_t*)&wl[buf][(wn * WN + i * 16 + i16) * kLdsStride + kg * 8];
+        for (int kk = 0; kk < KS; ++kk) {
+            frag_t a[FN], b[FT];
 #pragma unroll
-        for (int j = 0; j < FT; ++j)
-            b[j] = *(const frag_t*)&xl[buf][(wt * WT + j * 16 + i16) * kLdsStride + kg * 8];
+            for (int i = 0; i < FN; ++i)
+                a[i] = *(const frag_t*)&wl[buf][(wn * WN + i * 16 + i16) * STR + kk * 32 + kg * 8];
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
+            for (int j = 0; j < FT; ++j)
+                b[j] = *(const frag_t*)&xl[buf][(wt * WT + j * 16 + i16) * STR + kk * 32 + kg * 8];
 #pragma unroll
-            for (int j = 0; j < FT; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FT; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+        }
         if (more) lstore(buf ^ 1);
         __syncthreads();
     }
@@ -222,37 +253,60 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
     }
 }
 
-struct TileChoice {
-    int bn, bt;
+// Kernel variants: (BN, BT, waves along N, waves along T, 32-K blocks per stage).
+struct TileCfg {
+    int bn, bt, wgn, wgt, ks;
 };
+constexpr TileCfg kCfgs[] = {
+    {256, 256, 2, 4, 2},     // 8 waves, 128x64 wave tiles, 64-K stages
+    {256, 128, 2, 4, 2},     // 8 waves, 128x32
+    {128, 256, 2, 4, 2},     // 8 waves, 64x64
+    {128, 128, 2, 4, 2},     // 8 waves, 64x32
+    {256, 256, 2, 2, 1},     // 4 waves, 128x128 wave tiles, 32-K stages
+};
+constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-// Pick the workgroup tile that keeps the most of 256 CUs busy for this shape.
-TileChoice choose_tile(int T, int N) {
-    const TileChoice c[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
-    const double eff[] = {1.0, 0.92, 0.92, 0.8};   // per-workgroup MFMA efficiency guess by tile
+// Pick the variant that keeps the most of 256 CUs busy (Q4MI_PREFILL_CFG overrides).
+int choose_cfg(int T, int N, int K) {
+    static int forced = [] {
+        const char* e = getenv("Q4MI_PREFILL_CFG");
+        return e ? atoi(e) : -1;
+    }();
+    if (forced >= 0 && forced < kNumCfgs && K % (32 * kCfgs[forced].ks) == 0) return forced;
+    const double eff[] = {1.0, 0.9, 0.9, 0.75, 0.8};   // relative per-workgroup efficiency
     double best = 1e300;
-    TileChoice pick = c[3];
-    for (int i = 0; i < 4; ++i) {
-        const int64_t wgs = ceil_div(N, c[i].bn) * ceil_div(T, c[i].bt);
+    int pick = 4;
+    for (int i = 0; i < kNumCfgs; ++i) {
+        if (K % (32 * kCfgs[i].ks)) continue;
+        const int64_t wgs = ceil_div(N, kCfgs[i].bn) * ceil_div(T, kCfgs[i].bt);
         const int64_t rounds = ceil_div(wgs, 256);
-        const double cost = (double)rounds * c[i].bn * c[i].bt / eff[i];
+        const double cost = (double)rounds * kCfgs[i].bn * kCfgs[i].bt / eff[i];
         if (cost < best) {
             best = cost;
-            pick = c[i];
+            pick = i;
         }
     }
     return pick;
 }
 
-template <int BN, int BT>
-void launch_tile(int prec, int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const float* ts,
-                 float* y, int T, int N, int K, int tiles_t) {
-    if (prec == 0)
-        hipLaunchKernelGGL((prefill_kernel<BN, BT, 0>), dim3((unsigned)grid), dim3(256), 0, st, w, x16, ts, y, T,
-                           N, K, tiles_t);
-    else
-        hipLaunchKernelGGL((prefill_kernel<BN, BT, 1>), dim3((unsigned)grid), dim3(256), 0, st, w, x16, ts, y, T,
-                           N, K, tiles_t);
+template <int C, int PREC>
+void launch_cfg(int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const float* ts, float* y,
+                int T, int N, int K, int tiles_t) {
+    constexpr TileCfg c = kCfgs[C];
+    hipLaunchKernelGGL((prefill_kernel<c.bn, c.bt, c.wgn, c.wgt, c.ks, PREC>), dim3((unsigned)grid),
+                       dim3(64 * c.wgn * c.wgt), 0, st, w, x16, ts, y, T, N, K, tiles_t);
+}
+
+template <int PREC>
+void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const float* ts,
+                    float* y, int T, int N, int K, int tiles_t) {
+    switch (cfg) {
+        case 0: launch_cfg<0, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+        case 1: launch_cfg<1, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+        case 2: launch_cfg<2, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+        case 3: launch_cfg<3, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+        default: launch_cfg<4, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+    }
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -287,13 +341,11 @@ extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype
         else hipLaunchKernelGGL((prefill_xprep<false, 1>), dim3(T), dim3(256), 0, st, x, x16, ts, (int)K);
     }
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-    const TileChoice tc = choose_tile(T, (int)N);
-    const int tiles_t = (int)ceil_div(T, tc.bt);
-    const int64_t grid = ceil_div(N, tc.bn) * tiles_t;
+    const int cfg = choose_cfg(T, (int)N, (int)K);
+    const int tiles_t = (int)ceil_div(T, kCfgs[cfg].bt);
+    const int64_t grid = ceil_div(N, kCfgs[cfg].bn) * tiles_t;
     const float* tsp = precision == 0 ? ts : nullptr;
-    if (tc.bn == 256 && tc.bt == 256) launch_tile<256, 256>(precision, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
-    else if (tc.bn == 256) launch_tile<256, 128>(precision, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
-    else if (tc.bt == 256) launch_tile<128, 256>(precision, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
-    else launch_tile<128, 128>(precision, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
+    if (precision == 0) launch_prefill<0>(cfg, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
+    else launch_prefill<1>(cfg, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
     return launch_status();
 }

@@ -30,6 +30,7 @@ from ._lib import Q4MI_BF16, Q4MI_F32, Q4GemvDesc, check
 __all__ = [
     "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
+    "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes",
 ]
 
 ROWS = 64          # rows per mx tile / row group
@@ -169,17 +170,39 @@ _WS: dict = {}
 
 
 def _workspace(dev: torch.device, nbytes: int, op: str) -> torch.Tensor | None:
-    """A zero-filled scratch buffer per (operator, device, stream): operators
-    never share one, because q4_gemv keeps its arrival counters (left at zero
-    by every call) at the start of its workspace."""
+    """A cached scratch buffer per (operator, device, stream), grown on demand
+    (never allocated by the C library itself)."""
     if nbytes == 0:
         return None
     key = (op, dev.index, torch.cuda.current_stream(dev).cuda_stream)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _WS[key] = ws
     return ws
+
+
+def _ws_arg(dev, nbytes: int, op: str, workspace):
+    """(pointer, size) of the caller's workspace, else of the cached one."""
+    if workspace is None:
+        ws = _workspace(dev, nbytes, op)
+        return (_ptr(ws), ws.numel()) if ws is not None else (None, 0)
+    if workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, {nbytes} needed")
+    return _ptr(workspace), workspace.numel() * workspace.element_size()
+
+
+def gemv_workspace_bytes(m: int, n: int, k: int) -> int:
+    """Bytes of workspace gemm_q4 / gemv_q4 needs for this shape (0: none)."""
+    return int(_lib_handle().q4_gemv_workspace_bytes(m, n, k))
+
+
+def prefill_workspace_bytes(t: int, n: int, k: int) -> int:
+    return int(_lib_handle().q4_gemm_prefill_workspace_bytes(t, n, k))
+
+
+def moe_workspace_bytes(t: int, e: int, topk: int, h: int, f: int) -> int:
+    return int(_lib_handle().q4_moe_workspace_bytes(t, e, topk, h, f))
 
 
 def _x_dtype(x: torch.Tensor) -> int:
@@ -202,9 +225,10 @@ def _acts(x, dev: torch.device) -> torch.Tensor:
 # decode GEMV / skinny GEMM
 # --------------------------------------------------------------------------
 
-def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None) -> torch.Tensor:
+def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y[M, N] = X[M, K] @ W^T for 1 <= M <= 16 decode tokens, fp32 out
-    (gemm_q4.py:164-197's operator, logical [M, N] order)."""
+    (gemm_q4.py:164-197's operator, logical [M, N] order). ``workspace``
+    (>= gemv_workspace_bytes) avoids the cached one, e.g. under graph capture."""
     dev = w.device
     xt = _acts(x, dev)
     if xt.dim() == 1:
@@ -218,20 +242,18 @@ def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None) -> torch.Tensor:
         y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
-        nbytes = lib.q4_gemv_workspace_bytes(M, w.n, w.k)
-        ws = _workspace(dev, nbytes, "gemv")
-        check("q4_gemv", lib.q4_gemv(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), M, w.n, w.k,
-                                     _ptr(ws) if ws is not None else None,
-                                     ws.numel() if ws is not None else 0, _stream(dev)))
+        wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        check("q4_gemv", lib.q4_gemv(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), M, w.n, w.k, wp, wn,
+                                     _stream(dev)))
     return y
 
 
-def gemv_q4(w: PackedQ4, x, y: torch.Tensor | None = None) -> torch.Tensor:
+def gemv_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """y[N] = W[N, K] @ x[K], fp32 out (gemv_q4.py:118-123: pool in, bf16 x in, f32 y out)."""
     xt = _acts(x, w.device)
     if xt.dim() != 1:
         raise ValueError("gemv_q4 takes one activation vector x[K]")
-    out = gemm_q4(w, xt.unsqueeze(0), None if y is None else y.view(1, -1))
+    out = gemm_q4(w, xt.unsqueeze(0), None if y is None else y.view(1, -1), workspace)
     return out.view(-1)
 
 
@@ -295,7 +317,8 @@ class GemvGroup:
 _PRECISION = {"fp16": 0, "bf16": 1}
 
 
-def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16") -> torch.Tensor:
+def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16",
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y[T, N] = X[T, K] @ W^T for a prefill block of T tokens, fp32 out.
 
     precision "fp16": each weight rounded once to fp16 in LDS (fp16 MFMA);
@@ -309,11 +332,10 @@ def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: st
         y = torch.empty((T, w.n), dtype=torch.float32, device=dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
-        nbytes = lib.q4_gemm_prefill_workspace_bytes(T, w.n, w.k)
-        ws = _workspace(dev, nbytes, "prefill")
+        wp, wn = _ws_arg(dev, lib.q4_gemm_prefill_workspace_bytes(T, w.n, w.k), "prefill", workspace)
         check("q4_gemm_prefill", lib.q4_gemm_prefill(
-            _ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), T, w.n, w.k, _PRECISION[precision],
-            _ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0, _stream(dev)))
+            _ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), T, w.n, w.k, _PRECISION[precision], wp, wn,
+            _stream(dev)))
     return y
 
 
@@ -349,7 +371,7 @@ def pack_moe_experts(gate_blocks, up_blocks, down_blocks, device=None):
 
 
 def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
-              out: torch.Tensor | None = None) -> torch.Tensor:
+              out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """out[t] = sum_j w[t,j] * down_e(silu(gate_e x_t) * (up_e x_t)), e = ids[t,j]; fp32 h,
     fp32 out [T, H] (moe_batch.py's per-slot product plus core.cpp:5150-5245's
     gather/scatter, done on the device)."""
@@ -373,10 +395,8 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
         out = torch.empty((T, H), dtype=torch.float32, device=dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
-        nbytes = lib.q4_moe_workspace_bytes(T, E, topk, H, F)
-        ws = _workspace(dev, nbytes, "moe")
+        wp, wn = _ws_arg(dev, lib.q4_moe_workspace_bytes(T, E, topk, H, F), "moe", workspace)
         check("q4_moe_gemv", lib.q4_moe_gemv(
             _ptr(gate_up.data), _ptr(down.data), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts), _ptr(out),
-            T, E, topk, H, F, _ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0,
-            _stream(dev)))
+            T, E, topk, H, F, wp, wn, _stream(dev)))
     return out
