@@ -40,6 +40,15 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kMagic1024 = 0x64006400u;   // fp16 1024.0 in both halves
 
+// Workgroup -> output tile, XCD-aware. Workgroups are dispatched to the 8 XCDs
+// round-robin (workgroup b runs on XCD b % 8); each XCD gets a contiguous run of
+// tiles in (weight slab, token tile) order, so the workgroups sharing a weight
+// slab share that XCD's L2 instead of fetching the slab once per XCD.
+__device__ __forceinline__ int xcd_tile(int b, int G) {
+    const int x = b & 7, j = b >> 3, q = G >> 3, rem = G & 7;
+    return x * q + min(x, rem) + j;
+}
+
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -101,13 +110,17 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave % WGN, wt = wave / WGN;
-    const int bt = blockIdx.x % tiles_t, bn = blockIdx.x / tiles_t;
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int bt = tile % tiles_t, bn = tile / tiles_t;
     const int n0 = bn * BN, t0 = bt * BT;
     const int KB = K >> 5, NSTAGE = KB / KS;
     const int G = N >> 6;
     const int i16 = lane & 15, kg = lane >> 4;
 
-    // this wave's mx tiles: tile u = wave + NW*i -> (row group u % RG, block u / RG of the stage)
+    // This wave's mx tiles: tile u = wave + NW*i -> (row group u % RG, block u / RG of the
+    // stage). Tile bases are wave-uniform and advance by a uniform stride per stage, and
+    // the per-lane offsets are fixed 32-bit values, so no address register is rewritten
+    // inside the K loop (rewriting one that a pending load targets forces a vmcnt wait).
     const uint8_t* wbase[WPW];
     int wrow[WPW], wcol[WPW];
     bool wown[WPW];
@@ -121,13 +134,13 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
         wrow[i] = rgl * 64 + i16;
         wcol[i] = kbl * 32 + kg * 8;
     }
-    const int coff = lane * 16, soff = kCodeBytes + i16 * 16;
-    const uint16_t* xsrc[XCH];
-    int xdst[XCH];
+    const uint32_t coff = lane * 16, soff = kCodeBytes + i16 * 16;
+    const uint16_t* xbase = x16 + (int64_t)t0 * K;                    // workgroup-uniform
+    int xoff[XCH], xdst[XCH];
 #pragma unroll
     for (int c = 0; c < XCH; ++c) {
         const int ch = tid + NT * c, tok = ch / (KS * 4), part = ch % (KS * 4);
-        xsrc[c] = x16 + (int64_t)min(t0 + tok, T - 1) * K + part * 8;
+        xoff[c] = (min(t0 + tok, T - 1) - t0) * K + part * 8;            // halves, fits 32 bits
         xdst[c] = tok * STR + part * 8;
     }
     const uint32_t nib2 = vgpr_const(kNib2);
@@ -142,16 +155,17 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
     u32x4 wc[WPW], wsc[WPW];
     u32x4 xr[XCH];
     auto gload = [&](int st) {
+        const uint16_t* xs = xbase + st * BK;                            // uniform
+#pragma unroll
+        for (int c = 0; c < XCH; ++c) xr[c] = *(const u32x4*)(xs + xoff[c]);
 #pragma unroll
         for (int i = 0; i < WPW; ++i) {
             if (wown[i]) {
-                const uint8_t* tp = wbase[i] + (int64_t)st * KS * kTileBytes;
+                const uint8_t* tp = wbase[i] + st * (KS * kTileBytes);  // uniform
                 wc[i] = load_nt_u32x4(tp + coff);
                 wsc[i] = load_nt_u32x4(tp + soff);
             }
         }
-#pragma unroll
-        for (int c = 0; c < XCH; ++c) xr[c] = *(const u32x4*)(xsrc[c] + st * BK);
     };
     auto lstore = [&](int buf) {
 #pragma unroll
@@ -211,30 +225,276 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
     }
 }
 
+// ---------------------------------------------------------------------------
+// The pipelined variant (default for K % 64 == 0): 256 x 256 workgroup tile,
+// 8 waves (2 along N x 4 along T, 128 x 64 wave tiles), 64-K stages.
+//   * weights: each wave loads one mx tile (64 rows x 32 K) per stage into
+//     registers three stages ahead (three register sets) and dequantizes
+//     stage s+1 into the other 16-bit weight buffer during stage s,
+//     interleaved with the MFMAs of the stage's second half;
+//   * activations: LDS-DMA (global_load_lds_dwordx4) into a 3-deep ring, two
+//     stages ahead;
+//   * one barrier per stage; every wait names the youngest loads it may
+//     leave in flight (vector memory loads retire in issue order).
+// The DMA is issued from inline asm: the compiler's wait insertion would
+// otherwise assume the DMA may write the fragments read next and wait for it
+// right away.
+// LDS tiles are planar: [32-K plane][row][32 halves] (64 B rows, 16 KB per
+// plane of 256 rows). The 16-byte chunk c of row r sits at chunk slot
+// c ^ ((r >> 2) & 3), so the 16 lanes of a b128 fragment access (16
+// consecutive rows, one chunk) cover all 64 banks, and every fragment, store
+// and DMA address is one base register plus an immediate.
+// LDS map: weight buffers at 0 and 32 KB, activation ring at 64, 96, 128 KB.
+constexpr int kPlaneB = 256 * 64;                // one 32-K plane of a 256-row tile: 16 KB
+constexpr int kTileB = 2 * kPlaneB;              // one 64-K stage of a 256-row tile: 32 KB
+constexpr int kXRing = 2 * kTileB;               // LDS offset of the activation ring
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] + vmcnt_hi[15:14], expcnt[6:4], lgkmcnt[11:8]).
+constexpr int wait_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
+constexpr int kWaitVm0 = wait_imm(0, 15);
+constexpr int kWaitVm6 = wait_imm(6, 15);
+constexpr int kWaitVm10 = wait_imm(10, 15);
+constexpr int kWaitVm0Lgkm0 = wait_imm(0, 0);
+constexpr int kWaitVm4Lgkm0 = wait_imm(4, 0);
+constexpr int kWaitVm6Lgkm0 = wait_imm(6, 0);
+constexpr int kWaitLgkm0 = wait_imm(63, 0);
+
+// 16 bytes per lane from global memory (uniform base + 32-bit lane offset) into LDS at
+// m0 + 16 * lane.
+__device__ __forceinline__ void lds_dma16(const void* gbase, uint32_t goff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(goff), "s"(gbase), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+// 16 bytes per lane into registers, streaming (uniform base + 32-bit lane offset). The
+// compiler does not track this load: the caller waits for it (s_waitcnt vmcnt) and then
+// passes the registers through vgpr_landed before any other use.
+__device__ __forceinline__ void load16_async(u32x4& dst, const void* gbase, uint32_t goff) {
+    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(dst) : "v"(goff), "s"(gbase) : "memory");
+}
+__device__ __forceinline__ void vgpr_landed(u32x4& v) { asm volatile("" : "+v"(v)); }
+
+template <int PREC>
+__global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restrict__ packed,
+                                                          const uint16_t* __restrict__ x16,
+                                                          const float* __restrict__ tscale, float* __restrict__ y,
+                                                          int T, int N, int K, int tiles_t) {
+    constexpr int WN = 128, WT = 64, FN = WN / 16, FT = WT / 16;
+    typedef typename std::conditional<PREC == 0, f16x8, bf16x8>::type frag_t;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 1, wt = wave >> 1;
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int bt = tile % tiles_t, bn = tile / tiles_t;
+    const int n0 = bn * 256, t0 = bt * 256;
+    const int KB = K >> 5, NST = KB >> 1;
+    const int G = N >> 6;
+    const int i16 = lane & 15, kg = lane >> 4;
+    const uint32_t lane_row = i16 * 64 + ((kg ^ (i16 >> 2)) << 4);     // row i16, chunk kg, swizzled
+
+    // weights: this wave's mx tile of each stage (row group wave & 3, 32-K block wave >> 2)
+    const int rgl = wave & 3, kbl = wave >> 2;
+    const int rg = min(n0 / 64 + rgl, G - 1);                          // clamp ragged N
+    const uint8_t* const wsrc = packed + ((int64_t)rg * KB + kbl) * kTileBytes;
+    const uint32_t coff = lane * 16, soff = kCodeBytes + i16 * 16;
+    const uint32_t wst = kbl * kPlaneB + rgl * 64 * 64 + lane_row;     // + buffer + r * 1 KB
+
+    // activations: this wave's 32 rows of each stage as 4 DMAs of 16 rows x 32 K (1 KB of
+    // LDS each). The activation rows are padded to a multiple of 256, so no row needs
+    // clamping. DMA lane i lands at row i/4, chunk slot i%4 of the block: it fetches chunk
+    // (i & 3) ^ (i >> 4).
+    const uint8_t* const xsrc = (const uint8_t*)(x16 + (int64_t)t0 * K);
+    const uint32_t xoff = (uint32_t)((wave * 32 + (lane >> 2)) * K * 2 + (((lane & 3) ^ (lane >> 4)) << 4));
+    const uint32_t xdst = (uint32_t)(uintptr_t)lds + kXRing + wave * 32 * 64;   // LDS byte address
+
+    // fragment bases: A = weight rows wn*128 + 16i + i16, B = token rows wt*64 + 16j + i16
+    const uint32_t abase = (wn * WN) * 64 + lane_row;
+    const uint32_t bbase = kXRing + (wt * WT) * 64 + lane_row;
+    const uint32_t bbase2 = bbase + 2 * kTileB;                         // ring slot 2 (offset > 64 KB)
+    const uint32_t nib2 = vgpr_const(kNib2);
+    const uint32_t magic = vgpr_const(PREC == 0 ? kMagic1024 : kMagic128);
+
+    f32x4 acc[FN][FT];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 wc[3], ws[3];                          // three register sets of weight codes + scales
+    auto issue_x = [&](int st, int slot) {
+        const uint8_t* src = xsrc + st * 128;                          // uniform
+        const uint32_t dst = xdst + slot * kTileB;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+                lds_dma16(src + kk * 64 + (int64_t)h * 16 * K * 2, xoff, dst + kk * kPlaneB + h * 16 * 64);
+    };
+    auto issue_w = [&](int st, u32x4& c, u32x4& sc) {
+        const uint8_t* tp = wsrc + st * (2 * kTileBytes);               // uniform
+        load16_async(c, tp, coff);
+        load16_async(sc, tp, soff);
+    };
+    auto store_w = [&](int buf, const u32x4& c, const u32x4& sc, int r0, int r1) {
+#pragma unroll
+        for (int r = r0; r < r1; ++r)
+            *(u32x4*)(lds + wst + buf * kTileB + r * 1024) = dequant8<PREC>(c[r], sc[r], nib2, magic);
+    };
+    auto read_frags = [&](int buf, int slot, int kk, frag_t (&a)[FN], frag_t (&b)[FT]) {
+        const uint8_t* xp = lds + (slot == 2 ? bbase2 : bbase + slot * kTileB) + kk * kPlaneB;
+        const uint8_t* wp = lds + abase + buf * kTileB + kk * kPlaneB;
+#pragma unroll
+        for (int j = 0; j < FT; ++j) b[j] = *(const frag_t*)(xp + j * 1024);
+#pragma unroll
+        for (int i = 0; i < FN; ++i) a[i] = *(const frag_t*)(wp + i * 1024);
+    };
+    auto mfmas = [&](const frag_t (&a)[FN], const frag_t (&b)[FT]) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FT; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+    };
+
+    // Issue order: stage s's weights two stages before its activations (W(s+3) and X(s+2) at
+    // the start of stage s), so the in-order vmcnt lets each wait name the youngest loads it
+    // may leave in flight. Prologue: W(0), W(1), X(0), W(2), X(1).
+    issue_w(0, wc[0], ws[0]);
+    if (NST > 1) issue_w(1, wc[1], ws[1]);
+    issue_x(0, 0);
+    if (NST > 2) issue_w(2, wc[2], ws[2]);
+    if (NST > 1) issue_x(1, 1);
+    if (NST > 2) __builtin_amdgcn_s_waitcnt(kWaitVm6);        // W(0), W(1), X(0) landed
+    else __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    vgpr_landed(wc[0]);
+    vgpr_landed(ws[0]);
+    store_w(0, wc[0], ws[0], 0, 4);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    asm volatile("s_barrier" ::: "memory");
+
+    // Stage st, phase P = st % 6: weights in buffer P & 1, activations in ring slot P % 3.
+    // Start: wait for W(st+1) (issued at the start of stage st-2); W(st+3) -> register set
+    // P % 3 (W(st)'s, dequantized in stage st-1); X(st+2) -> slot (P+2) % 3 (X(st-1)'s,
+    // released by the barrier that ended stage st-1). The dequantization of W(st+1) into the
+    // other weight buffer is spread over both halves of the MFMAs: an MFMA hides about two
+    // independent VALU instructions, not more. End: wait for X(st+1) and the LDS stores,
+    // barrier.
+    auto stage = [&](auto phase, int st) {
+        constexpr int P = decltype(phase)::value;
+        constexpr int cur = P & 1, slot = P % 3, nslot = (P + 2) % 3, wset = P % 3, nset = (P + 1) % 3;
+        const bool w3 = st + 3 < NST, x2 = st + 2 < NST;
+        if (x2) __builtin_amdgcn_s_waitcnt(kWaitVm10);        // W(st+1) landed
+        else __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        vgpr_landed(wc[nset]);
+        vgpr_landed(ws[nset]);
+        if (w3) issue_w(st + 3, wc[wset], ws[wset]);
+        if (x2) issue_x(st + 2, nslot);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            frag_t a[FN], b[FT];
+            read_frags(cur, slot, kk, a, b);
+            store_w(cur ^ 1, wc[nset], ws[nset], 2 * kk, 2 * kk + 2);   // rows 16r.., r in [2kk, 2kk+2)
+            mfmas(a, b);
+            __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+            for (int g = 0; g < 20; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (w3) __builtin_amdgcn_s_waitcnt(kWaitVm6Lgkm0);    // X(st+1) landed, LDS stores done
+        else if (x2) __builtin_amdgcn_s_waitcnt(kWaitVm4Lgkm0);
+        else __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        asm volatile("s_barrier" ::: "memory");
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using I5 = std::integral_constant<int, 5>;
+    int st = 0;
+    for (; st + 6 <= NST; st += 6) {
+        stage(I0{}, st);
+        stage(I1{}, st + 1);
+        stage(I2{}, st + 2);
+        stage(I3{}, st + 3);
+        stage(I4{}, st + 4);
+        stage(I5{}, st + 5);
+    }
+    if (st < NST) stage(I0{}, st);
+    if (st + 1 < NST) stage(I1{}, st + 1);
+    if (st + 2 < NST) stage(I2{}, st + 2);
+    if (st + 3 < NST) stage(I3{}, st + 3);
+    if (st + 4 < NST) stage(I4{}, st + 4);
+
+    // lane holds D[n = 4*kg + r][t = i16] of each 16x16 fragment: 4 consecutive n of one token
+#pragma unroll
+    for (int j = 0; j < FT; ++j) {
+        const int t = t0 + wt * WT + j * 16 + i16;
+        if (t >= T) continue;
+        const float sc = tscale ? tscale[t] : 1.0f;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            const int n = n0 + wn * WN + i * 16 + kg * 4;
+            if (n < N) {
+                f32x4 v = acc[i][j];
+                v = v * sc;
+                *(f32x4*)(y + (int64_t)t * N + n) = v;
+            }
+        }
+    }
+}
+
 // Activations -> the MFMA's 16-bit type, one workgroup per token row.
 // PREC 0: fp16, with the row scaled by 2^-s (s >= 0 the least that keeps
 // max|x| 2^-s < 2^15) and tscale[t] = 2^s; PREC 1: bf16 (RNE from f32).
 template <bool XF32, int PREC>
 __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x, uint16_t* __restrict__ x16,
-                                                     float* __restrict__ tscale, int K) {
-    const int t = blockIdx.x;
+                                                     float* __restrict__ tscale, int T, int K) {
+    const int t = blockIdx.x, n8 = K >> 3;       // 8-element groups of the row (K % 32 == 0)
     const int64_t row = (int64_t)t * K;
-    auto ld = [&](int k) -> float {
-        if constexpr (XF32) return ((const float*)x)[row + k];
-        else return __builtin_bit_cast(float, (uint32_t)((const uint16_t*)x)[row + k] << 16);
+    u32x4* out = (u32x4*)(x16 + row);
+    if (t >= T) {                                // padding rows of the last token tile
+        for (int i = threadIdx.x; i < n8; i += 256) out[i] = u32x4{0u, 0u, 0u, 0u};
+        return;
+    }
+    auto ld8 = [&](int i, float (&v)[8]) {
+        if constexpr (XF32) {
+            const f32x4* p = (const f32x4*)((const float*)x + row) + 2 * i;
+            const f32x4 a = p[0], b = p[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = a[e], v[e + 4] = b[e];
+        } else {
+            const u32x4 w = ((const u32x4*)((const uint16_t*)x + row))[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[2 * e] = bf16_lo_to_f32(w[e]), v[2 * e + 1] = bf16_hi_to_f32(w[e]);
+        }
     };
     float scale = 1.0f;
     if constexpr (PREC == 0) {
-        __shared__ float red[256];
+        __shared__ float red[4];
         float mx = 0.f;
-        for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(ld(k)));
-        red[threadIdx.x] = mx;
-        __syncthreads();
-        for (int s = 128; s > 0; s >>= 1) {
-            if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-            __syncthreads();
+        for (int i = threadIdx.x; i < n8; i += 256) {
+            float v[8];
+            ld8(i, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
         }
-        mx = red[0];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
         int s = 0;
         if (mx >= 32768.0f && mx <= 3.0e38f) {
             int e;
@@ -244,12 +504,23 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
         scale = ldexpf(1.0f, -s);
         if (threadIdx.x == 0) tscale[t] = ldexpf(1.0f, s);
     }
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const float v = ld(k) * scale;
-        uint16_t o;
-        if constexpr (PREC == 0) o = __builtin_bit_cast(uint16_t, (_Float16)v);
-        else o = (uint16_t)f32_to_bf16_rne(v);
-        x16[row + k] = o;
+    for (int i = threadIdx.x; i < n8; i += 256) {
+        float v[8];
+        ld8(i, v);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t lo, hi;
+            if constexpr (PREC == 0) {
+                lo = __builtin_bit_cast(uint16_t, (_Float16)(v[2 * e] * scale));
+                hi = __builtin_bit_cast(uint16_t, (_Float16)(v[2 * e + 1] * scale));
+            } else {
+                lo = f32_to_bf16_rne(v[2 * e]);
+                hi = f32_to_bf16_rne(v[2 * e + 1]);
+            }
+            o[e] = lo | (hi << 16);
+        }
+        out[i] = o;
     }
 }
 
@@ -263,7 +534,9 @@ constexpr TileCfg kCfgs[] = {
     {128, 256, 2, 4, 2},     // 8 waves, 64x64
     {128, 128, 2, 4, 2},     // 8 waves, 64x32
     {256, 256, 2, 2, 1},     // 4 waves, 128x128 wave tiles, 32-K stages
+    {256, 256, 2, 4, 2},     // the LDS-DMA pipelined kernel (prefill_dma_kernel)
 };
+constexpr int kDmaCfg = 5;
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 // Pick the variant that keeps the most of 256 CUs busy (Q4MI_PREFILL_CFG overrides).
@@ -273,7 +546,7 @@ int choose_cfg(int T, int N, int K) {
         return e ? atoi(e) : -1;
     }();
     if (forced >= 0 && forced < kNumCfgs && K % (32 * kCfgs[forced].ks) == 0) return forced;
-    const double eff[] = {1.0, 0.9, 0.9, 0.75, 0.8};   // relative per-workgroup efficiency
+    const double eff[] = {1.0, 0.9, 0.9, 0.75, 0.8, 2.0};   // relative per-workgroup efficiency
     double best = 1e300;
     int pick = 4;
     for (int i = 0; i < kNumCfgs; ++i) {
@@ -305,7 +578,11 @@ void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, con
         case 1: launch_cfg<1, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
         case 2: launch_cfg<2, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
         case 3: launch_cfg<3, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
-        default: launch_cfg<4, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+        case 4: launch_cfg<4, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+        default:
+            hipLaunchKernelGGL((prefill_dma_kernel<PREC>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, ts, y, T, N, K,
+                               tiles_t);
+            break;
     }
 }
 
@@ -313,10 +590,13 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
 
+// Activation rows are padded with zeros to a multiple of 256 tokens (the widest token tile).
+size_t padded_tokens(int T) { return ((size_t)T + 255) / 256 * 256; }
+
 extern "C" size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K) {
     if (T <= 0 || K <= 0) return 0;
     (void)N;
-    return align256((size_t)T * K * 2) + align256((size_t)T * 4);
+    return align256(padded_tokens(T) * K * 2) + align256((size_t)T * 4);
 }
 
 extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype, float* y, int T, int64_t N,
@@ -330,15 +610,16 @@ extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype
     const size_t need = q4_gemm_prefill_workspace_bytes(T, N, K);
     if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
     uint16_t* x16 = (uint16_t*)workspace;
-    float* ts = (float*)((char*)workspace + align256((size_t)T * K * 2));
+    float* ts = (float*)((char*)workspace + align256(padded_tokens(T) * K * 2));
+    const dim3 xgrid((unsigned)padded_tokens(T));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
     if (precision == 0) {
-        if (xf32) hipLaunchKernelGGL((prefill_xprep<true, 0>), dim3(T), dim3(256), 0, st, x, x16, ts, (int)K);
-        else hipLaunchKernelGGL((prefill_xprep<false, 0>), dim3(T), dim3(256), 0, st, x, x16, ts, (int)K);
+        if (xf32) hipLaunchKernelGGL((prefill_xprep<true, 0>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
+        else hipLaunchKernelGGL((prefill_xprep<false, 0>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
     } else {
-        if (xf32) hipLaunchKernelGGL((prefill_xprep<true, 1>), dim3(T), dim3(256), 0, st, x, x16, ts, (int)K);
-        else hipLaunchKernelGGL((prefill_xprep<false, 1>), dim3(T), dim3(256), 0, st, x, x16, ts, (int)K);
+        if (xf32) hipLaunchKernelGGL((prefill_xprep<true, 1>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
+        else hipLaunchKernelGGL((prefill_xprep<false, 1>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
     }
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
     const int cfg = choose_cfg(T, (int)N, (int)K);
