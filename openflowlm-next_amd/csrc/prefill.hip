@@ -40,14 +40,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kMagic1024 = 0x64006400u;   // fp16 1024.0 in both halves
 
-// Workgroup -> output tile, XCD-aware. Workgroups are dispatched to the 8 XCDs
-// round-robin (workgroup b runs on XCD b % 8); each XCD gets a contiguous run of
-// tiles in (weight slab, token tile) order, so the workgroups sharing a weight
-// slab share that XCD's L2 instead of fetching the slab once per XCD.
-__device__ __forceinline__ int xcd_tile(int b, int G) {
-    const int x = b & 7, j = b >> 3, q = G >> 3, rem = G & 7;
-    return x * q + min(x, rem) + j;
-}
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -110,8 +102,7 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave % WGN, wt = wave / WGN;
-    const int tile = xcd_tile(blockIdx.x, gridDim.x);
-    const int bt = tile % tiles_t, bn = tile / tiles_t;
+    const int bt = blockIdx.x % tiles_t, bn = blockIdx.x / tiles_t;
     const int n0 = bn * BN, t0 = bt * BT;
     const int KB = K >> 5, NSTAGE = KB / KS;
     const int G = N >> 6;
@@ -278,7 +269,7 @@ template <int PREC>
 __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restrict__ packed,
                                                           const uint16_t* __restrict__ x16,
                                                           const float* __restrict__ tscale, float* __restrict__ y,
-                                                          int T, int N, int K, int tiles_t) {
+                                                          int T, int N, int K, int tiles_t, int splits) {
     constexpr int WN = 128, WT = 64, FN = WN / 16, FT = WT / 16;
     typedef typename std::conditional<PREC == 0, f16x8, bf16x8>::type frag_t;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
@@ -286,10 +277,14 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wt = wave >> 1;
-    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    // workgroup -> (output tile, K split); split s covers stages [st0, st0 + NST) of K / 64 and
+    // writes its partial sums to y + s * T * N (the host sums the splits in order)
+    const int tile = blockIdx.x / splits, split = blockIdx.x % splits;
     const int bt = tile % tiles_t, bn = tile / tiles_t;
     const int n0 = bn * 256, t0 = bt * 256;
-    const int KB = K >> 5, NST = KB >> 1;
+    const int KB = K >> 5, NSTK = KB >> 1;
+    const int st0 = (int)((int64_t)split * NSTK / splits), NST = (int)((int64_t)(split + 1) * NSTK / splits) - st0;
+    y += (int64_t)split * T * N;
     const int G = N >> 6;
     const int i16 = lane & 15, kg = lane >> 4;
     const uint32_t lane_row = i16 * 64 + ((kg ^ (i16 >> 2)) << 4);     // row i16, chunk kg, swizzled
@@ -297,16 +292,14 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
     // weights: this wave's mx tile of each stage (row group wave & 3, 32-K block wave >> 2)
     const int rgl = wave & 3, kbl = wave >> 2;
     const int rg = min(n0 / 64 + rgl, G - 1);                          // clamp ragged N
-    const uint8_t* const wsrc = packed + ((int64_t)rg * KB + kbl) * kTileBytes;
+    const uint8_t* const wsrc = packed + ((int64_t)rg * KB + kbl + 2 * st0) * kTileBytes;
     const uint32_t coff = lane * 16, soff = kCodeBytes + i16 * 16;
     const uint32_t wst = kbl * kPlaneB + rgl * 64 * 64 + lane_row;     // + buffer + r * 1 KB
 
-    // activations: this wave's 32 rows of each stage as 4 DMAs of 16 rows x 32 K (1 KB of
-    // LDS each). The activation rows are padded to a multiple of 256, so no row needs
-    // clamping. DMA lane i lands at row i/4, chunk slot i%4 of the block: it fetches chunk
-    // (i & 3) ^ (i >> 4).
-    const uint8_t* const xsrc = (const uint8_t*)(x16 + (int64_t)t0 * K);
-    const uint32_t xoff = (uint32_t)((wave * 32 + (lane >> 2)) * K * 2 + (((lane & 3) ^ (lane >> 4)) << 4));
+    // activations: pre-tiled as the LDS image of each stage (32 KB contiguous per token tile
+    // and stage, zero-padded to whole tiles); this wave copies its 32 rows as 4 DMAs of 1 KB.
+    const uint8_t* const xsrc = (const uint8_t*)x16 + (((int64_t)bt * NSTK + st0) * kTileB + wave * 32 * 64);
+    const uint32_t xoff = lane * 16;
     const uint32_t xdst = (uint32_t)(uintptr_t)lds + kXRing + wave * 32 * 64;   // LDS byte address
 
     // fragment bases: A = weight rows wn*128 + 16i + i16, B = token rows wt*64 + 16j + i16
@@ -324,13 +317,13 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
 
     u32x4 wc[3], ws[3];                          // three register sets of weight codes + scales
     auto issue_x = [&](int st, int slot) {
-        const uint8_t* src = xsrc + st * 128;                          // uniform
+        const uint8_t* src = xsrc + (int64_t)st * kTileB;               // uniform
         const uint32_t dst = xdst + slot * kTileB;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk)
-                lds_dma16(src + kk * 64 + (int64_t)h * 16 * K * 2, xoff, dst + kk * kPlaneB + h * 16 * 64);
+                lds_dma16(src + kk * kPlaneB + h * 1024, xoff, dst + kk * kPlaneB + h * 1024);
     };
     auto issue_w = [&](int st, u32x4& c, u32x4& sc) {
         const uint8_t* tp = wsrc + st * (2 * kTileBytes);               // uniform
@@ -458,14 +451,24 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
 // Activations -> the MFMA's 16-bit type, one workgroup per token row.
 // PREC 0: fp16, with the row scaled by 2^-s (s >= 0 the least that keeps
 // max|x| 2^-s < 2^15) and tscale[t] = 2^s; PREC 1: bf16 (RNE from f32).
-template <bool XF32, int PREC>
+// TILED: the 16-byte chunk i (k = 8i..8i+7) of token t goes to its place in the LDS image
+// of the pipelined kernel's activation tiles: [token tile][64-K stage][32-K plane][256 rows]
+// [4 chunks], chunk c of row r at slot c ^ ((r >> 2) & 3). Each stage of a token tile is then
+// one contiguous 32 KB block, copied to LDS verbatim. Otherwise rows stay [T][K].
+__device__ __forceinline__ int64_t xchunk_dst(int t, int i, int K) {
+    const int r = t & 255, st = i >> 3, kk = (i >> 2) & 1, c = i & 3;
+    return ((((int64_t)(t >> 8) * (K >> 6) + st) * 2 + kk) * 256 + r) * 4 + (c ^ ((r >> 2) & 3));
+}
+
+template <bool XF32, int PREC, bool TILED>
 __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x, uint16_t* __restrict__ x16,
                                                      float* __restrict__ tscale, int T, int K) {
     const int t = blockIdx.x, n8 = K >> 3;       // 8-element groups of the row (K % 32 == 0)
     const int64_t row = (int64_t)t * K;
-    u32x4* out = (u32x4*)(x16 + row);
+    u32x4* const out = (u32x4*)x16;
+    auto dst = [&](int i) -> int64_t { return TILED ? xchunk_dst(t, i, K) : row / 8 + i; };
     if (t >= T) {                                // padding rows of the last token tile
-        for (int i = threadIdx.x; i < n8; i += 256) out[i] = u32x4{0u, 0u, 0u, 0u};
+        for (int i = threadIdx.x; i < n8; i += 256) out[dst(i)] = u32x4{0u, 0u, 0u, 0u};
         return;
     }
     auto ld8 = [&](int i, float (&v)[8]) {
@@ -520,7 +523,7 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
             }
             o[e] = lo | (hi << 16);
         }
-        out[i] = o;
+        out[dst(i)] = o;
     }
 }
 
@@ -539,17 +542,20 @@ constexpr TileCfg kCfgs[] = {
 constexpr int kDmaCfg = 5;
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-// Pick the variant that keeps the most of 256 CUs busy (Q4MI_PREFILL_CFG overrides).
+// Kernel variant: the pipelined kernel whenever K % 64 == 0 (K splits keep small grids
+// busy); otherwise the generic variant with the fewest rounds of 256 workgroups
+// (Q4MI_PREFILL_CFG overrides).
 int choose_cfg(int T, int N, int K) {
     static int forced = [] {
         const char* e = getenv("Q4MI_PREFILL_CFG");
         return e ? atoi(e) : -1;
     }();
     if (forced >= 0 && forced < kNumCfgs && K % (32 * kCfgs[forced].ks) == 0) return forced;
-    const double eff[] = {1.0, 0.9, 0.9, 0.75, 0.8, 2.0};   // relative per-workgroup efficiency
+    if (K % 64 == 0) return kDmaCfg;
+    const double eff[] = {1.0, 0.9, 0.9, 0.75, 0.8};   // relative per-workgroup efficiency
     double best = 1e300;
     int pick = 4;
-    for (int i = 0; i < kNumCfgs; ++i) {
+    for (int i = 0; i < kDmaCfg; ++i) {
         if (K % (32 * kCfgs[i].ks)) continue;
         const int64_t wgs = ceil_div(N, kCfgs[i].bn) * ceil_div(T, kCfgs[i].bt);
         const int64_t rounds = ceil_div(wgs, 256);
@@ -572,7 +578,7 @@ void launch_cfg(int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* 
 
 template <int PREC>
 void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const float* ts,
-                    float* y, int T, int N, int K, int tiles_t) {
+                    float* y, int T, int N, int K, int tiles_t, int splits) {
     switch (cfg) {
         case 0: launch_cfg<0, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
         case 1: launch_cfg<1, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
@@ -581,22 +587,107 @@ void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, con
         case 4: launch_cfg<4, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
         default:
             hipLaunchKernelGGL((prefill_dma_kernel<PREC>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, ts, y, T, N, K,
-                               tiles_t);
+                               tiles_t, splits);
             break;
     }
 }
 
+// y = sum of the S partials in split order (deterministic), 4 floats per thread.
+__global__ __launch_bounds__(256) void prefill_reduce_kernel(const f32x4* __restrict__ part, f32x4* __restrict__ y,
+                                                             int64_t MN4, int S) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= MN4) return;
+    f32x4 s = part[i];
+    for (int q = 1; q < S; ++q) s += part[(int64_t)q * MN4 + i];
+    y[i] = s;
+}
+
+// CUs of the current device (the MI355X's 256 when no device is visible, e.g. for a
+// workspace query on a host without a GPU).
+int device_cus() {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            return 256;
+        }
+        return n;
+    }();
+    return cus;
+}
+
+// Launch plan of one prefill GEMM: the kernel variant, its token tiles and K splits. The
+// pipelined kernel holds one workgroup per CU (160 KB of LDS); when its output tiles do not
+// fill the CUs, K is split and the partial sums are reduced in order afterwards
+// (Q4MI_PREFILL_SPLITS overrides the choice).
+struct PrefillPlan {
+    int cfg, tiles_t, splits;
+    int64_t grid;
+};
+
+PrefillPlan make_plan(int T, int64_t N, int64_t K) {
+    PrefillPlan p;
+    p.cfg = choose_cfg(T, (int)N, (int)K);
+    p.tiles_t = (int)ceil_div(T, kCfgs[p.cfg].bt);
+    const int64_t tiles = ceil_div(N, kCfgs[p.cfg].bn) * p.tiles_t;
+    p.splits = 1;
+    if (p.cfg == kDmaCfg) {
+        static const int forced = [] {
+            const char* e = getenv("Q4MI_PREFILL_SPLITS");
+            return e ? atoi(e) : 0;
+        }();
+        const int nst = (int)(K / 64), cap = nst < 16 ? nst : 16;
+        if (forced > 0) {
+            p.splits = forced < cap ? forced : cap;
+        } else {
+            constexpr double kStageSec = 1.0e-6, kReduceBytesPerSec = 4.0e12;
+            const int cus = device_cus();
+            double best = 1e300;
+            for (int S = 1; S <= cap; ++S) {
+                double cost = (double)ceil_div(tiles * S, cus) * (double)ceil_div(nst, S) * kStageSec;
+                if (S > 1) cost += (double)(S + 1) * T * N * 4 / kReduceBytesPerSec;
+                if (cost < best) {
+                    best = cost;
+                    p.splits = S;
+                }
+            }
+        }
+    }
+    p.grid = tiles * p.splits;
+    return p;
+}
+
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+template <bool XF, int PR, bool TL>
+void launch_xprep_t(dim3 g, hipStream_t st, const void* x, uint16_t* x16, float* ts, int T, int K) {
+    hipLaunchKernelGGL((prefill_xprep<XF, PR, TL>), g, dim3(256), 0, st, x, x16, ts, T, K);
+}
+
+void launch_xprep(bool xf32, int prec, bool tiled, dim3 g, hipStream_t st, const void* x, uint16_t* x16, float* ts,
+                  int T, int K) {
+    typedef void (*fn_t)(dim3, hipStream_t, const void*, uint16_t*, float*, int, int);
+    static const fn_t table[8] = {launch_xprep_t<false, 0, false>, launch_xprep_t<false, 0, true>,
+                                  launch_xprep_t<false, 1, false>, launch_xprep_t<false, 1, true>,
+                                  launch_xprep_t<true, 0, false>,  launch_xprep_t<true, 0, true>,
+                                  launch_xprep_t<true, 1, false>,  launch_xprep_t<true, 1, true>};
+    table[(xf32 ? 4 : 0) + (prec ? 2 : 0) + (tiled ? 1 : 0)](g, st, x, x16, ts, T, K);
+}
 
 }  // namespace
 
 // Activation rows are padded with zeros to a multiple of 256 tokens (the widest token tile).
-size_t padded_tokens(int T) { return ((size_t)T + 255) / 256 * 256; }
+static size_t padded_tokens(int T) { return ((size_t)T + 255) / 256 * 256; }
+
+// Workspace: activations in the kernel's 16-bit layout, per-token scales, and the K-split
+// partial sums when the plan splits K.
+static size_t xprep_bytes(int T, int64_t K) { return align256(padded_tokens(T) * K * 2) + align256((size_t)T * 4); }
 
 extern "C" size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K) {
-    if (T <= 0 || K <= 0) return 0;
-    (void)N;
-    return align256(padded_tokens(T) * K * 2) + align256((size_t)T * 4);
+    if (T <= 0 || K <= 0 || N < 0 || N % 64 || K % 32) return 0;
+    const PrefillPlan p = make_plan(T, N, K);
+    return xprep_bytes(T, K) + (p.splits > 1 ? align256((size_t)p.splits * T * N * 4) : 0);
 }
 
 extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype, float* y, int T, int64_t N,
@@ -611,22 +702,23 @@ extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype
     if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
     uint16_t* x16 = (uint16_t*)workspace;
     float* ts = (float*)((char*)workspace + align256(padded_tokens(T) * K * 2));
+    const PrefillPlan plan = make_plan(T, N, K);
     const dim3 xgrid((unsigned)padded_tokens(T));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
-    if (precision == 0) {
-        if (xf32) hipLaunchKernelGGL((prefill_xprep<true, 0>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
-        else hipLaunchKernelGGL((prefill_xprep<false, 0>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
-    } else {
-        if (xf32) hipLaunchKernelGGL((prefill_xprep<true, 1>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
-        else hipLaunchKernelGGL((prefill_xprep<false, 1>), xgrid, dim3(256), 0, st, x, x16, ts, T, (int)K);
-    }
+    const int cfg = plan.cfg;
+    const bool tiled = cfg == kDmaCfg;
+    launch_xprep(xf32, precision, tiled, xgrid, st, x, x16, ts, T, (int)K);
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-    const int cfg = choose_cfg(T, (int)N, (int)K);
-    const int tiles_t = (int)ceil_div(T, kCfgs[cfg].bt);
-    const int64_t grid = ceil_div(N, kCfgs[cfg].bn) * tiles_t;
     const float* tsp = precision == 0 ? ts : nullptr;
-    if (precision == 0) launch_prefill<0>(cfg, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
-    else launch_prefill<1>(cfg, grid, st, packed, x16, tsp, y, T, (int)N, (int)K, tiles_t);
+    float* out = plan.splits > 1 ? (float*)((char*)workspace + xprep_bytes(T, K)) : y;
+    if (precision == 0) launch_prefill<0>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits);
+    else launch_prefill<1>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits);
+    if (plan.splits > 1) {
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        const int64_t MN4 = (int64_t)T * N / 4;
+        hipLaunchKernelGGL(prefill_reduce_kernel, dim3((unsigned)ceil_div(MN4, 256)), dim3(256), 0, st,
+                           (const f32x4*)out, (f32x4*)y, MN4, plan.splits);
+    }
     return launch_status();
 }
