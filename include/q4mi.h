@@ -6,7 +6,9 @@
  * these signatures, so ctypes / cgo / JNI bind them without HIP headers.
  *
  * Every function returns Q4MI_OK (0) or a negative Q4MI_E* code. All device
- * memory belongs to the caller; the library never allocates. Work is enqueued
+ * memory belongs to the caller; the library never allocates. Packed weights,
+ * activations, outputs and workspaces must be 16-byte aligned (Q4MI_E_ARG
+ * otherwise; the descriptors of q4_gemv_grouped are the caller's to check). Work is enqueued
  * on `stream` and is asynchronous to the host; the functions are re-entrant
  * and keep no global state (calls that share one caller-owned workspace must
  * be ordered on one stream).
@@ -42,7 +44,7 @@ extern "C" {
 /* status codes */
 #define Q4MI_OK            0
 #define Q4MI_E_SHAPE      -1   /* a dimension is not a multiple the layout needs, or <= 0 */
-#define Q4MI_E_ARG        -2   /* NULL pointer, bad enum, bad block width */
+#define Q4MI_E_ARG        -2   /* NULL or misaligned pointer, bad enum, bad block width */
 #define Q4MI_E_WORKSPACE  -3   /* workspace missing or too small */
 #define Q4MI_E_LAUNCH     -4   /* the HIP launch itself failed */
 #define Q4MI_E_RANGE      -5   /* M or another count out of the supported range */

@@ -149,6 +149,7 @@ extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float*
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
     if (!packed || !x || !y) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
     const int S = choose_splits(N, K);
     GemvParams P{};
     P.packed = packed;

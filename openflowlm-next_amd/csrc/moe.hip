@@ -184,6 +184,8 @@ extern "C" int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const vo
     if (T < 0 || E <= 0 || topk <= 0 || topk > 16 || (int64_t)T * topk > kMaxPairs) return Q4MI_E_RANGE;
     if (T == 0) return Q4MI_OK;
     if (!gate_up || !down || !x || !topk_ids || !topk_w || !out) return Q4MI_E_ARG;
+    if (misaligned16(gate_up) || misaligned16(down) || misaligned16(x) || misaligned16(out) || misaligned16(workspace))
+        return Q4MI_E_ARG;
     const size_t need = q4_moe_workspace_bytes(T, E, topk, (int)H, (int)F);
     if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
     const int P = T * topk;

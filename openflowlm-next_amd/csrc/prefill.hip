@@ -698,6 +698,7 @@ extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype
     if (N > 0x7FFFFFFF || K > 0x7FFFFFFF) return Q4MI_E_RANGE;
     if (T == 0 || N == 0) return Q4MI_OK;
     if (!packed || !x || !y) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
     const size_t need = q4_gemm_prefill_workspace_bytes(T, N, K);
     if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
     uint16_t* x16 = (uint16_t*)workspace;

@@ -15,4 +15,7 @@ inline int launch_status() {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The kernels move packed weights, activations, outputs and workspaces in 16-byte vectors.
+inline bool misaligned16(const void* p) { return ((uintptr_t)p & 15u) != 0; }
+
 }  // namespace q4mi

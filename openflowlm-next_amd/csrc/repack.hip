@@ -130,6 +130,7 @@ extern "C" int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* p
     if (scale_mode != 0) return Q4MI_E_ARG;
     if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;   // empty: nothing to touch
     if (!gguf_blocks || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     const int64_t KB = K / 32, total = N * KB;
     const unsigned grid = (unsigned)((total + 255) / 256);
@@ -142,6 +143,7 @@ extern "C" int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed, int6
     if (rs <= 0) return Q4MI_E_ARG;
     if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
     if (!pool || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
     if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
     const int64_t KB = K / 32, total = N * KB;
     const unsigned grid = (unsigned)((total + 255) / 256);
@@ -152,6 +154,7 @@ extern "C" int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed, int6
 extern "C" int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
     if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;
     if (!packed || !w) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(w)) return Q4MI_E_ARG;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     const int64_t total = N * (K / 8);
     const unsigned grid = (unsigned)((total + 255) / 256);

@@ -75,6 +75,31 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_gemv(fake, fake, 1, fake, 1, 4096, 4096, fake, need - 1, None) == -3
     assert lib.q4_gemv_grouped(None, 1, 1, 1, 1, None) == -2
     assert lib.q4_gemv_grouped(fake, 1, 1, 17, 1, None) == -5
+    # packed weights, activations, outputs and workspaces move in 16-byte vectors
+    odd = C.c_void_p(0x1004)
+    assert lib.q4_gemv(fake, odd, 1, fake, 1, 128256, 4096, None, 0, None) == -2
+    assert lib.q4_gemv(odd, fake, 1, fake, 1, 128256, 4096, None, 0, None) == -2
+    assert lib.q4_dequant(fake, odd, 64, 32, None) == -2
+    assert lib.q4_repack(fake, 20, odd, 64, 32, 0, None) == -2
+    need = lib.q4_gemm_prefill_workspace_bytes(64, 256, 1024)
+    assert lib.q4_gemm_prefill(fake, fake, 1, odd, 64, 256, 1024, 0, fake, need, None) == -2
+    assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 256, 1024, 0, odd, need, None) == -2
+    assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 256, 1024, 0, fake, need - 1, None) == -3
+    assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 256, 1024, 2, fake, need, None) == -2
+    assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 100, 1024, 0, fake, need, None) == -1
+    wsm = lib.q4_moe_workspace_bytes(16, 128, 8, 2048, 768)
+    assert lib.q4_moe_gemv(fake, fake, odd, 1, fake, fake, fake, 16, 128, 8, 2048, 768, fake, wsm, None) == -2
+
+
+def test_prefill_workspace_query(lib):
+    """Activations in the kernel's layout (zero-padded to 256-token tiles) + per-token
+    scales, plus K-split partials when a grid of 256x256 tiles cannot fill the GPU."""
+    x_only = lambda T, K: -(-((T + 255) // 256 * 256 * K * 2) // 256) * 256 + -(-(T * 4) // 256) * 256
+    assert lib.q4_gemm_prefill_workspace_bytes(2048, 14336, 4096) >= x_only(2048, 4096)
+    # 16 x 2 output tiles for 224 stages of K: split, partials [S][T][N] f32
+    assert lib.q4_gemm_prefill_workspace_bytes(512, 4096, 14336) >= x_only(512, 14336) + 2 * 512 * 4096 * 4
+    assert lib.q4_gemm_prefill_workspace_bytes(0, 4096, 4096) == 0
+    assert lib.q4_gemm_prefill_workspace_bytes(64, 100, 4096) == 0
 
 
 def test_gemv_workspace_query(lib):

@@ -1,0 +1,95 @@
+"""The pipelined prefill kernel issues its global loads from inline asm, so the
+compiler does not wait for them: every wait is explicit. This checks the gfx950
+ISA of that kernel's main loop: each register-destination load's registers are
+touched only after an s_waitcnt vmcnt(N) with N no larger than the number of
+vector-memory loads issued after it (vector-memory loads retire in issue order).
+A compiler change that schedules a use ahead of its wait would fail here.
+Needs hipcc (present on the build host); no GPU."""
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+SRC = ROOT / "openflowlm-next_amd" / "csrc" / "prefill.hip"
+
+
+def _regs(tok: str) -> set[int]:
+    m = re.match(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def _operands(line: str) -> list[str]:
+    parts = line.split(None, 1)
+    return [t.strip().split()[0] for t in parts[1].split(",") if t.strip()] if len(parts) > 1 else []
+
+
+def early_uses(asm: list[str]) -> tuple[int, list[str]]:
+    """(loads checked, descriptions of uses before the load's wait) for the first loop."""
+    head = next(i for i, l in enumerate(asm) if "Loop Header" in l)
+    label = asm[head].split(":")[0]
+    end = next(i for i in range(head + 1, len(asm))
+               if re.search(r"s_(?:cbranch_\w+|branch)\s+" + re.escape(label) + r"\b", asm[i]))
+    body = [l for l in asm[head:end + 1] if l.strip() and not l.strip().startswith((";", "."))]
+    bad, n = [], 0
+    for i, l in enumerate(body):
+        if not re.match(r"\s*global_load_dword", l) or "lds" in l:
+            continue
+        n += 1
+        dst, younger, done = _regs(_operands(l)[0]), 0, False
+        for k in range(1, 2 * len(body)):
+            m = body[(i + k) % len(body)]
+            if re.match(r"\s*global_load", m):
+                younger += 1
+            w = re.search(r"vmcnt\((\d+)\)", m)
+            # vmcnt(0) waits sit on the last stages' branches; only count steady-state waits
+            if w and 0 < int(w.group(1)) <= younger:
+                done = True
+            if re.match(r"\s*s_waitcnt", m):
+                continue
+            touched = set().union(*[_regs(t) for t in _operands(m)]) if _operands(m) else set()
+            if dst & touched:
+                if not done:
+                    bad.append(f"{l.strip()} -> {m.strip()}")
+                break
+    return n, bad
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+def test_prefill_loop_waits_cover_every_asm_load(tmp_path):
+    out = tmp_path / "prefill.s"
+    cmd = ["hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{ROOT / 'include'}", f"-I{SRC.parent}", "--cuda-device-only", "-S",
+           str(SRC), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    text = out.read_text().splitlines()
+    for prec in (0, 1):
+        start = next(i for i, l in enumerate(text)
+                     if re.match(rf"_ZN12_GLOBAL__N_118prefill_dma_kernelILi{prec}EE\w*:", l))
+        stop = next(i for i in range(start, len(text)) if "s_endpgm" in text[i])
+        n, bad = early_uses(text[start:stop])
+        assert n >= 6, f"precision {prec}: expected the weight loads of the unrolled loop, found {n}"
+        assert not bad, f"precision {prec}: registers used before their load's wait: {bad[:3]}"
+
+
+def test_checker_flags_an_early_use():
+    """Plant the mistake: a use of the loaded registers before any covering wait."""
+    asm = [".LBB0_1: ; Loop Header: Depth=1",
+           "\tglobal_load_dwordx4 v[4:7], v1, s[2:3] nt",
+           "\tv_add_u32_e32 v12, v5, v6",
+           "\ts_waitcnt vmcnt(1)",
+           "\ts_cbranch_scc1 .LBB0_1"]
+    n, bad = early_uses(asm)
+    assert n == 1 and len(bad) == 1 and "v12" in bad[0]
+    ok = asm[:2] + ["\tglobal_load_dwordx4 v[8:11], v1, s[2:3] nt", "\ts_waitcnt vmcnt(1)",
+                    "\tv_add_u32_e32 v12, v5, v6",
+                    "\tglobal_load_dwordx4 v[30:33], v1, s[2:3] nt", "\ts_waitcnt vmcnt(1)",
+                    "\tv_add_u32_e32 v13, v9, v10", asm[-1]]
+    assert early_uses(ok) == (3, [])
