@@ -119,6 +119,69 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
     }
 }
 
+// gemv_rows over NG row groups at once (tile bases gbase[i], same K range and
+// activations): per K position the activation fragment and the -128 sum x
+// MFMA are shared by the NG groups, and NG x UNR tiles are in flight per wave.
+template <int NTL, bool XF32, int NG, int UNR, class Rows>
+__device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG], const void* __restrict__ x, Rows rows,
+                                                int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kb0 = __builtin_amdgcn_readfirstlane(kb0);
+    kb1 = __builtin_amdgcn_readfirstlane(kb1);
+    const int i16 = lane & 15, kg = lane >> 4;
+    const int coff = lane * 16, soff = kCodeBytes + i16 * 16;
+    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const CodeConsts kc = code_consts();
+    const int64_t xrow = rows(i16);
+
+    for (int kb = kb0 + wave; kb < kb1; kb += kWaves * UNR) {
+        u32x4 c[UNR][NG], s[UNR][NG];
+        bf16x8 xh[UNR], xl[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int t = min(kb + kWaves * u, kb1 - 1);
+#pragma unroll
+            for (int i = 0; i < NG; ++i) {
+                const uint8_t* tp = gbase[i] + (int64_t)t * kTileBytes;
+                c[u][i] = load_nt_u32x4(tp + coff);
+                s[u][i] = load_nt_u32x4(tp + soff);
+            }
+            load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            if (kb + kWaves * u < kb1) {
+                f32x4 ns = mfma_bf16(xh[u], neg128, zero4);
+                if constexpr (XF32) ns = mfma_bf16(xl[u], neg128, ns);
+                float sx[NTL];
+#pragma unroll
+                for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
+#pragma unroll
+                for (int i = 0; i < NG; ++i) {
+                    f32x4 p[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const bf16x8 b = codes_to_bf16(c[u][i][r], kc);
+                        p[r] = mfma_bf16(xh[u], b, ns);
+                        if constexpr (XF32) p[r] = mfma_bf16(xl[u], b, p[r]);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float d = bf16_hi_to_f32(s[u][i][r]), m = bf16_lo_to_f32(s[u][i][r]);
+#pragma unroll
+                        for (int j = 0; j < NTL; ++j) {
+                            acc[i][r][j] = __builtin_fmaf(d, p[r][j], acc[i][r][j]);
+                            acc[i][r][j] = __builtin_fmaf(m, sx[j], acc[i][r][j]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Sum the four waves' accumulators through LDS. Afterwards thread t owns
 // row 16 r + lane % 16 of the row group (r = t >> 6, lane = t & 63) for the
 // tokens 4 (lane / 16) + j, j < NTL: v[j].

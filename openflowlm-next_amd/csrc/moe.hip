@@ -56,19 +56,23 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 template <int NTL, bool XF32>
 __device__ __forceinline__ void up_chunk(const uint8_t* wexp, const void* x, int H, int F, int rgp, const int* rows,
                                          const int* pairs, int M, float (*red)[4][4][64], float* __restrict__ hbuf) {
-    float ag[4][NTL], au[4][NTL];
+    // the gate rows (row group 2 rgp) and the up rows next to them (2 rgp + 1) in one stream
+    float acc[2][4][NTL];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < NTL; ++j) ag[r][j] = au[r][j] = 0.f;
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < NTL; ++j) acc[i][r][j] = 0.f;
     const int KB = H >> 5;
-    gemv_rows<NTL, XF32>(wexp, x, GatherRows{rows, M}, H, 2 * rgp, 0, KB, ag);       // gate rows
-    gemv_rows<NTL, XF32>(wexp, x, GatherRows{rows, M}, H, 2 * rgp + 1, 0, KB, au);   // the same up rows
+    const uint8_t* const gb[2] = {wexp + (int64_t)(2 * rgp) * KB * kTileBytes,
+                                  wexp + (int64_t)(2 * rgp + 1) * KB * kTileBytes};
+    gemv_rows_multi<NTL, XF32, 2, 4>(gb, x, GatherRows{rows, M}, H, 0, KB, acc);
     float (*rd)[4][NTL][64] = (float (*)[4][NTL][64])red;
     float vg[NTL], vu[NTL];
-    wave_sum<NTL>(ag, rd, vg);
+    wave_sum<NTL>(acc[0], rd, vg);
     __syncthreads();
-    wave_sum<NTL>(au, rd, vu);
+    wave_sum<NTL>(acc[1], rd, vu);
     const int tid = threadIdx.x, lane = tid & 63, r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int64_t f = (int64_t)rgp * 64 + r * 16 + i16;
 #pragma unroll
@@ -104,45 +108,58 @@ __global__ __launch_bounds__(256) void moe_up_kernel(const uint8_t* __restrict__
     }
 }
 
-template <int NTL>
-__device__ __forceinline__ void down_chunk(const uint8_t* wexp, const float* hbuf, int H, int F, int rg,
+// NG 64-row groups of H per down workgroup (4 when H % 256 == 0, else 1): K = F is short,
+// so one group alone is latency-bound.
+template <int NTL, int NG>
+__device__ __forceinline__ void down_chunk(const uint8_t* wexp, const float* hbuf, int H, int F, int rg0,
                                            const int* pairs, int M, float (*red)[4][4][64], float* __restrict__ ypair) {
-    float acc[4][NTL];
+    float acc[NG][4][NTL];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int i = 0; i < NG; ++i)
 #pragma unroll
-        for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
-    gemv_rows<NTL, true>(wexp, hbuf, GatherRows{pairs, M}, F, rg, 0, F >> 5, acc);
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < NTL; ++j) acc[i][r][j] = 0.f;
+    const int KB = F >> 5;
+    const uint8_t* gb[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) gb[i] = wexp + (int64_t)(rg0 + i) * KB * kTileBytes;
+    gemv_rows_multi<NTL, true, NG, NG == 1 ? 4 : 2>(gb, hbuf, GatherRows{pairs, M}, F, 0, KB, acc);
     float (*rd)[4][NTL][64] = (float (*)[4][NTL][64])red;
-    float v[NTL];
-    wave_sum<NTL>(acc, rd, v);
     const int tid = threadIdx.x, lane = tid & 63, r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
-    const int64_t n = (int64_t)rg * 64 + r * 16 + i16;
 #pragma unroll
-    for (int j = 0; j < NTL; ++j) {
-        const int tok = kg * 4 + j;
-        if (tok < M) ypair[(int64_t)pairs[tok] * H + n] = v[j];
+    for (int i = 0; i < NG; ++i) {
+        float v[NTL];
+        if (i) __syncthreads();
+        wave_sum<NTL>(acc[i], rd, v);
+        const int64_t n = (int64_t)(rg0 + i) * 64 + r * 16 + i16;
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) {
+            const int tok = kg * 4 + j;
+            if (tok < M) ypair[(int64_t)pairs[tok] * H + n] = v[j];
+        }
     }
 }
 
+template <int NG>
 __global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t* __restrict__ down,
                                                        const float* __restrict__ hbuf,
                                                        const int32_t* __restrict__ ids, int P, int H, int F,
                                                        float* __restrict__ ypair) {
     __shared__ int list[kMaxPairs];
     __shared__ float red[4][4][4][64];
-    const int hg = H >> 6;
-    const int e = blockIdx.x / hg, rg = blockIdx.x % hg;
+    const int hg = H >> 6, wg_per_e = hg / NG;
+    const int e = blockIdx.x / wg_per_e, rg0 = (blockIdx.x % wg_per_e) * NG;
     const int cnt = collect_pairs(ids, P, e, list);
     if (cnt == 0) return;
     const uint8_t* wexp = down + (int64_t)e * (H / 64) * (F / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 16) {
         const int M = min(16, cnt - c0);
         switch (M < 4 ? M : 4) {
-            case 1: down_chunk<1>(wexp, hbuf, H, F, rg, list + c0, M, red, ypair); break;
-            case 2: down_chunk<2>(wexp, hbuf, H, F, rg, list + c0, M, red, ypair); break;
-            case 3: down_chunk<3>(wexp, hbuf, H, F, rg, list + c0, M, red, ypair); break;
-            default: down_chunk<4>(wexp, hbuf, H, F, rg, list + c0, M, red, ypair); break;
+            case 1: down_chunk<1, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
+            case 2: down_chunk<2, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
+            case 3: down_chunk<3, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
+            default: down_chunk<4, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
         }
         __syncthreads();
     }
@@ -192,7 +209,8 @@ extern "C" int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const vo
     float* hbuf = (float*)workspace;
     float* ypair = (float*)((char*)workspace + align256((size_t)P * F * 4));
     const hipStream_t st = (hipStream_t)stream;
-    const dim3 gu((unsigned)(E * (F / 64))), dn((unsigned)(E * (H / 64)));
+    const int ng = H % 256 == 0 ? 4 : 1;
+    const dim3 gu((unsigned)(E * (F / 64))), dn((unsigned)(E * (H / (64 * ng))));
     if (x_dtype == Q4MI_F32)
         hipLaunchKernelGGL(moe_up_kernel<true>, gu, dim3(256), 0, st, gate_up, x, topk_ids, P, topk, (int)H, (int)F,
                            hbuf);
@@ -200,7 +218,10 @@ extern "C" int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const vo
         hipLaunchKernelGGL(moe_up_kernel<false>, gu, dim3(256), 0, st, gate_up, x, topk_ids, P, topk, (int)H,
                            (int)F, hbuf);
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-    hipLaunchKernelGGL(moe_down_kernel, dn, dim3(256), 0, st, down, hbuf, topk_ids, P, (int)H, (int)F, ypair);
+    if (ng == 4)
+        hipLaunchKernelGGL(moe_down_kernel<4>, dn, dim3(256), 0, st, down, hbuf, topk_ids, P, (int)H, (int)F, ypair);
+    else
+        hipLaunchKernelGGL(moe_down_kernel<1>, dn, dim3(256), 0, st, down, hbuf, topk_ids, P, (int)H, (int)F, ypair);
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
     const int64_t tot = (int64_t)T * H;
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st, ypair, topk_ids,

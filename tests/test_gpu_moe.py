@@ -33,6 +33,7 @@ def _make(oracle, pkg, gpu, E, H, F, seed):
     (16, 2048, 768, 16, 8, "bf16"),      # config 4's matrices (H=2048, F=768), 16 experts
     (4, 256, 192, 40, 2, "bf16"),        # ~20 tokens per expert: more than one 16-token chunk
     (8, 256, 128, 5, 3, "f32"),
+    (8, 192, 128, 5, 2, "bf16"),         # H % 256 != 0: one 64-row group per down workgroup
 ])
 def test_moe_matches_oracle(gpu, pkg, oracle, E, H, F, T, K, xdt):
     say(f"moe E={E} H={H} F={F} T={T} top{K} {xdt}")
