@@ -483,15 +483,36 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
             for (int e = 0; e < 4; ++e) v[2 * e] = bf16_lo_to_f32(w[e]), v[2 * e + 1] = bf16_hi_to_f32(w[e]);
         }
     };
+    // Rows of up to 2048 chunks (K <= 16384) are read once and held in registers for both
+    // the max and the conversion; longer rows are read twice.
+    constexpr int kHeld = 8;
+    const bool held = n8 <= 256 * kHeld;
+    float hv[kHeld][8];
+    if (held) {
+#pragma unroll
+        for (int c = 0; c < kHeld; ++c) {
+            const int i = threadIdx.x + 256 * c;
+            if (i < n8) ld8(i, hv[c]);
+        }
+    }
     float scale = 1.0f;
     if constexpr (PREC == 0) {
         __shared__ float red[4];
         float mx = 0.f;
-        for (int i = threadIdx.x; i < n8; i += 256) {
-            float v[8];
-            ld8(i, v);
+        if (held) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+            for (int c = 0; c < kHeld; ++c)
+                if (threadIdx.x + 256 * c < n8) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(hv[c][e]));
+                }
+        } else {
+            for (int i = threadIdx.x; i < n8; i += 256) {
+                float v[8];
+                ld8(i, v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+            }
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -507,9 +528,7 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
         scale = ldexpf(1.0f, -s);
         if (threadIdx.x == 0) tscale[t] = ldexpf(1.0f, s);
     }
-    for (int i = threadIdx.x; i < n8; i += 256) {
-        float v[8];
-        ld8(i, v);
+    auto cvt8 = [&](const float (&v)[8]) -> u32x4 {
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -523,7 +542,20 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
             }
             o[e] = lo | (hi << 16);
         }
-        out[dst(i)] = o;
+        return o;
+    };
+    if (held) {
+#pragma unroll
+        for (int c = 0; c < kHeld; ++c) {
+            const int i = threadIdx.x + 256 * c;
+            if (i < n8) out[dst(i)] = cvt8(hv[c]);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n8; i += 256) {
+            float v[8];
+            ld8(i, v);
+            out[dst(i)] = cvt8(v);
+        }
     }
 }
 

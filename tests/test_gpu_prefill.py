@@ -106,3 +106,22 @@ def test_prefill_empty(gpu, pkg, oracle):
     w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(64, 64, rng), gpu)
     Y = pkg.gemm_q4_prefill(w, torch.zeros(0, 64, dtype=torch.bfloat16, device=gpu))
     assert Y.shape == (0, 64)
+
+
+@pytest.mark.parametrize("T,N,K", [(300, 1024, 2048), (512, 4096, 14336)])
+def test_prefill_split_tiles_are_deterministic(gpu, pkg, oracle, T, N, K):
+    """Shapes whose output tiles are shared by several workgroups along K (the partial sums
+    meet in a fix-up): bit-identical across calls, and within the bar of the fp64 oracle."""
+    say(f"prefill split-tile determinism T={T} N={N} K={K}")
+    rng = np.random.default_rng(T + 7)
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    X = _x(rng, T, K)
+    w = pkg.pack_q4_1(blocks, gpu)
+    xg = X.to(gpu)
+    Y0 = pkg.gemm_q4_prefill(w, xg).cpu()
+    for _ in range(2):
+        Y1 = pkg.gemm_q4_prefill(w, xg).cpu()
+        assert torch.equal(Y0.view(torch.int32), Y1.view(torch.int32))
+    if T * N * K <= 1 << 31:
+        ref = oracle.prefill_reference(blocks, X.to(torch.float32).numpy())
+        assert oracle.maxrel(Y0.numpy(), ref) <= 1e-3

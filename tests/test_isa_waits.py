@@ -33,7 +33,11 @@ def _operands(line: str) -> list[str]:
 
 def early_uses(asm: list[str]) -> tuple[int, list[str]]:
     """(loads checked, descriptions of uses before the load's wait) for the first loop."""
-    head = next(i for i, l in enumerate(asm) if "Loop Header" in l)
+    # the innermost loop (the stage loop; an outer loop over tile segments may enclose it)
+    inner = any("Inner Loop Header" in l for l in asm)
+    head = next(i for i, l in enumerate(asm) if "Loop Header" in l and ("Inner" in l or not inner))
+    if not asm[head].startswith("."):           # header comment on its own line: label above
+        head -= 1
     label = asm[head].split(":")[0]
     end = next(i for i in range(head + 1, len(asm))
                if re.search(r"s_(?:cbranch_\w+|branch)\s+" + re.escape(label) + r"\b", asm[i]))
