@@ -81,6 +81,27 @@ int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* packed,
 int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed,
                    int64_t N, int64_t K, void* stream);
 
+/* GGUF Q4_K super-blocks -> mx layout, on the device. `q4k_blocks`:
+ * uint8[N][K/256][144] (fp16 d, fp16 dmin, 12 bytes of packed 6-bit sub-block
+ * scales/mins, 128 code bytes; llama.cpp's block_q4_K). Each 32-value sub-block
+ * is a Q4_1 block with d' = d * sc, m' = -dmin * min: both products are exact in
+ * f32 and are narrowed to bf16 (RNE), the arithmetic of the reference's Q4_K
+ * transcode (recipes/pack.py:266-310, q4k_to_q4_1) on GGUF's own block layout
+ * (model/gguf_ref.py:224-250). N % 64 == 0, K % 256 == 0. */
+int q4_repack_q4k(const uint8_t* q4k_blocks, uint8_t* packed, int64_t N, int64_t K, void* stream);
+
+/* The reference container's Q4_K chunks -> mx layout, on the device. `chunks`:
+ * 4736-byte 32-row x 256-K chunks in band order with row split `rs` (rs = 1 is
+ * the file's raster order): uint8 scales[8][32] @0 and mins @256 (index
+ * g*32 + r), codes @512 (row r of column k in byte 512 + 16k + r/2, even r in
+ * the low nibble), bf16 S[32] @4608, bf16 M[32] @4672 (negated). Each (row,
+ * 32-K block) becomes d = bf16_rne(S[r] * scales), m = bf16_rne(M[r] * mins),
+ * the reference's q4k_to_q4_1 (recipes/pack.py:266-310;
+ * src/open_qwen36/pools.cpp:642-663). K % 256 == 0, N % 64 == 0,
+ * N % (32*rs) == 0. */
+int q4_repack_q4k_chunks(const uint8_t* chunks, int rs, uint8_t* packed,
+                         int64_t N, int64_t K, void* stream);
+
 /* mx layout -> f32 W[N][K] row-major, w = fl32(q * d + m), bit-exact with
  * dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:155-180, q4nx.py:105-126). */
 int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);

@@ -91,6 +91,73 @@ __global__ __launch_bounds__(256) void repack_pool_kernel(const uint8_t* __restr
     mx_write_block(packed, KB, n, kb, code, (d16 << 16) | m16);
 }
 
+// GGUF Q4_K super-blocks (256 values, 144 B: fp16 d | fp16 dmin | 12 B of packed 6-bit
+// sub-block scales and mins | 128 B of codes) -> mx layout. Sub-block j (32 values) reads
+// d sc_j q - dmin m_j (llama.cpp's dequantize_row_q4_K; restated in the reference's
+// open_kernels/model/gguf_ref.py:224-250), i.e. a Q4_1 block with d' = d sc_j and
+// m' = -dmin m_j. Both products are exact in f32 (11-bit x 6-bit significands); they are
+// rounded to bf16 (RNE) as the reference's Q4_K transcode does (recipes/pack.py:266-310).
+// Codes: chunk c = j / 2 holds 32 bytes; sub-block 2c takes the low nibbles, 2c+1 the high.
+__global__ __launch_bounds__(256) void repack_q4k_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ packed,
+                                                         int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    const uint8_t* b = src + (n * (KB / 8) + kb / 8) * 144;
+    const int j = (int)(kb & 7);
+    const float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    const float dmin = f16_bits_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+    const uint8_t* sc = b + 4;
+    int s6, m6;
+    if (j < 4) {
+        s6 = sc[j] & 63;
+        m6 = sc[j + 4] & 63;
+    } else {
+        s6 = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4);
+        m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+    const float dd = d * (float)s6, mm = -(dmin * (float)m6);      // exact
+    const uint8_t* qs = b + 16 + 32 * (j >> 1);
+    const int sh = 4 * (j & 1);
+    uint8_t code[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) code[e] = (qs[e] >> sh) & 0xF;
+    mx_write_block(packed, KB, n, kb, code, (f32_to_bf16_rne(dd) << 16) | f32_to_bf16_rne(mm));
+}
+
+// The reference container's Q4_K chunks (4736 B, 32 rows x 256 K, in the pool's band
+// order with row split rs) -> mx layout (recipes/pack.py:266-310). Chunk: uint8
+// scales[8 g][32 r] @0, mins @256, codes @512 with row r of column k at byte
+// 512 + 16 k + r/2 (even r low nibble), bf16 S[32 r] @4608, bf16 M[32 r] @4672 (negated).
+// d = bf16_rne(S[r] * scales[g][r]), m = bf16_rne(M[r] * mins[g][r]); both f32 products
+// are exact (8-bit x 8-bit significands), so the one rounding is the reference's.
+__global__ __launch_bounds__(256) void repack_q4k_chunk_kernel(const uint8_t* __restrict__ chunks, int rs,
+                                                               uint8_t* __restrict__ packed, int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    const int64_t K = KB * 32;
+    const int64_t per_band = (int64_t)rs * K / 256;
+    const int64_t band = n / (32 * rs);
+    const int64_t ci = (kb / 8) * rs + (n % (32 * rs)) / 32;
+    const uint8_t* ch = chunks + (band * per_band + ci) * 4736;
+    const int r = (int)(n & 31);
+    const int g = (int)(kb & 7);
+    const float S = bf16_hi_to_f32(((uint32_t)ch[4608 + 2 * r] | ((uint32_t)ch[4609 + 2 * r] << 8)) << 16);
+    const float M = bf16_hi_to_f32(((uint32_t)ch[4672 + 2 * r] | ((uint32_t)ch[4673 + 2 * r] << 8)) << 16);
+    const float d = S * (float)ch[g * 32 + r], m = M * (float)ch[256 + g * 32 + r];   // exact
+    const uint8_t* codes = ch + 512 + (32 * g) * 16 + (r >> 1);
+    const int sh = 4 * (r & 1);
+    uint8_t code[32];
+#pragma unroll
+    for (int v = 0; v < 32; ++v) code[v] = (codes[v * 16] >> sh) & 0xF;
+    mx_write_block(packed, KB, n, kb, code, (f32_to_bf16_rne(d) << 16) | f32_to_bf16_rne(m));
+}
+
 // Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats.
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
                                                       int64_t N, int64_t K) {
@@ -159,5 +226,29 @@ extern "C" int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K,
     const int64_t total = N * (K / 8);
     const unsigned grid = (unsigned)((total + 255) / 256);
     hipLaunchKernelGGL(dequant_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, packed, w, N, K);
+    return launch_status();
+}
+
+extern "C" int q4_repack_q4k(const uint8_t* q4k_blocks, uint8_t* packed, int64_t N, int64_t K, void* stream) {
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!q4k_blocks || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % 256) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_q4k_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       q4k_blocks, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_repack_q4k_chunks(const uint8_t* chunks, int rs, uint8_t* packed, int64_t N, int64_t K,
+                                    void* stream) {
+    if (rs <= 0) return Q4MI_E_ARG;
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!chunks || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_q4k_chunk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, chunks, rs, packed, N, KB);
     return launch_status();
 }

@@ -19,6 +19,7 @@ torch's current stream of the tensors' device.
 from __future__ import annotations
 
 import ctypes as C
+import warnings
 from dataclasses import dataclass
 
 import numpy as np
@@ -28,7 +29,7 @@ from . import _lib
 from ._lib import Q4MI_BF16, Q4MI_F32, Q4GemvDesc, check
 
 __all__ = [
-    "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "dequant",
+    "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k", "pack_q4_k_chunks", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes",
 ]
@@ -56,7 +57,11 @@ def _stream(dev: torch.device) -> int:
 
 def _to_dev(a, dev: torch.device, dtype=None) -> torch.Tensor:
     if isinstance(a, np.ndarray):
-        t = torch.from_numpy(np.ascontiguousarray(a))
+        a = np.ascontiguousarray(a)
+        with warnings.catch_warnings():
+            # a read-only view (a memory-mapped file's tensor) is only read, to copy it over
+            warnings.filterwarnings("ignore", message="The given NumPy array is not writable")
+            t = torch.from_numpy(a)
     elif isinstance(a, torch.Tensor):
         t = a
     else:
@@ -149,6 +154,41 @@ def pack_q4_1_pool(pool, n: int, k: int, rs: int, device=None) -> PackedQ4:
     out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         check("q4_repack_pool", _lib_handle().q4_repack_pool(_ptr(src), rs, _ptr(out), n, k, _stream(dev)))
+    return PackedQ4(out, n, k)
+
+
+def pack_q4_k(blocks, device=None) -> PackedQ4:
+    """GGUF Q4_K super-blocks uint8[N, K/256, 144] -> mx layout on the GPU.
+
+    Every 32-value sub-block becomes a Q4_1 block with d = bf16(d*sc) and
+    m = bf16(-dmin*min): the products are exact, the bf16 rounding is the
+    reference's own Q4_K transcode (recipes/pack.py:266-310)."""
+    dev = _device(device if device is not None else (blocks.device if isinstance(blocks, torch.Tensor)
+                                                     and blocks.is_cuda else None))
+    src = _to_dev(blocks, dev, torch.uint8)
+    if src.dim() != 3 or src.shape[2] != 144:
+        raise ValueError(f"blocks must be uint8[N, K/256, 144], got {tuple(src.shape)}")
+    n, nsb, _ = src.shape
+    k = nsb * 256
+    out = torch.empty(packed_bytes(n, k), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_repack_q4k", _lib_handle().q4_repack_q4k(_ptr(src), _ptr(out), n, k, _stream(dev)))
+    return PackedQ4(out, n, k)
+
+
+def pack_q4_k_chunks(chunks, n: int, k: int, rs: int = 1, device=None) -> PackedQ4:
+    """The reference container's Q4_K chunks (4736 B per 32 rows x 256 K, band order
+    with row split rs; rs = 1 is the file raster) -> mx layout on the GPU, with
+    d = bf16(S*scale) and m = bf16(M*min) (recipes/pack.py:266-310)."""
+    dev = _device(device)
+    src = _to_dev(chunks, dev, torch.uint8).reshape(-1)
+    want = (n // 32) * (k // 256) * 4736 if n % 32 == 0 and k % 256 == 0 else -1
+    if src.numel() != want:
+        raise ValueError(f"Q4_K chunks hold {src.numel()} bytes, [{n}, {k}] needs {want} (4736 B per 32 x 256)")
+    out = torch.empty(packed_bytes(n, k), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_repack_q4k_chunks",
+              _lib_handle().q4_repack_q4k_chunks(_ptr(src), rs, _ptr(out), n, k, _stream(dev)))
     return PackedQ4(out, n, k)
 
 

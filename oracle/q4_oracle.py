@@ -457,3 +457,161 @@ def pack_mx_from_parts(d16: np.ndarray, m16: np.ndarray, q: np.ndarray) -> np.nd
     out[:, :, :MX_CODES] = np.ascontiguousarray(codes).reshape(G, nb, 256).view(np.uint8).reshape(G, nb, MX_CODES)
     out[:, :, MX_CODES:] = np.ascontiguousarray(sc).reshape(G, nb, 64).view(np.uint8).reshape(G, nb, 256)
     return out.reshape(-1)
+
+
+# --------------------------------------------------------------------------
+# Q4_K: GGUF super-blocks and the reference container's 4736 B chunks
+# --------------------------------------------------------------------------
+# GGUF Q4_K super-block, 144 B for 256 values along K (llama.cpp's block_q4_K, read by
+# open_kernels/model/gguf_ref.py:236-250 and src/gguf/gguf_file.cpp:611-635):
+#   [0, 2) fp16 d   [2, 4) fp16 dmin   [4, 16) eight packed 6-bit (scale, min) pairs
+#   [16, 144) codes: byte 32 c + l holds value 64 c + l (low nibble) and 64 c + 32 + l (high)
+# Sub-block j (values 32 j .. 32 j + 31) reads  d * sc_j * q - dmin * min_j.
+
+Q4_K_BYTES = 144
+Q4K_CHUNK = 4736     # container Q4_K chunk: 32 rows x 256 K (recipes/pack.py:272-283)
+
+
+def q4_k_scale_min(scales: np.ndarray, j: int):
+    """6-bit (sc_j, min_j) of sub-block j from the 12 packed bytes [..., 12]
+    (gguf_ref.py:224-233; get_scale_min_k4 in src/gguf/gguf_file.cpp). Sub-blocks 0-3
+    keep their pair in the low six bits of bytes j and j + 4; 4-7 keep the low four
+    bits in byte j + 4 (scale low nibble, min high nibble) and the top two bits in the
+    spare top bits of bytes j - 4 (scale) and j (min)."""
+    s = np.asarray(scales).astype(np.int32)
+    if j < 4:
+        return s[..., j] & 63, s[..., j + 4] & 63
+    return ((s[..., j + 4] & 0xF) | ((s[..., j - 4] >> 6) << 4),
+            (s[..., j + 4] >> 4) | ((s[..., j] >> 6) << 4))
+
+
+def unpack_q4_k_blocks(blocks: np.ndarray):
+    """uint8[n, K/256, 144] -> (d f32[n, K/32], m f32[n, K/32], q uint8[n, K]): each
+    sub-block as a Q4_1 block reading q*d + m, with d = fp16 d * sc_j and
+    m = -(fp16 dmin * min_j). Both products are exact in f32 (11-bit x 6-bit
+    significands), so this is a change of form, not of value (gguf_ref.py:236-250)."""
+    b = np.asarray(blocks, np.uint8)
+    n, ns, width = b.shape
+    if width != Q4_K_BYTES:
+        raise ValueError(f"block width {width} is not Q4_K ({Q4_K_BYTES})")
+    d = np.ascontiguousarray(b[..., 0:2]).view(np.float16).reshape(n, ns).astype(np.float32)
+    dmin = np.ascontiguousarray(b[..., 2:4]).view(np.float16).reshape(n, ns).astype(np.float32)
+    sc = b[..., 4:16]
+    qs = b[..., 16:144]
+    D = np.empty((n, ns, 8), np.float32)
+    M = np.empty((n, ns, 8), np.float32)
+    q = np.empty((n, ns, 8, BLK), np.uint8)
+    for j in range(8):
+        s6, m6 = q4_k_scale_min(sc, j)
+        D[..., j] = d * s6.astype(np.float32)
+        M[..., j] = -(dmin * m6.astype(np.float32))
+        half = qs[..., 32 * (j // 2):32 * (j // 2) + 32]
+        q[..., j, :] = (half >> 4) if j % 2 else (half & 0xF)
+    return D.reshape(n, ns * 8), M.reshape(n, ns * 8), q.reshape(n, ns * 256)
+
+
+def dequant_q4_k(blocks: np.ndarray) -> np.ndarray:
+    """GGUF Q4_K -> f32[n, K] as the reference reads it: fl32(d sc q - dmin min)
+    (gguf_file.cpp:627-630). d sc q is exact, so this equals fl32(q*D + M)."""
+    D, M, q = unpack_q4_k_blocks(blocks)
+    return q.astype(np.float32) * np.repeat(D, BLK, axis=1) + np.repeat(M, BLK, axis=1)
+
+
+def dequant_q4_k_bf16(blocks: np.ndarray) -> np.ndarray:
+    """What the kernels see of a Q4_K weight: D and M narrowed to bf16 (RNE), then
+    fl32(q*d + m) -- the reference's Q4_K -> q4_1 collapse (recipes/pack.py:266-310)."""
+    D, M, q = unpack_q4_k_blocks(blocks)
+    return q.astype(np.float32) * np.repeat(bf16_round(D), BLK, axis=1) + np.repeat(bf16_round(M), BLK, axis=1)
+
+
+def pack_mx_q4_k(blocks: np.ndarray) -> np.ndarray:
+    """GGUF Q4_K [N, K/256, 144] -> the MI355X layout bytes (D, M rounded to bf16)."""
+    D, M, q = unpack_q4_k_blocks(blocks)
+    return pack_mx_from_parts(f32_to_bf16(D), f32_to_bf16(M), q)
+
+
+def random_q4_k_blocks(n: int, k: int, rng: np.random.Generator, scale: float = 0.02) -> np.ndarray:
+    """Seeded GGUF Q4_K super-blocks: every packed scale/min byte and code uniform, fp16 d
+    and dmin positive and sized so d*sc*15 is about ``scale`` (llama.cpp's quantizer
+    makes d = max_j(scale_j)/63 and dmin = max_j(min_j)/63)."""
+    assert k % 256 == 0
+    ns = k // 256
+    b = rng.integers(0, 256, (n, ns, Q4_K_BYTES), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.5, (n, ns)) * scale / (15 * 40)).astype(np.float16)
+    dmin = (rng.uniform(0.5, 1.5, (n, ns)) * scale / 40).astype(np.float16)
+    b[..., 0:2] = d.view(np.uint8).reshape(n, ns, 2)
+    b[..., 2:4] = dmin.view(np.uint8).reshape(n, ns, 2)
+    return b
+
+
+def q4k_chunks_to_pool(chunks: np.ndarray) -> np.ndarray:
+    """Container Q4_K chunks [n, 4736] -> pool q4_1 chunks [n, 5120], same order
+    (recipes/pack.py:266-310; test_quant_q4k.py:7-13 gives the layout):
+
+      Q4_K chunk: scales u8[8 g][32 r] @0, mins u8 @256, codes @512 with row r of
+      column k at byte 512 + 16 k + r//2 (even r low nibble), S bf16[32 r] @4608,
+      M bf16[32 r] @4672 (stored negated); value S sc nib + M min.
+
+    Pool d = bf16_rne(S[r] sc[g][r]) and m = bf16_rne(M[r] min[g][r]) at index 32 g + r
+    (the f32 products are exact: 8-bit x 8-bit significands). Codes: pool byte
+    2048 h + 8 k + i = chunk byte 512 + 16 k + 8 h + i (rows 16 h .. 16 h + 15)."""
+    src = np.asarray(chunks, np.uint8).reshape(-1, Q4K_CHUNK)
+    n = src.shape[0]
+    S = bf16_to_f32(np.ascontiguousarray(src[:, 4608:4672]).view(np.uint16))   # [n, 32 r]
+    Mn = bf16_to_f32(np.ascontiguousarray(src[:, 4672:4736]).view(np.uint16))
+    sc = src[:, 0:256].reshape(n, 8, 32).astype(np.float32)                     # [n, g, r]
+    mn = src[:, 256:512].reshape(n, 8, 32).astype(np.float32)
+    d16 = f32_to_bf16(S[:, None, :] * sc).reshape(n, 256)
+    m16 = f32_to_bf16(Mn[:, None, :] * mn).reshape(n, 256)
+    out = np.empty((n, CH), np.uint8)
+    out[:, 0:512] = d16.view(np.uint8).reshape(n, 512)
+    out[:, 512:1024] = m16.view(np.uint8).reshape(n, 512)
+    codes = src[:, 512:4608].reshape(n, 256, 2, 8)                               # [k, h, i]
+    out[:, 1024:] = np.ascontiguousarray(codes.transpose(0, 2, 1, 3)).reshape(n, 4096)
+    return out
+
+
+def dequant_q4k_chunks_exact(chunks: np.ndarray) -> np.ndarray:
+    """Container Q4_K chunks -> f64 [n, 32 r, 256 k], the value the layout states, with no
+    bf16 collapse (test_quant_q4k.py:100-112's reading)."""
+    src = np.asarray(chunks, np.uint8).reshape(-1, Q4K_CHUNK)
+    n = src.shape[0]
+    S = bf16_to_f32(np.ascontiguousarray(src[:, 4608:4672]).view(np.uint16)).astype(np.float64)
+    Mn = bf16_to_f32(np.ascontiguousarray(src[:, 4672:4736]).view(np.uint16)).astype(np.float64)
+    sc = src[:, 0:256].reshape(n, 8, 32).astype(np.float64)
+    mn = src[:, 256:512].reshape(n, 8, 32).astype(np.float64)
+    cb = src[:, 512:4608].reshape(n, 256, 16)                                   # [k, r//2]
+    r = np.arange(32)
+    nib = np.where(r % 2 == 0, cb[:, :, r // 2] & 0xF, cb[:, :, r // 2] >> 4)  # [n, k, r]
+    nib = nib.transpose(0, 2, 1).astype(np.float64)                             # [n, r, k]
+    g = np.arange(256) // 32
+    scale = S[:, :, None] * sc[:, g, :].transpose(0, 2, 1)                      # [n, r, k]
+    off = Mn[:, :, None] * mn[:, g, :].transpose(0, 2, 1)
+    return scale * nib + off
+
+
+def q4k_vector(nch: int) -> np.ndarray:
+    """The reference's seeded container Q4_K chunks (test_quant_q4k.py:60-80): per chunk
+    c an LCG (x <- 1664525 x + 1013904223 mod 2^32, byte = x >> 24) seeded with
+    0x9E3779B9 (c + 1); 4608 plain bytes, then 32 bf16 S = 0x3B00 | byte and 32 bf16
+    M = 0xBB00 | byte (negative)."""
+    M32 = 0xFFFFFFFF
+    out = np.zeros((nch, Q4K_CHUNK), np.uint8)
+    for c in range(nch):
+        s = (0x9E3779B9 * (c + 1)) & M32
+        stream = np.empty(4672, np.uint32)
+        for i in range(4672):
+            s = (s * 1664525 + 1013904223) & M32
+            stream[i] = s >> 24
+        out[c, :4608] = stream[:4608]
+        sm = np.concatenate([0x3B00 | stream[4608:4640], 0xBB00 | stream[4640:4672]]).astype(np.uint16)
+        out[c, 4608:] = sm.view(np.uint8)
+    return out
+
+
+def fnv1a64(data) -> int:
+    """FNV-1a 64-bit hash of a byte string (test_pack_plan.py:183-187)."""
+    h = 0xCBF29CE484222325
+    for x in bytes(data):
+        h = ((h ^ x) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h

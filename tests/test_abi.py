@@ -20,8 +20,8 @@ def declared_functions() -> list[str]:
 
 def test_header_declares_the_expected_surface():
     names = declared_functions()
-    for must in ("q4_packed_bytes", "q4_repack", "q4_repack_pool", "q4_dequant", "q4_gemv",
-                 "q4_gemv_grouped", "q4_gemm_prefill", "q4_moe_gemv"):
+    for must in ("q4_packed_bytes", "q4_repack", "q4_repack_pool", "q4_repack_q4k", "q4_repack_q4k_chunks",
+                 "q4_dequant", "q4_gemv", "q4_gemv_grouped", "q4_gemm_prefill", "q4_moe_gemv"):
         assert must in names
 
 
@@ -62,6 +62,13 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_repack_pool(fake, 2, fake, 64, 128, None) == -1        # K % 256
     assert lib.q4_repack_pool(fake, 0, fake, 64, 256, None) == -2        # rs
     assert lib.q4_repack_pool(fake, 4, fake, 64, 256, None) == -1        # N % (32 rs)
+    assert lib.q4_repack_q4k(fake, fake, 64, 128, None) == -1            # K % 256
+    assert lib.q4_repack_q4k(fake, fake, 32, 256, None) == -1            # N % 64
+    assert lib.q4_repack_q4k(None, fake, 64, 256, None) == -2            # NULL
+    assert lib.q4_repack_q4k(None, None, 0, 256, None) == 0              # empty is a no-op
+    assert lib.q4_repack_q4k_chunks(fake, 1, fake, 64, 128, None) == -1  # K % 256
+    assert lib.q4_repack_q4k_chunks(fake, 0, fake, 64, 256, None) == -2  # rs
+    assert lib.q4_repack_q4k_chunks(fake, 4, fake, 64, 256, None) == -1  # N % (32 rs)
     assert lib.q4_dequant(fake, None, 64, 32, None) == -2
     assert lib.q4_dequant(None, None, 0, 32, None) == 0
     assert lib.q4_gemv(fake, fake, 2, fake, 1, 64, 32, None, 0, None) == -2    # dtype
@@ -81,6 +88,8 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_gemv(odd, fake, 1, fake, 1, 128256, 4096, None, 0, None) == -2
     assert lib.q4_dequant(fake, odd, 64, 32, None) == -2
     assert lib.q4_repack(fake, 20, odd, 64, 32, 0, None) == -2
+    assert lib.q4_repack_q4k(fake, odd, 64, 256, None) == -2
+    assert lib.q4_repack_q4k_chunks(fake, 1, odd, 64, 256, None) == -2
     need = lib.q4_gemm_prefill_workspace_bytes(64, 256, 1024)
     assert lib.q4_gemm_prefill(fake, fake, 1, odd, 64, 256, 1024, 0, fake, need, None) == -2
     assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 256, 1024, 0, odd, need, None) == -2
