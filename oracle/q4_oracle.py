@@ -19,6 +19,10 @@ this hot path (``/root/reference`` is read as text, never imported):
 * MoE routing + expert reference  open_kernels/model/replica.py:121-140,
                                   open_kernels/designs/moe_batch/make_test.py:87-98
 * Q4_0 -> Q4_1 transcode          open_kernels/recipes/pack.py:606-622
+* GGUF Q4_K super-blocks          open_kernels/model/gguf_ref.py:224-250,
+                                  src/gguf/gguf_file.cpp:611-635
+* container Q4_K -> q4_1 chunks   open_kernels/recipes/pack.py:266-310,
+                                  src/open_qwen36/pools.cpp:642-663
 
 ``ml_dtypes`` (which the reference uses for its bf16 casts) is absent here; the
 bf16 conversions are restated as IEEE round-to-nearest-even on the f32 bits.
@@ -28,7 +32,13 @@ Pinning (what fixes each function independently of its own formula) is done in
 ``specs/open-engine/tests/test_q4nx_decode_layout.py:8-30``, the pack->dequant
 identity of ``q4_1_pack._selftest`` (:194-209), torch's own fp16->bf16 RNE,
 brute-force scalar loops on tiny shapes, one-hot / all-ones activations, and
-the exact Q4_0 identity m = -8 d.  Functions with no such check are marked
+the exact Q4_0 identity m = -8 d.  The Q4_K functions are pinned in
+``tests/test_gguf.py``: against the reference's own C++ GGUF reader, built from
+its sources into ``oracle/_ref/gguf_dump`` (bit-exact f32 dequant), by an
+exhaustive encode -> decode of the packed 6-bit scales, a closed-form block,
+and the reference's property checks of the container transcode (the published
+FNV-1a of that transcode is not reproduced; the test records it as a strict
+xfail).  Functions with no such check are marked
 "parity unpinned" in their docstrings (there are none at present).
 
 The MI355X weight layout (``pack_mx`` / ``unpack_mx``) is this build's own
