@@ -185,7 +185,7 @@ def graph_time(torch, fn, outputs, replays: int = 20) -> float:
         fn()
     torch.cuda.synchronize()
     for o in outputs:
-        o.fill_(float("nan"))
+        o.fill_(float("nan") if o.is_floating_point() else -12345)
     g.replay()
     torch.cuda.synchronize()
     for o, e in zip(outputs, eager):
@@ -287,6 +287,37 @@ def extra_staged(torch, q4, model, acts, xhead):
             q4.gemm_q4(w, x, y, workspace=ws)
     ms = graph_time(torch, run, outs, replays=10)
     return {"ms": ms, "gbs": nbytes / ms / 1e6, "calls": len(calls), "bytes": nbytes}
+
+
+def extra_lm_head(torch, q4, dev, head=None, xhead=None):
+    """lm_head at vocabulary scale (128256 x 4096, M=1) with its sampling epilogue:
+    the GEMV alone, then GEMV + greedy argmax and GEMV + top-40 (the sampler's
+    bf16 view), each graph-timed, and the epilogue's own cost beside it."""
+    if head is None:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED + 7)
+        head = q4.pack_q4_1(gen_blocks(torch, LM_HEAD[1], LM_HEAD[2], gen, dev), dev)
+        xhead = torch.randn(1, LM_HEAD[2], generator=gen, device=dev).to(torch.bfloat16)
+    logits = torch.empty(1, head.n, dtype=torch.float32, device=dev)
+    ws = torch.empty(max(q4.gemv_workspace_bytes(1, head.n, head.k), 1 << 20), dtype=torch.uint8, device=dev)
+    out = {"N": head.n, "K": head.k, "weight_bytes": head.nbytes}
+    ms = graph_time(torch, lambda: q4.gemm_q4(head, xhead, logits, workspace=ws), [logits], replays=20)
+    out["gemv_us"] = round(ms * 1e3, 2)
+    out["gemv_gbs"] = round((head.nbytes + head.k * 2 + head.n * 4) / ms / 1e6, 1)
+    for k in (1, 40):
+        ids = torch.empty(1, k, dtype=torch.int32, device=dev)
+        vals = torch.empty(1, k, dtype=torch.float32, device=dev)
+
+        def full():
+            q4.lm_head_topk(head, xhead, k=k, mode="sampler", logits=logits, workspace=ws, ids=ids, vals=vals)
+        ms_full = graph_time(torch, full, [logits, ids, vals], replays=20)
+
+        def epi():
+            q4.logits_topk(logits, k, "sampler", workspace=ws, ids=ids, vals=vals)
+        ms_epi = graph_time(torch, epi, [ids, vals], replays=20)
+        out[f"top{k}_us"] = round(ms_full * 1e3, 2)
+        out[f"top{k}_epilogue_us"] = round(ms_epi * 1e3, 2)
+    return out
 
 
 def extra_peaks(torch, dev):
@@ -405,7 +436,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="staged,0,2,3,4,peaks", help="comma list (staged,0,2,3,4,peaks) or 'none'")
+    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,peaks",
+                    help="comma list (staged,0,2,3,4,lm_head,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=15, help="passes over one layer in the CPU baseline")
     ap.add_argument("--cpu-baseline-child", type=int, default=None, help=argparse.SUPPRESS)
@@ -449,6 +481,8 @@ def main() -> int:
                 out["config4_moe"] = extra_config4(torch, q4, dev)
             elif cfg == "peaks":
                 out["measured_peaks"] = extra_peaks(torch, dev)
+            elif cfg == "lm_head":
+                out["lm_head_topk"] = extra_lm_head(torch, q4, dev)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -480,6 +514,8 @@ def main() -> int:
                 extras["config3_prefill"] = extra_config3(torch, q4, dev)
             elif cfg == "4":
                 extras["config4_moe"] = extra_config4(torch, q4, dev)
+            elif cfg == "lm_head":
+                extras["lm_head_topk"] = extra_lm_head(torch, q4, dev, model.head, xhead)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
         log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")

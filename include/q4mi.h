@@ -141,6 +141,39 @@ typedef struct q4_gemv_desc {
 int q4_gemv_grouped(const q4_gemv_desc* descs, int count, int64_t total_items,
                     int M, int x_dtype, void* stream);
 
+/* Workspace bytes q4_logits_topk needs for M rows of n logits and k (0 if none). */
+size_t q4_topk_workspace_bytes(int M, int64_t n, int k);
+
+/* The sampling epilogue: for each of M rows of f32 logits (row stride ld >= n),
+ * the k largest of logits[m][0..n) (1 <= k <= 64), value descending and the
+ * lower id first on a tie, into ids int32[M][k] and (if not NULL) vals
+ * f32[M][k]. k = 1 is the greedy argmax. mode 1 ranks what the sampler sees:
+ * each logit rounded to bf16 (RNE), an f32 subnormal read as 0 -- the greedy
+ * pick of Sampler::sample_greedy over Engine::logits_view's bf16 logits
+ * (src/common/modules/sampler.cpp:355-430, src/open_qwen36/engine.cpp:125-131;
+ * stated as argmax_bf16, src/open_qwen36/cli.cpp:103-113), and the order of
+ * Sampler::sampler_topk_apply (sampler.cpp:222-245). mode 0 ranks the f32
+ * logits themselves. Both read -0 as +0 and NaN below every number; vals are
+ * the ranked values (bf16-rounded in mode 1). A row with fewer than k entries
+ * pads with id -1, value -inf. */
+int q4_logits_topk(const float* logits, int64_t ld, int M, int64_t n, int k, int mode,
+                   int32_t* ids, float* vals, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* Workspace bytes q4_lm_head_topk needs (0 if none). */
+size_t q4_lm_head_workspace_bytes(int M, int64_t N, int64_t K, int k);
+
+/* lm_head at vocabulary scale with its sampling epilogue: logits[M][N] =
+ * q4_gemv(packed [N, K], x [M][K]) (1 <= M <= 16), then q4_logits_topk over the
+ * first n_valid <= N rows of each token (rows past the tokenizer's vocabulary
+ * are padding, read as -inf by Engine::logits_view, engine.cpp:129-130).
+ * Replaces the lm_head_q4 design (designs/lm_head_q4/lm_head_q4.py: pool W,
+ * bf16 x, f32 logits) plus the host's greedy / top-k pass over its logits. */
+int q4_lm_head_topk(const uint8_t* packed, const void* x, int x_dtype, float* logits,
+                    int M, int64_t N, int64_t K, int64_t n_valid, int k, int mode,
+                    int32_t* ids, float* vals, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* Workspace bytes q4_gemm_prefill needs (0 if none). */
 size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K);
 

@@ -40,6 +40,11 @@ SIGNATURES = {
     "q4_gemv_grouped": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp]),
     "q4_gemm_prefill_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemm_prefill": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _vp, _sz, _vp]),
+    "q4_topk_workspace_bytes": (_sz, [_i32, _i64, _i32]),
+    "q4_logits_topk": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "q4_lm_head_workspace_bytes": (_sz, [_i32, _i64, _i64, _i32]),
+    "q4_lm_head_topk": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _sz,
+                               _vp]),
     "q4_moe_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "q4_moe_gemv": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp, _sz, _vp]),
 }

@@ -31,7 +31,7 @@ from ._lib import Q4MI_BF16, Q4MI_F32, Q4GemvDesc, check
 __all__ = [
     "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k", "pack_q4_k_chunks", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
-    "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes",
+    "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "logits_topk", "lm_head_topk",
 ]
 
 ROWS = 64          # rows per mx tile / row group
@@ -295,6 +295,85 @@ def gemv_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tens
         raise ValueError("gemv_q4 takes one activation vector x[K]")
     out = gemm_q4(w, xt.unsqueeze(0), None if y is None else y.view(1, -1), workspace)
     return out.view(-1)
+
+
+# --------------------------------------------------------------------------
+# lm_head and its sampling epilogue
+# --------------------------------------------------------------------------
+
+_TOPK_MODES = {"f32": 0, "sampler": 1}
+
+
+def _topk_mode(mode) -> int:
+    if mode not in _TOPK_MODES:
+        raise ValueError(f"mode must be one of {sorted(_TOPK_MODES)}, got {mode!r}")
+    return _TOPK_MODES[mode]
+
+
+def _topk_outputs(M: int, k: int, dev, ids, vals):
+    if ids is None:
+        ids = torch.empty((M, k), dtype=torch.int32, device=dev)
+    if vals is None:
+        vals = torch.empty((M, k), dtype=torch.float32, device=dev)
+    if ids.dtype != torch.int32 or vals.dtype != torch.float32 or ids.numel() < M * k or vals.numel() < M * k \
+            or not ids.is_contiguous() or not vals.is_contiguous():
+        raise ValueError("ids must be int32 and vals float32, contiguous, M*k elements each")
+    return ids, vals
+
+
+def logits_topk(logits: torch.Tensor, k: int = 1, mode: str = "sampler", n_valid: int | None = None,
+                workspace: torch.Tensor | None = None, ids: torch.Tensor | None = None,
+                vals: torch.Tensor | None = None):
+    """The k largest logits of each row (value descending, lower id first on a tie),
+    as (ids int32[M, k], vals f32[M, k]); k = 1 is the greedy argmax.
+
+    mode "sampler" ranks what the reference's sampler sees -- each logit rounded to
+    bf16, an f32 subnormal read as 0 (Sampler::sample_greedy / sampler_topk_apply,
+    src/common/modules/sampler.cpp:222-245, :355-430); "f32" ranks the logits as they
+    are. Rows past ``n_valid`` (padding beyond the tokenizer's vocabulary) are skipped."""
+    if logits.dtype != torch.float32 or not logits.is_cuda:
+        raise TypeError("logits must be a float32 GPU tensor")
+    lg = logits if logits.dim() == 2 else logits.view(1, -1)
+    if lg.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    M, N = lg.shape
+    n = N if n_valid is None else int(n_valid)
+    dev = lg.device
+    ids, vals = _topk_outputs(M, k, dev, ids, vals)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_topk_workspace_bytes(M, n, k), "topk", workspace)
+        check("q4_logits_topk", lib.q4_logits_topk(_ptr(lg), lg.stride(0), M, n, k, _topk_mode(mode),
+                                                   _ptr(ids), _ptr(vals), wp, wn, _stream(dev)))
+    return ids, vals
+
+
+def lm_head_topk(w: PackedQ4, x, k: int = 1, mode: str = "sampler", n_valid: int | None = None,
+                 logits: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                 ids: torch.Tensor | None = None, vals: torch.Tensor | None = None):
+    """lm_head over 1..16 tokens and its sampling epilogue in one call:
+    (ids int32[M, k], vals f32[M, k], logits f32[M, N]) (designs/lm_head_q4 plus the
+    host's greedy / top-k pass; see logits_topk for ``mode`` and ``n_valid``)."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != w.k:
+        raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
+    n = w.n if n_valid is None else int(n_valid)
+    if logits is None:
+        logits = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    elif logits.dtype != torch.float32 or not logits.is_contiguous() or logits.numel() < M * w.n:
+        raise ValueError("logits must be a contiguous float32 [M, N] tensor")
+    ids, vals = _topk_outputs(M, k, dev, ids, vals)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_lm_head_workspace_bytes(M, w.n, w.k, k), "lm_head", workspace)
+        check("q4_lm_head_topk", lib.q4_lm_head_topk(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(logits), M, w.n,
+                                                     w.k, n, k, _topk_mode(mode), _ptr(ids), _ptr(vals), wp, wn,
+                                                     _stream(dev)))
+    return ids, vals, logits
 
 
 class GemvGroup:

@@ -625,3 +625,41 @@ def fnv1a64(data) -> int:
     for x in bytes(data):
         h = ((h ^ x) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
     return h
+
+
+# --------------------------------------------------------------------------
+# The lm_head's sampling epilogue
+# --------------------------------------------------------------------------
+
+def sampler_view(logits: np.ndarray) -> np.ndarray:
+    """What the reference's sampler ranks: each f32 logit rounded to bf16 by the plain RNE
+    formula (src/open_qwen36/q4nx_file.hpp:97-101; Engine::logits_view,
+    src/open_qwen36/engine.cpp:125-131), an f32 subnormal read as +0
+    (argmax_bf16, src/open_qwen36/cli.cpp:103-113)."""
+    v = np.ascontiguousarray(logits, np.float32)
+    u = v.view(np.uint32)
+    r = bf16_to_f32(f32_to_bf16(v))
+    return np.where((u & np.uint32(0x7F800000)) == 0, np.float32(0.0), r).astype(np.float32)
+
+
+def topk_reference(logits: np.ndarray, k: int, mode: int = 1, n_valid: int | None = None):
+    """(ids int32[M, k], vals f32[M, k]): per row, the k largest of the first n_valid
+    values -- value descending, the lower id first on a tie (sampler.cpp:230-241's
+    comparator), -0 equal to +0, NaN below every number. mode 1 ranks sampler_view of
+    the logits, mode 0 the logits. Rows with fewer than k values pad with -1 / -inf."""
+    lg = np.atleast_2d(np.asarray(logits, np.float32))
+    M, N = lg.shape
+    n = N if n_valid is None else int(n_valid)
+    v = lg[:, :n]
+    if mode == 1:
+        v = sampler_view(v)
+    ids = np.full((M, k), -1, np.int32)
+    vals = np.full((M, k), -np.inf, np.float32)
+    idx = np.arange(n)
+    for m in range(M):
+        row = v[m]
+        nan = np.isnan(row)
+        order = np.lexsort((idx, -np.where(nan, 0.0, row).astype(np.float64), nan))[:k]
+        ids[m, :len(order)] = order
+        vals[m, :len(order)] = row[order]
+    return ids, vals

@@ -21,7 +21,8 @@ def declared_functions() -> list[str]:
 def test_header_declares_the_expected_surface():
     names = declared_functions()
     for must in ("q4_packed_bytes", "q4_repack", "q4_repack_pool", "q4_repack_q4k", "q4_repack_q4k_chunks",
-                 "q4_dequant", "q4_gemv", "q4_gemv_grouped", "q4_gemm_prefill", "q4_moe_gemv"):
+                 "q4_dequant", "q4_gemv", "q4_gemv_grouped", "q4_gemm_prefill", "q4_moe_gemv",
+                 "q4_logits_topk", "q4_lm_head_topk"):
         assert must in names
 
 
@@ -96,6 +97,18 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 256, 1024, 0, fake, need - 1, None) == -3
     assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 256, 1024, 2, fake, need, None) == -2
     assert lib.q4_gemm_prefill(fake, fake, 1, fake, 64, 100, 1024, 0, fake, need, None) == -1
+    assert lib.q4_logits_topk(fake, 10, 1, 10, 65, 1, fake, None, None, 0, None) == -5   # k > 64
+    assert lib.q4_logits_topk(fake, 10, 1, 10, 0, 1, fake, None, None, 0, None) == -5    # k < 1
+    assert lib.q4_logits_topk(fake, 10, 1, 10, 1, 2, fake, None, None, 0, None) == -5    # mode
+    assert lib.q4_logits_topk(fake, 5, 1, 10, 1, 1, fake, None, None, 0, None) == -1     # ld < n
+    assert lib.q4_logits_topk(None, 10, 1, 10, 1, 1, fake, None, None, 0, None) == -2    # NULL
+    assert lib.q4_logits_topk(None, 10, 0, 10, 1, 1, None, None, None, 0, None) == 0     # M = 0
+    need = lib.q4_topk_workspace_bytes(2, 128256, 40)
+    assert need >= 2 * 32 * 40 * 8
+    assert lib.q4_logits_topk(fake, 128256, 2, 128256, 40, 1, fake, None, fake, need - 1, None) == -3
+    assert lib.q4_topk_workspace_bytes(1, 1024, 64) == 0          # one block per token: none
+    assert lib.q4_lm_head_topk(fake, fake, 1, fake, 1, 128256, 4096, 128257, 1, 1, fake, None, None, 0,
+                               None) == -1                        # n_valid > N
     wsm = lib.q4_moe_workspace_bytes(16, 128, 8, 2048, 768)
     assert lib.q4_moe_gemv(fake, fake, odd, 1, fake, fake, fake, 16, 128, 8, 2048, 768, fake, wsm, None) == -2
 
