@@ -167,10 +167,14 @@ def time_launches(torch, fn, steps: int, warmup: int):
     return t0.elapsed_time(t1), sum(a.elapsed_time(b) for a, b in ev) / steps
 
 
-def graph_time(torch, fn, outputs, replays: int = 20) -> float:
+def graph_time(torch, fn, outputs, replays: int = 20, reset=None) -> float:
     """Capture fn() in a HIP graph, check one replay against the eager run
     (bit for bit: every kernel here is deterministic), then time `replays`
-    replays with events. Returns mean ms per replay."""
+    replays with events. Returns mean ms per replay. `reset` restores the state
+    of an fn that updates its inputs in place (a residual stream) before the
+    eager run and before the checked replay."""
+    if reset:
+        reset()
     fn()
     torch.cuda.synchronize()
     eager = [o.clone() for o in outputs]
@@ -184,8 +188,11 @@ def graph_time(torch, fn, outputs, replays: int = 20) -> float:
     with torch.cuda.graph(g, stream=side):
         fn()
     torch.cuda.synchronize()
-    for o in outputs:
-        o.fill_(float("nan") if o.is_floating_point() else -12345)
+    if reset:
+        reset()
+    else:
+        for o in outputs:
+            o.fill_(float("nan") if o.is_floating_point() else -12345)
     g.replay()
     torch.cuda.synchronize()
     for o, e in zip(outputs, eager):
@@ -320,6 +327,57 @@ def extra_lm_head(torch, q4, dev, head=None, xhead=None):
     return out
 
 
+def extra_ffn(torch, q4, model, acts):
+    """The decode FFN of all 32 layers at M=1, graph-timed two ways over the same
+    weights: fused (q4_rmsnorm_add -> q4_gemv_swiglu with bf16 h -> q4_gemv_residual in
+    place) and unfused (torch RMSNorm, the gate/up GEMV, torch silu * up, the down GEMV,
+    torch residual add). Bytes: gate/up + down weights + activations per layer."""
+    dev = model.head.device
+    F, H = 14336, 4096
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 11)
+    xres = torch.randn(1, H, generator=gen, device=dev)
+    nw = (1 + 0.1 * torch.randn(H, generator=gen, device=dev)).to(torch.bfloat16)
+    xn = torch.empty(1, H, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(1, F, dtype=torch.bfloat16, device=dev)
+    gu = torch.empty(1, 2 * F, dtype=torch.float32, device=dev)
+    yd = torch.empty(1, H, dtype=torch.float32, device=dev)
+    ws = torch.empty(1 << 24, dtype=torch.uint8, device=dev)
+    nbytes = sum(p["gate_up"].nbytes + p["down"].nbytes for p in model.layers)
+
+    def fused():
+        for p in model.layers:
+            q4.rmsnorm_add(xres, nw, xn=xn)
+            q4.swiglu_q4(p["gate"], p["up"], xn, out_dtype=torch.bfloat16, h=h, workspace=ws)
+            q4.gemm_q4(p["down"], h, y=xres, residual=xres, workspace=ws)
+
+    def unfused():
+        for p in model.layers:
+            xf = xres * torch.rsqrt(xres.pow(2).mean(-1, keepdim=True) + 1e-6) * nw.to(torch.float32)
+            xn.copy_(xf.to(torch.bfloat16))
+            q4.gemm_q4(p["gate_up"], xn, y=gu, workspace=ws)
+            h.copy_((torch.nn.functional.silu(gu[:, :F]) * gu[:, F:]).to(torch.bfloat16))
+            q4.gemm_q4(p["down"], h, y=yd, workspace=ws)
+            xres.add_(yd)
+
+    x0 = xres.clone()
+    out = {"layers": len(model.layers), "weight_bytes": nbytes}
+    results = {}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        ms = graph_time(torch, fn, [xres], replays=5, reset=lambda: xres.copy_(x0))
+        results[name] = xres.clone()
+        out[f"{name}_ms"] = round(ms, 4)
+        out[f"{name}_gbs"] = round(nbytes / ms / 1e6, 1)
+    xres.copy_(x0)
+    fused()
+    a = xres.clone()
+    xres.copy_(x0)
+    unfused()
+    out["fused_vs_unfused_maxrel"] = float(((a - xres).abs().max() / xres.abs().max()).item())
+    xres.copy_(x0)
+    return out
+
+
 def extra_peaks(torch, dev):
     """On-box reference points: HBM read bandwidth of a plain reduction over
     4 GiB (torch.sum, reads only) and dense bf16 GEMM throughput of the vendor
@@ -436,8 +494,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,peaks",
-                    help="comma list (staged,0,2,3,4,lm_head,peaks) or 'none'")
+    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,peaks",
+                    help="comma list (staged,0,2,3,4,lm_head,ffn,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=15, help="passes over one layer in the CPU baseline")
     ap.add_argument("--cpu-baseline-child", type=int, default=None, help=argparse.SUPPRESS)
@@ -516,6 +574,8 @@ def main() -> int:
                 extras["config4_moe"] = extra_config4(torch, q4, dev)
             elif cfg == "lm_head":
                 extras["lm_head_topk"] = extra_lm_head(torch, q4, dev, model.head, xhead)
+            elif cfg == "ffn":
+                extras["ffn_fused_decode"] = extra_ffn(torch, q4, model, acts)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
         log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")

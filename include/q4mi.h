@@ -122,6 +122,36 @@ int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
             int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
             void* stream);
 
+/* q4_gemv plus the residual: y = residual + X . W^T (residual f32 [M][N]; it may
+ * be y itself, which then accumulates in place). Same workspace as q4_gemv. The
+ * residual adds the reference makes after a projection: x_res + o_proj / down
+ * (open_kernels/model/replica.py:81, :144; designs/moe_combine/moe_fin.py:1-4). */
+int q4_gemv_residual(const uint8_t* packed, const void* x, int x_dtype, const float* residual,
+                     float* y, int M, int64_t N, int64_t K, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* Workspace bytes q4_gemv_swiglu needs for (M, F, K); 0 when it needs none. */
+size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K);
+
+/* The FFN's first half with SwiGLU fused: h[M][F] = silu(X . G^T) * (X . U^T), gate G
+ * and up U two mx matrices [F, K] (e.g. the two halves of one fused gate/up buffer),
+ * fp32 accumulate; h stored f32 or bf16 (RNE, h_dtype), ready for the down GEMV.
+ * silu(g) = g / (1 + exp(-g)). 1 <= M <= 16, F % 64 == 0. Replaces the gate/up GEMVs
+ * plus the silu_mul design (open_kernels/designs/silu_mul/silu_mul.cc: h = bf16(silu(g)
+ * * u)); the MoE kernel's own mb_silu_tile step (moe_batch.h:181-202) is q4_moe_gemv's. */
+int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void* x, int x_dtype,
+                   void* h, int h_dtype, int M, int64_t F, int64_t K,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* The activation producer: per row m < M of N values,
+ *   y = x + add (add may be NULL; y may be NULL, or x itself when N <= 16384),
+ *   xn = (y * r) * w, r = 1 / sqrt(mean(y^2) + eps) with the sum in fp64,
+ * w f32 or bf16 [N] (w_dtype), xn stored f32 or bf16 (RNE, xn_dtype). The reference's
+ * ln design (open_kernels/designs/ln/ln.py:1-6) and rms_vec
+ * (src/open_qwen36/block_host.cpp:42-47). */
+int q4_rmsnorm_add(const float* x, const float* add, const void* w, int w_dtype, float* y,
+                   void* xn, int xn_dtype, int M, int64_t N, float eps, void* stream);
+
 /* One matrix of a grouped GEMV launch (device-resident array of these). */
 typedef struct q4_gemv_desc {
     const uint8_t* packed;   /* mx layout, [N, K] */

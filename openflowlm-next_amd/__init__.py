@@ -11,13 +11,14 @@ name is not a Python identifier).
 from . import _lib
 from .q4 import (GemvGroup, PackedExperts, PackedQ4, dequant, gemm_q4, gemm_q4_prefill, gemv_q4,
                  gemv_workspace_bytes, lm_head_topk, logits_topk, moe_batch, moe_workspace_bytes, pack_moe_experts, pack_q4_1,
-                 pack_q4_1_pool, pack_q4_k, pack_q4_k_chunks, packed_bytes, prefill_workspace_bytes)
+                 pack_q4_1_pool, pack_q4_k, pack_q4_k_chunks, packed_bytes, prefill_workspace_bytes, rmsnorm_add,
+                 swiglu_q4)
 from .gguf import GGUFError, GGUFFile
 
 __all__ = [
     "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k",
     "pack_q4_k_chunks", "GGUFFile", "GGUFError", "dequant",
-    "gemv_q4", "gemm_q4", "gemm_q4_prefill", "lm_head_topk", "logits_topk", "moe_batch", "pack_moe_experts", "GemvGroup",
+    "gemv_q4", "gemm_q4", "gemm_q4_prefill", "lm_head_topk", "logits_topk", "swiglu_q4", "rmsnorm_add", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "load_library",
 ]
 

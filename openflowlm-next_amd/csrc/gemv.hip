@@ -25,13 +25,15 @@ struct GemvParams {
     int S;
     int64_t N, K;
     float* part;      // [S][M][N] partial sums (S > 1)
+    const float* res; // residual added to the result ([M][N], may alias y), or null
 };
 
 
-// Store the row group's result (S == 1) or this split's partial sums.
+// Store the row group's result (S == 1, plus the residual when one is given) or this
+// split's partial sums (res null).
 template <int NTL>
 __device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4][NTL][64], int M,
-                                            float* __restrict__ y, int64_t N, int64_t g) {
+                                            float* y, int64_t N, int64_t g, const float* res = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int64_t n = g * 64 + r * 16 + i16;
@@ -40,18 +42,27 @@ __device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
         const int tok = kg * 4 + j;
-        if (tok < M) y[(int64_t)tok * N + n] = v[j];
+        if (tok < M) y[(int64_t)tok * N + n] = res ? res[(int64_t)tok * N + n] + v[j] : v[j];
     }
 }
 
-// y[t][n] = sum over s = 0..S-1 of part[s][t][n], in split order.
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
-                                                           int64_t MN, int S) {
+// y[t][n] = sum over s = 0..S-1 of part[s][t][n], in split order (+ res[t][n]).
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* y,
+                                                           int64_t MN, int S, const float* res) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= MN) return;
+    // loads batched eight splits at a time (independent of the sum), added in split order
     float s = 0.f;
-    for (int q = 0; q < S; ++q) s += part[(int64_t)q * MN + i];
-    y[i] = s;
+    int q = 0;
+    for (; q + 8 <= S; q += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = part[(int64_t)(q + u) * MN + i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += t[u];
+    }
+    for (; q < S; ++q) s += part[(int64_t)q * MN + i];
+    y[i] = res ? res[i] + s : s;
 }
 
 template <int NTL, bool XF32>
@@ -69,8 +80,98 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
     gemv_rows<NTL, XF32>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
-    float* out = S == 1 ? P.y : P.part + (int64_t)s * P.M * P.N;
-    gemv_finish<NTL>(acc, red, P.M, out, P.N, g);
+    if (S == 1) gemv_finish<NTL>(acc, red, P.M, P.y, P.N, g, P.res);
+    else gemv_finish<NTL>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
+}
+
+// SwiGLU over a gate / up pair: one workgroup takes row group g of both matrices
+// (sharing the activation fragments) over its K range. S == 1: h[t][f] = silu(gate) *
+// up, stored f32 or bf16 (RNE); S > 1: this split's gate and up sums go to
+// part[s][t][0, F) and [F, 2F), and swiglu_reduce_kernel finishes in split order.
+struct SwigluParams {
+    const uint8_t* gate;
+    const uint8_t* up;
+    const void* x;
+    void* h;
+    int h_bf16;
+    int M;
+    int S;
+    int64_t F, K;
+    float* part;
+};
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ void store_h(void* h, bool bf16, int64_t i, float v) {
+    if (bf16) ((uint16_t*)h)[i] = (uint16_t)f32_to_bf16_rne(v);
+    else ((float*)h)[i] = v;
+}
+
+template <int NTL, bool XF32>
+__global__ __launch_bounds__(256) void gemv_swiglu_kernel(SwigluParams P) {
+    __shared__ float red[kWaves][4][NTL][64];
+    const int64_t item = blockIdx.x;
+    const int S = P.S;
+    const int64_t g = item / S;
+    const int s = (int)(item % S);
+    const int KB = (int)(P.K >> 5);
+    const int kb0 = (int)((int64_t)s * KB / S), kb1 = (int)((int64_t)(s + 1) * KB / S);
+    const uint8_t* const gb[2] = {P.gate + g * KB * kTileBytes, P.up + g * KB * kTileBytes};
+    float acc[2][4][NTL];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < NTL; ++j) acc[i][r][j] = 0.f;
+    gemv_rows_multi<NTL, XF32, 2, 4>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc);
+    float vg[NTL], vu[NTL];
+    wave_sum<NTL>(acc[0], red, vg);
+    __syncthreads();
+    wave_sum<NTL>(acc[1], red, vu);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t f = g * 64 + (tid >> 6) * 16 + (lane & 15);
+#pragma unroll
+    for (int j = 0; j < NTL; ++j) {
+        const int tok = (lane >> 4) * 4 + j;
+        if (tok >= P.M) continue;
+        if (S == 1) {
+            store_h(P.h, P.h_bf16, (int64_t)tok * P.F + f, silu(vg[j]) * vu[j]);
+        } else {
+            float* part = P.part + ((int64_t)s * P.M + tok) * 2 * P.F;
+            part[f] = vg[j];
+            part[P.F + f] = vu[j];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void swiglu_reduce_kernel(const float* __restrict__ part, void* h, int h_bf16,
+                                                            int M, int64_t F, int S) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)M * F) return;
+    const int64_t t = i / F, f = i % F;
+    float gs = 0.f, us = 0.f;
+    int q = 0;
+    for (; q + 4 <= S; q += 4) {               // loads batched, sums in split order
+        float tg[4], tu[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* p = part + ((int64_t)(q + u) * M + t) * 2 * F;
+            tg[u] = p[f];
+            tu[u] = p[F + f];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            gs += tg[u];
+            us += tu[u];
+        }
+    }
+    for (; q < S; ++q) {
+        const float* p = part + ((int64_t)q * M + t) * 2 * F;
+        gs += p[f];
+        us += p[F + f];
+    }
+    store_h(h, h_bf16, i, silu(gs) * us);
 }
 
 template <int NTL, bool XF32>
@@ -124,6 +225,12 @@ size_t workspace_for(int M, int64_t N, int64_t K, int S) {
 }
 
 template <int NTL>
+void launch_swiglu(bool xf32, dim3 grid, hipStream_t st, const SwigluParams& P) {
+    if (xf32) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, true>), grid, dim3(256), 0, st, P);
+    else hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false>), grid, dim3(256), 0, st, P);
+}
+
+template <int NTL>
 void launch_gemv(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
     if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
     else hipLaunchKernelGGL((gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
@@ -142,8 +249,10 @@ extern "C" size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K) {
     return workspace_for(M, N, K, choose_splits(N, K));
 }
 
-extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y, int M, int64_t N, int64_t K,
-                       void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* res, float* y, int M, int64_t N,
+              int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
     if (M < 0 || M > 16) return Q4MI_E_RANGE;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
@@ -159,6 +268,7 @@ extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float*
     P.S = S;
     P.N = N;
     P.K = K;
+    P.res = res;
     if (S > 1) {
         const size_t need = workspace_for(M, N, K, S);
         if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
@@ -177,7 +287,70 @@ extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float*
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
         const int64_t MN = (int64_t)M * N;
         hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)ceil_div(MN, 256)), dim3(256), 0, st, P.part, y, MN,
-                           S);
+                           S, res);
+    }
+    return launch_status();
+}
+
+}  // namespace
+
+extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y, int M, int64_t N, int64_t K,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+    return gemv_impl(packed, x, x_dtype, nullptr, y, M, N, K, workspace, workspace_bytes, stream);
+}
+
+extern "C" int q4_gemv_residual(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
+                                int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!residual && M > 0 && N > 0) return Q4MI_E_ARG;
+    return gemv_impl(packed, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K) {
+    if (M < 1 || M > 16 || F <= 0 || K <= 0 || F % 64 || K % 32) return 0;
+    const int S = choose_splits(F, K);
+    return S > 1 ? (size_t)S * M * 2 * F * sizeof(float) : 0;
+}
+
+extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void* x, int x_dtype, void* h,
+                              int h_dtype, int M, int64_t F, int64_t K, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (h_dtype != Q4MI_F32 && h_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (M < 0 || M > 16) return Q4MI_E_RANGE;
+    if (F < 0 || K <= 0 || F % 64 || K % 32) return Q4MI_E_SHAPE;
+    if (M == 0 || F == 0) return Q4MI_OK;
+    if (!gate || !up || !x || !h) return Q4MI_E_ARG;
+    if (misaligned16(gate) || misaligned16(up) || misaligned16(x) || misaligned16(workspace)) return Q4MI_E_ARG;
+    if (((uintptr_t)h & (h_dtype == Q4MI_BF16 ? 1 : 3)) != 0) return Q4MI_E_ARG;
+    const int S = choose_splits(F, K);
+    SwigluParams P{};
+    P.gate = gate;
+    P.up = up;
+    P.x = x;
+    P.h = h;
+    P.h_bf16 = h_dtype == Q4MI_BF16;
+    P.M = M;
+    P.S = S;
+    P.F = F;
+    P.K = K;
+    if (S > 1) {
+        if (!workspace || workspace_bytes < (size_t)S * M * 2 * F * sizeof(float)) return Q4MI_E_WORKSPACE;
+        P.part = (float*)workspace;
+    }
+    const dim3 grid((unsigned)((F / 64) * S));
+    const hipStream_t st = (hipStream_t)stream;
+    const bool xf32 = x_dtype == Q4MI_F32;
+    switch (M < 4 ? M : 4) {
+        case 1: launch_swiglu<1>(xf32, grid, st, P); break;
+        case 2: launch_swiglu<2>(xf32, grid, st, P); break;
+        case 3: launch_swiglu<3>(xf32, grid, st, P); break;
+        default: launch_swiglu<4>(xf32, grid, st, P); break;
+    }
+    if (S > 1) {
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        const int64_t MF = (int64_t)M * F;
+        hipLaunchKernelGGL(swiglu_reduce_kernel, dim3((unsigned)ceil_div(MF, 256)), dim3(256), 0, st, P.part, h,
+                           P.h_bf16, M, F, S);
     }
     return launch_status();
 }

@@ -32,6 +32,7 @@ __all__ = [
     "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k", "pack_q4_k_chunks", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "logits_topk", "lm_head_topk",
+    "swiglu_q4", "rmsnorm_add",
 ]
 
 ROWS = 64          # rows per mx tile / row group
@@ -265,10 +266,13 @@ def _acts(x, dev: torch.device) -> torch.Tensor:
 # decode GEMV / skinny GEMM
 # --------------------------------------------------------------------------
 
-def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+            residual: torch.Tensor | None = None) -> torch.Tensor:
     """Y[M, N] = X[M, K] @ W^T for 1 <= M <= 16 decode tokens, fp32 out
     (gemm_q4.py:164-197's operator, logical [M, N] order). ``workspace``
-    (>= gemv_workspace_bytes) avoids the cached one, e.g. under graph capture."""
+    (>= gemv_workspace_bytes) avoids the cached one, e.g. under graph capture.
+    ``residual`` (f32 [M, N]) is added in the epilogue -- the x_res + W h of
+    model/replica.py:81 -- and may be ``y`` itself to accumulate in place."""
     dev = w.device
     xt = _acts(x, dev)
     if xt.dim() == 1:
@@ -283,9 +287,73 @@ def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tens
     lib = _lib_handle()
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
-        check("q4_gemv", lib.q4_gemv(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), M, w.n, w.k, wp, wn,
-                                     _stream(dev)))
+        if residual is None:
+            check("q4_gemv", lib.q4_gemv(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(y), M, w.n, w.k, wp, wn,
+                                         _stream(dev)))
+        else:
+            if residual.dtype != torch.float32 or not residual.is_contiguous() or residual.numel() != M * w.n \
+                    or residual.device != dev:
+                raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
+            check("q4_gemv_residual", lib.q4_gemv_residual(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(residual),
+                                                           _ptr(y), M, w.n, w.k, wp, wn, _stream(dev)))
     return y
+
+
+def swiglu_q4(gate: PackedQ4, up: PackedQ4, x, out_dtype=torch.float32, h: torch.Tensor | None = None,
+              workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """h[M, F] = silu(X @ G^T) * (X @ U^T) for 1 <= M <= 16 tokens in one launch (two
+    when K is split): the gate/up GEMVs with the silu_mul design fused as their
+    epilogue (designs/silu_mul/silu_mul.cc). ``out_dtype`` float32 or bfloat16 (RNE),
+    the down projection's input."""
+    if gate.n != up.n or gate.k != up.k or gate.device != up.device:
+        raise ValueError(f"gate {gate.shape} and up {up.shape} must match")
+    dev = gate.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != gate.k:
+        raise ValueError(f"x has K={K}, gate/up are [{gate.n}, {gate.k}]")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("out_dtype must be float32 or bfloat16")
+    if h is None:
+        h = torch.empty((M, gate.n), dtype=out_dtype, device=dev)
+    elif h.dtype != out_dtype or not h.is_contiguous() or h.numel() != M * gate.n:
+        raise ValueError(f"h must be a contiguous {out_dtype} [{M}, {gate.n}] tensor")
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_swiglu_workspace_bytes(M, gate.n, gate.k), "swiglu", workspace)
+        check("q4_gemv_swiglu", lib.q4_gemv_swiglu(_ptr(gate.data), _ptr(up.data), _ptr(xt), _x_dtype(xt), _ptr(h),
+                                                   Q4MI_BF16 if out_dtype == torch.bfloat16 else Q4MI_F32, M,
+                                                   gate.n, gate.k, wp, wn, _stream(dev)))
+    return h
+
+
+def rmsnorm_add(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None = None, eps: float = 1e-6,
+                out_dtype=torch.bfloat16, y: torch.Tensor | None = None, xn: torch.Tensor | None = None):
+    """(y, xn): y = x + add (f32; x itself when add is None and y is not given) and
+    xn = (y * rsqrt(mean(y^2) + eps)) * w stored as ``out_dtype`` -- the ln design
+    (designs/ln/ln.py:1-6). ``w`` float32 or bfloat16 [N]; ``y`` may be ``x``."""
+    if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous():
+        raise TypeError("x must be a contiguous float32 GPU tensor")
+    x2 = x.view(-1, x.shape[-1])
+    M, N = x2.shape
+    dev = x.device
+    if w.numel() != N or w.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"w must be float32 or bfloat16 with {N} values")
+    wt = w.to(dev).contiguous()
+    if add is not None and (add.shape != x.shape or add.dtype != torch.float32 or not add.is_contiguous()):
+        raise ValueError("add must be a contiguous float32 tensor shaped like x")
+    if y is None and add is not None:
+        y = torch.empty_like(x)
+    if xn is None:
+        xn = torch.empty(x.shape, dtype=out_dtype, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_rmsnorm_add", _lib_handle().q4_rmsnorm_add(
+            _ptr(x), None if add is None else _ptr(add), _ptr(wt), Q4MI_BF16 if wt.dtype == torch.bfloat16 else Q4MI_F32,
+            None if y is None else _ptr(y), _ptr(xn), Q4MI_BF16 if xn.dtype == torch.bfloat16 else Q4MI_F32, M, N,
+            float(eps), _stream(dev)))
+    return (x if y is None else y), xn
 
 
 def gemv_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:

@@ -663,3 +663,27 @@ def topk_reference(logits: np.ndarray, k: int, mode: int = 1, n_valid: int | Non
         ids[m, :len(order)] = order
         vals[m, :len(order)] = row[order]
     return ids, vals
+
+
+# --------------------------------------------------------------------------
+# Epilogues either side of the GEMV
+# --------------------------------------------------------------------------
+
+def swiglu_reference(gate_blocks: np.ndarray, up_blocks: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """h[M, F] = silu(X G^T) * (X U^T) in fp64 from the bf16-scale dequant of both
+    matrices (designs/silu_mul/make_test.py:18-21's h, before its bf16 rounding;
+    model/replica.py:140's silu(gate x) * (up x))."""
+    xx = np.atleast_2d(np.asarray(x, np.float64))
+    g = xx @ dequant_q4_1(gate_blocks, bf16_scales=True).astype(np.float64).T
+    u = xx @ dequant_q4_1(up_blocks, bf16_scales=True).astype(np.float64).T
+    return silu(g) * u
+
+
+def rmsnorm_add_reference(x: np.ndarray, add, w: np.ndarray, eps: float = 1e-6):
+    """(y f32, xn f64): y = x + add in f32, xn = y / sqrt(mean(y^2) + eps) * w in fp64 per
+    row (designs/ln/make_test.py:44-50; model/replica.py:33-35's rms)."""
+    x = np.atleast_2d(np.asarray(x, np.float32))
+    y = x + np.atleast_2d(np.asarray(add, np.float32)) if add is not None else x.copy()
+    y64 = y.astype(np.float64)
+    xn = y64 / np.sqrt((y64 ** 2).mean(-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+    return y, xn

@@ -22,7 +22,7 @@ def test_header_declares_the_expected_surface():
     names = declared_functions()
     for must in ("q4_packed_bytes", "q4_repack", "q4_repack_pool", "q4_repack_q4k", "q4_repack_q4k_chunks",
                  "q4_dequant", "q4_gemv", "q4_gemv_grouped", "q4_gemm_prefill", "q4_moe_gemv",
-                 "q4_logits_topk", "q4_lm_head_topk"):
+                 "q4_logits_topk", "q4_lm_head_topk", "q4_gemv_residual", "q4_gemv_swiglu", "q4_rmsnorm_add"):
         assert must in names
 
 
@@ -109,6 +109,18 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_topk_workspace_bytes(1, 1024, 64) == 0          # one block per token: none
     assert lib.q4_lm_head_topk(fake, fake, 1, fake, 1, 128256, 4096, 128257, 1, 1, fake, None, None, 0,
                                None) == -1                        # n_valid > N
+    assert lib.q4_gemv_residual(fake, fake, 1, None, fake, 1, 64, 32, None, 0, None) == -2  # no residual
+    assert lib.q4_gemv_swiglu(fake, fake, fake, 1, fake, 2, 1, 64, 32, None, 0, None) == -2  # h dtype
+    assert lib.q4_gemv_swiglu(fake, fake, fake, 1, fake, 1, 17, 64, 32, None, 0, None) == -5  # M > 16
+    assert lib.q4_gemv_swiglu(fake, fake, fake, 1, fake, 1, 1, 100, 32, None, 0, None) == -1  # F % 64
+    assert lib.q4_gemv_swiglu(fake, odd, fake, 1, fake, 1, 1, 64, 32, None, 0, None) == -2   # misaligned up
+    sw = lib.q4_gemv_swiglu_workspace_bytes(1, 512, 4096)
+    assert sw > 0 and lib.q4_gemv_swiglu(fake, fake, fake, 1, fake, 1, 1, 512, 4096, fake, sw - 1, None) == -3
+    assert lib.q4_gemv_swiglu_workspace_bytes(1, 14336, 4096) == 0 or sw > 0
+    assert lib.q4_rmsnorm_add(fake, None, fake, 3, None, fake, 1, 1, 64, 1e-6, None) == -2     # w dtype
+    assert lib.q4_rmsnorm_add(fake, None, fake, 1, None, fake, 1, 1, 0, 1e-6, None) == -1      # N = 0
+    assert lib.q4_rmsnorm_add(None, None, fake, 1, None, fake, 1, 1, 64, 1e-6, None) == -2     # NULL x
+    assert lib.q4_rmsnorm_add(fake, None, fake, 1, None, fake, 1, 1, 64, -1.0, None) == -2     # eps < 0
     wsm = lib.q4_moe_workspace_bytes(16, 128, 8, 2048, 768)
     assert lib.q4_moe_gemv(fake, fake, odd, 1, fake, fake, fake, 16, 128, 8, 2048, 768, fake, wsm, None) == -2
 

@@ -1,0 +1,183 @@
+"""GPU parity of the fused epilogues either side of the GEMV:
+
+* q4_gemv_swiglu: h = silu(gate x) * (up x) -- f32 out maxrel <= 1e-3 against fp64; bf16
+  out against bf16(fp64) under the reference's silu_mul bars (designs/silu_mul/compare.py:
+  maxrel < 8e-3, cos > 0.999999, < 5 % bf16 mismatches) and within one bf16 rounding;
+* q4_gemv_residual: y = residual + W x, maxrel <= 1e-3, in place equal to out of place;
+* q4_rmsnorm_add: y = x + add bit-exact; xn against fp64 under the reference's ln bars
+  (designs/ln/compare.py: maxrel < 8e-3, cos > 0.999999, < 5 % mismatches) and within
+  one bf16 rounding.
+Shapes cover K-split (small F / N) and unsplit launches, M = 1..16, bf16 and f32 x."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+
+MAXREL = 1e-3
+
+
+def _bf16_bits_to_f64(t: torch.Tensor) -> np.ndarray:
+    return t.to(torch.float32).cpu().numpy().astype(np.float64)
+
+
+def _ref_bf16(ref64: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(ref64.astype(np.float32)).to(torch.bfloat16).to(torch.float64).numpy()
+
+
+def _bf16_bars(got: np.ndarray, ref64: np.ndarray):
+    rb = _ref_bf16(ref64)
+    rel = np.abs(got - rb).max() / (np.abs(rb).max() + 1e-30)
+    cos = float(got.ravel() @ rb.ravel() / (np.linalg.norm(got) * np.linalg.norm(rb) + 1e-30))
+    nd = int((got != rb).sum())
+    assert rel < 8e-3 and cos > 0.999999 and nd < got.size // 20, (rel, cos, nd)
+
+
+def _xs(rng, M, K, xdt):
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if xdt == "bf16":
+        xt = torch.from_numpy(x).to(torch.bfloat16)
+        return xt, xt.to(torch.float32).numpy()
+    return torch.from_numpy(x), x
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("M", [1, 3, 4, 16])
+@pytest.mark.parametrize("F,K", [(14336, 4096), (512, 4096), (64, 32), (768, 2048)])
+def test_swiglu_f32(gpu, pkg, oracle, F, K, M, xdt):
+    say(f"swiglu f32 F={F} K={K} M={M} x={xdt}")
+    rng = np.random.default_rng(F + K + M)
+    gb = oracle.baseline_q4_1_blocks(F, K, rng)
+    ub = oracle.baseline_q4_1_blocks(F, K, rng)
+    xt, x64 = _xs(rng, M, K, xdt)
+    g, u = pkg.pack_q4_1(gb, gpu), pkg.pack_q4_1(ub, gpu)
+    h = pkg.swiglu_q4(g, u, xt.to(gpu)).cpu().numpy()
+    ref = oracle.swiglu_reference(gb, ub, x64)
+    assert oracle.maxrel(h, ref) <= MAXREL
+
+
+@pytest.mark.parametrize("F,K", [(14336, 4096), (512, 4096)])
+def test_swiglu_bf16_out(gpu, pkg, oracle, F, K):
+    say(f"swiglu bf16 F={F} K={K}")
+    rng = np.random.default_rng(F)
+    gb = oracle.baseline_q4_1_blocks(F, K, rng)
+    ub = oracle.baseline_q4_1_blocks(F, K, rng)
+    xt, x64 = _xs(rng, 2, K, "bf16")
+    g, u = pkg.pack_q4_1(gb, gpu), pkg.pack_q4_1(ub, gpu)
+    h = pkg.swiglu_q4(g, u, xt.to(gpu), out_dtype=torch.bfloat16)
+    hf = pkg.swiglu_q4(g, u, xt.to(gpu))
+    got = _bf16_bits_to_f64(h)
+    ref = oracle.swiglu_reference(gb, ub, x64)
+    _bf16_bars(got, ref)
+    # the bf16 output is exactly the RNE of the kernel's own f32 result
+    assert torch.equal(h, hf.to(torch.bfloat16))
+
+
+def test_swiglu_is_deterministic_and_matches_separate_gemvs(gpu, pkg, oracle):
+    say("swiglu determinism")
+    rng = np.random.default_rng(5)
+    F, K = 512, 4096                        # split along K
+    gb = oracle.baseline_q4_1_blocks(F, K, rng)
+    ub = oracle.baseline_q4_1_blocks(F, K, rng)
+    g, u = pkg.pack_q4_1(gb, gpu), pkg.pack_q4_1(ub, gpu)
+    x = torch.from_numpy(rng.standard_normal((4, K)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    a = pkg.swiglu_q4(g, u, x)
+    b = pkg.swiglu_q4(g, u, x)
+    assert torch.equal(a, b)
+    gy, uy = pkg.gemm_q4(g, x), pkg.gemm_q4(u, x)
+    want = (gy / (1 + torch.exp(-gy))) * uy
+    assert torch.allclose(a, want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+@pytest.mark.parametrize("N,K,M", [(4096, 14336, 1), (4096, 4096, 4), (128256, 4096, 2), (256, 1024, 16)])
+def test_gemv_residual(gpu, pkg, oracle, N, K, M, inplace):
+    say(f"gemv residual N={N} K={K} M={M} inplace={inplace}")
+    rng = np.random.default_rng(N + K + M)
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    w = pkg.pack_q4_1(blocks, gpu)
+    xt, x64 = _xs(rng, M, K, "bf16")
+    res = rng.standard_normal((M, N)).astype(np.float32) * 10
+    rt = torch.from_numpy(res).to(gpu)
+    if inplace:
+        y = pkg.gemm_q4(w, xt.to(gpu), y=rt, residual=rt)
+        assert y.data_ptr() == rt.data_ptr()
+    else:
+        y = pkg.gemm_q4(w, xt.to(gpu), residual=rt)
+    ref = res.astype(np.float64) + oracle.gemv_reference(blocks, x64).astype(np.float64)
+    got = y.cpu().numpy()
+    assert oracle.maxrel(got, ref) <= MAXREL
+    plain = pkg.gemm_q4(w, xt.to(gpu)).cpu().numpy()
+    assert np.array_equal(got, (res + plain).astype(np.float32))     # the same f32 sum
+
+
+@pytest.mark.parametrize("wdt", ["bf16", "f32"])
+@pytest.mark.parametrize("N", [2048, 4096, 5120, 100])
+@pytest.mark.parametrize("M", [1, 16])
+def test_rmsnorm_add(gpu, pkg, oracle, N, M, wdt):
+    say(f"rmsnorm_add N={N} M={M} w={wdt}")
+    rng = np.random.default_rng(N + M)
+    x = (rng.standard_normal((M, N)) * 0.5).astype(np.float32)
+    add = (rng.standard_normal((M, N)) * 0.5).astype(np.float32)
+    w = (1.0 + rng.standard_normal(N) * 0.1).astype(np.float32)
+    wt = torch.from_numpy(w)
+    if wdt == "bf16":
+        wt = wt.to(torch.bfloat16)
+        w = wt.to(torch.float32).numpy()
+    y, xn = pkg.rmsnorm_add(torch.from_numpy(x).to(gpu), wt.to(gpu), torch.from_numpy(add).to(gpu), eps=1e-6)
+    ry, rxn = oracle.rmsnorm_add_reference(x, add, w, 1e-6)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    got = _bf16_bits_to_f64(xn)
+    _bf16_bars(got, rxn)
+    assert (np.abs(got - rxn) <= 2.0 ** -8 * np.abs(rxn) + 1e-30).all()
+    _, xf = pkg.rmsnorm_add(torch.from_numpy(x).to(gpu), wt.to(gpu), torch.from_numpy(add).to(gpu), eps=1e-6,
+                            out_dtype=torch.float32)
+    assert oracle.maxrel(xf.cpu().numpy(), rxn) <= 1e-6
+
+
+def test_rmsnorm_in_place_and_without_add(gpu, pkg, oracle):
+    say("rmsnorm in place / no add")
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 4096)).astype(np.float32)
+    add = rng.standard_normal((3, 4096)).astype(np.float32)
+    w = np.ones(4096, np.float32)
+    xt = torch.from_numpy(x).to(gpu)
+    y, xn = pkg.rmsnorm_add(xt, torch.from_numpy(w).to(gpu), torch.from_numpy(add).to(gpu), y=xt)
+    assert y.data_ptr() == xt.data_ptr() and np.array_equal(xt.cpu().numpy(), x + add)
+    ry, rxn = oracle.rmsnorm_add_reference(x, add, w)
+    _bf16_bars(_bf16_bits_to_f64(xn), rxn)
+    y2, xn2 = pkg.rmsnorm_add(torch.from_numpy(x).to(gpu), torch.from_numpy(w).to(gpu))
+    _, rxn2 = oracle.rmsnorm_add_reference(x, None, w)
+    assert np.array_equal(y2.cpu().numpy(), x)
+    _bf16_bars(_bf16_bits_to_f64(xn2), rxn2)
+
+
+def test_fused_ffn_block_end_to_end(gpu, pkg, oracle):
+    """rmsnorm_add -> swiglu (bf16 h) -> down with the residual in place: the decode
+    FFN of one layer as three calls, against fp64 of the same bytes."""
+    say("fused ffn block")
+    rng = np.random.default_rng(11)
+    H, F = 1024, 2048
+    gb = oracle.baseline_q4_1_blocks(F, H, rng)
+    ub = oracle.baseline_q4_1_blocks(F, H, rng)
+    db = oracle.baseline_q4_1_blocks(H, F, rng)
+    g, u, d = pkg.pack_q4_1(gb, gpu), pkg.pack_q4_1(ub, gpu), pkg.pack_q4_1(db, gpu)
+    xres = rng.standard_normal((2, H)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    xr = torch.from_numpy(xres).to(gpu)
+    _, xn = pkg.rmsnorm_add(xr, torch.from_numpy(w).to(gpu))
+    h = pkg.swiglu_q4(g, u, xn, out_dtype=torch.bfloat16)
+    pkg.gemm_q4(d, h, y=xr, residual=xr)
+    # fp64 reference through the same bf16 roundings of xn and h
+    _, rxn = oracle.rmsnorm_add_reference(xres, None, w)
+    xnb = xn.to(torch.float32).cpu().numpy()
+    assert (np.abs(xnb - rxn) <= 2.0 ** -8 * np.abs(rxn) + 1e-30).all()
+    rh = oracle.swiglu_reference(gb, ub, xnb)
+    hb = h.to(torch.float32).cpu().numpy()
+    _bf16_bars(hb.astype(np.float64), rh)
+    ref = xres.astype(np.float64) + oracle.gemv_reference(db, hb).astype(np.float64)
+    assert oracle.maxrel(xr.cpu().numpy(), ref) <= MAXREL
