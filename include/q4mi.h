@@ -102,6 +102,23 @@ int q4_repack_q4k(const uint8_t* q4k_blocks, uint8_t* packed, int64_t N, int64_t
 int q4_repack_q4k_chunks(const uint8_t* chunks, int rs, uint8_t* packed,
                          int64_t N, int64_t K, void* stream);
 
+/* Pool chunks of the SIGNED quantiser -> mx layout: 5120-byte chunks laid out as
+ * q4_1's, holding w = d * int4(q) with every min 0 (recipes/pack.py:583-603 tells them
+ * apart by those zero mins). Read the q4_1 way, exactly: code q ^ 8, m = -8 d
+ * (q4_0_to_q4_1, recipes/pack.py:606-622). Band order with row split rs, as
+ * q4_repack_pool. */
+int q4_repack_pool_signed(const uint8_t* pool, int rs, uint8_t* packed,
+                          int64_t N, int64_t K, void* stream);
+
+/* q8 chunks -> mx layout, re-quantised to q4_1 block for block as the reference's
+ * requant_q4_1 does (recipes/pack.py:224-263): 8704-byte 32-row x 256-K chunks (bf16
+ * scales[256] index kb*32 + r, then int8 codes in the q4_1 code raster), band order
+ * with row split rs. Per block: m = min rounded down to bf16, d = (max - m) / 15
+ * rounded up to bf16, nibble = clamp(trunc((v - m) * (1/d) + 0.5), 0, 15), each f32
+ * operation rounded on its own. Every value lands within d/2 of its reading. */
+int q4_repack_q8_chunks(const uint8_t* chunks, int rs, uint8_t* packed,
+                        int64_t N, int64_t K, void* stream);
+
 /* mx layout -> f32 W[N][K] row-major, w = fl32(q * d + m), bit-exact with
  * dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:155-180, q4nx.py:105-126). */
 int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);

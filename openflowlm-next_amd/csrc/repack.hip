@@ -158,6 +158,88 @@ __global__ __launch_bounds__(256) void repack_q4k_chunk_kernel(const uint8_t* __
     mx_write_block(packed, KB, n, kb, code, (f32_to_bf16_rne(d) << 16) | f32_to_bf16_rne(m));
 }
 
+// Chunk of row n, 32-K block kb in the pool's band order with row split rs (q4_1_pack.py:
+// 112-121; rs = 1 is the .q4nx file's raster, chunk = (n / 32) * K / 256 + kb / 8).
+__device__ __forceinline__ int64_t band_chunk(int64_t n, int64_t kb, int rs, int64_t K) {
+    const int64_t per_band = (int64_t)rs * K / 256;
+    return (n / (32 * rs)) * per_band + (kb / 8) * rs + (n % (32 * rs)) / 32;
+}
+
+// 5120 B chunks of the SIGNED quantiser (w = d * int4(q), every min stored as 0) -> mx
+// layout read the q4_1 way: int4(q) = (q ^ 8) - 8, so the code is q ^ 8 and m = -8 d,
+// both exact (recipes/pack.py:606-622).
+__global__ __launch_bounds__(256) void repack_pool_signed_kernel(const uint8_t* __restrict__ pool, int rs,
+                                                                 uint8_t* __restrict__ packed, int64_t N,
+                                                                 int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    const uint8_t* ch = pool + band_chunk(n, kb, rs, KB * 32) * 5120;
+    const int r = (int)(n & 31), kbl = (int)(kb & 7);
+    const uint32_t d16 = ((const uint16_t*)ch)[kbl * 32 + r];
+    const float d = bf16_hi_to_f32(d16 << 16);
+    const uint32_t m16 = f32_to_bf16_rne(-8.0f * d);
+    uint8_t code[32];
+    const uint8_t* nib = ch + 1024 + (r >> 4) * 2048 + (r & 15) / 2;
+    const int sh = 4 * (r & 1);
+#pragma unroll
+    for (int v = 0; v < 32; ++v) code[v] = ((nib[(32 * kbl + v) * 8] >> sh) & 0xF) ^ 0x8;
+    mx_write_block(packed, KB, n, kb, code, (d16 << 16) | m16);
+}
+
+__device__ __forceinline__ uint32_t bf16_floor_bits(float x) {          // toward -inf
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    return (u >> 31) ? (u + 0xFFFFu) >> 16 : u >> 16;
+}
+__device__ __forceinline__ uint32_t bf16_ceil_bits(float x) {           // toward +inf
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    return (u >> 31) ? u >> 16 : (u + 0xFFFFu) >> 16;
+}
+
+// 8704 B q8 chunks (bf16 scales[256] @0 index kb*32 + r; int8 codes @512, code (r, kb,
+// i) at (r/16)*4096 + kb*512 + i*16 + r%16) re-quantised to q4_1 block for block, the
+// reference's requant_q4_1 (recipes/pack.py:224-263) step for step in f32 with every
+// operation rounded on its own (no fused multiply-add): v = code * scale (exact); m = the
+// block minimum rounded down to bf16; d = (max - m) / 15 rounded up to bf16, so
+// [m, m + 15 d] covers the block; nibble = clamp(trunc((v - m) * (1 / d) + 0.5), 0, 15).
+// A -0 product (a negative code under a zero scale) is read as +0.
+__global__ __launch_bounds__(256) void repack_q8_chunk_kernel(const uint8_t* __restrict__ chunks, int rs,
+                                                              uint8_t* __restrict__ packed, int64_t N,
+                                                              int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    const uint8_t* ch = chunks + band_chunk(n, kb, rs, KB * 32) * 8704;
+    const int r = (int)(n & 31), kbl = (int)(kb & 7);
+    const float sc = bf16_hi_to_f32((uint32_t)((const uint16_t*)ch)[kbl * 32 + r] << 16);
+    const int8_t* cp = (const int8_t*)(ch + 512 + (r >> 4) * 4096 + kbl * 512 + (r & 15));
+    float v[32];
+    float mn = __builtin_inff(), mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        v[i] = __fadd_rn(__fmul_rn((float)cp[i * 16], sc), 0.0f);     // -0 (zero scale) read as +0
+        mn = fminf(mn, v[i]);
+        mx = fmaxf(mx, v[i]);
+    }
+    const uint32_t m_u = bf16_floor_bits(mn);
+    const float m = bf16_hi_to_f32(m_u << 16);
+    const uint32_t d_u = bf16_ceil_bits(__fdiv_rn(__fsub_rn(mx, m), 15.0f));
+    const float d = bf16_hi_to_f32(d_u << 16);
+    const float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint8_t code[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float t = __fadd_rn(__fmul_rn(__fsub_rn(v[i], m), inv), 0.5f);
+        const int q = (int)t;
+        code[i] = (uint8_t)(q < 0 ? 0 : (q > 15 ? 15 : q));
+    }
+    mx_write_block(packed, KB, n, kb, code, (d_u << 16) | m_u);
+}
+
 // Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats.
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
                                                       int64_t N, int64_t K) {
@@ -249,6 +331,32 @@ extern "C" int q4_repack_q4k_chunks(const uint8_t* chunks, int rs, uint8_t* pack
     if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
     const int64_t KB = K / 32, total = N * KB;
     hipLaunchKernelGGL(repack_q4k_chunk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, chunks, rs, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_repack_pool_signed(const uint8_t* pool, int rs, uint8_t* packed, int64_t N, int64_t K,
+                                     void* stream) {
+    if (rs <= 0) return Q4MI_E_ARG;
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!pool || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_pool_signed_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, pool, rs, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_repack_q8_chunks(const uint8_t* chunks, int rs, uint8_t* packed, int64_t N, int64_t K,
+                                   void* stream) {
+    if (rs <= 0) return Q4MI_E_ARG;
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!chunks || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_q8_chunk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, chunks, rs, packed, N, KB);
     return launch_status();
 }

@@ -32,7 +32,7 @@ __all__ = [
     "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k", "pack_q4_k_chunks", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "logits_topk", "lm_head_topk",
-    "swiglu_q4", "rmsnorm_add",
+    "swiglu_q4", "rmsnorm_add", "pack_chunks",
 ]
 
 ROWS = 64          # rows per mx tile / row group
@@ -190,6 +190,33 @@ def pack_q4_k_chunks(chunks, n: int, k: int, rs: int = 1, device=None) -> Packed
     with torch.cuda.device(dev):
         check("q4_repack_q4k_chunks",
               _lib_handle().q4_repack_q4k_chunks(_ptr(src), rs, _ptr(out), n, k, _stream(dev)))
+    return PackedQ4(out, n, k)
+
+
+_CHUNK_ENTRY = {   # chunk format -> (chunk bytes, C entry point)
+    "q4_1": (5120, "q4_repack_pool"),
+    "q4_0": (5120, "q4_repack_pool_signed"),
+    "q8": (8704, "q4_repack_q8_chunks"),
+    "q4_k": (4736, "q4_repack_q4k_chunks"),
+}
+
+
+def pack_chunks(chunks, fmt: str, n: int, k: int, rs: int = 1, device=None) -> PackedQ4:
+    """32-row x 256-K chunks of one matrix [n, k] (band order with row split rs; rs = 1
+    is a .q4nx file's raster) -> mx layout on the GPU. ``fmt``: "q4_1" (bytes carry over),
+    "q4_0" (the signed quantiser, read exactly as q4_1), "q8" (re-quantised to q4_1 as
+    recipes/pack.py:224-263 does) or "q4_k" (recipes/pack.py:266-310)."""
+    if fmt not in _CHUNK_ENTRY:
+        raise ValueError(f"chunk format must be one of {sorted(_CHUNK_ENTRY)}, got {fmt!r}")
+    cb, entry = _CHUNK_ENTRY[fmt]
+    dev = _device(device)
+    src = _to_dev(chunks, dev, torch.uint8).reshape(-1)
+    want = (n // 32) * (k // 256) * cb if n % 32 == 0 and k % 256 == 0 else -1
+    if src.numel() != want:
+        raise ValueError(f"{fmt} chunks hold {src.numel()} bytes, [{n}, {k}] needs {want} ({cb} B per 32 x 256)")
+    out = torch.empty(packed_bytes(n, k), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check(entry, getattr(_lib_handle(), entry)(_ptr(src), rs, _ptr(out), n, k, _stream(dev)))
     return PackedQ4(out, n, k)
 
 

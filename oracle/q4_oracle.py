@@ -687,3 +687,104 @@ def rmsnorm_add_reference(x: np.ndarray, add, w: np.ndarray, eps: float = 1e-6):
     y64 = y.astype(np.float64)
     xn = y64 / np.sqrt((y64 ** 2).mean(-1, keepdims=True) + eps) * np.asarray(w, np.float64)
     return y, xn
+
+
+# --------------------------------------------------------------------------
+# .q4nx chunk formats: the signed quantiser and q8, read as q4_1
+# --------------------------------------------------------------------------
+Q8_CHUNK = 8704      # bf16 scales[256] (index kb*32 + r) then int8 codes[8192] (q4nx.py)
+
+_R = np.arange(BLK)[:, None, None]
+_BC = np.arange(8)[None, :, None]
+_I = np.arange(BLK)[None, None, :]
+CHUNK_CODE_IDX = ((_R // 16) * 4096 + _BC * 512 + _I * 16 + (_R % 16)).reshape(-1)   # (r, block, lane)
+CHUNK_META_IDX = (_BC * 32 + _R + 0 * _I).reshape(-1)
+
+
+def signed_pool_to_q4_1(chunks: np.ndarray) -> np.ndarray:
+    """5120 B chunks of the signed quantiser (w = d * int4(q), mins 0) -> q4_1 chunks:
+    nibble q ^ 8, m = bf16(-8 d) (recipes/pack.py:606-622). Exact both ways."""
+    src = np.asarray(chunks, np.uint8).reshape(-1, CH)
+    out = src.copy()
+    d = bf16_to_f32(np.ascontiguousarray(src[:, :512]).view(np.uint16))
+    out[:, 512:1024] = f32_to_bf16(np.float32(-8.0) * d).view(np.uint8).reshape(-1, 512)
+    out[:, 1024:] = src[:, 1024:] ^ 0x88
+    return out
+
+
+def signed_pool_values(chunks: np.ndarray) -> np.ndarray:
+    """[n, 32 r, 8 block, 32 lane] f64 values d * int4(q) straight from the signed bytes."""
+    src = np.asarray(chunks, np.uint8).reshape(-1, CH)
+    nib = np.empty((src.shape[0], 8192), np.int64)
+    nib[:, 0::2] = src[:, 1024:] & 0xF
+    nib[:, 1::2] = src[:, 1024:] >> 4
+    q = np.where(nib >= 8, nib - 16, nib)[:, CHUNK_CODE_IDX]
+    d = bf16_to_f32(np.ascontiguousarray(src[:, :512]).view(np.uint16)).astype(np.float64)[:, CHUNK_META_IDX]
+    return (q * d).reshape(-1, 32, 8, 32)
+
+
+def q8_chunk_values(chunks: np.ndarray) -> np.ndarray:
+    """[n, 32 r, 8 block, 32 lane] f32 code * scale of q8 chunks (exact in f32)."""
+    src = np.asarray(chunks, np.uint8).reshape(-1, Q8_CHUNK)
+    sc = bf16_to_f32(np.ascontiguousarray(src[:, :512]).view(np.uint16))
+    code = np.ascontiguousarray(src[:, 512:]).view(np.int8)
+    return (code[:, CHUNK_CODE_IDX].astype(np.float32) * sc[:, CHUNK_META_IDX]).reshape(-1, 32, 8, 32)
+
+
+def _bf16_floor(x) -> np.ndarray:
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return np.where(u >> 31, (u + np.uint32(0xFFFF)) >> 16, u >> 16).astype(np.uint16)
+
+
+def _bf16_ceil(x) -> np.ndarray:
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return np.where(u >> 31, u >> 16, (u + np.uint32(0xFFFF)) >> 16).astype(np.uint16)
+
+
+def requant_q4_1(chunks: np.ndarray) -> np.ndarray:
+    """q8 chunks [n, 8704] -> q4_1 chunks [n, 5120], block for block (recipes/pack.py:
+    224-263): m = block min rounded down to bf16; d = f32((max - m) / 15) rounded up to
+    bf16; nibble = clip(trunc(f32(f32(v - m) * f32(1 / d)) + 0.5), 0, 15), each f32
+    operation rounded on its own. A -0 value (a negative code under a zero scale, which
+    no quantiser writes) is read as +0, so the block minimum has one sign whichever way
+    a min reduction breaks the tie between the zeros."""
+    v = q8_chunk_values(chunks) + np.float32(0.0)                # [n, r, block, lane]; -0 read as +0
+    n = v.shape[0]
+    m_u = _bf16_floor(v.min(-1))
+    m = bf16_to_f32(m_u)
+    d_u = _bf16_ceil(((v.max(-1) - m).astype(np.float32) / np.float32(15)).astype(np.float32))
+    d = bf16_to_f32(d_u)
+    inv = np.where(d > 0, np.float32(1) / np.where(d > 0, d, np.float32(1)), np.float32(0)).astype(np.float32)
+    t = ((v - m[..., None]).astype(np.float32) * inv[..., None]).astype(np.float32) + np.float32(0.5)
+    nib = np.clip(t.astype(np.int32), 0, 15).astype(np.uint8)
+    out = np.zeros((n, CH), np.uint8)
+    meta_d = np.zeros((n, 256), np.uint16)
+    meta_m = np.zeros((n, 256), np.uint16)
+    slot = (np.arange(8)[None, :] * 32 + np.arange(32)[:, None]).reshape(-1)   # (r, block) -> block*32 + r
+    meta_d[:, slot] = d_u.reshape(n, -1)
+    meta_m[:, slot] = m_u.reshape(n, -1)
+    out[:, :512] = meta_d.view(np.uint8).reshape(n, 512)
+    out[:, 512:1024] = meta_m.view(np.uint8).reshape(n, 512)
+    flat = np.zeros((n, 8192), np.uint8)
+    flat[:, CHUNK_CODE_IDX] = nib.reshape(n, -1)
+    out[:, 1024:] = flat[:, 0::2] | (flat[:, 1::2] << 4)
+    return out
+
+
+def random_q8_chunks(nch: int, rng: np.random.Generator) -> np.ndarray:
+    """Synthetic q8 chunks as the reference's tests draw them (test_qwen35.py:621-628):
+    bf16 scales U(0, 0.02) + 1e-3 (RNE), int8 codes uniform."""
+    out = np.zeros((nch, Q8_CHUNK), np.uint8)
+    sc = (rng.random((nch, 256), np.float32) * np.float32(0.02) + np.float32(1e-3)).astype(np.float32)
+    out[:, :512] = f32_to_bf16(sc).view(np.uint8).reshape(nch, 512)
+    out[:, 512:] = rng.integers(-128, 128, (nch, 8192), dtype=np.int8).view(np.uint8)
+    return out
+
+
+def random_signed_pool(nch: int, rng: np.random.Generator) -> np.ndarray:
+    """Synthetic chunks of the signed quantiser: positive bf16 d, mins 0, random nibbles."""
+    out = rng.integers(0, 256, (nch, CH), dtype=np.uint8)
+    d = (rng.random((nch, 256), np.float32) * np.float32(0.02) + np.float32(1e-3)).astype(np.float32)
+    out[:, :512] = f32_to_bf16(d).view(np.uint8).reshape(nch, 512)
+    out[:, 512:1024] = 0
+    return out

@@ -1,0 +1,179 @@
+"""The .q4nx container and its chunk formats, on the CPU.
+
+Pins, each independent of the formula it checks:
+* the reference's own C++ container reader (src/open_qwen36/q4nx_file.cpp, built into
+  oracle/_ref/q4nx_dump by oracle/Makefile): tensor table, chunk sizes, metadata, raw bytes
+  and BF16 / F32 decodes, against this build's parser (openflowlm-next_amd/q4nx.py);
+* the signed quantiser's transcode: its q4_1 reading equals d * int4(q) read straight off
+  the signed bytes, exactly;
+* the q8 requant: the reference's own property test (test_qwen35.py:631-654: every value
+  within d/2 of its reading, a real quantisation) plus the directed-rounding bounds
+  (m <= block min, m + 15 d >= block max) and exactness on constant blocks.
+* The reference's FNV-1a goldens for these byte layouts do not reproduce -- not even the
+  one over a plain transpose of a fixed byte pattern (test_qwen35.py:701-702) -- so they
+  are recorded as strict xfails, not used as pins.
+"""
+from __future__ import annotations
+
+import importlib
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from q4nx_writer import write_q4nx
+
+ROOT = Path(__file__).resolve().parents[1]
+Q4NX_DUMP = ROOT / "oracle" / "_ref" / "q4nx_dump"
+
+
+def q4nx_mod():
+    return importlib.import_module("openflowlm-next_amd.q4nx")
+
+
+def _container(tmp_path, oracle):
+    rng = np.random.default_rng(4)
+    q41 = oracle.pack_q4_1_pool(oracle.random_q4_1_blocks_ref(128, 512, rng), 1).reshape(-1, 5120)
+    tensors = [
+        ("model.layers.0.mlp.down_proj.weight", "I8", (q41.shape[0], 5120), q41),
+        ("model.layers.0.self_attn.q_proj.weight", "I8", (8, 5120), oracle.random_signed_pool(8, rng)),
+        ("model.layers.0.linear_attn.ssm_out_proj.weight", "I8", (8, 8704), oracle.random_q8_chunks(8, rng)),
+        ("model.layers.0.mlp.gate_proj.weight", "I8", (4, 4736), oracle.q4k_vector(4)),
+        ("model.embed_tokens.weight", "BF16", (16, 64),
+         oracle.f32_to_bf16(rng.standard_normal((16, 64)).astype(np.float32))),
+        ("model.norm.weight", "F32", (64,), rng.standard_normal(64).astype(np.float32)),
+        ("model.layers.0.mlp.up_proj.weight", "I8", (8, 1280), rng.integers(0, 256, (8, 1280), dtype=np.uint8)),
+    ]
+    p = tmp_path / "m.q4nx"
+    write_q4nx(p, tensors, {"format": "q4nx-1.0.2", "adapter": "none"}, pad_header_to=8)
+    return p, tensors
+
+
+def _ref(path, outdir, names, metas=()):
+    if not Q4NX_DUMP.is_file():
+        pytest.skip("oracle/_ref/q4nx_dump not built (the reference sources are absent)")
+    args = [str(Q4NX_DUMP), str(path), str(outdir)]
+    for k in metas:
+        args += ["--meta", k]
+    r = subprocess.run(args + list(names), capture_output=True, text=True, timeout=60)
+    return r.returncode, [line.split("\t") for line in r.stdout.splitlines()]
+
+
+def test_table_and_bytes_match_the_reference_reader(tmp_path, oracle):
+    p, tensors = _container(tmp_path, oracle)
+    names = [t[0] for t in tensors]
+    rc, recs = _ref(p, tmp_path, names, ["format", "adapter", "absent"])
+    assert rc == 0, recs
+    assert recs[0] == ["count", str(len(tensors))]
+    meta = {r[1]: r[2] for r in recs if r[0] == "meta"}
+    with q4nx_mod().Q4NXFile(p) as f:
+        assert f.metadata == {"format": "q4nx-1.0.2", "adapter": "none"}
+        assert meta == {"format": "q4nx-1.0.2", "adapter": "none", "absent": ""}
+        for r in (r for r in recs if r[0] == "tensor"):
+            _, idx, name, dtype, shape, start, end, cb = r
+            t = f.tensors[name]
+            assert (t["dtype"], t["shape"], t["start"], t["end"]) == \
+                (dtype, tuple(int(s) for s in shape.split(",")), int(start), int(end))
+            assert f.chunk_bytes_of(name) == int(cb)
+            assert f.raw(name).tobytes() == (tmp_path / f"{idx}.bin").read_bytes()
+            if dtype in ("BF16", "F32"):
+                ref = np.fromfile(tmp_path / f"{idx}.f32", np.float32)
+                assert np.array_equal(f.array(name).reshape(-1), ref)
+
+
+def test_chunk_formats_are_told_apart(tmp_path, oracle):
+    p, _ = _container(tmp_path, oracle)
+    with q4nx_mod().Q4NXFile(p) as f:
+        assert f.quant_format_of("model.layers.0.mlp.down_proj.weight") == "q4_1"
+        assert f.quant_format_of("model.layers.0.self_attn.q_proj.weight") == "q4_0"
+        assert f.quant_format_of("model.layers.0.linear_attn.ssm_out_proj.weight") == "q8"
+        assert f.quant_format_of("model.layers.0.mlp.gate_proj.weight") == "q4_k"
+        assert f.quant_format_of("model.norm.weight") == ""
+        with pytest.raises(q4nx_mod().Q4NXError, match="up_proj.*1280.*smaller chunk geometry"):
+            f.quant_format_of("model.layers.0.mlp.up_proj.weight")
+        with pytest.raises(q4nx_mod().Q4NXError, match="no tensor"):
+            f.raw("nope")
+
+
+def test_declared_format_wins(tmp_path, oracle):
+    rng = np.random.default_rng(1)
+    sig = oracle.random_signed_pool(2, rng)
+    p = tmp_path / "d.q4nx"
+    write_q4nx(p, [("w", "I8", (2, 5120), sig)], {"quant_format.w": "q4_1"})
+    with q4nx_mod().Q4NXFile(p) as f:
+        assert f.quant_format_of("w") == "q4_1"
+
+
+@pytest.mark.parametrize("cut", [4, 20, -10])
+def test_damaged_files_are_refused(tmp_path, oracle, cut):
+    p, _ = _container(tmp_path, oracle)
+    b = p.read_bytes()
+    bad = tmp_path / "bad.q4nx"
+    bad.write_bytes(b[:cut])
+    with pytest.raises(q4nx_mod().Q4NXError):
+        q4nx_mod().Q4NXFile(bad)
+
+
+def test_signed_transcode_reads_exactly_the_signed_values(oracle):
+    rng = np.random.default_rng(2)
+    sig = oracle.random_signed_pool(6, rng)
+    got = oracle.dq_chunks_q4_1(oracle.signed_pool_to_q4_1(sig)).astype(np.float64)
+    assert np.array_equal(got, oracle.signed_pool_values(sig))
+    # and read as q4_1 unchanged they would be the one-sided, wrong values
+    assert not np.array_equal(oracle.dq_chunks_q4_1(sig).astype(np.float64), oracle.signed_pool_values(sig))
+
+
+def test_requant_is_within_half_a_step(oracle):
+    """test_qwen35.py:631-654, restated: every q8 value within d/2 of its q4_1 reading,
+    the nibble in range, and a real quantisation."""
+    rng = np.random.default_rng(7)
+    src = oracle.random_q8_chunks(12, rng)
+    got = oracle.requant_q4_1(src)
+    assert got.shape == (12, 5120) and got.dtype == np.uint8
+    a = oracle.q8_chunk_values(src).astype(np.float64)
+    b = oracle.dq_chunks_q4_1(got).astype(np.float64)
+    d = oracle.bf16_to_f32(np.ascontiguousarray(got[:, :512]).view(np.uint16))
+    dd = d[:, oracle.CHUNK_META_IDX].reshape(-1, 32, 8, 32).astype(np.float64)
+    assert np.all(np.abs(a - b) <= dd / 2 + 1e-30)
+    assert 0.0 < np.abs(a - b).max() < dd.max()
+
+
+def test_requant_directed_rounding_covers_each_block(oracle):
+    rng = np.random.default_rng(9)
+    src = oracle.random_q8_chunks(6, rng)
+    src[0, 512:] = 4                   # chunk 0: every block constant, 4 * scale exact in bf16
+    v = oracle.q8_chunk_values(src).astype(np.float64)
+    got = oracle.requant_q4_1(src)
+    meta = oracle.bf16_to_f32(np.ascontiguousarray(got[:, :1024]).view(np.uint16)).astype(np.float64)
+    slot = (np.arange(8)[None, :] * 32 + np.arange(32)[:, None])
+    d, m = meta[:, :256][:, slot], meta[:, 256:][:, slot]            # [n, r, block]
+    assert (m <= v.min(-1)).all() and (m + 15 * d >= v.max(-1)).all()
+    assert np.array_equal(oracle.dq_chunks_q4_1(got[:1]).astype(np.float64), v[:1])
+
+
+def _fnv(oracle, b):
+    return oracle.fnv1a64(bytes(b))
+
+
+@pytest.mark.xfail(strict=True, reason="the reference's FNV-1a goldens do not reproduce, even this one over a "
+                   "plain transpose of a fixed byte pattern (test_qwen35.py:701-702); none is used as a pin")
+def test_reference_transpose_golden(oracle):
+    t = np.frombuffer(bytes(((i * 37 + 11) & 0xFF) for i in range(32 * 64 * 2)), np.uint8)
+    td = np.ascontiguousarray(t.reshape(32, 64, 2).transpose(1, 0, 2)).reshape(-1)
+    assert _fnv(oracle, td) == 0xB27D0B6F7149FD83
+
+
+@pytest.mark.xfail(strict=True, reason="see test_reference_transpose_golden (test_qwen35.py:699)")
+def test_reference_requant_golden(oracle):
+    M32 = 0xFFFFFFFF
+    out = np.zeros((12, 8704), np.uint8)
+    for c in range(12):                                  # _shared_q8_vector (test_qwen35.py:668-684)
+        s = (0x9E3779B9 * (c + 1)) & M32
+        stream = []
+        for _ in range(256 + 8192):
+            s = (s * 1664525 + 1013904223) & M32
+            stream.append(s >> 24)
+        out[c, :512] = (0x3B00 | np.array(stream[:256], np.uint32)).astype(np.uint16).view(np.uint8)
+        out[c, 512:] = np.array(stream[256:], np.uint8)
+    assert _fnv(oracle, oracle.requant_q4_1(out)) == 0x4AC3BABAD266DD49
