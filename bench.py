@@ -378,6 +378,37 @@ def extra_ffn(torch, q4, model, acts):
     return out
 
 
+def extra_q8(torch, q4, dev):
+    """The q8 GEMV (exact hi/lo planes, one launch) at M=1 on the Llama-3-8B gate_up and
+    lm_head shapes, graph-timed over 8 rotating copies (the set exceeds the caches):
+    bytes = both planes + bf16 x + f32 y; and the same weights requantised to q4_1."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 13)
+    out = {}
+    for name, n, k in (("gate_up", 28672, 4096), ("lm_head", 128256, 4096)):
+        nb = n * (k // 32)
+        blocks = torch.empty((n, k // 32, 34), dtype=torch.uint8, device=dev)
+        d = (torch.randn(n, k // 32, generator=gen, device=dev).abs() * 0.002 + 1e-4).to(torch.float16)
+        blocks[..., 0:2] = d.view(torch.uint8).view(n, k // 32, 2)
+        blocks[..., 2:] = torch.randint(0, 256, (n, k // 32, 32), generator=gen, device=dev, dtype=torch.uint8)
+        ws = [q4.pack_q8(blocks, n, k, "q8_0", device=dev) for _ in range(2 if n > 100000 else 8)]
+        del blocks
+        x = torch.randn(1, k, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty(1, n, dtype=torch.float32, device=dev)
+        wsp = torch.empty(max(q4.gemv_workspace_bytes(1, n, k), 256), dtype=torch.uint8, device=dev)
+
+        def run():
+            for w in ws:
+                q4.gemm_q8(w, x, y, workspace=wsp)
+        ms = graph_time(torch, run, [y], replays=10) / len(ws)
+        nbytes = ws[0].nbytes + k * 2 + n * 4
+        out[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2), "gbs": round(nbytes / ms / 1e6, 1),
+                     "q8_equivalent_gbs": round((nb * 34 + k * 2 + n * 4) / ms / 1e6, 1)}
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def extra_peaks(torch, dev):
     """On-box reference points: HBM read bandwidth of a plain reduction over
     4 GiB (torch.sum, reads only) and dense bf16 GEMM throughput of the vendor
@@ -494,8 +525,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,peaks",
-                    help="comma list (staged,0,2,3,4,lm_head,ffn,peaks) or 'none'")
+    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,q8,peaks",
+                    help="comma list (staged,0,2,3,4,lm_head,ffn,q8,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=15, help="passes over one layer in the CPU baseline")
     ap.add_argument("--cpu-baseline-child", type=int, default=None, help=argparse.SUPPRESS)
@@ -541,6 +572,8 @@ def main() -> int:
                 out["measured_peaks"] = extra_peaks(torch, dev)
             elif cfg == "lm_head":
                 out["lm_head_topk"] = extra_lm_head(torch, q4, dev)
+            elif cfg == "q8":
+                out["q8_gemv"] = extra_q8(torch, q4, dev)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -576,6 +609,8 @@ def main() -> int:
                 extras["lm_head_topk"] = extra_lm_head(torch, q4, dev, model.head, xhead)
             elif cfg == "ffn":
                 extras["ffn_fused_decode"] = extra_ffn(torch, q4, model, acts)
+            elif cfg == "q8":
+                extras["q8_gemv"] = extra_q8(torch, q4, dev)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
         log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")

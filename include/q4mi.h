@@ -119,6 +119,14 @@ int q4_repack_pool_signed(const uint8_t* pool, int rs, uint8_t* packed,
 int q4_repack_q8_chunks(const uint8_t* chunks, int rs, uint8_t* packed,
                         int64_t N, int64_t K, void* stream);
 
+/* One plane of a q8 matrix held exactly as two q4_1 mx matrices (part 0 "hi":
+ * d = 16 s, m = -128 s, code (q >> 4) + 8; part 1 "lo": d = s, m = 0, code q & 15;
+ * hi + lo = s q exactly -- split_q8_q4_1, recipes/pack.py:94-117). src_format 0:
+ * 8704-byte q8 chunks in band order with row split rs (N % (32 rs) == 0, K % 256 == 0);
+ * 1: GGUF Q8_0 blocks uint8[N][K/32][34] (fp16 d narrowed to bf16 by RNE, K % 32 == 0). */
+int q4_repack_q8_split(const uint8_t* src, int src_format, int rs, int part, uint8_t* packed,
+                       int64_t N, int64_t K, void* stream);
+
 /* mx layout -> f32 W[N][K] row-major, w = fl32(q * d + m), bit-exact with
  * dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:155-180, q4nx.py:105-126). */
 int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
@@ -146,6 +154,14 @@ int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
 int q4_gemv_residual(const uint8_t* packed, const void* x, int x_dtype, const float* residual,
                      float* y, int M, int64_t N, int64_t K, void* workspace,
                      size_t workspace_bytes, void* stream);
+
+/* The q8 GEMV (the reference's gemv_q8 sibling, designs/gemv_q4's q8 twin): Y[M][N] =
+ * X . (HI + LO)^T for a q8 matrix split by q4_repack_q8_split, exact in the weights;
+ * both planes stream in one launch with shared activation fragments. residual (f32
+ * [M][N], may be y) is added when not NULL. Same shapes and workspace as q4_gemv. */
+int q4_gemv_q8(const uint8_t* hi, const uint8_t* lo, const void* x, int x_dtype,
+               const float* residual, float* y, int M, int64_t N, int64_t K,
+               void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes q4_gemv_swiglu needs for (M, F, K); 0 when it needs none. */
 size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K);

@@ -36,6 +36,8 @@ SIGNATURES = {
     "q4_repack_q4k_chunks": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),
     "q4_repack_pool_signed": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),
     "q4_repack_q8_chunks": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),
+    "q4_repack_q8_split": (_i32, [_vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp]),
+    "q4_gemv_q8": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_dequant": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "q4_gemv_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemv": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),

@@ -84,6 +84,35 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     else gemv_finish<NTL>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
 
+// The q8 GEMV as two q4_1 planes (hi, lo) of one matrix: one workgroup streams row group
+// g of both (sharing the activation fragments) and stores y = hi . x + lo . x (S == 1, plus
+// the residual when one is given) or this split's partial of that sum.
+template <int NTL, bool XF32>
+__global__ __launch_bounds__(256) void gemv_pair_kernel(GemvParams P, const uint8_t* lo) {
+    __shared__ float red[kWaves][4][NTL][64];
+    const int64_t item = blockIdx.x;
+    const int S = P.S;
+    const int64_t g = item / S;
+    const int s = (int)(item % S);
+    const int KB = (int)(P.K >> 5);
+    const int kb0 = (int)((int64_t)s * KB / S), kb1 = (int)((int64_t)(s + 1) * KB / S);
+    const uint8_t* const gb[2] = {P.packed + g * KB * kTileBytes, lo + g * KB * kTileBytes};
+    float acc[2][4][NTL];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < NTL; ++j) acc[i][r][j] = 0.f;
+    gemv_rows_multi<NTL, XF32, 2, 4>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) acc[0][r][j] += acc[1][r][j];
+    if (S == 1) gemv_finish<NTL>(acc[0], red, P.M, P.y, P.N, g, P.res);
+    else gemv_finish<NTL>(acc[0], red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
+}
+
 // SwiGLU over a gate / up pair: one workgroup takes row group g of both matrices
 // (sharing the activation fragments) over its K range. S == 1: h[t][f] = silu(gate) *
 // up, stored f32 or bf16 (RNE); S > 1: this split's gate and up sums go to
@@ -231,6 +260,12 @@ void launch_swiglu(bool xf32, dim3 grid, hipStream_t st, const SwigluParams& P) 
 }
 
 template <int NTL>
+void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, const uint8_t* lo) {
+    if (xf32) hipLaunchKernelGGL((gemv_pair_kernel<NTL, true>), grid, dim3(256), 0, st, P, lo);
+    else hipLaunchKernelGGL((gemv_pair_kernel<NTL, false>), grid, dim3(256), 0, st, P, lo);
+}
+
+template <int NTL>
 void launch_gemv(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
     if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
     else hipLaunchKernelGGL((gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
@@ -252,7 +287,7 @@ extern "C" size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K) {
 namespace {
 
 int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* res, float* y, int M, int64_t N,
-              int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+              int64_t K, void* workspace, size_t workspace_bytes, void* stream, const uint8_t* lo = nullptr) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
     if (M < 0 || M > 16) return Q4MI_E_RANGE;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
@@ -277,11 +312,20 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     const dim3 grid((unsigned)((N / 64) * S));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
-    switch (M < 4 ? M : 4) {
-        case 1: launch_gemv<1>(xf32, grid, st, P); break;
-        case 2: launch_gemv<2>(xf32, grid, st, P); break;
-        case 3: launch_gemv<3>(xf32, grid, st, P); break;
-        default: launch_gemv<4>(xf32, grid, st, P); break;
+    if (lo) {
+        switch (M < 4 ? M : 4) {
+            case 1: launch_pair<1>(xf32, grid, st, P, lo); break;
+            case 2: launch_pair<2>(xf32, grid, st, P, lo); break;
+            case 3: launch_pair<3>(xf32, grid, st, P, lo); break;
+            default: launch_pair<4>(xf32, grid, st, P, lo); break;
+        }
+    } else {
+        switch (M < 4 ? M : 4) {
+            case 1: launch_gemv<1>(xf32, grid, st, P); break;
+            case 2: launch_gemv<2>(xf32, grid, st, P); break;
+            case 3: launch_gemv<3>(xf32, grid, st, P); break;
+            default: launch_gemv<4>(xf32, grid, st, P); break;
+        }
     }
     if (S > 1) {
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
@@ -303,6 +347,13 @@ extern "C" int q4_gemv_residual(const uint8_t* packed, const void* x, int x_dtyp
                                 int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
     if (!residual && M > 0 && N > 0) return Q4MI_E_ARG;
     return gemv_impl(packed, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream);
+}
+
+extern "C" int q4_gemv_q8(const uint8_t* hi, const uint8_t* lo, const void* x, int x_dtype, const float* residual,
+                          float* y, int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+    if (M > 0 && N > 0 && (!lo || misaligned16(lo))) return Q4MI_E_ARG;
+    return gemv_impl(hi, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream, lo);
 }
 
 extern "C" size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K) {

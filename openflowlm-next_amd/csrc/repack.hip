@@ -240,6 +240,52 @@ __global__ __launch_bounds__(256) void repack_q8_chunk_kernel(const uint8_t* __r
     mx_write_block(packed, KB, n, kb, code, (d_u << 16) | m_u);
 }
 
+// q8 weights as the exact sum of two q4_1 matrices (recipes/pack.py:94-117,
+// split_q8_q4_1): with q = 16 (q >> 4) + (q & 15) for a signed byte q,
+//   part 0 "hi": d = 16 s, m = -128 s, code (q >> 4) + 8  -> reads 16 s (q >> 4)
+//   part 1 "lo": d = s,    m = 0,      code q & 15        -> reads s (q & 15)
+// and hi + lo = s q exactly (16 s and -128 s only move a bf16 exponent). Sources:
+// 8704 B q8 chunks (src_format 0, band order rs; s the chunk's bf16 scale) or GGUF Q8_0
+// blocks (src_format 1: fp16 d then 32 int8, 34 B per 32 K; s = RNE_bf16(d), the same
+// narrowing the Q4_1 blocks get).
+__global__ __launch_bounds__(256) void repack_q8_split_kernel(const uint8_t* __restrict__ src, int src_format,
+                                                              int rs, int part, uint8_t* __restrict__ packed,
+                                                              int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    uint32_t s16;
+    int8_t q[32];
+    if (src_format == 0) {
+        const uint8_t* ch = src + band_chunk(n, kb, rs, KB * 32) * 8704;
+        const int r = (int)(n & 31), kbl = (int)(kb & 7);
+        s16 = ((const uint16_t*)ch)[kbl * 32 + r];
+        const int8_t* cp = (const int8_t*)(ch + 512 + (r >> 4) * 4096 + kbl * 512 + (r & 15));
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = cp[i * 16];
+    } else {
+        const uint8_t* b = src + (n * KB + kb) * 34;
+        s16 = f32_to_bf16_rne(f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8)));
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = (int8_t)b[2 + i];
+    }
+    const float sv = bf16_hi_to_f32(s16 << 16);
+    uint8_t code[32];
+    uint32_t word;
+    if (part == 0) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) code[i] = (uint8_t)((q[i] >> 4) + 8);
+        word = (f32_to_bf16_rne(16.0f * sv) << 16) | f32_to_bf16_rne(-128.0f * sv);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) code[i] = (uint8_t)(q[i] & 15);
+        word = s16 << 16;
+    }
+    mx_write_block(packed, KB, n, kb, code, word);
+}
+
 // Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats.
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
                                                       int64_t N, int64_t K) {
@@ -358,5 +404,19 @@ extern "C" int q4_repack_q8_chunks(const uint8_t* chunks, int rs, uint8_t* packe
     const int64_t KB = K / 32, total = N * KB;
     hipLaunchKernelGGL(repack_q8_chunk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, chunks, rs, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_repack_q8_split(const uint8_t* src, int src_format, int rs, int part, uint8_t* packed, int64_t N,
+                                  int64_t K, void* stream) {
+    if ((src_format != 0 && src_format != 1) || (part != 0 && part != 1) || rs <= 0) return Q4MI_E_ARG;
+    const int64_t kq = src_format == 0 ? 256 : 32;
+    if (N == 0 && K > 0 && K % kq == 0) return Q4MI_OK;
+    if (!src || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % kq || N % 64 || (src_format == 0 && N % (32 * rs))) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_q8_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, src, src_format, rs, part, packed, N, KB);
     return launch_status();
 }

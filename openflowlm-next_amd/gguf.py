@@ -179,14 +179,17 @@ class GGUFFile:
         return a.reshape(t.shape)
 
     def packed(self, name: str, device=None):
-        """A Q4_0 / Q4_1 / Q4_K weight [N, K] (N % 64 == 0) packed for the kernels on the GPU."""
+        """A Q4_0 / Q4_1 / Q4_K weight [N, K] (N % 64 == 0) packed for the kernels on the GPU
+        (a PackedQ4), or a Q8_0 one as the exact q8 pair (a PackedQ8, for gemm_q8)."""
         from . import q4                                  # needs the HIP library: imported on use
         t = self.tensor(name)
-        if t.type_name not in Q4_TYPES:
-            raise GGUFError(f"{name!r} is {t.type_name}; the kernels take {sorted(Q4_TYPES)}")
+        if t.type_name not in Q4_TYPES | {"Q8_0"}:
+            raise GGUFError(f"{name!r} is {t.type_name}; the kernels take {sorted(Q4_TYPES | {'Q8_0'})}")
         if len(t.shape) != 2:
             raise GGUFError(f"{name!r} has shape {t.shape}, not a matrix")
         b = self.blocks(name)
+        if t.type_name == "Q8_0":
+            return q4.pack_q8(b, t.shape[0], t.shape[1], fmt="q8_0", device=device)
         return q4.pack_q4_k(b, device) if t.type_name == "Q4_K" else q4.pack_q4_1(b, device)
 
     # ---- lifetime -----------------------------------------------------

@@ -32,7 +32,7 @@ __all__ = [
     "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k", "pack_q4_k_chunks", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "logits_topk", "lm_head_topk",
-    "swiglu_q4", "rmsnorm_add", "pack_chunks",
+    "swiglu_q4", "rmsnorm_add", "pack_chunks", "PackedQ8", "pack_q8", "gemm_q8",
 ]
 
 ROWS = 64          # rows per mx tile / row group
@@ -193,6 +193,57 @@ def pack_q4_k_chunks(chunks, n: int, k: int, rs: int = 1, device=None) -> Packed
     return PackedQ4(out, n, k)
 
 
+@dataclass
+class PackedQ8:
+    """A q8 matrix [n, k] held exactly as two mx q4_1 planes, hi + lo = s q
+    (split_q8_q4_1, recipes/pack.py:94-117); 1.25 B per weight."""
+    hi: PackedQ4
+    lo: PackedQ4
+
+    @property
+    def n(self) -> int:
+        return self.hi.n
+
+    @property
+    def k(self) -> int:
+        return self.hi.k
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def device(self):
+        return self.hi.device
+
+    @property
+    def nbytes(self) -> int:
+        return self.hi.nbytes + self.lo.nbytes
+
+
+def pack_q8(src, n: int, k: int, fmt: str = "chunks", rs: int = 1, device=None) -> PackedQ8:
+    """q8 weights -> the exact hi/lo mx pair on the GPU. ``fmt`` "chunks": 8704 B q8
+    chunks in band order with row split rs (rs = 1: a .q4nx raster); "q8_0": GGUF Q8_0
+    blocks uint8[n, k/32, 34] (fp16 d narrowed to bf16 by RNE)."""
+    if fmt not in ("chunks", "q8_0"):
+        raise ValueError(f"fmt must be 'chunks' or 'q8_0', got {fmt!r}")
+    dev = _device(device if device is not None else (src.device if isinstance(src, torch.Tensor)
+                                                     and src.is_cuda else None))
+    t = _to_dev(src, dev, torch.uint8).reshape(-1)
+    want = ((n // 32) * (k // 256) * 8704 if n % 32 == 0 and k % 256 == 0 else -1) if fmt == "chunks" \
+        else (n * (k // 32) * 34 if k % 32 == 0 else -1)
+    if t.numel() != want:
+        raise ValueError(f"{fmt} source holds {t.numel()} bytes, [{n}, {k}] needs {want}")
+    planes = []
+    with torch.cuda.device(dev):
+        for part in (0, 1):
+            out = torch.empty(packed_bytes(n, k), dtype=torch.uint8, device=dev)
+            check("q4_repack_q8_split", _lib_handle().q4_repack_q8_split(_ptr(t), 0 if fmt == "chunks" else 1, rs,
+                                                                         part, _ptr(out), n, k, _stream(dev)))
+            planes.append(PackedQ4(out, n, k))
+    return PackedQ8(*planes)
+
+
 _CHUNK_ENTRY = {   # chunk format -> (chunk bytes, C entry point)
     "q4_1": (5120, "q4_repack_pool"),
     "q4_0": (5120, "q4_repack_pool_signed"),
@@ -323,6 +374,33 @@ def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tens
                 raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
             check("q4_gemv_residual", lib.q4_gemv_residual(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(residual),
                                                            _ptr(y), M, w.n, w.k, wp, wn, _stream(dev)))
+    return y
+
+
+def gemm_q8(w: PackedQ8, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+            residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Y[M, N] = X[M, K] @ W^T for a q8 matrix (the exact hi/lo pair), 1 <= M <= 16, in
+    one launch (the gemv_q8 sibling of gemm_q4); ``residual`` as in gemm_q4."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != w.k:
+        raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q8 takes 1..16 tokens, got {M}")
+    if y is None:
+        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
+                                 or residual.numel() != M * w.n or residual.device != dev):
+        raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        check("q4_gemv_q8", lib.q4_gemv_q8(_ptr(w.hi.data), _ptr(w.lo.data), _ptr(xt), _x_dtype(xt),
+                                           None if residual is None else _ptr(residual), _ptr(y), M, w.n, w.k,
+                                           wp, wn, _stream(dev)))
     return y
 
 

@@ -131,9 +131,11 @@ class Q4NXFile:
             raise Q4NXError(f"{name!r} is {t['dtype']}; use packed() for quantised matrices")
         return a.reshape(t["shape"])
 
-    def packed(self, name: str, out_dim: int, in_dim: int, device=None):
+    def packed(self, name: str, out_dim: int, in_dim: int, device=None, q8: str = "requant"):
         """A quantised matrix [out_dim, in_dim] (out_dim % 64 == 0, in_dim % 256 == 0)
-        transcoded into the mx layout on the GPU, from its chunks as they lie in the file."""
+        transcoded into the mx layout on the GPU, from its chunks as they lie in the file.
+        A q8 tensor is re-quantised to q4_1 (``q8="requant"``, the reference packer's
+        default) or kept exact as the hi/lo pair (``q8="exact"``, a PackedQ8 for gemm_q8)."""
         from . import q4                                 # needs the HIP library: imported on use
         fmt = self.quant_format_of(name)
         if not fmt:
@@ -145,6 +147,10 @@ class Q4NXFile:
         raw = self.raw(name)
         if raw.size != want:
             raise Q4NXError(f"{name!r} holds {raw.size} bytes; [{out_dim}, {in_dim}] in {cb}-byte chunks is {want}")
+        if fmt == "q8" and q8 == "exact":
+            return q4.pack_q8(raw, out_dim, in_dim, fmt="chunks", rs=1, device=device)
+        if q8 not in ("requant", "exact"):
+            raise ValueError(f"q8 must be 'requant' or 'exact', got {q8!r}")
         return q4.pack_chunks(raw, fmt, out_dim, in_dim, rs=1, device=device)
 
     # ---- lifetime -----------------------------------------------------

@@ -788,3 +788,55 @@ def random_signed_pool(nch: int, rng: np.random.Generator) -> np.ndarray:
     out[:, :512] = f32_to_bf16(d).view(np.uint8).reshape(nch, 512)
     out[:, 512:1024] = 0
     return out
+
+
+# --------------------------------------------------------------------------
+# q8 held exactly as two q4_1 planes (recipes/pack.py:94-117, split_q8_q4_1)
+# --------------------------------------------------------------------------
+
+def q8_chunks_rows(chunks: np.ndarray, n: int, k: int, rs: int):
+    """q8 chunks in band order -> (scale bits uint16[n, k/32], codes int8[n, k])."""
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    src = np.asarray(chunks, np.uint8).reshape(nch, Q8_CHUNK)
+    s16 = np.empty((n, k // BLK), np.uint16)
+    q = np.empty((n, k), np.int8)
+    sc = np.ascontiguousarray(src[:, :512]).view(np.uint16)                       # [c, block*32 + r]
+    code = np.ascontiguousarray(src[:, 512:]).view(np.int8)[:, CHUNK_CODE_IDX].reshape(nch, 32, 8, 32)
+    for c in range(nch):
+        r0, c0 = int(rows0[c]), int(cols0[c])
+        s16[r0:r0 + 32, c0 // BLK:c0 // BLK + 8] = sc[c].reshape(8, 32).T
+        q[r0:r0 + 32, c0:c0 + 256] = code[c].reshape(32, 256)
+    return s16, q
+
+
+def q8_0_rows(blocks: np.ndarray):
+    """GGUF Q8_0 blocks uint8[n, k/32, 34] -> (bf16 scale bits [n, k/32], codes int8[n, k])."""
+    b = np.asarray(blocks, np.uint8)
+    n, nb, _ = b.shape
+    d = np.ascontiguousarray(b[..., 0:2]).view(np.float16).reshape(n, nb).astype(np.float32)
+    return f32_to_bf16(d), np.ascontiguousarray(b[..., 2:34]).view(np.int8).reshape(n, nb * BLK)
+
+
+def q8_split_parts(s16: np.ndarray, q: np.ndarray, part: int):
+    """(d16, m16, codes) of plane `part` (0 hi: d = 16 s, m = -128 s, code (q >> 4) + 8;
+    1 lo: d = s, m = 0, code q & 15), for pack_mx_from_parts."""
+    s = bf16_to_f32(s16)
+    q = np.asarray(q, np.int8).astype(np.int32)
+    if part == 0:
+        return f32_to_bf16(np.float32(16) * s), f32_to_bf16(np.float32(-128) * s), ((q >> 4) + 8).astype(np.uint8)
+    return s16.copy(), np.zeros_like(s16), (q & 15).astype(np.uint8)
+
+
+def q8_values(s16: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """s * q in f64 per weight (exact)."""
+    return np.repeat(bf16_to_f32(s16).astype(np.float64), BLK, axis=1) * np.asarray(q, np.float64)
+
+
+def random_q8_0_blocks(n: int, k: int, rng: np.random.Generator) -> np.ndarray:
+    """Seeded GGUF Q8_0 blocks: fp16 d = |N(0,1)| * 0.002 + 1e-4, int8 codes uniform."""
+    nb = k // BLK
+    b = np.empty((n, nb, 34), np.uint8)
+    d = (np.abs(rng.standard_normal((n, nb))) * 0.002 + 1e-4).astype(np.float16)
+    b[..., 0:2] = d.view(np.uint8).reshape(n, nb, 2)
+    b[..., 2:] = rng.integers(-128, 128, (n, nb, 32), dtype=np.int8).view(np.uint8)
+    return b

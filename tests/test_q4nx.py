@@ -177,3 +177,23 @@ def test_reference_requant_golden(oracle):
         out[c, :512] = (0x3B00 | np.array(stream[:256], np.uint32)).astype(np.uint16).view(np.uint8)
         out[c, 512:] = np.array(stream[256:], np.uint8)
     assert _fnv(oracle, oracle.requant_q4_1(out)) == 0x4AC3BABAD266DD49
+
+
+def test_q8_split_planes_sum_to_the_q8_values_exactly(oracle):
+    """test_qwen35.py:890-903's property: the hi and lo q4_1 readings add up to every q8
+    value exactly (the requant is lossy; this is not), from chunks and from GGUF Q8_0."""
+    rng = np.random.default_rng(12)
+    n, k = 128, 512
+    src = oracle.random_q8_chunks((n // 32) * (k // 256), rng)
+    src[0, 512:520] = [0x80, 0x7F, 0xFF, 0x00, 0x01, 0xF0, 0x0F, 0x88]     # -128, 127, -1, 0, 1, -16, 15, -120
+    for s16, q in (oracle.q8_chunks_rows(src, n, k, 1), oracle.q8_0_rows(oracle.random_q8_0_blocks(n, k, rng))):
+        total = np.zeros((n, k))
+        for part in (0, 1):
+            d16, m16, codes = oracle.q8_split_parts(s16, q, part)
+            assert codes.max() <= 15
+            total += oracle.dequant_mx(oracle.pack_mx_from_parts(d16, m16, codes), n, k).astype(np.float64)
+        assert np.array_equal(total, oracle.q8_values(s16, q))
+    # the chunk reader agrees with the chunk values read straight off the layout
+    s16, q = oracle.q8_chunks_rows(src, n, k, 1)
+    v = oracle.q8_chunk_values(src).reshape(-1, 32, 256)
+    assert np.array_equal(oracle.q8_values(s16, q)[:32, :256], v[0])
