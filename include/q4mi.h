@@ -81,6 +81,15 @@ int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* packed,
 int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed,
                    int64_t N, int64_t K, void* stream);
 
+/* The GGUF-direct pool's chunks -> mx layout, on the device: 6144-byte 32-row x 256-K
+ * chunks with f32 d[256] @0 and f32 m[256] @1024 (index kb*32 + r, exact widenings of
+ * GGUF's fp16 scales; Q4_0's m = -8 d) and the codes @2048 in the pool raster
+ * (open_kernels/gguf_pool/gguf_pool.py:19-33, pack_q4_pool :191-213), band order with
+ * row split rs. d and m are narrowed to bf16 by RNE, as that pool's kernel does in
+ * flight (gguf_pool.py:10-16): the result equals q4_repack of the same GGUF blocks. */
+int q4_repack_pool_f32(const uint8_t* pool, int rs, uint8_t* packed,
+                       int64_t N, int64_t K, void* stream);
+
 /* GGUF Q4_K super-blocks -> mx layout, on the device. `q4k_blocks`:
  * uint8[N][K/256][144] (fp16 d, fp16 dmin, 12 bytes of packed 6-bit sub-block
  * scales/mins, 128 code bytes; llama.cpp's block_q4_K). Each 32-value sub-block
@@ -123,7 +132,9 @@ int q4_repack_q8_chunks(const uint8_t* chunks, int rs, uint8_t* packed,
  * d = 16 s, m = -128 s, code (q >> 4) + 8; part 1 "lo": d = s, m = 0, code q & 15;
  * hi + lo = s q exactly -- split_q8_q4_1, recipes/pack.py:94-117). src_format 0:
  * 8704-byte q8 chunks in band order with row split rs (N % (32 rs) == 0, K % 256 == 0);
- * 1: GGUF Q8_0 blocks uint8[N][K/32][34] (fp16 d narrowed to bf16 by RNE, K % 32 == 0). */
+ * 1: GGUF Q8_0 blocks uint8[N][K/32][34] (fp16 d narrowed to bf16 by RNE, K % 32 == 0);
+ * 2: the GGUF-direct pool's 9216-byte q8 chunks (f32 scales @0, codes @1024; scales
+ * narrowed to bf16 by RNE; gguf_pool.py:28-33), band order with row split rs. */
 int q4_repack_q8_split(const uint8_t* src, int src_format, int rs, int part, uint8_t* packed,
                        int64_t N, int64_t K, void* stream);
 

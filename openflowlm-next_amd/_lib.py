@@ -32,6 +32,7 @@ SIGNATURES = {
     "q4_packed_bytes": (_i64, [_i64, _i64]),
     "q4_repack": (_i32, [_vp, _i32, _vp, _i64, _i64, _i32, _vp]),
     "q4_repack_pool": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),
+    "q4_repack_pool_f32": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),
     "q4_repack_q4k": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "q4_repack_q4k_chunks": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),
     "q4_repack_pool_signed": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),

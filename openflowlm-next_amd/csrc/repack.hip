@@ -66,7 +66,10 @@ __global__ __launch_bounds__(256) void repack_gguf_kernel(const uint8_t* __restr
     mx_write_block(packed, KB, n, kb, code, (f32_to_bf16_rne(d) << 16) | f32_to_bf16_rne(m));
 }
 
-__global__ __launch_bounds__(256) void repack_pool_kernel(const uint8_t* __restrict__ pool, int rs,
+// f32_scales: the GGUF-direct pool's 6144 B chunks (open_kernels/gguf_pool/gguf_pool.py:
+// 19-33: f32 d[256] @0, f32 m[256] @1024, codes @2048), narrowed to bf16 by RNE as that
+// pool's kernel does in flight; else the 5120 B chunks, bytes carried over.
+__global__ __launch_bounds__(256) void repack_pool_kernel(const uint8_t* __restrict__ pool, int rs, int f32_scales,
                                                           uint8_t* __restrict__ packed, int64_t N, int64_t KB) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= N * KB) return;
@@ -77,14 +80,22 @@ __global__ __launch_bounds__(256) void repack_pool_kernel(const uint8_t* __restr
     const int64_t per_band = (int64_t)rs * K / 256;
     const int64_t band = n / (32 * rs);
     const int64_t ci = (kb / 8) * rs + (n % (32 * rs)) / 32;
-    const uint8_t* ch = pool + (band * per_band + ci) * 5120;
+    const int64_t chb = f32_scales ? 6144 : 5120;
+    const uint8_t* ch = pool + (band * per_band + ci) * chb;
     const int r = (int)(n & 31);
     const int kbl = (int)(kb & 7);
-    const uint16_t* sc = (const uint16_t*)ch;
-    const uint32_t d16 = sc[kbl * 32 + r];
-    const uint32_t m16 = sc[256 + kbl * 32 + r];
+    uint32_t d16, m16;
+    if (f32_scales) {
+        const float* sc = (const float*)ch;
+        d16 = f32_to_bf16_rne(sc[kbl * 32 + r]);
+        m16 = f32_to_bf16_rne(sc[256 + kbl * 32 + r]);
+    } else {
+        const uint16_t* sc = (const uint16_t*)ch;
+        d16 = sc[kbl * 32 + r];
+        m16 = sc[256 + kbl * 32 + r];
+    }
     uint8_t code[32];
-    const uint8_t* nib = ch + 1024 + (r >> 4) * 2048 + (r & 15) / 2;
+    const uint8_t* nib = ch + (chb - 4096) + (r >> 4) * 2048 + (r & 15) / 2;
     const int sh = 4 * (r & 1);
 #pragma unroll
     for (int v = 0; v < 32; ++v) code[v] = (nib[(32 * kbl + v) * 8] >> sh) & 0xF;
@@ -245,9 +256,10 @@ __global__ __launch_bounds__(256) void repack_q8_chunk_kernel(const uint8_t* __r
 //   part 0 "hi": d = 16 s, m = -128 s, code (q >> 4) + 8  -> reads 16 s (q >> 4)
 //   part 1 "lo": d = s,    m = 0,      code q & 15        -> reads s (q & 15)
 // and hi + lo = s q exactly (16 s and -128 s only move a bf16 exponent). Sources:
-// 8704 B q8 chunks (src_format 0, band order rs; s the chunk's bf16 scale) or GGUF Q8_0
+// 8704 B q8 chunks (src_format 0, band order rs; s the chunk's bf16 scale), GGUF Q8_0
 // blocks (src_format 1: fp16 d then 32 int8, 34 B per 32 K; s = RNE_bf16(d), the same
-// narrowing the Q4_1 blocks get).
+// narrowing the Q4_1 blocks get) or the GGUF-direct pool's 9216 B q8 chunks (src_format
+// 2: f32 scales[256] @0, codes @1024; s = RNE_bf16(scale); gguf_pool.py:28-33).
 __global__ __launch_bounds__(256) void repack_q8_split_kernel(const uint8_t* __restrict__ src, int src_format,
                                                               int rs, int part, uint8_t* __restrict__ packed,
                                                               int64_t N, int64_t KB) {
@@ -258,11 +270,12 @@ __global__ __launch_bounds__(256) void repack_q8_split_kernel(const uint8_t* __r
     const int64_t kb = tile % KB;
     uint32_t s16;
     int8_t q[32];
-    if (src_format == 0) {
-        const uint8_t* ch = src + band_chunk(n, kb, rs, KB * 32) * 8704;
+    if (src_format != 1) {
+        const bool f32s = src_format == 2;
+        const uint8_t* ch = src + band_chunk(n, kb, rs, KB * 32) * (f32s ? 9216 : 8704);
         const int r = (int)(n & 31), kbl = (int)(kb & 7);
-        s16 = ((const uint16_t*)ch)[kbl * 32 + r];
-        const int8_t* cp = (const int8_t*)(ch + 512 + (r >> 4) * 4096 + kbl * 512 + (r & 15));
+        s16 = f32s ? f32_to_bf16_rne(((const float*)ch)[kbl * 32 + r]) : ((const uint16_t*)ch)[kbl * 32 + r];
+        const int8_t* cp = (const int8_t*)(ch + (f32s ? 1024 : 512) + (r >> 4) * 4096 + kbl * 512 + (r & 15));
 #pragma unroll
         for (int i = 0; i < 32; ++i) q[i] = cp[i * 16];
     } else {
@@ -342,7 +355,19 @@ extern "C" int q4_repack_pool(const uint8_t* pool, int rs, uint8_t* packed, int6
     if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
     const int64_t KB = K / 32, total = N * KB;
     const unsigned grid = (unsigned)((total + 255) / 256);
-    hipLaunchKernelGGL(repack_pool_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, pool, rs, packed, N, KB);
+    hipLaunchKernelGGL(repack_pool_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, pool, rs, 0, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_repack_pool_f32(const uint8_t* pool, int rs, uint8_t* packed, int64_t N, int64_t K, void* stream) {
+    if (rs <= 0) return Q4MI_E_ARG;
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!pool || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed) || ((uintptr_t)pool & 3)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_pool_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       pool, rs, 1, packed, N, KB);
     return launch_status();
 }
 
@@ -409,12 +434,13 @@ extern "C" int q4_repack_q8_chunks(const uint8_t* chunks, int rs, uint8_t* packe
 
 extern "C" int q4_repack_q8_split(const uint8_t* src, int src_format, int rs, int part, uint8_t* packed, int64_t N,
                                   int64_t K, void* stream) {
-    if ((src_format != 0 && src_format != 1) || (part != 0 && part != 1) || rs <= 0) return Q4MI_E_ARG;
-    const int64_t kq = src_format == 0 ? 256 : 32;
+    if (src_format < 0 || src_format > 2 || (part != 0 && part != 1) || rs <= 0) return Q4MI_E_ARG;
+    const int64_t kq = src_format == 1 ? 32 : 256;
     if (N == 0 && K > 0 && K % kq == 0) return Q4MI_OK;
     if (!src || !packed) return Q4MI_E_ARG;
     if (misaligned16(packed)) return Q4MI_E_ARG;
-    if (N < 0 || K <= 0 || K % kq || N % 64 || (src_format == 0 && N % (32 * rs))) return Q4MI_E_SHAPE;
+    if (src_format == 2 && ((uintptr_t)src & 3)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % kq || N % 64 || (src_format != 1 && N % (32 * rs))) return Q4MI_E_SHAPE;
     const int64_t KB = K / 32, total = N * KB;
     hipLaunchKernelGGL(repack_q8_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, src, src_format, rs, part, packed, N, KB);

@@ -224,13 +224,15 @@ class PackedQ8:
 def pack_q8(src, n: int, k: int, fmt: str = "chunks", rs: int = 1, device=None) -> PackedQ8:
     """q8 weights -> the exact hi/lo mx pair on the GPU. ``fmt`` "chunks": 8704 B q8
     chunks in band order with row split rs (rs = 1: a .q4nx raster); "q8_0": GGUF Q8_0
-    blocks uint8[n, k/32, 34] (fp16 d narrowed to bf16 by RNE)."""
-    if fmt not in ("chunks", "q8_0"):
-        raise ValueError(f"fmt must be 'chunks' or 'q8_0', got {fmt!r}")
+    blocks uint8[n, k/32, 34] (fp16 d narrowed to bf16 by RNE); "chunks_f32": the
+    GGUF-direct pool's 9216 B q8 chunks (f32 scales narrowed to bf16 by RNE)."""
+    if fmt not in ("chunks", "q8_0", "chunks_f32"):
+        raise ValueError(f"fmt must be 'chunks', 'q8_0' or 'chunks_f32', got {fmt!r}")
     dev = _device(device if device is not None else (src.device if isinstance(src, torch.Tensor)
                                                      and src.is_cuda else None))
     t = _to_dev(src, dev, torch.uint8).reshape(-1)
-    want = ((n // 32) * (k // 256) * 8704 if n % 32 == 0 and k % 256 == 0 else -1) if fmt == "chunks" \
+    cb = {"chunks": 8704, "chunks_f32": 9216}.get(fmt)
+    want = ((n // 32) * (k // 256) * cb if n % 32 == 0 and k % 256 == 0 else -1) if cb \
         else (n * (k // 32) * 34 if k % 32 == 0 else -1)
     if t.numel() != want:
         raise ValueError(f"{fmt} source holds {t.numel()} bytes, [{n}, {k}] needs {want}")
@@ -238,7 +240,8 @@ def pack_q8(src, n: int, k: int, fmt: str = "chunks", rs: int = 1, device=None) 
     with torch.cuda.device(dev):
         for part in (0, 1):
             out = torch.empty(packed_bytes(n, k), dtype=torch.uint8, device=dev)
-            check("q4_repack_q8_split", _lib_handle().q4_repack_q8_split(_ptr(t), 0 if fmt == "chunks" else 1, rs,
+            check("q4_repack_q8_split", _lib_handle().q4_repack_q8_split(_ptr(t), {"chunks": 0, "q8_0": 1,
+                                                                                   "chunks_f32": 2}[fmt], rs,
                                                                          part, _ptr(out), n, k, _stream(dev)))
             planes.append(PackedQ4(out, n, k))
     return PackedQ8(*planes)
@@ -246,6 +249,7 @@ def pack_q8(src, n: int, k: int, fmt: str = "chunks", rs: int = 1, device=None) 
 
 _CHUNK_ENTRY = {   # chunk format -> (chunk bytes, C entry point)
     "q4_1": (5120, "q4_repack_pool"),
+    "q4_f32": (6144, "q4_repack_pool_f32"),
     "q4_0": (5120, "q4_repack_pool_signed"),
     "q8": (8704, "q4_repack_q8_chunks"),
     "q4_k": (4736, "q4_repack_q4k_chunks"),
@@ -255,6 +259,7 @@ _CHUNK_ENTRY = {   # chunk format -> (chunk bytes, C entry point)
 def pack_chunks(chunks, fmt: str, n: int, k: int, rs: int = 1, device=None) -> PackedQ4:
     """32-row x 256-K chunks of one matrix [n, k] (band order with row split rs; rs = 1
     is a .q4nx file's raster) -> mx layout on the GPU. ``fmt``: "q4_1" (bytes carry over),
+    "q4_f32" (the GGUF-direct pool's 6144 B chunks, f32 scales narrowed to bf16),
     "q4_0" (the signed quantiser, read exactly as q4_1), "q8" (re-quantised to q4_1 as
     recipes/pack.py:224-263 does) or "q4_k" (recipes/pack.py:266-310)."""
     if fmt not in _CHUNK_ENTRY:

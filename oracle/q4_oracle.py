@@ -840,3 +840,63 @@ def random_q8_0_blocks(n: int, k: int, rng: np.random.Generator) -> np.ndarray:
     b[..., 0:2] = d.view(np.uint8).reshape(n, nb, 2)
     b[..., 2:] = rng.integers(-128, 128, (n, nb, 32), dtype=np.int8).view(np.uint8)
     return b
+
+
+# --------------------------------------------------------------------------
+# The GGUF-direct pool: f32 scales (open_kernels/gguf_pool/gguf_pool.py)
+# --------------------------------------------------------------------------
+CH_F32 = 6144        # q4 chunk with f32 d[256], f32 m[256], codes[4096]   (gguf_pool.py:19-27)
+CH_Q8_F32 = 9216     # q8 chunk with f32 scales[256], int8 codes[8192]    (gguf_pool.py:28)
+
+
+def pack_gguf_pool_f32(blocks: np.ndarray, rs: int) -> np.ndarray:
+    """GGUF Q4_1 / Q4_0 blocks -> the direct pool's 6144 B chunks in band order: fp16 d, m
+    widened exactly to f32 (Q4_0: m = -8 d), index kb*32 + r; codes in the pool raster
+    (gguf_pool.py:191-213)."""
+    n, nb, _ = blocks.shape
+    k = nb * BLK
+    d, m, q = unpack_q4_1_blocks(blocks)                       # f32, exact widenings
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    out = np.empty((nch, CH_F32), np.uint8)
+    for c in range(nch):
+        r0, c0 = int(rows0[c]), int(cols0[c])
+        kb0 = c0 // BLK
+        out[c, 0:1024] = np.ascontiguousarray(d[r0:r0 + 32, kb0:kb0 + 8].T).reshape(-1).view(np.uint8)
+        out[c, 1024:2048] = np.ascontiguousarray(m[r0:r0 + 32, kb0:kb0 + 8].T).reshape(-1).view(np.uint8)
+        qq = q[r0:r0 + 32, c0:c0 + 256].reshape(2, 16, 256).transpose(0, 2, 1).reshape(-1)
+        out[c, 2048:] = qq[0::2] | (qq[1::2] << 4)
+    return out.reshape(-1)
+
+
+def dequant_gguf_pool_f32(pool: np.ndarray, n: int, k: int, rs: int) -> np.ndarray:
+    """The direct pool's own f32 reading fl32(q * d + m) -> f32[n, k] (gguf_pool.py:269-320)."""
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    ch = np.asarray(pool, np.uint8).reshape(nch, CH_F32)
+    w = np.empty((n, k), np.float32)
+    for c in range(nch):
+        d = np.ascontiguousarray(ch[c, 0:1024]).view(np.float32).reshape(8, 32)
+        m = np.ascontiguousarray(ch[c, 1024:2048]).view(np.float32).reshape(8, 32)
+        nib = np.empty(8192, np.uint8)
+        nib[0::2] = ch[c, 2048:] & 0xF
+        nib[1::2] = ch[c, 2048:] >> 4
+        q = nib.reshape(2, 256, 16).transpose(0, 2, 1).reshape(32, 256).astype(np.float32)
+        g = np.arange(256) // 32
+        r0, c0 = int(rows0[c]), int(cols0[c])
+        w[r0:r0 + 32, c0:c0 + 256] = q * d[g, :].T + m[g, :].T
+    return w
+
+
+def pack_gguf_pool_q8_f32(blocks: np.ndarray, rs: int) -> np.ndarray:
+    """GGUF Q8_0 blocks -> the direct pool's 9216 B q8 chunks (gguf_pool.py:182-189, 216-227)."""
+    b = np.asarray(blocks, np.uint8)
+    n, nb, _ = b.shape
+    k = nb * BLK
+    d = np.ascontiguousarray(b[..., 0:2]).view(np.float16).reshape(n, nb).astype(np.float32)
+    q = np.ascontiguousarray(b[..., 2:34]).view(np.int8).reshape(n, k)
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    out = np.empty((nch, CH_Q8_F32), np.uint8)
+    for c in range(nch):
+        r0, c0 = int(rows0[c]), int(cols0[c])
+        out[c, 0:1024] = np.ascontiguousarray(d[r0:r0 + 32, c0 // BLK:c0 // BLK + 8].T).reshape(-1).view(np.uint8)
+        out[c, 1024:] = q[r0:r0 + 32, c0:c0 + 256].reshape(2, 16, 256).transpose(0, 2, 1).reshape(-1).view(np.uint8)
+    return out.reshape(-1)

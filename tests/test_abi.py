@@ -21,7 +21,7 @@ def declared_functions() -> list[str]:
 def test_header_declares_the_expected_surface():
     names = declared_functions()
     for must in ("q4_packed_bytes", "q4_repack", "q4_repack_pool", "q4_repack_q4k", "q4_repack_q4k_chunks",
-                 "q4_repack_pool_signed", "q4_repack_q8_chunks", "q4_repack_q8_split", "q4_gemv_q8",
+                 "q4_repack_pool_signed", "q4_repack_q8_chunks", "q4_repack_q8_split", "q4_gemv_q8", "q4_repack_pool_f32",
                  "q4_dequant", "q4_gemv", "q4_gemv_grouped", "q4_gemm_prefill", "q4_moe_gemv",
                  "q4_logits_topk", "q4_lm_head_topk", "q4_gemv_residual", "q4_gemv_swiglu", "q4_rmsnorm_add"):
         assert must in names
@@ -71,7 +71,9 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_repack_q4k_chunks(fake, 1, fake, 64, 128, None) == -1  # K % 256
     assert lib.q4_repack_q4k_chunks(fake, 0, fake, 64, 256, None) == -2  # rs
     assert lib.q4_repack_q4k_chunks(fake, 4, fake, 64, 256, None) == -1  # N % (32 rs)
-    assert lib.q4_repack_q8_split(fake, 2, 1, 0, fake, 64, 256, None) == -2   # source format
+    assert lib.q4_repack_q8_split(fake, 3, 1, 0, fake, 64, 256, None) == -2   # source format
+    assert lib.q4_repack_pool_f32(fake, 1, fake, 64, 128, None) == -1          # K % 256
+    assert lib.q4_repack_pool_f32(C.c_void_p(0x1002), 1, fake, 64, 256, None) == -2   # f32 scales misaligned
     assert lib.q4_repack_q8_split(fake, 0, 1, 2, fake, 64, 256, None) == -2   # part
     assert lib.q4_repack_q8_split(fake, 0, 1, 0, fake, 64, 128, None) == -1   # chunks need K % 256
     assert lib.q4_repack_q8_split(fake, 1, 1, 0, fake, 64, 48, None) == -1    # Q8_0 needs K % 32

@@ -91,3 +91,21 @@ def test_q8_from_files(gpu, pkg, oracle, tmp_path):
     ref = x.astype(np.float64) @ oracle.q8_values(*oracle.q8_chunks_rows(src, n, k, 1)).T
     assert oracle.maxrel(ye, ref) <= 1e-3
     assert oracle.maxrel(yr, ref) > oracle.maxrel(ye, ref)          # the requant is the lossy one
+
+
+@pytest.mark.parametrize("rs", [1, 2])
+def test_gguf_direct_pools(gpu, pkg, oracle, rs):
+    """The GGUF-direct pool's 6144 B q4 chunks land on the same mx bytes as q4_repack of
+    the GGUF blocks; its 9216 B q8 chunks on the same planes as the Q8_0 blocks."""
+    say(f"gguf direct pools rs={rs}")
+    rng = np.random.default_rng(30 + rs)
+    n, k = 256, 1024
+    for blocks in (oracle.random_q4_1_blocks_ref(n, k, rng), oracle.random_q4_0_blocks_ref(n, k, rng)):
+        w = pkg.pack_chunks(oracle.pack_gguf_pool_f32(blocks, rs), "q4_f32", n, k, rs, gpu)
+        torch.cuda.synchronize()
+        assert np.array_equal(w.data.cpu().numpy(), oracle.pack_mx(blocks))
+    b8 = oracle.random_q8_0_blocks(n, k, rng)
+    w8 = pkg.pack_q8(oracle.pack_gguf_pool_q8_f32(b8, rs), n, k, "chunks_f32", rs, gpu)
+    torch.cuda.synchronize()
+    hi, lo = _planes_want(oracle, *oracle.q8_0_rows(b8))
+    assert np.array_equal(w8.hi.data.cpu().numpy(), hi) and np.array_equal(w8.lo.data.cpu().numpy(), lo)

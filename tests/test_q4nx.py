@@ -197,3 +197,26 @@ def test_q8_split_planes_sum_to_the_q8_values_exactly(oracle):
     s16, q = oracle.q8_chunks_rows(src, n, k, 1)
     v = oracle.q8_chunk_values(src).reshape(-1, 32, 256)
     assert np.array_equal(oracle.q8_values(s16, q)[:32, :256], v[0])
+
+
+@pytest.mark.parametrize("kind", ["q4_1", "q4_0"])
+def test_gguf_direct_pool_reads_the_gguf_values_exactly(oracle, kind):
+    """gguf_pool.py's self-test (:388+), restated: the direct pool's own f32 reading equals
+    the GGUF blocks' fp16-scale dequant bit for bit (the widening is exact), and the
+    q8 pool holds every d * q exactly."""
+    rng = np.random.default_rng(21)
+    n, k = 128, 512
+    blocks = oracle.random_q4_1_blocks_ref(n, k, rng) if kind == "q4_1" else oracle.random_q4_0_blocks_ref(n, k, rng)
+    for rs in (1, 2):
+        pool = oracle.pack_gguf_pool_f32(blocks, rs)
+        got = oracle.dequant_gguf_pool_f32(pool, n, k, rs)
+        assert got.tobytes() == oracle.dequant_q4_1(blocks, bf16_scales=False).tobytes()
+    q8b = oracle.random_q8_0_blocks(n, k, rng)
+    pool8 = oracle.pack_gguf_pool_q8_f32(q8b, 1).reshape(-1, 9216)
+    d = np.ascontiguousarray(q8b[..., 0:2]).view(np.float16).reshape(n, k // 32).astype(np.float64)
+    q = np.ascontiguousarray(q8b[..., 2:]).view(np.int8).reshape(n, k).astype(np.float64)
+    want = np.repeat(d, 32, axis=1) * q
+    sc = np.ascontiguousarray(pool8[0, :1024]).view(np.float32).astype(np.float64)
+    code = np.ascontiguousarray(pool8[0, 1024:]).view(np.int8)[oracle.CHUNK_CODE_IDX].astype(np.float64)
+    got8 = (code * sc[oracle.CHUNK_META_IDX]).reshape(32, 8, 32).reshape(32, 256)
+    assert np.array_equal(got8, want[:32, :256])
