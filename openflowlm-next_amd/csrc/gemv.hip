@@ -247,6 +247,14 @@ int choose_splits(int64_t N, int64_t K) {
     return (int)(S < 1 ? 1 : S);
 }
 
+// The SwiGLU kernel streams two row groups per work item, so it takes half the splits
+// a plain GEMV of F rows would (measured on Llama-3-8B's 14336 x 4096 pair: 2 splits
+// 1.10 ms per 32 layers, 5 splits 1.15, 3 splits 1.14, none 1.22).
+int swiglu_splits(int64_t F, int64_t K) {
+    const int s = choose_splits(F, K) / 2;
+    return s < 1 ? 1 : s;
+}
+
 size_t workspace_for(int M, int64_t N, int64_t K, int S) {
     (void)K;
     if (S <= 1) return 0;
@@ -358,7 +366,7 @@ extern "C" int q4_gemv_q8(const uint8_t* hi, const uint8_t* lo, const void* x, i
 
 extern "C" size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K) {
     if (M < 1 || M > 16 || F <= 0 || K <= 0 || F % 64 || K % 32) return 0;
-    const int S = choose_splits(F, K);
+    const int S = swiglu_splits(F, K);
     return S > 1 ? (size_t)S * M * 2 * F * sizeof(float) : 0;
 }
 
@@ -373,7 +381,7 @@ extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void
     if (!gate || !up || !x || !h) return Q4MI_E_ARG;
     if (misaligned16(gate) || misaligned16(up) || misaligned16(x) || misaligned16(workspace)) return Q4MI_E_ARG;
     if (((uintptr_t)h & (h_dtype == Q4MI_BF16 ? 1 : 3)) != 0) return Q4MI_E_ARG;
-    const int S = choose_splits(F, K);
+    const int S = swiglu_splits(F, K);
     SwigluParams P{};
     P.gate = gate;
     P.up = up;
