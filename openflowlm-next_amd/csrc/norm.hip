@@ -24,6 +24,24 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
+// Wave sum of an f32 in every lane: DPP steps within rows (xor 1, xor 2 quad permutes,
+// the half-row and row mirrors), row broadcasts into lane 63, then readlane. Every lane's
+// addends arrive in the same tree order, so the result is deterministic.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                    0xF, false));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v = dpp_add<0xB1, 0xF>(v);        // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);        // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xF>(v);       // row_half_mirror
+    v = dpp_add<0x140, 0xF>(v);       // row_mirror
+    v = dpp_add<0x142, 0xA>(v);       // row_bcast:15 -> rows 1, 3
+    v = dpp_add<0x143, 0xC>(v);       // row_bcast:31 -> rows 2, 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // PER: values each thread keeps in registers (N <= 256 PER); the row is read once, and
 // y is written only after every read of x, so y may be x.
 template <int PER>
@@ -36,17 +54,21 @@ __global__ __launch_bounds__(256) void rmsnorm_add_kernel(const float* x, const 
     const int tid = threadIdx.x;
     const float* xr = x + row * N;
     const float* ar = add ? add + row * N : nullptr;
-    float v[PER];
+    float v[PER], wv[PER];
     double ss = 0.0;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
+    for (int j = 0; j < PER; ++j) {            // x, add and w all issued before the reduction
         const int64_t i = tid + 256 * j;
         v[j] = i < N ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f;
+        wv[j] = i >= N ? 0.0f
+                       : (w_bf16 ? bf16_hi_to_f32((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i]);
     }
 #pragma unroll
     for (int j = 0; j < PER; ++j) ss += (double)v[j] * (double)v[j];
-    ss = wave_sum_f64(ss);
-    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    // the lane sums are exact in f64; the wave tree adds them as two f32 halves (hi + lo)
+    const float hi = (float)ss, lo = (float)(ss - (double)hi);
+    const double ws = (double)wave_sum_f32(hi) + (double)wave_sum_f32(lo);
+    if ((tid & 63) == 0) part[tid >> 6] = ws;
     __syncthreads();
     if (y) {
         float* yr = y + row * N;
@@ -62,8 +84,7 @@ __global__ __launch_bounds__(256) void rmsnorm_add_kernel(const float* x, const 
     for (int j = 0; j < PER; ++j) {
         const int64_t i = tid + 256 * j;
         if (i >= N) break;
-        const float wi = w_bf16 ? bf16_hi_to_f32((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i];
-        const float o = v[j] * r * wi;
+        const float o = v[j] * r * wv[j];
         if (xn_bf16) ((uint16_t*)xn)[row * N + i] = (uint16_t)f32_to_bf16_rne(o);
         else ((float*)xn)[row * N + i] = o;
     }
