@@ -232,9 +232,12 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
 // right away.
 // LDS tiles are planar: [32-K plane][row][32 halves] (64 B rows, 16 KB per
 // plane of 256 rows). The 16-byte chunk c of row r sits at chunk slot
-// c ^ ((r >> 2) & 3), so the 16 lanes of a b128 fragment access (16
-// consecutive rows, one chunk) cover all 64 banks, and every fragment, store
-// and DMA address is one base register plus an immediate.
+// c ^ ((r >> 1) & 3). A fragment access is 16 consecutive rows x one chunk
+// per 16 lanes; with this swizzle ds_read_b128 runs conflict-free on gfx950
+// (measured 543 B/ns per CU, against 284 with slot c ^ ((r >> 2) & 3), which
+// also spreads each 16-lane group over all 64 banks but conflicts between
+// the groups the hardware serves together), and every fragment, store and
+// DMA address is one base register plus an immediate.
 // LDS map: weight buffers at 0 and 32 KB, activation ring at 64, 96, 128 KB.
 constexpr int kPlaneB = 256 * 64;                // one 32-K plane of a 256-row tile: 16 KB
 constexpr int kTileB = 2 * kPlaneB;              // one 64-K stage of a 256-row tile: 32 KB
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
     y += (int64_t)split * T * N;
     const int G = N >> 6;
     const int i16 = lane & 15, kg = lane >> 4;
-    const uint32_t lane_row = i16 * 64 + ((kg ^ (i16 >> 2)) << 4);     // row i16, chunk kg, swizzled
+    const uint32_t lane_row = i16 * 64 + ((kg ^ ((i16 >> 1) & 3)) << 4);   // row i16, chunk kg, swizzled
 
     // weights: this wave's mx tile of each stage (row group wave & 3, 32-K block wave >> 2)
     const int rgl = wave & 3, kbl = wave >> 2;
@@ -453,11 +456,11 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
 // max|x| 2^-s < 2^15) and tscale[t] = 2^s; PREC 1: bf16 (RNE from f32).
 // TILED: the 16-byte chunk i (k = 8i..8i+7) of token t goes to its place in the LDS image
 // of the pipelined kernel's activation tiles: [token tile][64-K stage][32-K plane][256 rows]
-// [4 chunks], chunk c of row r at slot c ^ ((r >> 2) & 3). Each stage of a token tile is then
+// [4 chunks], chunk c of row r at slot c ^ ((r >> 1) & 3). Each stage of a token tile is then
 // one contiguous 32 KB block, copied to LDS verbatim. Otherwise rows stay [T][K].
 __device__ __forceinline__ int64_t xchunk_dst(int t, int i, int K) {
     const int r = t & 255, st = i >> 3, kk = (i >> 2) & 1, c = i & 3;
-    return ((((int64_t)(t >> 8) * (K >> 6) + st) * 2 + kk) * 256 + r) * 4 + (c ^ ((r >> 2) & 3));
+    return ((((int64_t)(t >> 8) * (K >> 6) + st) * 2 + kk) * 256 + r) * 4 + (c ^ ((r >> 1) & 3));
 }
 
 template <bool XF32, int PREC, bool TILED>
