@@ -477,7 +477,17 @@ def extra_config3(torch, q4, dev):
                     q4.gemm_q4_prefill(packed[name], x, y, workspace=ws)
             ms = graph_time(torch, run, [y], replays=5) / 3
             tf = 2.0 * T * n * k / ms / 1e9
-            out[f"T{T}_{name}"] = {"ms": ms, "tflops": tf, "frac_of_peak": tf / MFMA_PEAK_TFLOPS}
+            # the vendor library's dense GEMM on the same shape (fp16 weights already
+            # dequantized, [K, N] contiguous): the rate this box sustains for a plain
+            # GEMM of this problem, as a yardstick for the dequant GEMM
+            xd = x.to(torch.float16)
+            wd = (torch.randn(k, n, generator=gen, device=dev) * 0.01).to(torch.float16)
+            _, dms = time_launches(torch, lambda: torch.matmul(xd, wd), 10, 3)
+            out[f"T{T}_{name}"] = {"ms": ms, "tflops": tf, "frac_of_peak": tf / MFMA_PEAK_TFLOPS,
+                                   "dense_fp16_matmul_ms": dms,
+                                   "dense_fp16_matmul_tflops": 2.0 * T * n * k / dms / 1e9,
+                                   "vs_dense_fp16_matmul": dms / ms}
+            del xd, wd
     return out
 
 
