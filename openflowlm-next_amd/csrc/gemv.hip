@@ -41,7 +41,7 @@ __device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4
     wave_sum<NTL>(acc, red, v);
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
-        const int tok = kg * 4 + j;
+        const int tok = token_of(kg, j);
         if (tok < M) y[(int64_t)tok * N + n] = res ? res[(int64_t)tok * N + n] + v[j] : v[j];
     }
 }
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256) void gemv_swiglu_kernel(SwigluParams P) {
     const int64_t f = g * 64 + (tid >> 6) * 16 + (lane & 15);
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
-        const int tok = (lane >> 4) * 4 + j;
+        const int tok = token_of(lane >> 4, j);
         if (tok >= P.M) continue;
         if (S == 1) {
             store_h(P.h, P.h_bf16, (int64_t)tok * P.F + f, silu(vg[j]) * vu[j]);
@@ -321,14 +321,14 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
     if (lo) {
-        switch (M < 4 ? M : 4) {
+        switch ((M + 3) / 4) {
             case 1: launch_pair<1>(xf32, grid, st, P, lo); break;
             case 2: launch_pair<2>(xf32, grid, st, P, lo); break;
             case 3: launch_pair<3>(xf32, grid, st, P, lo); break;
             default: launch_pair<4>(xf32, grid, st, P, lo); break;
         }
     } else {
-        switch (M < 4 ? M : 4) {
+        switch ((M + 3) / 4) {
             case 1: launch_gemv<1>(xf32, grid, st, P); break;
             case 2: launch_gemv<2>(xf32, grid, st, P); break;
             case 3: launch_gemv<3>(xf32, grid, st, P); break;
@@ -399,7 +399,7 @@ extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void
     const dim3 grid((unsigned)((F / 64) * S));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
-    switch (M < 4 ? M : 4) {
+    switch ((M + 3) / 4) {
         case 1: launch_swiglu<1>(xf32, grid, st, P); break;
         case 2: launch_swiglu<2>(xf32, grid, st, P); break;
         case 3: launch_swiglu<3>(xf32, grid, st, P); break;
@@ -423,7 +423,7 @@ extern "C" int q4_gemv_grouped(const q4_gemv_desc* descs, int count, int64_t tot
     const dim3 grid((unsigned)total_items);
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
-    switch (M < 4 ? M : 4) {
+    switch ((M + 3) / 4) {
         case 1: launch_grouped<1>(xf32, grid, st, descs, count, M); break;
         case 2: launch_grouped<2>(xf32, grid, st, descs, count, M); break;
         case 3: launch_grouped<3>(xf32, grid, st, descs, count, M); break;

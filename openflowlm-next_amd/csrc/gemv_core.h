@@ -13,9 +13,12 @@
 // (open_kernels/designs/gemv_q4/gemv_q4.h:33-34), here with the exact 4-bit
 // codes and bf16 activations on the bf16 MFMA and the scales applied in fp32.
 // The MFMA's A operand is the activation (tokens as rows), so each lane's
-// 4 outputs are 4 tokens of one weight row: one d and one m per lane per row
-// tile. f32 activations are split x = hi + lo (two bf16s, |residual| <=
-// 2^-18 |x|) and both halves go through the MFMA.
+// outputs are tokens of one weight row: one d and one m per lane per row
+// tile. MFMA row r carries token slot (r % 4) * 4 + r / 4, so the lane of
+// k-group kg holds tokens kg, kg + 4, kg + 8, kg + 12 in its outputs j = 0..3
+// and M tokens need only NTL = ceil(M / 4) accumulators per row (M <= 4: one,
+// as for a single token). f32 activations are split x = hi + lo (two bf16s,
+// |residual| <= 2^-18 |x|) and both halves go through the MFMA.
 #pragma once
 
 #include "q4mi_device.h"
@@ -25,6 +28,11 @@ namespace q4mi {
 constexpr int kWaves = 4;      // waves per workgroup
 constexpr int kUnroll = 4;     // tiles in flight per wave
 
+
+// MFMA row r (A operand row, output row) <-> token slot: rows 4 kg + j hold
+// token j * 4 + kg, so a lane's j-th output is token token_of(kg, j).
+__device__ __forceinline__ int token_of_row(int r) { return (r & 3) * 4 + (r >> 2); }
+__device__ __forceinline__ int token_of(int kg, int j) { return j * 4 + kg; }
 
 // Token slot -> activation row. Slots at or past M map to the last real
 // token: MFMA rows (tokens) are independent and those rows of the result are
@@ -77,7 +85,7 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
     const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     const CodeConsts kc = code_consts();
-    const int64_t xrow = rows(i16);
+    const int64_t xrow = rows(token_of_row(i16));
 
     for (int kb = kb0 + wave; kb < kb1; kb += kWaves * kUnroll) {
         u32x4 c[kUnroll], s[kUnroll];
@@ -134,7 +142,7 @@ __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG
     const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     const CodeConsts kc = code_consts();
-    const int64_t xrow = rows(i16);
+    const int64_t xrow = rows(token_of_row(i16));
 
     for (int kb = kb0 + wave; kb < kb1; kb += kWaves * UNR) {
         u32x4 c[UNR][NG], s[UNR][NG];
@@ -184,7 +192,7 @@ __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG
 
 // Sum the four waves' accumulators through LDS. Afterwards thread t owns
 // row 16 r + lane % 16 of the row group (r = t >> 6, lane = t & 63) for the
-// tokens 4 (lane / 16) + j, j < NTL: v[j].
+// tokens token_of(lane / 16, j), j < NTL: v[j].
 template <int NTL>
 __device__ __forceinline__ void wave_sum(float (&acc)[4][NTL], float (*red)[4][NTL][64], float (&v)[NTL]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -77,7 +77,7 @@ __device__ __forceinline__ void up_chunk(const uint8_t* wexp, const void* x, int
     const int64_t f = (int64_t)rgp * 64 + r * 16 + i16;
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
-        const int tok = kg * 4 + j;
+        const int tok = token_of(kg, j);
         if (tok < M) hbuf[(int64_t)pairs[tok] * F + f] = silu(vg[j]) * vu[j];
     }
 }
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void moe_up_kernel(const uint8_t* __restrict__
         const int M = min(16, cnt - c0);
         if (threadIdx.x < 16) rows[threadIdx.x] = list[c0 + min((int)threadIdx.x, M - 1)] / topk;
         __syncthreads();
-        switch (M < 4 ? M : 4) {
+        switch ((M + 3) / 4) {
             case 1: up_chunk<1, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
             case 2: up_chunk<2, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
             case 3: up_chunk<3, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
@@ -135,7 +135,7 @@ __device__ __forceinline__ void down_chunk(const uint8_t* wexp, const float* hbu
         const int64_t n = (int64_t)(rg0 + i) * 64 + r * 16 + i16;
 #pragma unroll
         for (int j = 0; j < NTL; ++j) {
-            const int tok = kg * 4 + j;
+            const int tok = token_of(kg, j);
             if (tok < M) ypair[(int64_t)pairs[tok] * H + n] = v[j];
         }
     }
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t* __restrict
     const uint8_t* wexp = down + (int64_t)e * (H / 64) * (F / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 16) {
         const int M = min(16, cnt - c0);
-        switch (M < 4 ? M : 4) {
+        switch ((M + 3) / 4) {
             case 1: down_chunk<1, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
             case 2: down_chunk<2, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
             case 3: down_chunk<3, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
