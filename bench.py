@@ -409,6 +409,51 @@ def extra_q8(torch, q4, dev):
     return out
 
 
+def extra_q4k(torch, q4, dev):
+    """GGUF Q4_K weights at M=1 on the Llama-3-8B gate_up, down and lm_head shapes: the
+    native Q4_K kernel (the super-block's integers, 0.594 B/weight, exact) against the
+    same blocks collapsed to the mx q4_1 layout (0.625 B/weight, d sc and m mn rounded
+    to bf16), each graph-timed over rotating copies that exceed the caches. GB/s counts
+    each layout's own bytes + bf16 x + f32 y; us is the number to compare."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 17)
+    out = {}
+    for name, n, k in (("gate_up", 28672, 4096), ("down", 4096, 14336), ("lm_head", 128256, 4096)):
+        ns = k // 256
+        blocks = torch.randint(0, 256, (n, ns, 144), generator=gen, device=dev, dtype=torch.uint8)
+        d = (torch.rand(n, ns, generator=gen, device=dev) + 0.5) * (0.02 / 600)
+        dmin = (torch.rand(n, ns, generator=gen, device=dev) + 0.5) * (0.02 / 40)
+        blocks[..., 0:2] = d.to(torch.float16).view(torch.uint8).view(n, ns, 2)
+        blocks[..., 2:4] = dmin.to(torch.float16).view(torch.uint8).view(n, ns, 2)
+        copies = 1 if n > 100000 else 8
+        native = [q4.pack_q4_k_native(blocks, dev) for _ in range(copies)]
+        collapsed = [q4.pack_q4_k(blocks, dev) for _ in range(copies)]
+        del blocks
+        x = torch.randn(1, k, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty(1, n, dtype=torch.float32, device=dev)
+        wsp = torch.empty(max(q4.gemv_workspace_bytes(1, n, k), 256), dtype=torch.uint8, device=dev)
+        wsk = torch.empty(max(q4.load_library().q4_gemv_q4k_workspace_bytes(1, n, k), 256), dtype=torch.uint8,
+                          device=dev)
+
+        def run_native():
+            for w in native:
+                q4.gemm_q4k(w, x, y, workspace=wsk)
+
+        def run_collapsed():
+            for w in collapsed:
+                q4.gemm_q4(w, x, y, workspace=wsp)
+        ms_n = graph_time(torch, run_native, [y], replays=10) / copies
+        ms_c = graph_time(torch, run_collapsed, [y], replays=10) / copies
+        io = k * 2 + n * 4
+        out[name] = {"N": n, "K": k,
+                     "native_us": round(ms_n * 1e3, 2), "native_gbs": round((native[0].nbytes + io) / ms_n / 1e6, 1),
+                     "collapsed_us": round(ms_c * 1e3, 2),
+                     "collapsed_gbs": round((collapsed[0].nbytes + io) / ms_c / 1e6, 1)}
+        del native, collapsed
+        torch.cuda.empty_cache()
+    return out
+
+
 def extra_peaks(torch, dev):
     """On-box reference points: HBM read bandwidth of a plain reduction over
     4 GiB (torch.sum, reads only) and dense bf16 GEMM throughput of the vendor
@@ -535,8 +580,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,q8,peaks",
-                    help="comma list (staged,0,2,3,4,lm_head,ffn,q8,peaks) or 'none'")
+    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks",
+                    help="comma list (staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=15, help="passes over one layer in the CPU baseline")
     ap.add_argument("--cpu-baseline-child", type=int, default=None, help=argparse.SUPPRESS)
@@ -584,6 +629,8 @@ def main() -> int:
                 out["lm_head_topk"] = extra_lm_head(torch, q4, dev)
             elif cfg == "q8":
                 out["q8_gemv"] = extra_q8(torch, q4, dev)
+            elif cfg == "q4k":
+                out["q4k_native_gemv"] = extra_q4k(torch, q4, dev)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -621,6 +668,8 @@ def main() -> int:
                 extras["ffn_fused_decode"] = extra_ffn(torch, q4, model, acts)
             elif cfg == "q8":
                 extras["q8_gemv"] = extra_q8(torch, q4, dev)
+            elif cfg == "q4k":
+                extras["q4k_native_gemv"] = extra_q4k(torch, q4, dev)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
         log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")

@@ -111,6 +111,41 @@ int q4_repack_q4k(const uint8_t* q4k_blocks, uint8_t* packed, int64_t N, int64_t
 int q4_repack_q4k_chunks(const uint8_t* chunks, int rs, uint8_t* packed,
                          int64_t N, int64_t K, void* stream);
 
+/* Native Q4_K ("mxk" layout): the super-block's own integers, no bf16 collapse. A
+ * 64-row x 256-K tile (one super-block per row) is 9728 bytes: the 8 sub-blocks'
+ * codes in the mx code layout, per row and sub-block the 8-bit multipliers (sc, mn),
+ * per row the f32 bases d and m. Weight = fl32(d sc q + m mn), with d sc and m mn exact
+ * in f32: the value the reference's Q4_K GEMM reads (open_kernels/designs/gemm_q4/
+ * gemm_q4.h:456-507, gemm_q4k_tile4 :555: value = d sc nib + mcoef mn) and, for GGUF
+ * blocks, the GGUF reader's dequant (src/gguf/gguf_file.cpp:611-635). 0.594 bytes per
+ * weight against the mx layout's 0.625. Bytes of an [N, K] matrix (N % 64 == 0,
+ * K % 256 == 0), or -1: */
+int64_t q4_q4k_packed_bytes(int64_t N, int64_t K);
+
+/* GGUF Q4_K super-blocks (uint8[N][K/256][144], as q4_repack_q4k) -> mxk, on the
+ * device: d = fp16 d, m = -fp16 dmin, (sc_j, mn_j) the packed 6-bit pairs. */
+int q4_repack_q4k_native(const uint8_t* q4k_blocks, uint8_t* packed, int64_t N, int64_t K, void* stream);
+
+/* The reference container's Q4_K chunks (as q4_repack_q4k_chunks) -> mxk, on the
+ * device: d = bf16 S[r], m = bf16 M[r], (sc, mn) = (scales[g][r], mins[g][r]). */
+int q4_repack_q4k_chunks_native(const uint8_t* chunks, int rs, uint8_t* packed,
+                                int64_t N, int64_t K, void* stream);
+
+/* mxk -> f32 [N][K] row-major, w = fl32(q (d sc) + m mn), bit-exact with the values
+ * above (the mxk twin of q4_dequant). */
+int q4_dequant_q4k(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
+
+/* Workspace bytes q4_gemv_q4k needs (0 if none). */
+size_t q4_gemv_q4k_workspace_bytes(int M, int64_t N, int64_t K);
+
+/* Y[M][N] = X[M][K] . W^T over an mxk matrix, 1 <= M <= 16, fp32 accumulate, plus
+ * residual (f32 [M][N], may be y) when not NULL: the Q4_K-native skinny GEMM, the
+ * counterpart of the reference's gemm_q4k_tile4 (gemm_q4.h:555). Per 32-K block the
+ * kernel applies the exact f32 scale d sc and offset m mn to the MFMA's sum of q x.
+ * K is split (on whole super-blocks) for matrices of few row groups, as q4_gemv. */
+int q4_gemv_q4k(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
+                int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Pool chunks of the SIGNED quantiser -> mx layout: 5120-byte chunks laid out as
  * q4_1's, holding w = d * int4(q) with every min 0 (recipes/pack.py:583-603 tells them
  * apart by those zero mins). Read the q4_1 way, exactly: code q ^ 8, m = -8 d

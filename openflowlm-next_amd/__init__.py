@@ -9,7 +9,8 @@ Import with ``importlib.import_module("openflowlm-next_amd")`` (the directory
 name is not a Python identifier).
 """
 from . import _lib
-from .q4 import (GemvGroup, PackedExperts, PackedQ4, PackedQ8, dequant, gemm_q4, gemm_q4_prefill, gemm_q8, gemv_q4,
+from .q4 import (GemvGroup, PackedExperts, PackedQ4, PackedQ4K, PackedQ8, dequant, dequant_q4k, gemm_q4, gemm_q4k,
+                 gemm_q4_prefill, gemm_q8, gemv_q4, pack_q4_k_native, pack_q4_k_chunks_native, q4k_packed_bytes,
                  gemv_workspace_bytes, lm_head_topk, logits_topk, moe_batch, pack_chunks, moe_workspace_bytes, pack_moe_experts, pack_q4_1,
                  pack_q4_1_pool, pack_q4_k, pack_q4_k_chunks, pack_q8, packed_bytes, prefill_workspace_bytes, rmsnorm_add,
                  swiglu_q4)
@@ -17,7 +18,8 @@ from .gguf import GGUFError, GGUFFile
 from .q4nx import Q4NXError, Q4NXFile
 
 __all__ = [
-    "PackedQ4", "PackedQ8", "PackedExperts", "packed_bytes", "pack_q8", "gemm_q8", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k",
+    "PackedQ4", "PackedQ4K", "PackedQ8", "PackedExperts", "pack_q4_k_native", "pack_q4_k_chunks_native",
+    "dequant_q4k", "gemm_q4k", "q4k_packed_bytes", "packed_bytes", "pack_q8", "gemm_q8", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k",
     "pack_q4_k_chunks", "pack_chunks", "GGUFFile", "GGUFError", "Q4NXFile", "Q4NXError", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "lm_head_topk", "logits_topk", "swiglu_q4", "rmsnorm_add", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "load_library",

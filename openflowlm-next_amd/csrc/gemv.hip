@@ -84,6 +84,27 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     else gemv_finish<NTL>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
 
+// The GEMV over the native Q4_K layout: split s takes super-blocks [sb0, sb1) of K / 256
+// (each wave whole super-blocks), then stores as gemv_kernel.
+template <int NTL, bool XF32>
+__global__ __launch_bounds__(256) void q4k_gemv_kernel(GemvParams P) {
+    __shared__ float red[kWaves][4][NTL][64];
+    const int64_t item = blockIdx.x;
+    const int S = P.S;
+    const int64_t g = item / S;
+    const int s = (int)(item % S);
+    const int SB = (int)(P.K >> 8);
+    const int sb0 = (int)((int64_t)s * SB / S), sb1 = (int)((int64_t)(s + 1) * SB / S);
+    float acc[4][NTL];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
+    q4k_rows<NTL, XF32>(P.packed, P.x, DenseRows{P.M}, P.K, g, sb0, sb1, acc);
+    if (S == 1) gemv_finish<NTL>(acc, red, P.M, P.y, P.N, g, P.res);
+    else gemv_finish<NTL>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
+}
+
 // The q8 GEMV as two q4_1 planes (hi, lo) of one matrix: one workgroup streams row group
 // g of both (sharing the activation fragments) and stores y = hi . x + lo . x (S == 1, plus
 // the residual when one is given) or this split's partial of that sum.
@@ -247,6 +268,23 @@ int choose_splits(int64_t N, int64_t K) {
     return (int)(S < 1 ? 1 : S);
 }
 
+// Native Q4_K: split on whole super-blocks. A wave takes whole super-blocks, so S is the
+// smallest divisor of SB / 4 that reaches the workgroup target (every wave of every split
+// then gets the same count), else SB / 4 (one per wave). From 256 row groups on there is
+// no split: its reduce launch costs more than the longer waves (measured on the Llama-3-8B
+// gate_up pair, 28672 x 4096: 15.9 us unsplit, 17.9 us in 4 splits).
+constexpr int64_t kQ4kNoSplitGroups = 256;
+
+int q4k_splits(int64_t N, int64_t K) {
+    const int64_t G = N / 64, SB = K / 256;
+    const int64_t target = target_workgroups();
+    if (G >= target || G >= kQ4kNoSplitGroups || SB < 8) return 1;
+    const int64_t want = ceil_div(target, G), per_wave = SB / 4;
+    for (int64_t S = 1; S <= per_wave; ++S)
+        if (per_wave % S == 0 && S >= want) return (int)S;
+    return (int)per_wave;
+}
+
 // The SwiGLU kernel streams two row groups per work item, so it takes half the splits
 // a plain GEMV of F rows would (measured on Llama-3-8B's 14336 x 4096 pair: 2 splits
 // 1.10 ms per 32 layers, 5 splits 1.15, 3 splits 1.14, none 1.22).
@@ -277,6 +315,12 @@ template <int NTL>
 void launch_gemv(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
     if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
     else hipLaunchKernelGGL((gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
+}
+
+template <int NTL>
+void launch_q4k(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (xf32) hipLaunchKernelGGL((q4k_gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
+    else hipLaunchKernelGGL((q4k_gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
 }
 
 template <int NTL>
@@ -428,6 +472,51 @@ extern "C" int q4_gemv_grouped(const q4_gemv_desc* descs, int count, int64_t tot
         case 2: launch_grouped<2>(xf32, grid, st, descs, count, M); break;
         case 3: launch_grouped<3>(xf32, grid, st, descs, count, M); break;
         default: launch_grouped<4>(xf32, grid, st, descs, count, M); break;
+    }
+    return launch_status();
+}
+
+extern "C" size_t q4_gemv_q4k_workspace_bytes(int M, int64_t N, int64_t K) {
+    if (M < 1 || M > 16 || N <= 0 || K <= 0 || N % 64 || K % 256) return 0;
+    return workspace_for(M, N, K, q4k_splits(N, K));
+}
+
+extern "C" int q4_gemv_q4k(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y, int M,
+                           int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (M < 0 || M > 16) return Q4MI_E_RANGE;
+    if (N < 0 || K <= 0 || N % 64 || K % 256) return Q4MI_E_SHAPE;
+    if (M == 0 || N == 0) return Q4MI_OK;
+    if (!packed || !x || !y) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
+    const int S = q4k_splits(N, K);
+    GemvParams P{};
+    P.packed = packed;
+    P.x = x;
+    P.y = y;
+    P.M = M;
+    P.S = S;
+    P.N = N;
+    P.K = K;
+    P.res = residual;
+    if (S > 1) {
+        if (!workspace || workspace_bytes < workspace_for(M, N, K, S)) return Q4MI_E_WORKSPACE;
+        P.part = (float*)workspace;
+    }
+    const dim3 grid((unsigned)((N / 64) * S));
+    const hipStream_t st = (hipStream_t)stream;
+    const bool xf32 = x_dtype == Q4MI_F32;
+    switch ((M + 3) / 4) {
+        case 1: launch_q4k<1>(xf32, grid, st, P); break;
+        case 2: launch_q4k<2>(xf32, grid, st, P); break;
+        case 3: launch_q4k<3>(xf32, grid, st, P); break;
+        default: launch_q4k<4>(xf32, grid, st, P); break;
+    }
+    if (S > 1) {
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        const int64_t MN = (int64_t)M * N;
+        hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)ceil_div(MN, 256)), dim3(256), 0, st, P.part, y, MN,
+                           S, residual);
     }
     return launch_status();
 }

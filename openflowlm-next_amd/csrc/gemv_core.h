@@ -127,6 +127,68 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
     }
 }
 
+// gemv_rows over the native Q4_K layout (kKTileBytes tiles): wave w takes the whole
+// super-blocks sb0 + w, sb0 + w + kWaves, ... of [sb0, sb1): its 8 code sub-tiles and
+// activation fragments, its rows' 16 (sc, mn) bytes and its d and m, then per 32-K block
+// the scale d * sc and offset m * mn (both exact in f32), applied as above.
+template <int NTL, bool XF32, class Rows>
+__device__ __forceinline__ void q4k_rows(const uint8_t* __restrict__ packed, const void* __restrict__ x, Rows rows,
+                                         int64_t K, int64_t g, int sb0, int sb1, float (&acc)[4][NTL]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    sb0 = __builtin_amdgcn_readfirstlane(sb0);
+    sb1 = __builtin_amdgcn_readfirstlane(sb1);
+    const int i16 = lane & 15, kg = lane >> 4;
+    const int64_t SB = K >> 8;
+    const uint8_t* gbase = packed + g * SB * kKTileBytes;
+    const int coff = lane * 16, soff = kKScOff + i16 * 64, doff = kKDOff + i16 * 16, moff = kKMOff + i16 * 16;
+    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const CodeConsts kc = code_consts();
+    const int64_t xrow = rows(token_of_row(i16));
+
+    for (int sb = sb0 + wave; sb < sb1; sb += kWaves) {
+        const uint8_t* tp = gbase + (int64_t)sb * kKTileBytes;                 // wave-uniform
+        // the super-block's scales first: loads land in issue order, so block 0's
+        // epilogue then waits for its own codes only, not for every block's
+        u32x4 c[8], sm[4];
+        bf16x8 xh[8], xl[8];
+        const f32x4 dv = *(const f32x4*)(tp + doff), mv = *(const f32x4*)(tp + moff);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sm[r] = load_nt_u32x4(tp + soff + r * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            c[j] = load_nt_u32x4(tp + j * 1024 + coff);
+            load_xfrag<XF32>(x, K, xrow, (int64_t)sb * 256 + j * 32 + kg * 8, xh[j], xl[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            f32x4 ns = mfma_bf16(xh[j], neg128, zero4);
+            if constexpr (XF32) ns = mfma_bf16(xl[j], neg128, ns);
+            f32x4 p[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bf16x8 b = codes_to_bf16(c[j][r], kc);
+                p[r] = mfma_bf16(xh[j], b, ns);
+                if constexpr (XF32) p[r] = mfma_bf16(xl[j], b, p[r]);
+            }
+            float sx[NTL];
+#pragma unroll
+            for (int t = 0; t < NTL; ++t) sx[t] = ns[t] * (-1.0f / 128.0f);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float d = dv[r] * (float)((sm[r][j >> 2] >> (8 * (j & 3))) & 0xFF);
+                const float m = mv[r] * (float)((sm[r][2 + (j >> 2)] >> (8 * (j & 3))) & 0xFF);
+#pragma unroll
+                for (int t = 0; t < NTL; ++t) {
+                    acc[r][t] = __builtin_fmaf(d, p[r][t], acc[r][t]);
+                    acc[r][t] = __builtin_fmaf(m, sx[t], acc[r][t]);
+                }
+            }
+        }
+    }
+}
+
 // gemv_rows over NG row groups at once (tile bases gbase[i], same K range and
 // activations): per K position the activation fragment and the -128 sum x
 // MFMA are shared by the NG groups, and NG x UNR tiles are in flight per wave.

@@ -18,6 +18,18 @@
 
 namespace q4mi {
 
+// The native Q4_K ("mxk") layout of an [N, K] matrix (N % 64 == 0, K % 256 == 0): tile
+// (g, sb) = 64 rows x 256 K (one Q4_K super-block per row), 9728 B, at byte
+// (g * K/256 + sb) * 9728:
+//   codes [0, 8192): sub-block j (32 K) at j * 1024, laid out as the mx codes above;
+//   sc/mn [8192, 9216): row 16 r + i16 at 8192 + i16 * 64 + r * 16: the 8-bit integer
+//         multipliers sc[0..7] of its 8 sub-blocks, then mn[0..7];
+//   d     [9216, 9472): f32 at 9216 + i16 * 16 + r * 4;  m [9472, 9728): same order.
+// Weight = fl32(d sc q + m mn): d sc and m mn are exact in f32 (<= 11-bit x 8-bit
+// significands), so a block reads as Q4_1 with scale d sc and offset m mn, exactly.
+constexpr int kKTileBytes = 9728;
+constexpr int kKScOff = 8192, kKDOff = 9216, kKMOff = 9472;
+
 constexpr int kRows = 64;        // rows per tile / row group
 constexpr int kBlk = 32;         // K per tile (one GGUF block)
 constexpr int kTileBytes = 1280;
@@ -81,6 +93,9 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // way (the "nt" bit on the global load).
 __device__ __forceinline__ u32x4 load_nt_u32x4(const void* p) {
     return __builtin_nontemporal_load((const u32x4*)p);
+}
+__device__ __forceinline__ u32x2 load_nt_u32x2(const void* p) {
+    return __builtin_nontemporal_load((const u32x2*)p);
 }
 __device__ __forceinline__ uint32_t load_nt_u32(const void* p) {
     return __builtin_nontemporal_load((const uint32_t*)p);

@@ -169,6 +169,117 @@ __global__ __launch_bounds__(256) void repack_q4k_chunk_kernel(const uint8_t* __
     mx_write_block(packed, KB, n, kb, code, (f32_to_bf16_rne(d) << 16) | f32_to_bf16_rne(m));
 }
 
+// --- native Q4_K ("mxk", q4mi_device.h): the super-block's own integers, no collapse ---
+
+// Row n's share of mxk tile (n / 64, sb): 8 sub-blocks of 32 codes, their (sc, mn) bytes
+// and the f32 bases d, m.
+__device__ __forceinline__ void mxk_write_row(uint8_t* packed, int64_t SB, int64_t n, int64_t sb,
+                                              const uint8_t (&code)[8][32], const uint8_t (&sc)[8],
+                                              const uint8_t (&mn)[8], float d, float m) {
+    const int i = (int)(n & 63);
+    const int r = i >> 4, i16 = i & 15;
+    uint8_t* tile = packed + ((n >> 6) * SB + sb) * kKTileBytes;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int kg = 0; kg < 4; ++kg) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) w |= (uint32_t)code[j][8 * kg + e] << (16 * (e & 1) + 4 * (e >> 1));
+            *(uint32_t*)(tile + j * 1024 + (kg * 16 + i16) * 16 + r * 4) = w;
+        }
+        tile[kKScOff + i16 * 64 + r * 16 + j] = sc[j];
+        tile[kKScOff + i16 * 64 + r * 16 + 8 + j] = mn[j];
+    }
+    *(float*)(tile + kKDOff + i16 * 16 + r * 4) = d;
+    *(float*)(tile + kKMOff + i16 * 16 + r * 4) = m;
+}
+
+// GGUF Q4_K super-block (144 B: fp16 d | fp16 dmin | 12 B of packed 6-bit (sc, min) |
+// 128 B of codes) -> mxk, one thread per (row, super-block): d = fp16 d, m = -fp16 dmin,
+// (sc_j, mn_j) = llama.cpp's get_scale_min_k4 pairs; weight d sc q - dmin min exactly as
+// the GGUF reader dequantizes it (src/gguf/gguf_file.cpp:611-635).
+__global__ __launch_bounds__(256) void repack_mxk_gguf_kernel(const uint8_t* __restrict__ src,
+                                                              uint8_t* __restrict__ packed, int64_t N, int64_t SB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * SB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / SB) * 64 + (idx & 63);
+    const int64_t sb = tile % SB;
+    const uint8_t* b = src + (n * SB + sb) * 144;
+    const float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    const float dmin = f16_bits_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+    const uint8_t* q6 = b + 4;
+    uint8_t sc[8], mn[8], code[8][32];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if (j < 4) {
+            sc[j] = q6[j] & 63;
+            mn[j] = q6[j + 4] & 63;
+        } else {
+            sc[j] = (q6[j + 4] & 0xF) | ((q6[j - 4] >> 6) << 4);
+            mn[j] = (q6[j + 4] >> 4) | ((q6[j] >> 6) << 4);
+        }
+        const uint8_t* qs = b + 16 + 32 * (j >> 1);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) code[j][e] = (qs[e] >> (4 * (j & 1))) & 0xF;
+    }
+    mxk_write_row(packed, SB, n, sb, code, sc, mn, d, -dmin);
+}
+
+// The reference container's Q4_K chunks (4736 B, 32 rows x 256 K, band order with row
+// split rs) -> mxk: d = bf16 S[r], m = bf16 M[r] (stored negated), (sc, mn) =
+// (scales[g][r], mins[g][r]); weight S sc nib + M mn as the reference's Q4_K kernel reads
+// the chunk (open_kernels/designs/gemm_q4/gemm_q4.h:456-507).
+__global__ __launch_bounds__(256) void repack_mxk_chunk_kernel(const uint8_t* __restrict__ chunks, int rs,
+                                                               uint8_t* __restrict__ packed, int64_t N, int64_t SB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * SB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / SB) * 64 + (idx & 63);
+    const int64_t sb = tile % SB;
+    const int64_t per_band = (int64_t)rs * SB;
+    const uint8_t* ch = chunks + ((n / (32 * rs)) * per_band + sb * rs + (n % (32 * rs)) / 32) * 4736;
+    const int r = (int)(n & 31);
+    const float d = bf16_hi_to_f32(((uint32_t)ch[4608 + 2 * r] | ((uint32_t)ch[4609 + 2 * r] << 8)) << 16);
+    const float m = bf16_hi_to_f32(((uint32_t)ch[4672 + 2 * r] | ((uint32_t)ch[4673 + 2 * r] << 8)) << 16);
+    const int sh = 4 * (r & 1);
+    uint8_t sc[8], mn[8], code[8][32];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = ch[j * 32 + r];
+        mn[j] = ch[256 + j * 32 + r];
+        const uint8_t* cb = ch + 512 + (32 * j) * 16 + (r >> 1);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) code[j][e] = (cb[e * 16] >> sh) & 0xF;
+    }
+    mxk_write_row(packed, SB, n, sb, code, sc, mn, d, m);
+}
+
+// mxk -> f32: w = fl32(q * (d sc) + m mn); q (d sc) is exact, so one fma is the
+// reference's multiply-then-add bit for bit. One thread per 8 consecutive k of a row.
+__global__ __launch_bounds__(256) void dequant_mxk_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
+                                                          int64_t N, int64_t K) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t K8 = K >> 3;
+    if (idx >= N * K8) return;
+    const int64_t n = idx / K8, k8 = idx % K8;
+    const int64_t kb = k8 >> 2, sb = kb >> 3;
+    const int j = (int)(kb & 7), kg = (int)(k8 & 3);
+    const int i = (int)(n & 63), r = i >> 4, i16 = i & 15;
+    const uint8_t* tile = packed + ((n >> 6) * (K >> 8) + sb) * kKTileBytes;
+    const uint32_t c = *(const uint32_t*)(tile + j * 1024 + (kg * 16 + i16) * 16 + r * 4);
+    const uint8_t* sm = tile + kKScOff + i16 * 64 + r * 16;
+    const float D = *(const float*)(tile + kKDOff + i16 * 16 + r * 4) * (float)sm[j];
+    const float M = *(const float*)(tile + kKMOff + i16 * 16 + r * 4) * (float)sm[8 + j];
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf((float)((c >> (16 * (e & 1) + 4 * (e >> 1))) & 0xF), D, M);
+    f32x4* dst = (f32x4*)(w + n * K + k8 * 8);
+    dst[0] = f32x4{o[0], o[1], o[2], o[3]};
+    dst[1] = f32x4{o[4], o[5], o[6], o[7]};
+}
+
 // Chunk of row n, 32-K block kb in the pool's band order with row split rs (q4_1_pack.py:
 // 112-121; rs = 1 is the .q4nx file's raster, chunk = (n / 32) * K / 256 + kb / 8).
 __device__ __forceinline__ int64_t band_chunk(int64_t n, int64_t kb, int rs, int64_t K) {
@@ -444,5 +555,45 @@ extern "C" int q4_repack_q8_split(const uint8_t* src, int src_format, int rs, in
     const int64_t KB = K / 32, total = N * KB;
     hipLaunchKernelGGL(repack_q8_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, src, src_format, rs, part, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int64_t q4_q4k_packed_bytes(int64_t N, int64_t K) {
+    if (N < 0 || K <= 0 || N % 64 || K % 256) return -1;
+    return (N / 64) * (K / 256) * (int64_t)kKTileBytes;
+}
+
+extern "C" int q4_repack_q4k_native(const uint8_t* q4k_blocks, uint8_t* packed, int64_t N, int64_t K, void* stream) {
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!q4k_blocks || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % 256) return Q4MI_E_SHAPE;
+    const int64_t SB = K / 256, total = N * SB;
+    hipLaunchKernelGGL(repack_mxk_gguf_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, q4k_blocks, packed, N, SB);
+    return launch_status();
+}
+
+extern "C" int q4_repack_q4k_chunks_native(const uint8_t* chunks, int rs, uint8_t* packed, int64_t N, int64_t K,
+                                           void* stream) {
+    if (rs <= 0) return Q4MI_E_ARG;
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!chunks || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || K % 256 || N % 64 || N % (32 * rs)) return Q4MI_E_SHAPE;
+    const int64_t SB = K / 256, total = N * SB;
+    hipLaunchKernelGGL(repack_mxk_chunk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, chunks, rs, packed, N, SB);
+    return launch_status();
+}
+
+extern "C" int q4_dequant_q4k(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
+    if (N == 0 && K > 0 && K % 256 == 0) return Q4MI_OK;
+    if (!packed || !w) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(w)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % 256) return Q4MI_E_SHAPE;
+    const int64_t total = N * (K / 8);
+    hipLaunchKernelGGL(dequant_mxk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       packed, w, N, K);
     return launch_status();
 }

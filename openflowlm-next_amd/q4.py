@@ -193,6 +193,109 @@ def pack_q4_k_chunks(chunks, n: int, k: int, rs: int = 1, device=None) -> Packed
     return PackedQ4(out, n, k)
 
 
+# --------------------------------------------------------------------------
+# native Q4_K (the "mxk" layout: the super-block's own integers, no bf16 collapse)
+# --------------------------------------------------------------------------
+
+def q4k_packed_bytes(n: int, k: int) -> int:
+    """Bytes of the native Q4_K layout for an [n, k] matrix (n % 64 == 0, k % 256 == 0)."""
+    b = _lib_handle().q4_q4k_packed_bytes(n, k)
+    if b < 0:
+        raise ValueError(f"[{n}, {k}] does not fit the Q4_K layout (n % 64 == 0, k % 256 == 0)")
+    return int(b)
+
+
+@dataclass
+class PackedQ4K:
+    """One [n, k] Q4_K matrix in the native layout: weight fl32(d sc q + m mn) with d sc
+    and m mn exact, as the reference's Q4_K GEMM reads it (gemm_q4.h:456-507); 0.594 B
+    per weight."""
+    data: torch.Tensor
+    n: int
+    k: int
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+
+def pack_q4_k_native(blocks, device=None) -> PackedQ4K:
+    """GGUF Q4_K super-blocks uint8[N, K/256, 144] -> the native Q4_K layout on the GPU:
+    weight d sc q - dmin min, exactly the GGUF reader's value (gguf_file.cpp:611-635)."""
+    dev = _device(device if device is not None else (blocks.device if isinstance(blocks, torch.Tensor)
+                                                     and blocks.is_cuda else None))
+    src = _to_dev(blocks, dev, torch.uint8)
+    if src.dim() != 3 or src.shape[2] != 144:
+        raise ValueError(f"blocks must be uint8[N, K/256, 144], got {tuple(src.shape)}")
+    n, nsb, _ = src.shape
+    k = nsb * 256
+    out = torch.empty(q4k_packed_bytes(n, k), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_repack_q4k_native", _lib_handle().q4_repack_q4k_native(_ptr(src), _ptr(out), n, k, _stream(dev)))
+    return PackedQ4K(out, n, k)
+
+
+def pack_q4_k_chunks_native(chunks, n: int, k: int, rs: int = 1, device=None) -> PackedQ4K:
+    """The reference container's Q4_K chunks (4736 B per 32 rows x 256 K, band order with
+    row split rs) -> the native Q4_K layout: weight S sc nib + M mn, the chunk's own value
+    (gemm_q4.h:456-507), with no bf16 collapse."""
+    dev = _device(device)
+    src = _to_dev(chunks, dev, torch.uint8).reshape(-1)
+    want = (n // 32) * (k // 256) * 4736 if n % 32 == 0 and k % 256 == 0 else -1
+    if src.numel() != want:
+        raise ValueError(f"Q4_K chunks hold {src.numel()} bytes, [{n}, {k}] needs {want} (4736 B per 32 x 256)")
+    out = torch.empty(q4k_packed_bytes(n, k), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_repack_q4k_chunks_native",
+              _lib_handle().q4_repack_q4k_chunks_native(_ptr(src), rs, _ptr(out), n, k, _stream(dev)))
+    return PackedQ4K(out, n, k)
+
+
+def dequant_q4k(w: PackedQ4K, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Native Q4_K layout -> f32[n, k], w = fl32(q (d sc) + m mn), bit-exact."""
+    dev = w.device
+    if out is None:
+        out = torch.empty((w.n, w.k), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_dequant_q4k", _lib_handle().q4_dequant_q4k(_ptr(w.data), _ptr(out), w.n, w.k, _stream(dev)))
+    return out
+
+
+def gemm_q4k(w: PackedQ4K, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+             residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Y[M, N] = X[M, K] @ W^T over a native Q4_K matrix, 1 <= M <= 16, fp32 out (the
+    reference's gemm_q4k_tile4 operator, gemm_q4.h:555); ``residual`` as in gemm_q4."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != w.k:
+        raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q4k takes 1..16 tokens, got {M}")
+    if y is None:
+        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
+                                 or residual.numel() != M * w.n or residual.device != dev):
+        raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_q4k_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        check("q4_gemv_q4k", lib.q4_gemv_q4k(_ptr(w.data), _ptr(xt), _x_dtype(xt),
+                                             None if residual is None else _ptr(residual), _ptr(y), M, w.n, w.k,
+                                             wp, wn, _stream(dev)))
+    return y
+
+
 @dataclass
 class PackedQ8:
     """A q8 matrix [n, k] held exactly as two mx q4_1 planes, hi + lo = s q

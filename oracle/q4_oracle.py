@@ -23,6 +23,8 @@ this hot path (``/root/reference`` is read as text, never imported):
                                   src/gguf/gguf_file.cpp:611-635
 * container Q4_K -> q4_1 chunks   open_kernels/recipes/pack.py:266-310,
                                   src/open_qwen36/pools.cpp:642-663
+* native Q4_K values              open_kernels/designs/gemm_q4/gemm_q4.h:456-507
+  (value d sc nib + mcoef mn of the container chunk; d sc q - dmin min of GGUF)
 
 ``ml_dtypes`` (which the reference uses for its bf16 casts) is absent here; the
 bf16 conversions are restated as IEEE round-to-nearest-even on the f32 bits.
@@ -41,9 +43,12 @@ FNV-1a of that transcode is not reproduced; the test records it as a strict
 xfail).  Functions with no such check are marked
 "parity unpinned" in their docstrings (there are none at present).
 
-The MI355X weight layout (``pack_mx`` / ``unpack_mx``) is this build's own
-format, not the reference's; its oracle is pinned by round trips against the
-GGUF blocks and the reference pool layout.
+The MI355X weight layouts (``pack_mx`` / ``unpack_mx``, and the native Q4_K
+``pack_mxk_*`` / ``unpack_mxk``) are this build's own formats, not the
+reference's; their oracles are pinned by round trips against the GGUF blocks
+and the reference pool and chunk layouts (``dequant_mxk`` of a packed GGUF
+matrix equals ``dequant_q4_k``, which the reference's C++ reader pins; of packed
+container chunks, the f32 rounding of ``dequant_q4k_chunks_exact``).
 """
 from __future__ import annotations
 
@@ -617,6 +622,132 @@ def q4k_vector(nch: int) -> np.ndarray:
         sm = np.concatenate([0x3B00 | stream[4608:4640], 0xBB00 | stream[4640:4672]]).astype(np.uint16)
         out[c, 4608:] = sm.view(np.uint8)
     return out
+
+
+# --------------------------------------------------------------------------
+# The native Q4_K layout ("mxk", this build's own format)
+# --------------------------------------------------------------------------
+#
+# An [N, K] matrix (N % 64 == 0, K % 256 == 0) is a grid of tiles (g, sb): row group
+# g = n // 64, super-block sb = k // 256, 9728 bytes at (g * K/256 + sb) * 9728:
+#   codes [0, 8192): sub-block j = 0..7 at j * 1024 in the mx code layout above;
+#   sc/mn [8192, 9216): row 16 r + i at 8192 + i * 64 + r * 16: sc[0..7] of its 8
+#         sub-blocks, then mn[0..7];
+#   d     [9216, 9472): f32 of row 16 r + i at 9216 + i * 16 + r * 4;  m at 9472 + ...
+# weight = fl32(q * (d sc) + m mn); d sc and m mn are exact in f32.
+
+MXK_TILE = 9728
+
+
+def mxk_bytes(n: int, k: int) -> int:
+    assert n % MX_ROWS == 0 and k % 256 == 0
+    return (n // MX_ROWS) * (k // 256) * MXK_TILE
+
+
+def pack_mxk_from_parts(d: np.ndarray, m: np.ndarray, sc: np.ndarray, mn: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """(f32 d [N, K/256], f32 m [N, K/256], uint8 sc [N, K/256, 8], uint8 mn, codes uint8[N, K])
+    -> native Q4_K layout bytes."""
+    n, SB = d.shape
+    assert n % MX_ROWS == 0 and q.shape == (n, SB * 256) and sc.shape == (n, SB, 8) == mn.shape
+    G = n // MX_ROWS
+    nb = SB * 8
+    q5 = q.reshape(n, nb, 4, 8).astype(np.uint32)
+    dw = np.zeros((n, nb, 4), np.uint32)                                   # [n, kb, kg]
+    for e in range(8):
+        dw |= q5[..., e] << np.uint32(_NIB_SHIFT[e])
+    codes = dw.reshape(G, 4, 16, SB, 8, 4).transpose(0, 3, 4, 5, 2, 1)    # [G, sb, j, kg, i, r]
+    pair = np.concatenate([sc, mn], axis=2).astype(np.uint8)              # [n, sb, 16]
+    pair = pair.reshape(G, 4, 16, SB, 16).transpose(0, 3, 2, 1, 4)        # [G, sb, i, r, 16]
+    dd = np.asarray(d, np.float32).reshape(G, 4, 16, SB).transpose(0, 3, 2, 1)   # [G, sb, i, r]
+    mm = np.asarray(m, np.float32).reshape(G, 4, 16, SB).transpose(0, 3, 2, 1)
+    out = np.empty((G, SB, MXK_TILE), np.uint8)
+    out[:, :, :8192] = np.ascontiguousarray(codes).view(np.uint8).reshape(G, SB, 8192)
+    out[:, :, 8192:9216] = np.ascontiguousarray(pair).view(np.uint8).reshape(G, SB, 1024)
+    out[:, :, 9216:9472] = np.ascontiguousarray(dd).view(np.uint8).reshape(G, SB, 256)
+    out[:, :, 9472:] = np.ascontiguousarray(mm).view(np.uint8).reshape(G, SB, 256)
+    return out.reshape(-1)
+
+
+def unpack_mxk(packed: np.ndarray, n: int, k: int):
+    """Native Q4_K layout bytes -> (d f32[n, k/256], m f32, sc uint8[n, k/256, 8], mn, q uint8[n, k])."""
+    G, SB = n // MX_ROWS, k // 256
+    t = np.asarray(packed, np.uint8).reshape(G, SB, MXK_TILE)
+    codes = np.ascontiguousarray(t[:, :, :8192]).view(np.uint32).reshape(G, SB, 8, 4, 16, 4)  # [G,sb,j,kg,i,r]
+    dw = codes.transpose(0, 5, 4, 1, 2, 3).reshape(n, SB * 8, 4)                              # [n, kb, kg]
+    q = np.empty((n, SB * 8, 4, 8), np.uint8)
+    for e in range(8):
+        q[..., e] = (dw >> np.uint32(_NIB_SHIFT[e])) & np.uint32(0xF)
+    pair = t[:, :, 8192:9216].reshape(G, SB, 16, 4, 16).transpose(0, 3, 2, 1, 4).reshape(n, SB, 16)  # [n,sb,16]
+    d = np.ascontiguousarray(t[:, :, 9216:9472]).view(np.float32).reshape(G, SB, 16, 4).transpose(0, 3, 2, 1)
+    m = np.ascontiguousarray(t[:, :, 9472:]).view(np.float32).reshape(G, SB, 16, 4).transpose(0, 3, 2, 1)
+    return (d.reshape(n, SB), m.reshape(n, SB), np.ascontiguousarray(pair[:, :, :8]),
+            np.ascontiguousarray(pair[:, :, 8:]), q.reshape(n, k))
+
+
+def dequant_mxk(packed: np.ndarray, n: int, k: int) -> np.ndarray:
+    """Native Q4_K layout -> f32[n, k] = fl32(q * (d sc) + m mn), d sc and m mn exact in f32."""
+    d, m, sc, mn, q = unpack_mxk(packed, n, k)
+    D = (d[:, :, None] * sc.astype(np.float32)).reshape(n, -1)
+    M = (m[:, :, None] * mn.astype(np.float32)).reshape(n, -1)
+    return q.astype(np.float32) * np.repeat(D, BLK, axis=1) + np.repeat(M, BLK, axis=1)
+
+
+def q4_k_native_parts(blocks: np.ndarray):
+    """GGUF Q4_K [N, K/256, 144] -> the native layout's parts: d = fp16 d, m = -fp16 dmin,
+    (sc_j, mn_j) = the packed 6-bit pairs (gguf_ref.py:224-250; get_scale_min_k4), codes."""
+    b = np.asarray(blocks, np.uint8)
+    n, ns, width = b.shape
+    if width != Q4_K_BYTES:
+        raise ValueError(f"block width {width} is not Q4_K ({Q4_K_BYTES})")
+    d = np.ascontiguousarray(b[..., 0:2]).view(np.float16).reshape(n, ns).astype(np.float32)
+    dmin = np.ascontiguousarray(b[..., 2:4]).view(np.float16).reshape(n, ns).astype(np.float32)
+    sc = np.empty((n, ns, 8), np.uint8)
+    mn = np.empty((n, ns, 8), np.uint8)
+    q = np.empty((n, ns, 8, BLK), np.uint8)
+    for j in range(8):
+        s6, m6 = q4_k_scale_min(b[..., 4:16], j)
+        sc[..., j], mn[..., j] = s6, m6
+        half = b[..., 16 + 32 * (j // 2):16 + 32 * (j // 2) + 32]
+        q[..., j, :] = (half >> 4) if j % 2 else (half & 0xF)
+    return d, -dmin, sc, mn, q.reshape(n, ns * 256)
+
+
+def pack_mxk_q4_k(blocks: np.ndarray) -> np.ndarray:
+    """GGUF Q4_K super-blocks -> native Q4_K layout bytes (no rounding of any value)."""
+    return pack_mxk_from_parts(*q4_k_native_parts(blocks))
+
+
+def q4k_chunks_native_parts(chunks: np.ndarray, n: int, k: int, rs: int):
+    """Container Q4_K chunks (4736 B, band order with row split rs) -> the native layout's
+    parts in [n, k] order: d = bf16 S[r], m = bf16 M[r] (stored negated), (sc, mn) =
+    (scales[g][r], mins[g][r]), codes (row r of column kk at byte 512 + 16 kk + r // 2,
+    even r low nibble) -- the chunk's own value S sc nib + M mn (gemm_q4.h:456-507)."""
+    nch, _, rows0, cols0 = chunk_geometry(n, k, rs)
+    src = np.asarray(chunks, np.uint8).reshape(nch, Q4K_CHUNK)
+    SB = k // 256
+    d = np.empty((n, SB), np.float32)
+    m = np.empty((n, SB), np.float32)
+    sc = np.empty((n, SB, 8), np.uint8)
+    mn = np.empty((n, SB, 8), np.uint8)
+    q = np.empty((n, k), np.uint8)
+    r = np.arange(32)
+    for c in range(nch):
+        r0, c0 = int(rows0[c]), int(cols0[c])
+        sb = c0 // 256
+        ch = src[c]
+        d[r0:r0 + 32, sb] = bf16_to_f32(np.ascontiguousarray(ch[4608:4672]).view(np.uint16))
+        m[r0:r0 + 32, sb] = bf16_to_f32(np.ascontiguousarray(ch[4672:4736]).view(np.uint16))
+        sc[r0:r0 + 32, sb, :] = ch[0:256].reshape(8, 32).T
+        mn[r0:r0 + 32, sb, :] = ch[256:512].reshape(8, 32).T
+        cb = ch[512:4608].reshape(256, 16)                                     # [kk, r // 2]
+        nib = np.where(r % 2 == 0, cb[:, r // 2] & 0xF, cb[:, r // 2] >> 4)    # [kk, r]
+        q[r0:r0 + 32, c0:c0 + 256] = nib.T
+    return d, m, sc, mn, q
+
+
+def pack_mxk_q4k_chunks(chunks: np.ndarray, n: int, k: int, rs: int) -> np.ndarray:
+    """Container Q4_K chunks -> native Q4_K layout bytes (no rounding of any value)."""
+    return pack_mxk_from_parts(*q4k_chunks_native_parts(chunks, n, k, rs))
 
 
 def fnv1a64(data) -> int:

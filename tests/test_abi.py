@@ -160,3 +160,23 @@ def test_loader_fails_loudly_without_the_library(tmp_path):
     L = import_module("openflowlm-next_amd._lib")
     with pytest.raises(ImportError):
         L.load(tmp_path / "libq4mi.so")
+
+
+def test_native_q4k_argument_errors(lib):
+    """The native Q4_K entry points validate before any launch, like the others."""
+    fake = C.c_void_p(0x1000)
+    assert lib.q4_q4k_packed_bytes(64, 256) == 9728
+    assert lib.q4_q4k_packed_bytes(64, 128) == -1 and lib.q4_q4k_packed_bytes(32, 256) == -1
+    assert lib.q4_repack_q4k_native(fake, fake, 64, 128, None) == -1           # K % 256
+    assert lib.q4_repack_q4k_native(None, fake, 64, 256, None) == -2           # NULL
+    assert lib.q4_repack_q4k_native(None, None, 0, 256, None) == 0             # empty
+    assert lib.q4_repack_q4k_chunks_native(fake, 0, fake, 64, 256, None) == -2 # rs
+    assert lib.q4_repack_q4k_chunks_native(fake, 4, fake, 64, 256, None) == -1 # N % (32 rs)
+    assert lib.q4_dequant_q4k(fake, C.c_void_p(0x1004), 64, 256, None) == -2   # misaligned
+    assert lib.q4_gemv_q4k(fake, fake, 1, None, fake, 1, 64, 128, None, 0, None) == -1   # K % 256
+    assert lib.q4_gemv_q4k(fake, fake, 1, None, fake, 17, 64, 256, None, 0, None) == -5  # M > 16
+    assert lib.q4_gemv_q4k(fake, fake, 2, None, fake, 1, 64, 256, None, 0, None) == -2   # dtype
+    need = lib.q4_gemv_q4k_workspace_bytes(1, 256, 14336)
+    assert need > 0
+    assert lib.q4_gemv_q4k(fake, fake, 1, None, fake, 1, 256, 14336, fake, need - 1, None) == -3
+    assert lib.q4_gemv_q4k_workspace_bytes(1, 128256, 4096) == 0
