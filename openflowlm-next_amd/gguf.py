@@ -178,9 +178,11 @@ class GGUFFile:
             raise GGUFError(f"{name!r} is {t.type_name}; use blocks() or packed()")
         return a.reshape(t.shape)
 
-    def packed(self, name: str, device=None):
+    def packed(self, name: str, device=None, q4k: str = "mx"):
         """A Q4_0 / Q4_1 / Q4_K weight [N, K] (N % 64 == 0) packed for the kernels on the GPU
-        (a PackedQ4), or a Q8_0 one as the exact q8 pair (a PackedQ8, for gemm_q8)."""
+        (a PackedQ4), or a Q8_0 one as the exact q8 pair (a PackedQ8, for gemm_q8). A Q4_K
+        weight goes to the mx layout (``q4k="mx"``: d sc and m mn rounded to bf16, for every
+        kernel) or stays Q4_K (``q4k="native"``: a PackedQ4K for gemm_q4k, exact)."""
         from . import q4                                  # needs the HIP library: imported on use
         t = self.tensor(name)
         if t.type_name not in Q4_TYPES | {"Q8_0"}:
@@ -190,7 +192,11 @@ class GGUFFile:
         b = self.blocks(name)
         if t.type_name == "Q8_0":
             return q4.pack_q8(b, t.shape[0], t.shape[1], fmt="q8_0", device=device)
-        return q4.pack_q4_k(b, device) if t.type_name == "Q4_K" else q4.pack_q4_1(b, device)
+        if t.type_name == "Q4_K":
+            if q4k not in ("mx", "native"):
+                raise ValueError(f"q4k must be 'mx' or 'native', got {q4k!r}")
+            return q4.pack_q4_k_native(b, device) if q4k == "native" else q4.pack_q4_k(b, device)
+        return q4.pack_q4_1(b, device)
 
     # ---- lifetime -----------------------------------------------------
     def close(self):

@@ -131,11 +131,13 @@ class Q4NXFile:
             raise Q4NXError(f"{name!r} is {t['dtype']}; use packed() for quantised matrices")
         return a.reshape(t["shape"])
 
-    def packed(self, name: str, out_dim: int, in_dim: int, device=None, q8: str = "requant"):
+    def packed(self, name: str, out_dim: int, in_dim: int, device=None, q8: str = "requant", q4k: str = "mx"):
         """A quantised matrix [out_dim, in_dim] (out_dim % 64 == 0, in_dim % 256 == 0)
         transcoded into the mx layout on the GPU, from its chunks as they lie in the file.
         A q8 tensor is re-quantised to q4_1 (``q8="requant"``, the reference packer's
-        default) or kept exact as the hi/lo pair (``q8="exact"``, a PackedQ8 for gemm_q8)."""
+        default) or kept exact as the hi/lo pair (``q8="exact"``, a PackedQ8 for gemm_q8).
+        A Q4_K tensor is collapsed to q4_1 (``q4k="mx"``, recipes/pack.py:266-310) or kept
+        as Q4_K (``q4k="native"``, a PackedQ4K for gemm_q4k, the chunk's exact value)."""
         from . import q4                                 # needs the HIP library: imported on use
         fmt = self.quant_format_of(name)
         if not fmt:
@@ -151,6 +153,10 @@ class Q4NXFile:
             return q4.pack_q8(raw, out_dim, in_dim, fmt="chunks", rs=1, device=device)
         if q8 not in ("requant", "exact"):
             raise ValueError(f"q8 must be 'requant' or 'exact', got {q8!r}")
+        if q4k not in ("mx", "native"):
+            raise ValueError(f"q4k must be 'mx' or 'native', got {q4k!r}")
+        if fmt == "q4_k" and q4k == "native":
+            return q4.pack_q4_k_chunks_native(raw, out_dim, in_dim, rs=1, device=device)
         return q4.pack_chunks(raw, fmt, out_dim, in_dim, rs=1, device=device)
 
     # ---- lifetime -----------------------------------------------------

@@ -102,3 +102,34 @@ def test_gemv_is_deterministic_across_splits(gpu, pkg, oracle):
     a = pkg.gemm_q4k(w, x).cpu()
     for _ in range(3):
         assert torch.equal(a, pkg.gemm_q4k(w, x).cpu())
+
+
+def test_file_readers_keep_q4k_native(gpu, pkg, oracle, tmp_path):
+    """GGUFFile.packed(..., q4k="native") and Q4NXFile.packed(..., q4k="native") hand the
+    file's own Q4_K bytes to the native repack: the oracle's bytes, and a GEMV at the bar."""
+    from gguf_writer import STR, write_gguf
+    from q4nx_writer import write_q4nx
+    say("q4k native from gguf / q4nx files")
+    rng = np.random.default_rng(23)
+    n, k = 256, 1024
+    blocks = oracle.random_q4_k_blocks(n, k, rng)
+    pg = tmp_path / "m.gguf"
+    write_gguf(pg, [("blk.0.ffn_gate.weight", "Q4_K", (n, k), blocks)], [("general.architecture", STR, "llama")])
+    nch = (n // 32) * (k // 256)
+    chunks = oracle.q4k_vector(nch)
+    pq = tmp_path / "m.q4nx"
+    write_q4nx(pq, [("d", "I8", (nch, 4736), chunks)])
+    with pkg.GGUFFile(pg) as f:
+        wg = f.packed("blk.0.ffn_gate.weight", gpu, q4k="native")
+        with pytest.raises(ValueError):
+            f.packed("blk.0.ffn_gate.weight", gpu, q4k="bogus")
+    with pkg.Q4NXFile(pq) as f:
+        wq = f.packed("d", n, k, gpu, q4k="native")
+    torch.cuda.synchronize()
+    assert isinstance(wg, pkg.PackedQ4K) and isinstance(wq, pkg.PackedQ4K)
+    assert np.array_equal(wg.data.cpu().numpy(), oracle.pack_mxk_q4_k(blocks))
+    assert np.array_equal(wq.data.cpu().numpy(), oracle.pack_mxk_q4k_chunks(chunks, n, k, 1))
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    for w, wt in ((wg, oracle.dequant_q4_k(blocks)), (wq, oracle.dequant_mxk(oracle.pack_mxk_q4k_chunks(chunks, n, k, 1), n, k))):
+        y = pkg.gemm_q4k(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
+        assert oracle.maxrel(y, x.astype(np.float64) @ wt.astype(np.float64).T) <= MAXREL
