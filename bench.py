@@ -379,9 +379,10 @@ def extra_ffn(torch, q4, model, acts):
 
 
 def extra_q8(torch, q4, dev):
-    """The q8 GEMV (exact hi/lo planes, one launch) at M=1 on the Llama-3-8B gate_up and
-    lm_head shapes, graph-timed over 8 rotating copies (the set exceeds the caches):
-    bytes = both planes + bf16 x + f32 y; and the same weights requantised to q4_1."""
+    """The q8 GEMV at M=1 on the Llama-3-8B gate_up and lm_head shapes, graph-timed over
+    rotating copies (the set exceeds the caches): the exact hi/lo planes in one launch
+    (bytes = both planes + bf16 x + f32 y) and the native mx8 layout (its own bytes), the
+    same values s * q either way."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED + 13)
     out = {}
@@ -391,7 +392,9 @@ def extra_q8(torch, q4, dev):
         d = (torch.randn(n, k // 32, generator=gen, device=dev).abs() * 0.002 + 1e-4).to(torch.float16)
         blocks[..., 0:2] = d.view(torch.uint8).view(n, k // 32, 2)
         blocks[..., 2:] = torch.randint(0, 256, (n, k // 32, 32), generator=gen, device=dev, dtype=torch.uint8)
-        ws = [q4.pack_q8(blocks, n, k, "q8_0", device=dev) for _ in range(2 if n > 100000 else 8)]
+        copies = 2 if n > 100000 else 8
+        ws = [q4.pack_q8(blocks, n, k, "q8_0", device=dev) for _ in range(copies)]
+        wn = [q4.pack_q8_native(blocks, n, k, "q8_0", device=dev) for _ in range(copies)]
         del blocks
         x = torch.randn(1, k, generator=gen, device=dev).to(torch.bfloat16)
         y = torch.empty(1, n, dtype=torch.float32, device=dev)
@@ -400,11 +403,17 @@ def extra_q8(torch, q4, dev):
         def run():
             for w in ws:
                 q4.gemm_q8(w, x, y, workspace=wsp)
-        ms = graph_time(torch, run, [y], replays=10) / len(ws)
-        nbytes = ws[0].nbytes + k * 2 + n * 4
-        out[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2), "gbs": round(nbytes / ms / 1e6, 1),
-                     "q8_equivalent_gbs": round((nb * 34 + k * 2 + n * 4) / ms / 1e6, 1)}
-        del ws
+
+        def run_native():
+            for w in wn:
+                q4.gemm_q8_native(w, x, y, workspace=wsp)
+        ms = graph_time(torch, run, [y], replays=10) / copies
+        ms_n = graph_time(torch, run_native, [y], replays=10) / copies
+        io = k * 2 + n * 4
+        out[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2), "gbs": round((ws[0].nbytes + io) / ms / 1e6, 1),
+                     "q8_equivalent_gbs": round((nb * 34 + io) / ms / 1e6, 1),
+                     "native_us": round(ms_n * 1e3, 2), "native_gbs": round((wn[0].nbytes + io) / ms_n / 1e6, 1)}
+        del ws, wn
         torch.cuda.empty_cache()
     return out
 

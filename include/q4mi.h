@@ -209,6 +209,31 @@ int q4_gemv_q8(const uint8_t* hi, const uint8_t* lo, const void* x, int x_dtype,
                const float* residual, float* y, int M, int64_t N, int64_t K,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Native q8 ("mx8" layout): a 64-row x 32-K tile is 2176 bytes, the 8-bit codes as
+ * b = q + 128 plus one bf16 scale per row (1.0625 bytes per weight, GGUF Q8_0's density,
+ * against the split pair's 1.25). Weight = s * q, exact: the same values as the split's
+ * hi + lo planes. The counterpart of the reference's q8 GEMV (designs/gemv_q4/gemv_q8.h,
+ * designs/lm_head_q8). Bytes of an [N, K] matrix (N % 64 == 0, K % 32 == 0), or -1: */
+int64_t q4_q8_native_packed_bytes(int64_t N, int64_t K);
+
+/* q8 weights -> mx8, on the device; src_format and rs as q4_repack_q8_split (0: 8704-byte
+ * chunks, 1: GGUF Q8_0 blocks, 2: the GGUF-direct pool's 9216-byte chunks), scales
+ * narrowed to bf16 as there. */
+int q4_repack_q8_native(const uint8_t* src, int src_format, int rs, uint8_t* packed,
+                        int64_t N, int64_t K, void* stream);
+
+/* mx8 -> f32 [N][K] row-major, w = s * q (exact). */
+int q4_dequant_q8_native(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
+
+/* Workspace bytes q4_gemv_q8_native needs (0 if none; the same as q4_gemv's). */
+size_t q4_gemv_q8_native_workspace_bytes(int M, int64_t N, int64_t K);
+
+/* Y[M][N] = X[M][K] . W^T over an mx8 matrix, 1 <= M <= 16, fp32 accumulate, plus
+ * residual (f32 [M][N], may be y) when not NULL. Per 64 x 32 tile one code load feeds two
+ * MFMAs per row tile on the code's nibble planes; acc += s (16 P_hi + P_lo) - 128 s sum x. */
+int q4_gemv_q8_native(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
+                      int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes q4_gemv_swiglu needs for (M, F, K); 0 when it needs none. */
 size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K);
 

@@ -105,6 +105,26 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(GemvParams P) {
     else gemv_finish<NTL>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
 
+// The GEMV over the native q8 layout: the same work items, splits and stores as gemv_kernel.
+template <int NTL, bool XF32>
+__global__ __launch_bounds__(256) void q8n_gemv_kernel(GemvParams P) {
+    __shared__ float red[kWaves][4][NTL][64];
+    const int64_t item = blockIdx.x;
+    const int S = P.S;
+    const int64_t g = item / S;
+    const int s = (int)(item % S);
+    const int KB = (int)(P.K >> 5);
+    const int kb0 = (int)((int64_t)s * KB / S), kb1 = (int)((int64_t)(s + 1) * KB / S);
+    float acc[4][NTL];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
+    q8n_rows<NTL, XF32>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
+    if (S == 1) gemv_finish<NTL>(acc, red, P.M, P.y, P.N, g, P.res);
+    else gemv_finish<NTL>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
+}
+
 // The q8 GEMV as two q4_1 planes (hi, lo) of one matrix: one workgroup streams row group
 // g of both (sharing the activation fragments) and stores y = hi . x + lo . x (S == 1, plus
 // the residual when one is given) or this split's partial of that sum.
@@ -324,6 +344,12 @@ void launch_q4k(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
 }
 
 template <int NTL>
+void launch_q8n(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (xf32) hipLaunchKernelGGL((q8n_gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
+    else hipLaunchKernelGGL((q8n_gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
+}
+
+template <int NTL>
 void launch_grouped(bool xf32, dim3 grid, hipStream_t st, const q4_gemv_desc* d, int count, int M) {
     if (xf32) hipLaunchKernelGGL((gemv_grouped_kernel<NTL, true>), grid, dim3(256), 0, st, d, count, M);
     else hipLaunchKernelGGL((gemv_grouped_kernel<NTL, false>), grid, dim3(256), 0, st, d, count, M);
@@ -511,6 +537,50 @@ extern "C" int q4_gemv_q4k(const uint8_t* packed, const void* x, int x_dtype, co
         case 2: launch_q4k<2>(xf32, grid, st, P); break;
         case 3: launch_q4k<3>(xf32, grid, st, P); break;
         default: launch_q4k<4>(xf32, grid, st, P); break;
+    }
+    if (S > 1) {
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        const int64_t MN = (int64_t)M * N;
+        hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)ceil_div(MN, 256)), dim3(256), 0, st, P.part, y, MN,
+                           S, residual);
+    }
+    return launch_status();
+}
+
+extern "C" size_t q4_gemv_q8_native_workspace_bytes(int M, int64_t N, int64_t K) {
+    return q4_gemv_workspace_bytes(M, N, K);
+}
+
+extern "C" int q4_gemv_q8_native(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
+                                 int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (M < 0 || M > 16) return Q4MI_E_RANGE;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    if (M == 0 || N == 0) return Q4MI_OK;
+    if (!packed || !x || !y) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
+    const int S = choose_splits(N, K);
+    GemvParams P{};
+    P.packed = packed;
+    P.x = x;
+    P.y = y;
+    P.M = M;
+    P.S = S;
+    P.N = N;
+    P.K = K;
+    P.res = residual;
+    if (S > 1) {
+        if (!workspace || workspace_bytes < workspace_for(M, N, K, S)) return Q4MI_E_WORKSPACE;
+        P.part = (float*)workspace;
+    }
+    const dim3 grid((unsigned)((N / 64) * S));
+    const hipStream_t st = (hipStream_t)stream;
+    const bool xf32 = x_dtype == Q4MI_F32;
+    switch ((M + 3) / 4) {
+        case 1: launch_q8n<1>(xf32, grid, st, P); break;
+        case 2: launch_q8n<2>(xf32, grid, st, P); break;
+        case 3: launch_q8n<3>(xf32, grid, st, P); break;
+        default: launch_q8n<4>(xf32, grid, st, P); break;
     }
     if (S > 1) {
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;

@@ -189,6 +189,77 @@ __device__ __forceinline__ void q4k_rows(const uint8_t* __restrict__ packed, con
     }
 }
 
+// gemv_rows over the native q8 layout (kQ8TileBytes tiles). Each code byte b = q + 128
+// splits into nibbles, q = 16 hi + lo - 128; per row tile two MFMAs on the nibble planes
+// (the bf16 128 + nibble trick, offset taken out by the -128 sum x C input) give
+// P_hi = sum hi x and P_lo = sum lo x, and acc += s (16 P_hi + P_lo) - 128 s sum x.
+template <int NTL, bool XF32, class Rows>
+__device__ __forceinline__ void q8n_rows(const uint8_t* __restrict__ packed, const void* __restrict__ x, Rows rows,
+                                         int64_t K, int64_t g, int kb0, int kb1, float (&acc)[4][NTL]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kb0 = __builtin_amdgcn_readfirstlane(kb0);
+    kb1 = __builtin_amdgcn_readfirstlane(kb1);
+    const int i16 = lane & 15, kg = lane >> 4;
+    const int64_t KB = K >> 5;
+    const uint8_t* gbase = packed + g * KB * kQ8TileBytes;
+    const int coff = lane * 16, soff = kQ8ScaleOff + i16 * 8;
+    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const CodeConsts kc = code_consts();
+    const int64_t xrow = rows(token_of_row(i16));
+
+    for (int kb = kb0 + wave; kb < kb1; kb += kWaves * kUnroll) {
+        u32x4 c[kUnroll][2];
+        u32x2 sv[kUnroll];
+        bf16x8 xh[kUnroll], xl[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int t = min(kb + kWaves * u, kb1 - 1);
+            const uint8_t* tp = gbase + (int64_t)t * kQ8TileBytes;              // wave-uniform
+            c[u][0] = load_nt_u32x4(tp + coff);
+            c[u][1] = load_nt_u32x4(tp + coff + 1024);
+            sv[u] = load_nt_u32x2(tp + soff);
+            load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (kb + kWaves * u < kb1) {
+                f32x4 ns = mfma_bf16(xh[u], neg128, zero4);
+                if constexpr (XF32) ns = mfma_bf16(xl[u], neg128, ns);
+                float sx[NTL];
+#pragma unroll
+                for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t w0 = c[u][r >> 1][2 * (r & 1)], w1 = c[u][r >> 1][2 * (r & 1) + 1];
+                    const bf16x8 blo = __builtin_bit_cast(bf16x8, u32x4{(w0 & kc.nib2) | kc.magic,
+                                                                        ((w0 >> 8) & kc.nib2) | kc.magic,
+                                                                        (w1 & kc.nib2) | kc.magic,
+                                                                        ((w1 >> 8) & kc.nib2) | kc.magic});
+                    const bf16x8 bhi = __builtin_bit_cast(bf16x8, u32x4{((w0 >> 4) & kc.nib2) | kc.magic,
+                                                                        ((w0 >> 12) & kc.nib2) | kc.magic,
+                                                                        ((w1 >> 4) & kc.nib2) | kc.magic,
+                                                                        ((w1 >> 12) & kc.nib2) | kc.magic});
+                    f32x4 plo = mfma_bf16(xh[u], blo, ns), phi = mfma_bf16(xh[u], bhi, ns);
+                    if constexpr (XF32) {
+                        plo = mfma_bf16(xl[u], blo, plo);
+                        phi = mfma_bf16(xl[u], bhi, phi);
+                    }
+                    const float s = __builtin_bit_cast(float, (sv[u][r >> 1] >> (16 * (r & 1))) << 16);
+                    const float ms = -128.0f * s;
+#pragma unroll
+                    for (int j = 0; j < NTL; ++j) {
+                        const float t16 = __builtin_fmaf(16.0f, phi[j], plo[j]);
+                        acc[r][j] = __builtin_fmaf(s, t16, acc[r][j]);
+                        acc[r][j] = __builtin_fmaf(ms, sx[j], acc[r][j]);
+                    }
+                }
+            }
+        }
+    }
+}
+
 // gemv_rows over NG row groups at once (tile bases gbase[i], same K range and
 // activations): per K position the activation fragment and the -128 sum x
 // MFMA are shared by the NG groups, and NG x UNR tiles are in flight per wave.

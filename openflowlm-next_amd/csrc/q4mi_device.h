@@ -30,6 +30,18 @@ namespace q4mi {
 constexpr int kKTileBytes = 9728;
 constexpr int kKScOff = 8192, kKDOff = 9216, kKMOff = 9472;
 
+// The native q8 ("mx8") layout of an [N, K] matrix (N % 64 == 0, K % 32 == 0): tile
+// (g, kb) = 64 rows x 32 K, 2176 B, at byte (g * K/32 + kb) * 2176:
+//   codes [0, 2048): lane (kg * 16 + i16) holds at (r / 2) * 1024 + lane * 16 + (r % 2) * 8
+//         the 8 codes of row 16 r + i16 at k = 32 kb + 8 kg + 0..7 as unsigned bytes
+//         b = q + 128, each dword in the order (k0, k2, k1, k3) so that masking nibble
+//         pairs out of it yields consecutive k (one 16-byte load per lane covers rows r and
+//         r + 1 and a wave's load is 1 KB contiguous);
+//   scale [2048, 2176): bf16 s of row 16 r + i16 at 2048 + i16 * 8 + r * 2.
+// Weight = s * q, exact in f32 (8-bit x 8-bit). 1.0625 bytes per weight, as GGUF Q8_0.
+constexpr int kQ8TileBytes = 2176;
+constexpr int kQ8ScaleOff = 2048;
+
 constexpr int kRows = 64;        // rows per tile / row group
 constexpr int kBlk = 32;         // K per tile (one GGUF block)
 constexpr int kTileBytes = 1280;

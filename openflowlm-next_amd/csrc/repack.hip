@@ -371,16 +371,10 @@ __global__ __launch_bounds__(256) void repack_q8_chunk_kernel(const uint8_t* __r
 // blocks (src_format 1: fp16 d then 32 int8, 34 B per 32 K; s = RNE_bf16(d), the same
 // narrowing the Q4_1 blocks get) or the GGUF-direct pool's 9216 B q8 chunks (src_format
 // 2: f32 scales[256] @0, codes @1024; s = RNE_bf16(scale); gguf_pool.py:28-33).
-__global__ __launch_bounds__(256) void repack_q8_split_kernel(const uint8_t* __restrict__ src, int src_format,
-                                                              int rs, int part, uint8_t* __restrict__ packed,
-                                                              int64_t N, int64_t KB) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= N * KB) return;
-    const int64_t tile = idx >> 6;
-    const int64_t n = (tile / KB) * 64 + (idx & 63);
-    const int64_t kb = tile % KB;
-    uint32_t s16;
-    int8_t q[32];
+// One q8 block (row n, 32-K block kb) of any of the three sources: its bf16 scale bits
+// and its 32 signed codes.
+__device__ __forceinline__ void q8_source_block(const uint8_t* __restrict__ src, int src_format, int rs, int64_t n,
+                                                int64_t kb, int64_t KB, uint32_t& s16, int8_t (&q)[32]) {
     if (src_format != 1) {
         const bool f32s = src_format == 2;
         const uint8_t* ch = src + band_chunk(n, kb, rs, KB * 32) * (f32s ? 9216 : 8704);
@@ -395,6 +389,19 @@ __global__ __launch_bounds__(256) void repack_q8_split_kernel(const uint8_t* __r
 #pragma unroll
         for (int i = 0; i < 32; ++i) q[i] = (int8_t)b[2 + i];
     }
+}
+
+__global__ __launch_bounds__(256) void repack_q8_split_kernel(const uint8_t* __restrict__ src, int src_format,
+                                                              int rs, int part, uint8_t* __restrict__ packed,
+                                                              int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    uint32_t s16;
+    int8_t q[32];
+    q8_source_block(src, src_format, rs, n, kb, KB, s16, q);
     const float sv = bf16_hi_to_f32(s16 << 16);
     uint8_t code[32];
     uint32_t word;
@@ -408,6 +415,59 @@ __global__ __launch_bounds__(256) void repack_q8_split_kernel(const uint8_t* __r
         word = s16 << 16;
     }
     mx_write_block(packed, KB, n, kb, code, word);
+}
+
+// The same q8 sources -> the native q8 layout (q4mi_device.h), one thread per (row, 32-K
+// block): codes as b = q + 128, bytes of each dword in the order (k0, k2, k1, k3), and
+// the bf16 scale as the split planes take it.
+__global__ __launch_bounds__(256) void repack_mx8_kernel(const uint8_t* __restrict__ src, int src_format, int rs,
+                                                         uint8_t* __restrict__ packed, int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    uint32_t s16;
+    int8_t q[32];
+    q8_source_block(src, src_format, rs, n, kb, KB, s16, q);
+    const int i = (int)(n & 63), r = i >> 4, i16 = i & 15;
+    uint8_t* t = packed + ((n >> 6) * KB + kb) * kQ8TileBytes;
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k0 = 8 * kg + 4 * h;
+            const uint32_t b0 = (uint8_t)q[k0] ^ 0x80u, b1 = (uint8_t)q[k0 + 1] ^ 0x80u;
+            const uint32_t b2 = (uint8_t)q[k0 + 2] ^ 0x80u, b3 = (uint8_t)q[k0 + 3] ^ 0x80u;
+            *(uint32_t*)(t + (r >> 1) * 1024 + (kg * 16 + i16) * 16 + (r & 1) * 8 + h * 4) =
+                b0 | (b2 << 8) | (b1 << 16) | (b3 << 24);
+        }
+    *(uint16_t*)(t + kQ8ScaleOff + i16 * 8 + r * 2) = (uint16_t)s16;
+}
+
+// mx8 -> f32, w = s * q (exact). One thread per 8 consecutive k of a row.
+__global__ __launch_bounds__(256) void dequant_mx8_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
+                                                          int64_t N, int64_t K) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t K8 = K >> 3;
+    if (idx >= N * K8) return;
+    const int64_t n = idx / K8, k8 = idx % K8;
+    const int64_t kb = k8 >> 2;
+    const int kg = (int)(k8 & 3), i = (int)(n & 63), r = i >> 4, i16 = i & 15;
+    const uint8_t* t = packed + ((n >> 6) * (K >> 5) + kb) * kQ8TileBytes;
+    const u32x2 c = *(const u32x2*)(t + (r >> 1) * 1024 + (kg * 16 + i16) * 16 + (r & 1) * 8);
+    const float s = bf16_hi_to_f32((uint32_t)*(const uint16_t*)(t + kQ8ScaleOff + i16 * 8 + r * 2) << 16);
+    float o[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t d = c[h];
+        const int kx[4] = {0, 2, 1, 3};           // byte j holds k = kx[j]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[4 * h + kx[j]] = s * (float)((int)((d >> (8 * j)) & 0xFF) - 128);
+    }
+    f32x4* dst = (f32x4*)(w + n * K + k8 * 8);
+    dst[0] = f32x4{o[0], o[1], o[2], o[3]};
+    dst[1] = f32x4{o[4], o[5], o[6], o[7]};
 }
 
 // Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats.
@@ -594,6 +654,36 @@ extern "C" int q4_dequant_q4k(const uint8_t* packed, float* w, int64_t N, int64_
     if (N < 0 || K <= 0 || N % 64 || K % 256) return Q4MI_E_SHAPE;
     const int64_t total = N * (K / 8);
     hipLaunchKernelGGL(dequant_mxk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       packed, w, N, K);
+    return launch_status();
+}
+
+extern "C" int64_t q4_q8_native_packed_bytes(int64_t N, int64_t K) {
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return -1;
+    return (N / 64) * (K / 32) * (int64_t)kQ8TileBytes;
+}
+
+extern "C" int q4_repack_q8_native(const uint8_t* src, int src_format, int rs, uint8_t* packed, int64_t N, int64_t K,
+                                   void* stream) {
+    if (src_format < 0 || src_format > 2 || rs <= 0) return Q4MI_E_ARG;
+    const int64_t kmod = src_format == 1 ? 32 : 256;
+    if (N == 0 && K > 0 && K % kmod == 0) return Q4MI_OK;
+    if (!src || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed) || (src_format == 2 && ((uintptr_t)src & 3))) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % kmod || (src_format != 1 && N % (32 * rs))) return Q4MI_E_SHAPE;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_mx8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       src, src_format, rs, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_dequant_q8_native(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
+    if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;
+    if (!packed || !w) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(w)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    const int64_t total = N * (K / 8);
+    hipLaunchKernelGGL(dequant_mx8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        packed, w, N, K);
     return launch_status();
 }

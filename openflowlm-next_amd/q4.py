@@ -350,6 +350,89 @@ def pack_q8(src, n: int, k: int, fmt: str = "chunks", rs: int = 1, device=None) 
     return PackedQ8(*planes)
 
 
+@dataclass
+class PackedQ8N:
+    """A q8 matrix [n, k] in the native mx8 layout: 8-bit codes + a bf16 scale per row
+    and 32-K block, weight s * q exactly (1.0625 B per weight)."""
+    data: torch.Tensor
+    n: int
+    k: int
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+
+def pack_q8_native(src, n: int, k: int, fmt: str = "chunks", rs: int = 1, device=None) -> PackedQ8N:
+    """q8 weights (``fmt`` and ``rs`` as pack_q8) -> the native mx8 layout on the GPU: the
+    same values s * q as the exact hi/lo pair, at 1.0625 B per weight instead of 1.25."""
+    if fmt not in ("chunks", "q8_0", "chunks_f32"):
+        raise ValueError(f"fmt must be 'chunks', 'q8_0' or 'chunks_f32', got {fmt!r}")
+    dev = _device(device if device is not None else (src.device if isinstance(src, torch.Tensor)
+                                                     and src.is_cuda else None))
+    t = _to_dev(src, dev, torch.uint8).reshape(-1)
+    cb = {"chunks": 8704, "chunks_f32": 9216}.get(fmt)
+    want = ((n // 32) * (k // 256) * cb if n % 32 == 0 and k % 256 == 0 else -1) if cb \
+        else (n * (k // 32) * 34 if k % 32 == 0 else -1)
+    if t.numel() != want:
+        raise ValueError(f"{fmt} source holds {t.numel()} bytes, [{n}, {k}] needs {want}")
+    lib = _lib_handle()
+    nbytes = lib.q4_q8_native_packed_bytes(n, k)
+    if nbytes < 0:
+        raise ValueError(f"[{n}, {k}] does not fit the mx8 layout (n % 64 == 0, k % 32 == 0)")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_repack_q8_native", lib.q4_repack_q8_native(_ptr(t), {"chunks": 0, "q8_0": 1, "chunks_f32": 2}[fmt],
+                                                             rs, _ptr(out), n, k, _stream(dev)))
+    return PackedQ8N(out, n, k)
+
+
+def dequant_q8_native(w: PackedQ8N, out: torch.Tensor | None = None) -> torch.Tensor:
+    """mx8 -> f32[n, k], w = s * q (exact)."""
+    dev = w.device
+    if out is None:
+        out = torch.empty((w.n, w.k), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_dequant_q8_native", _lib_handle().q4_dequant_q8_native(_ptr(w.data), _ptr(out), w.n, w.k,
+                                                                         _stream(dev)))
+    return out
+
+
+def gemm_q8_native(w: PackedQ8N, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                   residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Y[M, N] = X[M, K] @ W^T over a native q8 matrix, 1 <= M <= 16 (the gemv_q8 sibling of
+    gemm_q4 on the mx8 layout); ``residual`` as in gemm_q4."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != w.k:
+        raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q8_native takes 1..16 tokens, got {M}")
+    if y is None:
+        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
+                                 or residual.numel() != M * w.n or residual.device != dev):
+        raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_q8_native_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        check("q4_gemv_q8_native", lib.q4_gemv_q8_native(_ptr(w.data), _ptr(xt), _x_dtype(xt),
+                                                         None if residual is None else _ptr(residual), _ptr(y),
+                                                         M, w.n, w.k, wp, wn, _stream(dev)))
+    return y
+
+
 _CHUNK_ENTRY = {   # chunk format -> (chunk bytes, C entry point)
     "q4_1": (5120, "q4_repack_pool"),
     "q4_f32": (6144, "q4_repack_pool_f32"),

@@ -23,6 +23,8 @@ this hot path (``/root/reference`` is read as text, never imported):
                                   src/gguf/gguf_file.cpp:611-635
 * container Q4_K -> q4_1 chunks   open_kernels/recipes/pack.py:266-310,
                                   src/open_qwen36/pools.cpp:642-663
+* native q8 values (s * q)        open_kernels/recipes/pack.py:94-117 (the split's sum),
+                                  open_kernels/designs/gemv_q4/gemv_q8.h
 * native Q4_K values              open_kernels/designs/gemm_q4/gemm_q4.h:456-507
   (value d sc nib + mcoef mn of the container chunk; d sc q - dmin min of GGUF)
 
@@ -961,6 +963,52 @@ def q8_split_parts(s16: np.ndarray, q: np.ndarray, part: int):
 def q8_values(s16: np.ndarray, q: np.ndarray) -> np.ndarray:
     """s * q in f64 per weight (exact)."""
     return np.repeat(bf16_to_f32(s16).astype(np.float64), BLK, axis=1) * np.asarray(q, np.float64)
+
+
+# The native q8 layout ("mx8", this build's own format): tile (g, kb) = 64 rows x 32 K,
+# 2176 bytes at (g * K/32 + kb) * 2176. Codes [0, 2048): lane l = kg * 16 + i holds at
+# (r // 2) * 1024 + l * 16 + (r % 2) * 8 the 8 codes of row 16 r + i, k = 32 kb + 8 kg +
+# 0..7, as b = q + 128, each dword's bytes in the k order (0, 2, 1, 3); scale
+# [2048, 2176): bf16 of row 16 r + i at 2048 + i * 8 + r * 2. Weight s * q.
+
+MX8_TILE = 2176
+_MX8_ORDER = np.array([0, 2, 1, 3, 4, 6, 5, 7])     # byte j of an 8-byte group holds k = _MX8_ORDER[j]
+
+
+def mx8_bytes(n: int, k: int) -> int:
+    assert n % MX_ROWS == 0 and k % BLK == 0
+    return (n // MX_ROWS) * (k // BLK) * MX8_TILE
+
+
+def pack_mx8_from_parts(s16: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """(bf16 scale bits [N, K/32], int8 codes [N, K]) -> native q8 layout bytes."""
+    n, nb = s16.shape
+    assert n % MX_ROWS == 0 and q.shape == (n, nb * BLK)
+    G = n // MX_ROWS
+    b = (np.asarray(q, np.int8).view(np.uint8) ^ 0x80).reshape(n, nb, 4, 8)[..., _MX8_ORDER]   # [n, kb, kg, 8]
+    codes = b.reshape(G, 2, 2, 16, nb, 4, 8).transpose(0, 4, 1, 5, 3, 2, 6)               # [G, kb, r//2, kg, i, r%2, 8]
+    sc = np.asarray(s16, np.uint16).reshape(G, 4, 16, nb).transpose(0, 3, 2, 1)             # [G, kb, i, r]
+    out = np.empty((G, nb, MX8_TILE), np.uint8)
+    out[:, :, :2048] = np.ascontiguousarray(codes).reshape(G, nb, 2048)
+    out[:, :, 2048:] = np.ascontiguousarray(sc).view(np.uint8).reshape(G, nb, 128)
+    return out.reshape(-1)
+
+
+def unpack_mx8(packed: np.ndarray, n: int, k: int):
+    """Native q8 layout bytes -> (bf16 scale bits uint16[n, k/32], codes int8[n, k])."""
+    nb, G = k // BLK, n // MX_ROWS
+    t = np.asarray(packed, np.uint8).reshape(G, nb, MX8_TILE)
+    codes = t[:, :, :2048].reshape(G, nb, 2, 4, 16, 2, 8).transpose(0, 2, 5, 4, 1, 3, 6).reshape(n, nb, 4, 8)
+    q = np.empty_like(codes)
+    q[..., _MX8_ORDER] = codes
+    sc = np.ascontiguousarray(t[:, :, 2048:]).view(np.uint16).reshape(G, nb, 16, 4).transpose(0, 3, 2, 1)
+    return sc.reshape(n, nb), (q.reshape(n, k) ^ 0x80).view(np.int8)
+
+
+def dequant_mx8(packed: np.ndarray, n: int, k: int) -> np.ndarray:
+    """Native q8 layout -> f32[n, k] = s * q (exact)."""
+    s16, q = unpack_mx8(packed, n, k)
+    return (np.repeat(bf16_to_f32(s16), BLK, axis=1) * q.astype(np.float32)).astype(np.float32)
 
 
 def random_q8_0_blocks(n: int, k: int, rng: np.random.Generator) -> np.ndarray:

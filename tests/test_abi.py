@@ -180,3 +180,18 @@ def test_native_q4k_argument_errors(lib):
     assert need > 0
     assert lib.q4_gemv_q4k(fake, fake, 1, None, fake, 1, 256, 14336, fake, need - 1, None) == -3
     assert lib.q4_gemv_q4k_workspace_bytes(1, 128256, 4096) == 0
+
+
+def test_native_q8_argument_errors(lib):
+    fake = C.c_void_p(0x1000)
+    assert lib.q4_q8_native_packed_bytes(64, 32) == 2176
+    assert lib.q4_q8_native_packed_bytes(64, 48) == -1
+    assert lib.q4_repack_q8_native(fake, 3, 1, fake, 64, 256, None) == -2       # source format
+    assert lib.q4_repack_q8_native(fake, 0, 1, fake, 64, 128, None) == -1       # chunks need K % 256
+    assert lib.q4_repack_q8_native(fake, 1, 1, fake, 64, 48, None) == -1        # Q8_0 needs K % 32
+    assert lib.q4_repack_q8_native(None, 1, 1, None, 0, 32, None) == 0          # empty
+    assert lib.q4_gemv_q8_native(fake, fake, 1, None, fake, 17, 64, 32, None, 0, None) == -5
+    assert lib.q4_gemv_q8_native(fake, fake, 1, None, fake, 1, 64, 48, None, 0, None) == -1
+    need = lib.q4_gemv_q8_native_workspace_bytes(1, 1024, 4096)
+    assert need > 0
+    assert lib.q4_gemv_q8_native(fake, fake, 1, None, fake, 1, 1024, 4096, fake, need - 1, None) == -3
