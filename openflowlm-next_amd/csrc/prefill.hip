@@ -268,23 +268,26 @@ __device__ __forceinline__ void load16_async(u32x4& dst, const void* gbase, uint
 }
 __device__ __forceinline__ void vgpr_landed(u32x4& v) { asm volatile("" : "+v"(v)); }
 
-template <int PREC>
-__global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restrict__ packed,
-                                                          const uint16_t* __restrict__ x16,
-                                                          const float* __restrict__ tscale, float* __restrict__ y,
-                                                          int T, int N, int K, int tiles_t, int splits) {
-    constexpr int WN = 128, WT = 64, FN = WN / 16, FT = WT / 16;
+// One output tile of the pipelined kernel: 32 * FN weight rows from n0 x 256 tokens from
+// 256 * bt, K split `split` of `splits` (split s covers stages [st0, st0 + NST) of K / 64 and
+// writes its partial sums to y + s * T * N; the host sums the splits in order).
+// FN = 8: 256 rows, 128x64 wave tiles. FN = 6: 192 rows, 96x64 wave tiles, with the 256-row
+// tile's loads, DMA and dequant unchanged: the waves of row group 3 load row group 2's mx
+// tile again and store it to LDS rows 192..255, which no fragment reads, so every wave
+// issues the same loads and the wait counts below hold for both.
+template <int PREC, int FN>
+__device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict__ packed,
+                                         const uint16_t* __restrict__ x16, const float* __restrict__ tscale,
+                                         float* __restrict__ y, int T, int N, int K, int n0, int bt, int split,
+                                         int splits) {
+    static_assert(FN == 8 || FN == 6, "256- or 192-row tiles");
+    constexpr int WN = 16 * FN, WT = 64, FT = WT / 16, RG = FN / 2;
     typedef typename std::conditional<PREC == 0, f16x8, bf16x8>::type frag_t;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wt = wave >> 1;
-    // workgroup -> (output tile, K split); split s covers stages [st0, st0 + NST) of K / 64 and
-    // writes its partial sums to y + s * T * N (the host sums the splits in order)
-    const int tile = blockIdx.x / splits, split = blockIdx.x % splits;
-    const int bt = tile % tiles_t, bn = tile / tiles_t;
-    const int n0 = bn * 256, t0 = bt * 256;
+    const int t0 = bt * 256;
     const int KB = K >> 5, NSTK = KB >> 1;
     const int st0 = (int)((int64_t)split * NSTK / splits), NST = (int)((int64_t)(split + 1) * NSTK / splits) - st0;
     y += (int64_t)split * T * N;
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
 
     // weights: this wave's mx tile of each stage (row group wave & 3, 32-K block wave >> 2)
     const int rgl = wave & 3, kbl = wave >> 2;
-    const int rg = min(n0 / 64 + rgl, G - 1);                          // clamp ragged N
+    const int rg = min(n0 / 64 + min(rgl, RG - 1), G - 1);              // clamp ragged N
     const uint8_t* const wsrc = packed + ((int64_t)rg * KB + kbl + 2 * st0) * kTileBytes;
     const uint32_t coff = lane * 16, soff = kCodeBytes + i16 * 16;
     const uint32_t wst = kbl * kPlaneB + rgl * 64 * 64 + lane_row;     // + buffer + r * 1 KB
@@ -392,7 +395,7 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
             read_frags(cur, slot, kk, a, b);
             store_w(cur ^ 1, wc[nset], ws[nset], 2 * kk, 2 * kk + 2);   // rows 16r.., r in [2kk, 2kk+2)
             mfmas(a, b);
-            __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, FN + FT, 0);
 #pragma unroll
             for (int g = 0; g < 20; ++g) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, FN * FT - 22, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (w3) __builtin_amdgcn_s_waitcnt(kWaitVm6Lgkm0);    // X(st+1) landed, LDS stores done
@@ -448,6 +451,30 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
                 *(f32x4*)(y + (int64_t)t * N + n) = v;
             }
         }
+    }
+}
+
+// Workgroups [0, wide_wgs) take the 256-row tiles of rows [0, narrow_row0), the rest the
+// 192-row tiles from narrow_row0 on (token tile fastest, then K split innermost). The longer
+// tiles come first in dispatch order, so the shorter ones fill the CUs the last round of
+// long tiles leaves idle. MIXED = false: 256-row tiles only (wide_wgs = the grid), an
+// instance without the 192-row body.
+template <int PREC, bool MIXED>
+__global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restrict__ packed,
+                                                          const uint16_t* __restrict__ x16,
+                                                          const float* __restrict__ tscale, float* __restrict__ y,
+                                                          int T, int N, int K, int tiles_t, int splits, int wide_wgs,
+                                                          int narrow_row0) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
+    const int b = blockIdx.x;
+    if (!MIXED || b < wide_wgs) {
+        const int tile = b / splits;
+        dma_tile<PREC, 8>(lds, packed, x16, tscale, y, T, N, K, (tile / tiles_t) * 256, tile % tiles_t, b % splits,
+                          splits);
+    } else {
+        const int i = b - wide_wgs, tile = i / splits;
+        dma_tile<PREC, 6>(lds, packed, x16, tscale, y, T, N, K, narrow_row0 + (tile / tiles_t) * 192,
+                          tile % tiles_t, i % splits, splits);
     }
 }
 
@@ -613,7 +640,7 @@ void launch_cfg(int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* 
 
 template <int PREC>
 void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const float* ts,
-                    float* y, int T, int N, int K, int tiles_t, int splits) {
+                    float* y, int T, int N, int K, int tiles_t, int splits, int wide_wgs, int narrow_row0) {
     switch (cfg) {
         case 0: launch_cfg<0, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
         case 1: launch_cfg<1, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
@@ -621,8 +648,12 @@ void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, con
         case 3: launch_cfg<3, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
         case 4: launch_cfg<4, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
         default:
-            hipLaunchKernelGGL((prefill_dma_kernel<PREC>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, ts, y, T, N, K,
-                               tiles_t, splits);
+            if (wide_wgs < grid)
+                hipLaunchKernelGGL((prefill_dma_kernel<PREC, true>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, ts,
+                                   y, T, N, K, tiles_t, splits, wide_wgs, narrow_row0);
+            else
+                hipLaunchKernelGGL((prefill_dma_kernel<PREC, false>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, ts,
+                                   y, T, N, K, tiles_t, splits, wide_wgs, narrow_row0);
             break;
     }
 }
@@ -652,44 +683,110 @@ int device_cus() {
     return cus;
 }
 
-// Launch plan of one prefill GEMM: the kernel variant, its token tiles and K splits. The
-// pipelined kernel holds one workgroup per CU (160 KB of LDS); when its output tiles do not
-// fill the CUs, K is split and the partial sums are reduced in order afterwards
-// (Q4MI_PREFILL_SPLITS overrides the choice).
+// Launch plan of one prefill GEMM: the kernel variant, its token tiles and K splits, and for
+// the pipelined kernel the rows covered by 256-row tiles ([0, narrow_row0), wide_wgs
+// workgroups) and by 192-row tiles (the rest). That kernel holds one workgroup per CU (160 KB
+// of LDS). Two levers fit its work to the CUs: a K split (partial sums reduced in order
+// afterwards) and 192-row tiles, which fill the CUs the last round of 256-row tiles leaves
+// idle without any partial traffic (Llama-3-8B gate_up at T = 2048: 448 tiles of 256 rows
+// run in 2 rounds of 256 CUs; 256 of 256 rows + 256 of 192 rows in 1 + 3/4). 192-row
+// strips also cover N % 256 != 0 without repeating rows.
+// Q4MI_PREFILL_SPLITS and Q4MI_PREFILL_NARROW (the count of 192-row strips) override.
 struct PrefillPlan {
-    int cfg, tiles_t, splits;
+    int cfg, tiles_t, splits, wide_wgs, narrow_row0;
     int64_t grid;
 };
 
-PrefillPlan make_plan(int T, int64_t N, int64_t K) {
+// Finish time of A units of cost cw followed by B units of cost cn when each starts on the
+// earliest free of C CUs (workgroups dispatch in index order, one per CU).
+double makespan(int64_t A, int64_t B, int64_t C, double cw, double cn) {
+    const int64_t q = A / C, r = A % C;
+    const double wide_end = (double)(q + (r ? 1 : 0)) * cw;
+    if (B == 0) return wide_end;
+    double t[2] = {(double)q * cw, (double)(q + 1) * cw};   // C - r CUs free at t[0], r at t[1]
+    const int64_t cnt[2] = {C - r, r};
+    double last = 0;
+    for (int64_t left = B; left > 0;) {
+        const int g = (cnt[1] > 0 && t[1] < t[0]) ? 1 : 0;
+        last = t[g];
+        left -= cnt[g];
+        t[g] += cn;
+    }
+    return last + cn > wide_end ? last + cn : wide_end;
+}
+
+PrefillPlan make_plan_uncached(int T, int64_t N, int64_t K) {
     PrefillPlan p;
     p.cfg = choose_cfg(T, (int)N, (int)K);
     p.tiles_t = (int)ceil_div(T, kCfgs[p.cfg].bt);
-    const int64_t tiles = ceil_div(N, kCfgs[p.cfg].bn) * p.tiles_t;
+    int64_t tiles = ceil_div(N, kCfgs[p.cfg].bn) * p.tiles_t;
     p.splits = 1;
+    p.wide_wgs = (int)tiles;
+    p.narrow_row0 = (int)N;
     if (p.cfg == kDmaCfg) {
         static const int forced = [] {
             const char* e = getenv("Q4MI_PREFILL_SPLITS");
             return e ? atoi(e) : 0;
         }();
+        static const int forced_narrow = [] {
+            const char* e = getenv("Q4MI_PREFILL_NARROW");
+            return e ? atoi(e) : -1;
+        }();
+        // kNarrowRel: a 192-row tile's time relative to a 256-row tile's over the same stages
+        constexpr double kStageSec = 1.0e-6, kReduceBytesPerSec = 4.0e12, kNarrowRel = 0.8;
         const int nst = (int)(K / 64), cap = nst < 16 ? nst : 16;
-        if (forced > 0) {
-            p.splits = forced < cap ? forced : cap;
-        } else {
-            constexpr double kStageSec = 1.0e-6, kReduceBytesPerSec = 4.0e12;
-            const int cus = device_cus();
-            double best = 1e300;
+        const int64_t G = N / 64, tt = p.tiles_t;
+        const int cus = device_cus();
+        // a forced strip count is used only where it fits: 3b <= G and 4 | G - 3b
+        const int64_t fb = forced_narrow > 0 && 3 * (int64_t)forced_narrow <= G &&
+                                   (G - 3 * (int64_t)forced_narrow) % 4 == 0
+                               ? forced_narrow
+                               : forced_narrow == 0 ? 0 : -1;
+        double best = 1e300;
+        // b 192-row strips and a 256-row strips with 4a + 3b = G (b = 0: 256-row strips only,
+        // the last one clamped when G % 4 != 0). 192-row tiles only fill the last round of
+        // 256-row ones, so at most two rounds of them are considered.
+        for (int64_t b = 0; 3 * b <= G && (b * tt <= 2 * cus || b == fb); ++b) {
+            if (b > 0 && (G - 3 * b) % 4) continue;
+            if (fb >= 0 && b != fb) continue;
+            const int64_t a = b > 0 ? (G - 3 * b) / 4 : ceil_div(G, 4);
             for (int S = 1; S <= cap; ++S) {
-                double cost = (double)ceil_div(tiles * S, cus) * (double)ceil_div(nst, S) * kStageSec;
+                if (forced > 0 && S != (forced < cap ? forced : cap)) continue;
+                if (b > 0 && b != fb && b * tt * S > 2 * cus) break;
+                const double cw = (double)ceil_div(nst, S) * kStageSec;
+                double cost = makespan(a * tt * S, b * tt * S, cus, cw, cw * kNarrowRel);
                 if (S > 1) cost += (double)(S + 1) * T * N * 4 / kReduceBytesPerSec;
+                // ties: fewer rows computed (a clamped last 256-row strip repeats rows)
+                cost += 1e-12 * (double)(256 * a + 192 * b);
                 if (cost < best) {
                     best = cost;
                     p.splits = S;
+                    p.wide_wgs = (int)(a * tt * S);
+                    p.narrow_row0 = b > 0 ? (int)(256 * a) : (int)N;
+                    tiles = (a + b) * tt;
                 }
             }
         }
     }
     p.grid = tiles * p.splits;
+    return p;
+}
+
+// The plans of the last few shapes per host thread (the workspace query and the call that
+// follows it plan the same shape).
+PrefillPlan make_plan(int T, int64_t N, int64_t K) {
+    struct Entry {
+        int T;
+        int64_t N, K;
+        PrefillPlan p;
+    };
+    thread_local Entry cache[4] = {};
+    thread_local int next = 0;
+    for (const Entry& e : cache)
+        if (e.T == T && e.N == N && e.K == K && T > 0) return e.p;
+    const PrefillPlan p = make_plan_uncached(T, N, K);
+    cache[next] = Entry{T, N, K, p};
+    next = (next + 1) & 3;
     return p;
 }
 
@@ -748,8 +845,12 @@ extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
     const float* tsp = precision == 0 ? ts : nullptr;
     float* out = plan.splits > 1 ? (float*)((char*)workspace + xprep_bytes(T, K)) : y;
-    if (precision == 0) launch_prefill<0>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits);
-    else launch_prefill<1>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits);
+    if (precision == 0)
+        launch_prefill<0>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits,
+                          plan.wide_wgs, plan.narrow_row0);
+    else
+        launch_prefill<1>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits,
+                          plan.wide_wgs, plan.narrow_row0);
     if (plan.splits > 1) {
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
         const int64_t MN4 = (int64_t)T * N / 4;

@@ -125,3 +125,36 @@ def test_prefill_split_tiles_are_deterministic(gpu, pkg, oracle, T, N, K):
     if T * N * K <= 1 << 31:
         ref = oracle.prefill_reference(blocks, X.to(torch.float32).numpy())
         assert oracle.maxrel(Y0.numpy(), ref) <= 1e-3
+
+
+@pytest.mark.parametrize("T,N,K", [(256, 192, 64), (256, 448, 256), (1000, 704, 512)])
+def test_prefill_192_row_tiles(gpu, pkg, oracle, T, N, K):
+    """Shapes the planner gives 192-row tiles: N = 192 alone (one 192-row tile instead of a
+    clamped 256-row one), 448 = 256 + 192 with a 4-way K split, 704 = 2 x 256 + 192 with a
+    ragged token count. Same bar as the 256-row tiles."""
+    say(f"prefill 192-row tiles T={T} N={N} K={K}")
+    rng = np.random.default_rng(T + N + K + 1)
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    X = _x(rng, T, K)
+    w = pkg.pack_q4_1(blocks, gpu)
+    Y = pkg.gemm_q4_prefill(w, X.to(gpu)).cpu().numpy()
+    ref = oracle.prefill_reference(blocks, X.to(torch.float32).numpy())
+    assert Y.shape == (T, N) and np.isfinite(Y).all()
+    assert oracle.maxrel(Y, ref) <= 1e-3
+
+
+def test_prefill_gate_up_t2048(gpu, pkg, oracle):
+    """Llama-3-8B gate_up at T = 2048, the bench shape: 24 tokens (3 from each 256-token
+    tile) against fp64 over every row, per token."""
+    say("prefill gate_up T=2048")
+    rng = np.random.default_rng(2048)
+    N, K, T = 14336, 4096, 2048
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    X = _x(rng, T, K)
+    w = pkg.pack_q4_1(blocks, gpu)
+    Y = pkg.gemm_q4_prefill(w, X.to(gpu)).cpu().numpy()
+    assert np.isfinite(Y).all()
+    toks = np.array([bt * 256 + o for bt in range(8) for o in (0, 131, 255)])
+    ref = oracle.prefill_reference(blocks, X[toks].to(torch.float32).numpy())
+    for i, t in enumerate(toks):
+        assert oracle.maxrel(Y[t], ref[i]) <= 1e-3, int(t)

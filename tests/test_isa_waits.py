@@ -31,17 +31,28 @@ def _operands(line: str) -> list[str]:
     return [t.strip().split()[0] for t in parts[1].split(",") if t.strip()] if len(parts) > 1 else []
 
 
-def early_uses(asm: list[str]) -> tuple[int, list[str]]:
-    """(loads checked, descriptions of uses before the load's wait) for the first loop."""
-    # the innermost loop (the stage loop; an outer loop over tile segments may enclose it)
-    inner = any("Inner Loop Header" in l for l in asm)
-    head = next(i for i, l in enumerate(asm) if "Loop Header" in l and ("Inner" in l or not inner))
-    if not asm[head].startswith("."):           # header comment on its own line: label above
-        head -= 1
-    label = asm[head].split(":")[0]
-    end = next(i for i in range(head + 1, len(asm))
-               if re.search(r"s_(?:cbranch_\w+|branch)\s+" + re.escape(label) + r"\b", asm[i]))
-    body = [l for l in asm[head:end + 1] if l.strip() and not l.strip().startswith((";", "."))]
+def inner_loops(asm: list[str]) -> list[list[str]]:
+    """The instructions of each innermost loop, in layout order: the header's block, the
+    blocks marked as inside it (a latch may sit above the header and fall into it), up to
+    the last branch back to any of them."""
+    loops = []
+    inner = any("Inner Loop Header" in l for l in asm)     # else: a lone loop's "Loop Header"
+    for h, line in enumerate(asm):
+        if "Loop Header" not in line or (inner and "Inner" not in line):
+            continue
+        label = line.split(":")[0].strip()
+        name = label[2:] if label.startswith(".L") else label.lstrip(".")   # ".LBB0_1" -> "BB0_1"
+        members = {label} | {l.split(":")[0].strip() for l in asm if f"in Loop: Header={name} " in l + " "}
+        first = min(i for i, l in enumerate(asm) if l.split(":")[0].strip() in members and ":" in l)
+        last = max(i for i, l in enumerate(asm)
+                   if re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l)
+                   and re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l).group(1) in members)
+        loops.append([l for l in asm[first:last + 1] if l.strip() and not l.strip().startswith((";", "."))])
+    return loops
+
+
+def early_uses_in(body: list[str]) -> tuple[int, list[str]]:
+    """(loads checked, descriptions of uses before the load's wait) for one loop body."""
     bad, n = [], 0
     for i, l in enumerate(body):
         if not re.match(r"\s*global_load_dword", l) or "lds" in l:
@@ -66,6 +77,15 @@ def early_uses(asm: list[str]) -> tuple[int, list[str]]:
     return n, bad
 
 
+def early_uses(asm: list[str]) -> tuple[int, list[str]]:
+    """(loads checked, early uses) summed over every innermost loop of asm."""
+    n, bad = 0, []
+    for body in inner_loops(asm):
+        k, b = early_uses_in(body)
+        n, bad = n + k, bad + b
+    return n, bad
+
+
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
 def test_prefill_loop_waits_cover_every_asm_load(tmp_path):
     out = tmp_path / "prefill.s"
@@ -75,12 +95,17 @@ def test_prefill_loop_waits_cover_every_asm_load(tmp_path):
     subprocess.run(cmd, check=True, capture_output=True, timeout=600)
     text = out.read_text().splitlines()
     for prec in (0, 1):
-        start = next(i for i, l in enumerate(text)
-                     if re.match(rf"_ZN12_GLOBAL__N_118prefill_dma_kernelILi{prec}EE\w*:", l))
-        stop = next(i for i in range(start, len(text)) if "s_endpgm" in text[i])
-        n, bad = early_uses(text[start:stop])
-        assert n >= 6, f"precision {prec}: expected the weight loads of the unrolled loop, found {n}"
-        assert not bad, f"precision {prec}: registers used before their load's wait: {bad[:3]}"
+        for mixed, nloops in ((0, 1), (1, 2)):      # 256-row tiles only; + the 192-row body
+            start = next(i for i, l in enumerate(text)
+                         if re.match(rf"_ZN12_GLOBAL__N_118prefill_dma_kernelILi{prec}ELb{mixed}EE\w*:", l))
+            stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
+            loops = inner_loops(text[start:stop])
+            what = f"precision {prec} mixed {mixed}"
+            assert len(loops) == nloops, f"{what}: expected {nloops} tile loops, found {len(loops)}"
+            for body in loops:
+                n, bad = early_uses_in(body)
+                assert n >= 6, f"{what}: expected the weight loads of the unrolled loop, found {n}"
+                assert not bad, f"{what}: registers used before their load's wait: {bad[:3]}"
 
 
 def test_checker_flags_an_early_use():
