@@ -584,6 +584,64 @@ def extra_config4(torch, q4, dev):
 
 # --------------------------------------------------------------------------
 
+def q4nx_decode_harness(model_dir, tensor: str, shape=None, reps: int = 10) -> dict:
+    """The reference's decode benchmark (utilities/benchmark-q4-decode.py:37-54) on one q4_1
+    tensor of a .q4nx container, with the MI355X path beside its two CPU decoders.
+
+    CPU (restatements in oracle/, the baseline leg): the frozen strided-indexing decode
+    (``legacy_seconds``) and the contiguous dq_chunks_q4_1 (``contiguous_seconds``), checked
+    byte-identical as the reference checks them. GPU: the same chunks copied to HBM, repacked
+    to the mx layout (q4_repack_pool, rs = 1, the file raster) and dequantized there
+    (q4_dequant); the device values, put back in chunk order, must equal the legacy decode byte
+    for byte. Repack, dequant and the M = 1 GEMV over the matrix are then timed with their
+    inputs resident in HBM (HIP events, ``reps`` calls each). The container does not hold the
+    logical [out, in]: ``shape`` gives it, else the chunks are read as [32 * chunks, 256] (one
+    chunk per 32 rows; the same bytes and values, only the GEMV's shape differs)."""
+    import numpy as np
+    import torch
+    from oracle import q4_oracle as O
+    q4 = importlib.import_module("openflowlm-next_amd")
+    with q4.Q4NXFile(Path(model_dir) / "model.q4nx") as f:
+        fmt = f.quant_format_of(tensor)
+        if fmt != "q4_1":
+            raise ValueError(f"{tensor}: {fmt or 'not a quantised tensor'}; the decode benchmark reads q4_1 chunks")
+        raw = np.array(f.raw(tensor))
+    chunks = raw.reshape(-1, 5120)
+    nch = chunks.shape[0]
+    out_dim, in_dim = (int(shape[0]), int(shape[1])) if shape else (32 * nch, 256)
+    if out_dim % 64 or in_dim % 256 or (out_dim // 32) * (in_dim // 256) != nch:
+        raise ValueError(f"{tensor}: {nch} chunks do not tile [{out_dim}, {in_dim}] (64-row groups of 256-K chunks)")
+
+    t = time.perf_counter()
+    old = O.legacy_decode(chunks)
+    legacy_s = time.perf_counter() - t
+    t = time.perf_counter()
+    new = O.dq_chunks_q4_1(chunks)
+    contiguous_s = time.perf_counter() - t
+    identical = old.tobytes() == new.tobytes()
+
+    dev = torch.device("cuda", 0)
+    src = torch.from_numpy(raw).to(dev)
+    w = q4.pack_chunks(src, "q4_1", out_dim, in_dim, rs=1, device=dev)
+    deq = q4.dequant(w)
+    in_chunk_order = deq.view(out_dim // 32, 32, in_dim // 256, 8, 32).permute(0, 2, 1, 3, 4)
+    gpu_identical = in_chunk_order.contiguous().cpu().numpy().tobytes() == old.tobytes()
+    x = torch.randn(1, in_dim, device=dev).to(torch.bfloat16)
+    y = torch.empty(1, out_dim, device=dev)
+    _, repack_ms = time_launches(torch, lambda: q4.pack_chunks(src, "q4_1", out_dim, in_dim, rs=1, device=dev), reps, 2)
+    _, dequant_ms = time_launches(torch, lambda: q4.dequant(w, out=deq), reps, 2)
+    _, gemv_ms = time_launches(torch, lambda: q4.gemm_q4(w, x, y), reps, 2)
+    wb = w.nbytes
+    gpu = {"shape": [out_dim, in_dim], "shape_given": bool(shape), "byte_identical": gpu_identical,
+           "repack_us": round(repack_ms * 1e3, 2), "repack_gbs": round(2 * raw.nbytes / repack_ms / 1e6, 1),
+           "dequant_us": round(dequant_ms * 1e3, 2),
+           "dequant_gbs": round((wb + out_dim * in_dim * 4) / dequant_ms / 1e6, 1),
+           "gemv_m1_us": round(gemv_ms * 1e3, 2), "gemv_m1_gbs": round((wb + in_dim * 2 + out_dim * 4) / gemv_ms / 1e6, 1),
+           "dequant_speedup_vs_contiguous_cpu": round(contiguous_s / (dequant_ms * 1e-3), 1)}
+    return {"tensor": tensor, "chunks": nch, "byte_identical": identical, "legacy_seconds": legacy_s,
+            "contiguous_seconds": contiguous_s, "speedup": legacy_s / contiguous_s, "gpu": gpu}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -596,6 +654,12 @@ def main() -> int:
     ap.add_argument("--cpu-baseline-child", type=int, default=None, help=argparse.SUPPRESS)
     ap.add_argument("--only-extras", action="store_true",
                     help="skip the headline sweep; run the --extras list and print them (profiling runs)")
+    ap.add_argument("--model-dir", default=None,
+                    help="decode benchmark on a .q4nx container (model-dir/model.q4nx): the reference "
+                         "harness's JSON (benchmark-q4-decode.py) plus the GPU repack, dequant and GEMV")
+    ap.add_argument("--tensor", default="model.layers.0.mlp.up_proj.weight", help="the tensor --model-dir decodes")
+    ap.add_argument("--shape", type=int, nargs=2, default=None, metavar=("OUT", "IN"),
+                    help="the tensor's logical [out, in] for --model-dir (default [32 * chunks, 256])")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only copy this many bytes device-to-device 5 times (calibrates HBM traffic counters)")
     a = ap.parse_args()
@@ -614,6 +678,10 @@ def main() -> int:
     q4.load_library()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if a.model_dir:
+        r = q4nx_decode_harness(a.model_dir, a.tensor, a.shape)
+        print(json.dumps(r, indent=2))
+        return 0 if r["byte_identical"] and r["gpu"]["byte_identical"] else 1
     if a.copy_probe:
         src = torch.randint(0, 256, (a.copy_probe,), dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

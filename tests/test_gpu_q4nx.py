@@ -83,3 +83,23 @@ def test_container_end_to_end(gpu, pkg, oracle, tmp_path):
         y = pkg.gemm_q4(w, torch.from_numpy(x).to(gpu)).cpu().numpy()
         ref = x.astype(np.float64) @ pkg.dequant(w).cpu().numpy().astype(np.float64).T
         assert oracle.maxrel(y, ref) <= 1e-3
+
+
+def test_decode_benchmark_harness(gpu, pkg, oracle, tmp_path):
+    """bench.py --model-dir: the reference harness's JSON (benchmark-q4-decode.py:37-54) on a
+    container's q4_1 tensor, its two CPU decoders byte-identical, and the GPU repack + dequant
+    byte-identical with them, with the logical shape given and without."""
+    import bench
+    say("q4nx decode benchmark harness")
+    rng = np.random.default_rng(12)
+    n, k = 512, 2048
+    nch = (n // 32) * (k // 256)
+    blocks = oracle.random_q4_1_blocks_ref(n, k, rng)
+    name = "model.layers.0.mlp.up_proj.weight"
+    write_q4nx(tmp_path / "model.q4nx", [(name, "I8", (nch, 5120), oracle.pack_q4_1_pool(blocks, 1).reshape(nch, 5120))])
+    for shape in ((n, k), None):
+        r = bench.q4nx_decode_harness(tmp_path, name, shape, reps=3)
+        assert r["tensor"] == name and r["chunks"] == nch
+        assert r["byte_identical"] and r["gpu"]["byte_identical"], r
+        assert r["gpu"]["shape"] == ([n, k] if shape else [32 * nch, 256])
+        assert r["legacy_seconds"] > 0 and r["contiguous_seconds"] > 0 and r["gpu"]["dequant_us"] > 0

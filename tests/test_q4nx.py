@@ -220,3 +220,19 @@ def test_gguf_direct_pool_reads_the_gguf_values_exactly(oracle, kind):
     code = np.ascontiguousarray(pool8[0, 1024:]).view(np.int8)[oracle.CHUNK_CODE_IDX].astype(np.float64)
     got8 = (code * sc[oracle.CHUNK_META_IDX]).reshape(32, 8, 32).reshape(32, 256)
     assert np.array_equal(got8, want[:32, :256])
+
+
+def test_decode_benchmark_harness_rejects_what_it_cannot_read(tmp_path):
+    """bench.q4nx_decode_harness: a non-q4_1 tensor and a shape the chunks do not tile are
+    refused before any GPU work."""
+    import bench
+    rng = np.random.default_rng(3)
+    write_q4nx(tmp_path / "model.q4nx", [("q8", "I8", (4, 8704), rng.integers(-128, 128, (4, 8704), dtype=np.int8)),
+                                         ("q4", "I8", (4, 5120), rng.integers(1, 256, (4, 5120), dtype=np.uint8)),
+                                         ("norm", "BF16", (64,), np.zeros(64, np.uint16))])
+    with pytest.raises(ValueError, match="q4_1"):
+        bench.q4nx_decode_harness(tmp_path, "q8", None)
+    with pytest.raises(ValueError, match="q4_1"):
+        bench.q4nx_decode_harness(tmp_path, "norm", None)
+    with pytest.raises(ValueError, match="do not tile"):
+        bench.q4nx_decode_harness(tmp_path, "q4", (128, 512))
