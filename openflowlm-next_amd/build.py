@@ -33,6 +33,24 @@ COMMON = [
 ]
 
 
+# Per-source flags. The grouped GEMV keeps its MFMA accumulators in VGPRs: in the AGPR
+# form the compiler reads every MFMA result back with v_accvgpr_read (one VALU per result
+# register, 20 per 4 tiles at M = 1) and the AGPRs add to the wave's register allocation
+# (the files are unified; 102 VGPRs + 20 AGPRs at M = 1 against 89 VGPRs). Measured on the
+# Llama-3-8B sweep (8 layers, M = 1): 197.1 -> 193.6 us. The same flag made the
+# single-matrix kernels of gemv.hip slower (native Q4_K gate_up 14.9 -> 21.0 us, the mx
+# lm_head 55.7 -> 58.6 us) and changes the prefill kernel's hand-scheduled loop, so it is
+# set per source file.
+EXTRA = {
+    "gemv_grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
+def flags(src: Path) -> list[str]:
+    """The device-compile flags of one csrc/*.hip file."""
+    return [*COMMON, *EXTRA.get(src.name, [])]
+
+
 def hipcc() -> str:
     for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if c and Path(c).exists():
@@ -42,7 +60,7 @@ def hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *flags(src), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -29,23 +29,6 @@ struct GemvParams {
 };
 
 
-// Store the row group's result (S == 1, plus the residual when one is given) or this
-// split's partial sums (res null).
-template <int NTL>
-__device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4][NTL][64], int M,
-                                            float* y, int64_t N, int64_t g, const float* res = nullptr) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
-    const int64_t n = g * 64 + r * 16 + i16;
-    float v[NTL];
-    wave_sum<NTL>(acc, red, v);
-#pragma unroll
-    for (int j = 0; j < NTL; ++j) {
-        const int tok = token_of(kg, j);
-        if (tok < M) y[(int64_t)tok * N + n] = res ? res[(int64_t)tok * N + n] + v[j] : v[j];
-    }
-}
-
 // y[t][n] = sum over s = 0..S-1 of part[s][t][n], in split order (+ res[t][n]).
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* y,
                                                            int64_t MN, int S, const float* res) {
@@ -244,28 +227,6 @@ __global__ __launch_bounds__(256) void swiglu_reduce_kernel(const float* __restr
     store_h(h, h_bf16, i, silu(gs) * us);
 }
 
-template <int NTL, bool XF32>
-__global__ __launch_bounds__(256) void gemv_grouped_kernel(const q4_gemv_desc* __restrict__ descs, int count, int M) {
-    __shared__ float red[kWaves][4][NTL][64];
-    const int64_t item = blockIdx.x;
-    int lo = 0, hi = count - 1;
-    while (lo < hi) {               // last descriptor with item_begin <= item
-        const int mid = (lo + hi + 1) >> 1;
-        if (descs[mid].item_begin <= item) lo = mid;
-        else hi = mid - 1;
-    }
-    const q4_gemv_desc D = descs[lo];
-    const int64_t g = item - D.item_begin;
-    if (g < 0 || g >= (D.N >> 6)) return;   // inconsistent total_items: the whole workgroup leaves
-    float acc[4][NTL];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
-    gemv_rows<NTL, XF32>(D.packed, D.x, DenseRows{M}, D.K, g, 0, (int)(D.K >> 5), acc);
-    gemv_finish<NTL>(acc, red, M, D.y, D.N, g);
-}
-
 // Workgroups to aim for when a matrix has few row groups.
 int64_t target_workgroups() {
     static int64_t t = [] {
@@ -347,12 +308,6 @@ template <int NTL>
 void launch_q8n(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
     if (xf32) hipLaunchKernelGGL((q8n_gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
     else hipLaunchKernelGGL((q8n_gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
-}
-
-template <int NTL>
-void launch_grouped(bool xf32, dim3 grid, hipStream_t st, const q4_gemv_desc* d, int count, int M) {
-    if (xf32) hipLaunchKernelGGL((gemv_grouped_kernel<NTL, true>), grid, dim3(256), 0, st, d, count, M);
-    else hipLaunchKernelGGL((gemv_grouped_kernel<NTL, false>), grid, dim3(256), 0, st, d, count, M);
 }
 
 }  // namespace
@@ -480,24 +435,6 @@ extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void
         const int64_t MF = (int64_t)M * F;
         hipLaunchKernelGGL(swiglu_reduce_kernel, dim3((unsigned)ceil_div(MF, 256)), dim3(256), 0, st, P.part, h,
                            P.h_bf16, M, F, S);
-    }
-    return launch_status();
-}
-
-extern "C" int q4_gemv_grouped(const q4_gemv_desc* descs, int count, int64_t total_items, int M, int x_dtype,
-                               void* stream) {
-    if (!descs || count <= 0 || total_items <= 0) return Q4MI_E_ARG;
-    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
-    if (M < 1 || M > 16) return Q4MI_E_RANGE;
-    if (total_items > 0x7FFFFFFF) return Q4MI_E_RANGE;
-    const dim3 grid((unsigned)total_items);
-    const hipStream_t st = (hipStream_t)stream;
-    const bool xf32 = x_dtype == Q4MI_F32;
-    switch ((M + 3) / 4) {
-        case 1: launch_grouped<1>(xf32, grid, st, descs, count, M); break;
-        case 2: launch_grouped<2>(xf32, grid, st, descs, count, M); break;
-        case 3: launch_grouped<3>(xf32, grid, st, descs, count, M); break;
-        default: launch_grouped<4>(xf32, grid, st, descs, count, M); break;
     }
     return launch_status();
 }

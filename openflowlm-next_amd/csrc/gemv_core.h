@@ -52,8 +52,8 @@ template <bool XF32>
 __device__ __forceinline__ void load_xfrag(const void* __restrict__ x, int64_t K, int64_t row, int64_t k0,
                                            bf16x8& hi, bf16x8& lo) {
     if constexpr (XF32) {
-        const f32x4* p = (const f32x4*)((const float*)x + row * K + k0);
-        const f32x4 a = p[0], b = p[1];
+        const float* p = (const float*)x + row * K + k0;
+        const f32x4 a = load_global<f32x4>(p), b = load_global<f32x4>(p + 4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const __bf16 ha = (__bf16)a[e], hb = (__bf16)b[e];
@@ -63,7 +63,7 @@ __device__ __forceinline__ void load_xfrag(const void* __restrict__ x, int64_t K
             lo[e + 4] = (__bf16)(b[e] - (float)hb);
         }
     } else {
-        hi = *(const bf16x8*)((const __bf16*)x + row * K + k0);
+        hi = load_global<bf16x8>((const __bf16*)x + row * K + k0);
     }
 }
 
@@ -338,6 +338,23 @@ __device__ __forceinline__ void wave_sum(float (&acc)[4][NTL], float (*red)[4][N
 #pragma unroll
     for (int j = 0; j < NTL; ++j)
         v[j] = (red[0][r][j][lane] + red[1][r][j][lane]) + (red[2][r][j][lane] + red[3][r][j][lane]);
+}
+
+// Store the row group's result (S == 1, plus the residual when one is given) or this
+// split's partial sums (res null).
+template <int NTL>
+__device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4][NTL][64], int M,
+                                            float* y, int64_t N, int64_t g, const float* res = nullptr) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
+    const int64_t n = g * 64 + r * 16 + i16;
+    float v[NTL];
+    wave_sum<NTL>(acc, red, v);
+#pragma unroll
+    for (int j = 0; j < NTL; ++j) {
+        const int tok = token_of(kg, j);
+        if (tok < M) y[(int64_t)tok * N + n] = res ? res[(int64_t)tok * N + n] + v[j] : v[j];
+    }
 }
 
 }  // namespace q4mi

@@ -101,16 +101,28 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+// Device buffers are global memory. Loads through these address-space-1 pointers are
+// global_load instructions whatever the pointer's origin: a pointer read from memory (a
+// descriptor table) is otherwise a flat pointer, and flat loads count on lgkmcnt too, so
+// their waits cannot leave younger loads in flight.
+template <class T>
+using global_ptr = const __attribute__((address_space(1))) T*;
+
+template <class T>
+__device__ __forceinline__ T load_global(const void* p) {
+    return *(global_ptr<T>)p;
+}
+
 // Streaming loads of weight bytes: read once, keep them out of the caches'
 // way (the "nt" bit on the global load).
 __device__ __forceinline__ u32x4 load_nt_u32x4(const void* p) {
-    return __builtin_nontemporal_load((const u32x4*)p);
+    return __builtin_nontemporal_load((global_ptr<u32x4>)p);
 }
 __device__ __forceinline__ u32x2 load_nt_u32x2(const void* p) {
-    return __builtin_nontemporal_load((const u32x2*)p);
+    return __builtin_nontemporal_load((global_ptr<u32x2>)p);
 }
 __device__ __forceinline__ uint32_t load_nt_u32(const void* p) {
-    return __builtin_nontemporal_load((const uint32_t*)p);
+    return __builtin_nontemporal_load((global_ptr<uint32_t>)p);
 }
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {

@@ -44,9 +44,12 @@ def inner_loops(asm: list[str]) -> list[list[str]]:
         name = label[2:] if label.startswith(".L") else label.lstrip(".")   # ".LBB0_1" -> "BB0_1"
         members = {label} | {l.split(":")[0].strip() for l in asm if f"in Loop: Header={name} " in l + " "}
         first = min(i for i, l in enumerate(asm) if l.split(":")[0].strip() in members and ":" in l)
-        last = max(i for i, l in enumerate(asm)
-                   if re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l)
-                   and re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l).group(1) in members)
+        back = [i for i, l in enumerate(asm)
+                if re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l)
+                and re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l).group(1) in members]
+        if not back:                            # no branch back to the loop's blocks: not a loop body
+            continue
+        last = max(back)
         loops.append([l for l in asm[first:last + 1] if l.strip() and not l.strip().startswith((";", "."))])
     return loops
 
@@ -122,3 +125,36 @@ def test_checker_flags_an_early_use():
                     "\tglobal_load_dwordx4 v[30:33], v1, s[2:3] nt", "\ts_waitcnt vmcnt(1)",
                     "\tv_add_u32_e32 v13, v9, v10", asm[-1]]
     assert early_uses(ok) == (3, [])
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+@pytest.mark.parametrize("src", ["gemv.hip", "gemv_grouped.hip", "moe.hip"])
+def test_gemv_kernels_load_global_and_keep_accumulators_in_vgprs(tmp_path, src):
+    """The decode kernels' weight and activation loads are global loads in every kernel,
+    also where the pointers come from a descriptor table (flat loads count on lgkmcnt too,
+    which turns every wait into a wait for all loads); the sources the build compiles with
+    VGPR-form MFMA hold no AGPRs (MFMA results read back one VALU per register, and AGPRs
+    add to the wave's allocation)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("q4mi_build", ROOT / "openflowlm-next_amd" / "build.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    path = SRC.parent / src
+    out = tmp_path / (path.stem + ".s")
+    cmd = ["hipcc", *b.flags(path), "--cuda-device-only", "-S", str(path), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    text = out.read_text()
+    lines = text.splitlines()
+    kernels = [l.split(":")[0] for l in lines if re.match(r"_ZN12_GLOBAL__N_1\w*(gemv|moe)\w*kernel\w*:", l)]
+    assert kernels
+    for k in kernels:
+        start = next(i for i, l in enumerate(lines) if l.startswith(k + ":"))
+        stop = next(i for i in range(start, len(lines)) if lines[i].startswith(".Lfunc_end"))
+        for body in inner_loops(lines[start:stop]):
+            flat = [l.strip() for l in body if l.strip().startswith("flat_load")]
+            assert not flat, f"{k}: flat loads in its loop: {flat[:2]}"
+    if "-amdgpu-mfma-vgpr-form" not in b.flags(path):
+        return
+    for m in re.finditer(r"\.agpr_count:\s+(\d+).*?\.name:\s+(\S+)", text, re.S):
+        if m.group(2) in kernels:
+            assert int(m.group(1)) == 0, f"{m.group(2)} holds {m.group(1)} AGPRs"
