@@ -95,3 +95,22 @@ def test_moe_empty_and_limits(gpu, pkg, oracle):
     with pytest.raises(Exception):
         pkg.moe_batch(gu, dn, torch.zeros(600, H, dtype=torch.bfloat16, device=gpu),
                       np.zeros((600, 8), np.int32), np.zeros((600, 8), np.float32))   # 4800 pairs > 4096
+
+
+def test_moe_few_pairs_path_with_popular_experts(gpu, pkg, oracle):
+    """T * topk <= 2E takes the one-accumulator kernels (chunks of 4 routed tokens): here
+    every token picks the same 8 of 32 experts, so each of those streams its rows in two
+    chunks. Same bar as the other shapes."""
+    say("moe few-pairs path, 8 tokens on the same 8 experts")
+    E, H, F, T, K = 32, 512, 256, 8, 8
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 321)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    ids = np.tile(np.arange(3, 3 + K, dtype=np.int32), (T, 1))
+    w = rng.uniform(0.5, 1.5, (T, K)).astype(np.float32)
+    w /= w.sum(1, keepdims=True)
+    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w).cpu().numpy()
+    ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy(), ids, w)
+    assert np.isfinite(out).all()
+    assert oracle.maxrel(out, ref) <= 1e-3, oracle.maxrel(out, ref)
+    assert oracle.rel_fro(out, ref) <= 5e-3
