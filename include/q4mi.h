@@ -345,6 +345,18 @@ int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const void* x, int 
                 int T, int E, int topk, int64_t H, int64_t F,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same block with the residual and a gated shared expert folded into the combine:
+ *   out[t] = (residual[t] + sum_j topk_w[t][j] * y[t][j]) + sigmoid(x[t] . sgw) * shared[t],
+ * residual f32 [T][H] (may be NULL, may alias out), shared f32 [T][H] (the shared expert's
+ * output) and shared_gate_w bf16 [H] (sgw), both NULL or both given. The gate's dot product
+ * runs in fp32. Replaces the routed-weight combine plus residual of moe_fin
+ * (designs/moe_combine/moe_fin.py:1-4, designs/moe_experts/moe_fin.cc; moe_acc.cc's sum). */
+int q4_moe_gemv_fin(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype,
+                    const int32_t* topk_ids, const float* topk_w, const float* residual,
+                    const float* shared, const uint16_t* shared_gate_w, float* out,
+                    int T, int E, int topk, int64_t H, int64_t F,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,8 @@ SIGNATURES = {
                                _vp]),
     "q4_moe_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "q4_moe_gemv": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp, _sz, _vp]),
+    "q4_moe_gemv_fin": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp,
+                               _sz, _vp]),
 }
 
 _LIB = None

@@ -193,6 +193,47 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     out[idx] = s;
 }
 
+// The block output with the residual and the gated shared expert folded into the combine,
+// one workgroup per token (moe_fin, designs/moe_combine/moe_fin.py:1-4 and
+// designs/moe_experts/moe_fin.cc: out = xres + sum_j w y + sigmoid(xm . sgw) * shared):
+//   g = sigmoid(x[t] . sgw) (sgw bf16 [H], the dot product in fp32, fixed reduction order),
+//   out[t][n] = (res[t][n] + sum_j w[t][j] y_pair[t][j][n]) + g shared[t][n].
+// res may be null (no residual) and may alias out; shared null leaves the gate out.
+template <bool XF32>
+__global__ __launch_bounds__(256) void moe_fin_kernel(const float* __restrict__ ypair, const int32_t* __restrict__ ids,
+                                                      const float* __restrict__ w, int topk, int E, int H,
+                                                      const void* __restrict__ x, const uint16_t* __restrict__ sgw,
+                                                      const float* __restrict__ shared, const float* res, float* out) {
+    __shared__ float red[4];
+    const int64_t t = blockIdx.x;
+    float g = 0.f;
+    if (shared) {
+        float dot = 0.f;
+        for (int h = threadIdx.x; h < H; h += 256) {
+            const float xv = XF32 ? ((const float*)x)[t * H + h]
+                                  : bf16_hi_to_f32((uint32_t)((const uint16_t*)x)[t * H + h] << 16);
+            dot = __builtin_fmaf(xv, bf16_hi_to_f32((uint32_t)sgw[h] << 16), dot);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = dot;
+        __syncthreads();
+        dot = (red[0] + red[1]) + (red[2] + red[3]);
+        g = 1.0f / (1.0f + expf(-dot));
+    }
+    for (int n = threadIdx.x; n < H; n += 256) {
+        float s = 0.f;
+        for (int j = 0; j < topk; ++j) {
+            const int64_t p = t * topk + j;
+            const int e = ids[p];
+            if (e >= 0 && e < E) s += w[p] * ypair[p * H + n];
+        }
+        float v = res ? res[t * H + n] + s : s;
+        if (shared) v = __builtin_fmaf(g, shared[t * H + n], v);
+        out[t * H + n] = v;
+    }
+}
+
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
@@ -204,10 +245,14 @@ extern "C" size_t q4_moe_workspace_bytes(int T, int E, int topk, int H, int F) {
     return align256(P * F * 4) + align256(P * H * 4);
 }
 
-extern "C" int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype,
-                           const int32_t* topk_ids, const float* topk_w, float* out, int T, int E, int topk,
-                           int64_t H, int64_t F, void* workspace, size_t workspace_bytes, void* stream) {
+// The expert kernels, then the plain combine (fin == false) or the finish with residual and
+// gated shared expert (fin == true).
+static int moe_impl(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype, const int32_t* topk_ids,
+                    const float* topk_w, float* out, int T, int E, int topk, int64_t H, int64_t F, void* workspace,
+                    size_t workspace_bytes, void* stream, bool fin, const float* residual, const float* shared,
+                    const uint16_t* shared_gate_w) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (fin && (!shared) != (!shared_gate_w)) return Q4MI_E_ARG;
     if (H <= 0 || F <= 0 || H % 64 || F % 64) return Q4MI_E_SHAPE;
     if (H > (1 << 24) || F > (1 << 24)) return Q4MI_E_RANGE;
     if (T < 0 || E <= 0 || topk <= 0 || topk > 16 || (int64_t)T * topk > kMaxPairs) return Q4MI_E_RANGE;
@@ -260,8 +305,33 @@ extern "C" int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const vo
                                ypair);
     }
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    if (fin) {
+        if (x_dtype == Q4MI_F32)
+            hipLaunchKernelGGL(moe_fin_kernel<true>, dim3((unsigned)T), dim3(256), 0, st, ypair, topk_ids, topk_w, topk,
+                               E, (int)H, x, shared_gate_w, shared, residual, out);
+        else
+            hipLaunchKernelGGL(moe_fin_kernel<false>, dim3((unsigned)T), dim3(256), 0, st, ypair, topk_ids, topk_w,
+                               topk, E, (int)H, x, shared_gate_w, shared, residual, out);
+        return launch_status();
+    }
     const int64_t tot = (int64_t)T * H;
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st, ypair, topk_ids,
                        topk_w, T, topk, E, (int)H, out);
     return launch_status();
+}
+
+extern "C" int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype,
+                           const int32_t* topk_ids, const float* topk_w, float* out, int T, int E, int topk,
+                           int64_t H, int64_t F, void* workspace, size_t workspace_bytes, void* stream) {
+    return moe_impl(gate_up, down, x, x_dtype, topk_ids, topk_w, out, T, E, topk, H, F, workspace, workspace_bytes,
+                    stream, false, nullptr, nullptr, nullptr);
+}
+
+extern "C" int q4_moe_gemv_fin(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype,
+                               const int32_t* topk_ids, const float* topk_w, const float* residual,
+                               const float* shared, const uint16_t* shared_gate_w, float* out, int T, int E, int topk,
+                               int64_t H, int64_t F, void* workspace, size_t workspace_bytes, void* stream) {
+    if ((residual && misaligned16(residual)) || (shared && misaligned16(shared))) return Q4MI_E_ARG;
+    return moe_impl(gate_up, down, x, x_dtype, topk_ids, topk_w, out, T, E, topk, H, F, workspace, workspace_bytes,
+                    stream, true, residual, shared, shared_gate_w);
 }

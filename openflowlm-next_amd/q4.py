@@ -854,10 +854,17 @@ def pack_moe_experts(gate_blocks, up_blocks, down_blocks, device=None):
 
 
 def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
-              out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+              out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+              residual: torch.Tensor | None = None, shared: torch.Tensor | None = None,
+              shared_gate_w=None) -> torch.Tensor:
     """out[t] = sum_j w[t,j] * down_e(silu(gate_e x_t) * (up_e x_t)), e = ids[t,j]; fp32 h,
     fp32 out [T, H] (moe_batch.py's per-slot product plus core.cpp:5150-5245's
-    gather/scatter, done on the device)."""
+    gather/scatter, done on the device).
+
+    With ``residual`` (f32 [T, H], may be ``out``) and/or ``shared`` (the shared expert's
+    f32 [T, H] output) with ``shared_gate_w`` (sgw, [H], rounded to bf16 if given wider),
+    the block's finish is folded into the combine, as moe_fin does
+    (designs/moe_combine/moe_fin.py:1-4): out = (residual + routed sum) + sigmoid(x . sgw) * shared."""
     dev = gate_up.data.device
     xt = _acts(x, dev)
     if xt.dim() == 1:
@@ -876,10 +883,30 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
     topk = ids.shape[1]
     if out is None:
         out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    if (shared is None) != (shared_gate_w is None):
+        raise ValueError("shared and shared_gate_w go together")
+    for name, t_ in (("residual", residual), ("shared", shared)):
+        if t_ is not None and (t_.dtype != torch.float32 or not t_.is_contiguous() or t_.numel() != T * H
+                               or t_.device != dev):
+            raise ValueError(f"{name} must be a contiguous float32 [{T}, {H}] tensor on {dev}")
+    sgw = None
+    if shared_gate_w is not None:
+        sgw = _to_dev(shared_gate_w, dev)
+        if sgw.dtype != torch.bfloat16:
+            sgw = sgw.to(torch.float32).to(torch.bfloat16)
+        sgw = sgw.contiguous().reshape(-1)
+        if sgw.numel() != H:
+            raise ValueError(f"shared_gate_w must have {H} values, got {sgw.numel()}")
     lib = _lib_handle()
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_moe_workspace_bytes(T, E, topk, H, F), "moe", workspace)
-        check("q4_moe_gemv", lib.q4_moe_gemv(
-            _ptr(gate_up.data), _ptr(down.data), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts), _ptr(out),
-            T, E, topk, H, F, wp, wn, _stream(dev)))
+        if residual is None and shared is None:
+            check("q4_moe_gemv", lib.q4_moe_gemv(
+                _ptr(gate_up.data), _ptr(down.data), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts), _ptr(out),
+                T, E, topk, H, F, wp, wn, _stream(dev)))
+        else:
+            check("q4_moe_gemv_fin", lib.q4_moe_gemv_fin(
+                _ptr(gate_up.data), _ptr(down.data), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts),
+                None if residual is None else _ptr(residual), None if shared is None else _ptr(shared),
+                None if sgw is None else _ptr(sgw), _ptr(out), T, E, topk, H, F, wp, wn, _stream(dev)))
     return out

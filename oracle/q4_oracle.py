@@ -397,6 +397,21 @@ def moe_reference(gate_w, up_w, down_w, x: np.ndarray, ids: np.ndarray, wts: np.
 # eight k of row lane%16 in k-group lane//16), so one 128-bit load per lane
 # feeds four MFMAs (r = 0..3) and a wave streams 1 KB per load.
 
+
+def moe_fin_reference(moe_out: np.ndarray, residual, shared, x: np.ndarray, sgw_bf16_bits) -> np.ndarray:
+    """The MoE block's finish in fp64: out = xres + acc + sigmoid(xm . sgw) * shared
+    (designs/moe_combine/moe_fin.py:1-4; designs/moe_experts/moe_fin.cc), acc the routed
+    sum (moe_reference), xm the block's input rows, sgw the shared-expert gate vector as
+    bf16 bits [H]. ``residual`` / ``shared`` may be None (that term left out)."""
+    out = np.asarray(moe_out, np.float64).copy()
+    if residual is not None:
+        out += np.asarray(residual, np.float64)
+    if shared is not None:
+        sgw = (np.asarray(sgw_bf16_bits, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        g = 1.0 / (1.0 + np.exp(-(np.atleast_2d(np.asarray(x, np.float64)) @ sgw)))
+        out += g[:, None] * np.asarray(shared, np.float64)
+    return out
+
 def mx_bytes(n: int, k: int) -> int:
     assert n % MX_ROWS == 0 and k % BLK == 0
     return (n // MX_ROWS) * (k // BLK) * MX_TILE

@@ -195,3 +195,18 @@ def test_native_q8_argument_errors(lib):
     need = lib.q4_gemv_q8_native_workspace_bytes(1, 1024, 4096)
     assert need > 0
     assert lib.q4_gemv_q8_native(fake, fake, 1, None, fake, 1, 1024, 4096, fake, need - 1, None) == -3
+
+
+def test_moe_fin_argument_errors(lib):
+    """q4_moe_gemv_fin refuses a shared expert without its gate weights (and the reverse),
+    misaligned residual / shared pointers and a short workspace, all before any launch."""
+    fake = C.c_void_p(0x1000)
+    odd = C.c_void_p(0x1004)
+    ws = lib.q4_moe_workspace_bytes(16, 128, 8, 2048, 768)
+    args = lambda res, sh, sgw, wsb: (fake, fake, fake, 1, fake, fake, res, sh, sgw, fake, 16, 128, 8, 2048, 768,
+                                      fake, wsb, None)
+    assert lib.q4_moe_gemv_fin(*args(None, fake, None, ws)) == -2      # shared without sgw
+    assert lib.q4_moe_gemv_fin(*args(None, None, fake, ws)) == -2      # sgw without shared
+    assert lib.q4_moe_gemv_fin(*args(odd, None, None, ws)) == -2       # misaligned residual
+    assert lib.q4_moe_gemv_fin(*args(None, odd, fake, ws)) == -2       # misaligned shared
+    assert lib.q4_moe_gemv_fin(*args(fake, fake, fake, ws - 1)) == -3  # short workspace

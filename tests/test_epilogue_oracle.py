@@ -47,3 +47,24 @@ def test_swiglu_reference_composes_the_gemv_reference(oracle):
     gg = oracle.gemv_reference(g, x).astype(np.float64)
     uu = oracle.gemv_reference(u, x).astype(np.float64)
     assert np.allclose(h, gg * expit(gg) * uu, rtol=1e-5, atol=1e-7)
+
+
+def test_moe_fin_reference_pins(oracle):
+    """moe_fin_reference (moe_fin.py:1-4): the gate against scipy's expit of the dot product,
+    sgw = 0 gives the gate 0.5 exactly, no shared expert leaves residual + routed sum, and
+    neither term leaves the routed sum alone."""
+    from scipy.special import expit
+    rng = np.random.default_rng(11)
+    T, H = 5, 64
+    acc = rng.standard_normal((T, H))
+    res = rng.standard_normal((T, H))
+    sh = rng.standard_normal((T, H))
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    sgw = oracle.f32_to_bf16(rng.standard_normal(H).astype(np.float32) * 0.1)
+    sgw_f = (sgw.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    g = expit(x.astype(np.float64) @ sgw_f)
+    assert np.allclose(oracle.moe_fin_reference(acc, res, sh, x, sgw), res + acc + g[:, None] * sh, rtol=1e-14, atol=0)
+    zero = np.zeros(H, np.uint16)
+    assert np.array_equal(oracle.moe_fin_reference(acc, res, sh, x, zero), res + acc + 0.5 * sh)
+    assert np.array_equal(oracle.moe_fin_reference(acc, res, None, x, None), acc + res)
+    assert np.array_equal(oracle.moe_fin_reference(acc, None, None, x, None), acc)

@@ -114,3 +114,34 @@ def test_moe_few_pairs_path_with_popular_experts(gpu, pkg, oracle):
     assert np.isfinite(out).all()
     assert oracle.maxrel(out, ref) <= 1e-3, oracle.maxrel(out, ref)
     assert oracle.rel_fro(out, ref) <= 5e-3
+
+
+@pytest.mark.parametrize("E,H,F,T,K,xdt", [(16, 512, 256, 6, 4, "bf16"), (8, 256, 128, 5, 3, "f32")])
+def test_moe_fin_residual_and_shared_expert(gpu, pkg, oracle, E, H, F, T, K, xdt):
+    """The block's finish folded into the combine (moe_fin.py:1-4):
+    out = (residual + routed sum) + sigmoid(x . sgw) * shared. Against fp64 of the same
+    formula; the residual-only form equals moe_batch + residual bit for bit; sgw = 0 gives the
+    gate 0.5 exactly; the residual may be the output buffer."""
+    say(f"moe fin E={E} H={H} F={F} T={T} top{K} {xdt}")
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 900 + H)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xt = (torch.from_numpy(x).to(torch.bfloat16) if xdt == "bf16" else torch.from_numpy(x)).to(gpu)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    res = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(gpu)
+    sh = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(gpu)
+    sgw = torch.from_numpy(rng.standard_normal(H).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu)
+    out = pkg.moe_batch(gu, dn, xt, ids, w, residual=res, shared=sh, shared_gate_w=sgw).cpu().numpy()
+    xr = xt.to(torch.float32).cpu().numpy()
+    acc = oracle.moe_reference(g_of, u_of, d_of, xr, ids, w)
+    ref = oracle.moe_fin_reference(acc, res.cpu().numpy(), sh.cpu().numpy(), xr, sgw.cpu().view(torch.int16).numpy().view(np.uint16))
+    assert np.isfinite(out).all()
+    assert oracle.maxrel(out, ref) <= 1e-3, oracle.maxrel(out, ref)
+    plain = pkg.moe_batch(gu, dn, xt, ids, w)
+    only_res = pkg.moe_batch(gu, dn, xt, ids, w, residual=res)
+    assert torch.equal(only_res, res + plain)
+    half = pkg.moe_batch(gu, dn, xt, ids, w, residual=res, shared=sh,
+                         shared_gate_w=torch.zeros(H, dtype=torch.bfloat16, device=gpu))
+    assert torch.equal(half, (res + plain) + 0.5 * sh)
+    acc_buf = res.clone()
+    pkg.moe_batch(gu, dn, xt, ids, w, out=acc_buf, residual=acc_buf, shared=sh, shared_gate_w=sgw)
+    assert np.array_equal(acc_buf.cpu().numpy(), out)
