@@ -732,8 +732,10 @@ PrefillPlan make_plan_uncached(int T, int64_t N, int64_t K) {
             const char* e = getenv("Q4MI_PREFILL_NARROW");
             return e ? atoi(e) : -1;
         }();
-        // kNarrowRel: a 192-row tile's time relative to a 256-row tile's over the same stages
-        constexpr double kStageSec = 1.0e-6, kReduceBytesPerSec = 4.0e12, kNarrowRel = 0.8;
+        // kNarrowRel: a 192-row tile's time relative to a 256-row tile's over the same stages,
+        // measured: gate_up at T = 2048 took 236.6 us as 2 rounds of 256-row tiles and 224.9 us
+        // as 1 round of each, so the 192-row round ran at ~0.9 of a 256-row one.
+        constexpr double kStageSec = 1.0e-6, kReduceBytesPerSec = 4.0e12, kNarrowRel = 0.9;
         const int nst = (int)(K / 64), cap = nst < 16 ? nst : 16;
         const int64_t G = N / 64, tt = p.tiles_t;
         const int cus = device_cus();
