@@ -326,7 +326,9 @@ __device__ __forceinline__ uint32_t bf16_ceil_bits(float x) {           // towar
 // operation rounded on its own (no fused multiply-add): v = code * scale (exact); m = the
 // block minimum rounded down to bf16; d = (max - m) / 15 rounded up to bf16, so
 // [m, m + 15 d] covers the block; nibble = clamp(trunc((v - m) * (1 / d) + 0.5), 0, 15).
-// A -0 product (a negative code under a zero scale) is read as +0.
+// The block's min and max are scanned as the reference's C++ does (pools.cpp:591-601):
+// start at lane 0 and replace only on a strict < or >, so the first lane holding the
+// extreme keeps its sign (a leading -0, a negative code under a zero scale, gives m = -0).
 __global__ __launch_bounds__(256) void repack_q8_chunk_kernel(const uint8_t* __restrict__ chunks, int rs,
                                                               uint8_t* __restrict__ packed, int64_t N,
                                                               int64_t KB) {
@@ -340,12 +342,13 @@ __global__ __launch_bounds__(256) void repack_q8_chunk_kernel(const uint8_t* __r
     const float sc = bf16_hi_to_f32((uint32_t)((const uint16_t*)ch)[kbl * 32 + r] << 16);
     const int8_t* cp = (const int8_t*)(ch + 512 + (r >> 4) * 4096 + kbl * 512 + (r & 15));
     float v[32];
-    float mn = __builtin_inff(), mx = -__builtin_inff();
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        v[i] = __fadd_rn(__fmul_rn((float)cp[i * 16], sc), 0.0f);     // -0 (zero scale) read as +0
-        mn = fminf(mn, v[i]);
-        mx = fmaxf(mx, v[i]);
+    for (int i = 0; i < 32; ++i) v[i] = __fmul_rn((float)cp[i * 16], sc);
+    float mn = v[0], mx = v[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) {
+        mn = v[i] < mn ? v[i] : mn;
+        mx = v[i] > mx ? v[i] : mx;
     }
     const uint32_t m_u = bf16_floor_bits(mn);
     const float m = bf16_hi_to_f32(m_u << 16);

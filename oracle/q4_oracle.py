@@ -40,10 +40,14 @@ the exact Q4_0 identity m = -8 d.  The Q4_K functions are pinned in
 ``tests/test_gguf.py``: against the reference's own C++ GGUF reader, built from
 its sources into ``oracle/_ref/gguf_dump`` (bit-exact f32 dequant), by an
 exhaustive encode -> decode of the packed 6-bit scales, a closed-form block,
-and the reference's property checks of the container transcode (the published
-FNV-1a of that transcode is not reproduced; the test records it as a strict
-xfail).  Functions with no such check are marked
-"parity unpinned" in their docstrings (there are none at present).
+and the reference's property checks of the container transcode.  The chunk
+transcodes (``requant_q4_1``, ``q4k_chunks_to_pool``, ``signed_pool_to_q4_1``,
+``split_q8_chunks``) are pinned in ``tests/test_pools_ref.py`` byte for byte
+against the reference's own C++ (src/open_qwen36/pools.cpp, built from its
+sources into ``oracle/_ref/pools_dump``) and by the reference's published FNV-1a
+goldens (``fnv1a64`` uses the reference's offset basis).  Functions with no such
+check are marked "parity unpinned" in their docstrings (there are none at
+present).
 
 The MI355X weight layouts (``pack_mx`` / ``unpack_mx``, and the native Q4_K
 ``pack_mxk_*`` / ``unpack_mxk``) are this build's own formats, not the
@@ -767,12 +771,42 @@ def pack_mxk_q4k_chunks(chunks: np.ndarray, n: int, k: int, rs: int) -> np.ndarr
     return pack_mxk_from_parts(*q4k_chunks_native_parts(chunks, n, k, rs))
 
 
-def fnv1a64(data) -> int:
-    """FNV-1a 64-bit hash of a byte string (test_pack_plan.py:183-187)."""
-    h = 0xCBF29CE484222325
-    for x in bytes(data):
-        h = ((h ^ x) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+# The offset basis the reference's hash starts from: 1469598103934665603
+# (specs/open-engine/tests/test_pack_plan.py:184, src/open_qwen36/pools_test.cpp:84). It is
+# the textbook FNV-1a basis 14695981039346656037 with its last digit dropped, so the
+# reference's goldens are hashes under this basis, not under the textbook one.
+FNV_BASIS_REF = 1469598103934665603
+FNV_BASIS_TEXTBOOK = 0xCBF29CE484222325
+FNV_PRIME = 0x100000001B3          # 1099511628211, the same in both
+
+
+def fnv1a64(data, basis: int = FNV_BASIS_REF) -> int:
+    """FNV-1a 64-bit hash of a byte string as the reference computes it
+    (test_pack_plan.py:183-187, pools_test.cpp:83-90): its own offset basis by default;
+    ``basis=FNV_BASIS_TEXTBOOK`` gives the published FNV-1a."""
+    b = np.frombuffer(bytes(data), np.uint8)
+    h = basis
+    # byte loop in chunks of numpy-free Python ints (the hash is sequential)
+    for x in b.tolist():
+        h = ((h ^ x) * FNV_PRIME) & 0xFFFFFFFFFFFFFFFF
     return h
+
+
+def shared_q8_vector(nch: int) -> np.ndarray:
+    """The q8 chunks both reference packers hash (test_qwen35.py:668-684,
+    src/open_qwen36/pools_test.cpp:60-80): per chunk an LCG seeded 0x9E3779B9 * (c + 1),
+    256 bf16 scales 0x3B00 | (s >> 24), then 8192 code bytes s >> 24."""
+    M32 = 0xFFFFFFFF
+    out = np.zeros((nch, Q8_CHUNK), np.uint8)
+    for c in range(nch):
+        s = (0x9E3779B9 * (c + 1)) & M32
+        stream = np.empty(256 + 8192, np.uint32)
+        for i in range(256 + 8192):
+            s = (s * 1664525 + 1013904223) & M32
+            stream[i] = s >> 24
+        out[c, :512] = (np.uint32(0x3B00) | stream[:256]).astype(np.uint16).view(np.uint8)
+        out[c, 512:] = stream[256:].astype(np.uint8)
+    return out
 
 
 # --------------------------------------------------------------------------
@@ -893,14 +927,18 @@ def requant_q4_1(chunks: np.ndarray) -> np.ndarray:
     """q8 chunks [n, 8704] -> q4_1 chunks [n, 5120], block for block (recipes/pack.py:
     224-263): m = block min rounded down to bf16; d = f32((max - m) / 15) rounded up to
     bf16; nibble = clip(trunc(f32(f32(v - m) * f32(1 / d)) + 0.5), 0, 15), each f32
-    operation rounded on its own. A -0 value (a negative code under a zero scale, which
-    no quantiser writes) is read as +0, so the block minimum has one sign whichever way
-    a min reduction breaks the tie between the zeros."""
-    v = q8_chunk_values(chunks) + np.float32(0.0)                # [n, r, block, lane]; -0 read as +0
+    operation rounded on its own. The block's min and max are taken as the reference's
+    C++ scans them (pools.cpp:591-601: start at lane 0, replace only on a strict < or >),
+    i.e. the first lane holding the extreme value keeps its sign: a -0 (a negative code
+    under a zero scale) that comes first makes m = bf16 -0 (0x8000)."""
+    v = q8_chunk_values(chunks)                                  # [n, r, block, lane]
     n = v.shape[0]
-    m_u = _bf16_floor(v.min(-1))
+    first_min = np.argmax(v == v.min(-1, keepdims=True), axis=-1)[..., None]
+    m_u = _bf16_floor(np.take_along_axis(v, first_min, -1)[..., 0])
     m = bf16_to_f32(m_u)
-    d_u = _bf16_ceil(((v.max(-1) - m).astype(np.float32) / np.float32(15)).astype(np.float32))
+    first_max = np.argmax(v == v.max(-1, keepdims=True), axis=-1)[..., None]
+    mx = np.take_along_axis(v, first_max, -1)[..., 0]
+    d_u = _bf16_ceil(((mx - m).astype(np.float32) / np.float32(15)).astype(np.float32))
     d = bf16_to_f32(d_u)
     inv = np.where(d > 0, np.float32(1) / np.where(d > 0, d, np.float32(1)), np.float32(0)).astype(np.float32)
     t = ((v - m[..., None]).astype(np.float32) * inv[..., None]).astype(np.float32) + np.float32(0.5)
@@ -973,6 +1011,23 @@ def q8_split_parts(s16: np.ndarray, q: np.ndarray, part: int):
     if part == 0:
         return f32_to_bf16(np.float32(16) * s), f32_to_bf16(np.float32(-128) * s), ((q >> 4) + 8).astype(np.uint8)
     return s16.copy(), np.zeros_like(s16), (q & 15).astype(np.uint8)
+
+
+def split_q8_chunks(chunks: np.ndarray, part: int) -> np.ndarray:
+    """q8 chunks [n, 8704] -> 5120 B q4_1 chunks of one plane of the exact split, in the
+    same chunk order (split_q8_q4_1, recipes/pack.py:94-117; pools.cpp split_q4_1_chunks):
+    the scales at the same meta index, built by q8_split_parts; code i of the q8 chunk is
+    nibble i of the q4_1 chunk (even i low), since the two formats share the code raster."""
+    src = np.asarray(chunks, np.uint8).reshape(-1, Q8_CHUNK)
+    n = src.shape[0]
+    s16 = np.ascontiguousarray(src[:, :512]).view(np.uint16)
+    code = np.ascontiguousarray(src[:, 512:]).view(np.int8)
+    d16, m16, q = q8_split_parts(s16, code, part)
+    out = np.zeros((n, CH), np.uint8)
+    out[:, :512] = np.ascontiguousarray(d16, np.uint16).view(np.uint8).reshape(n, 512)
+    out[:, 512:1024] = np.ascontiguousarray(m16, np.uint16).view(np.uint8).reshape(n, 512)
+    out[:, 1024:] = q[:, 0::2] | (q[:, 1::2] << 4)
+    return out
 
 
 def q8_values(s16: np.ndarray, q: np.ndarray) -> np.ndarray:

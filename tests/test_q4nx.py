@@ -9,9 +9,10 @@ Pins, each independent of the formula it checks:
 * the q8 requant: the reference's own property test (test_qwen35.py:631-654: every value
   within d/2 of its reading, a real quantisation) plus the directed-rounding bounds
   (m <= block min, m + 15 d >= block max) and exactness on constant blocks.
-* The reference's FNV-1a goldens for these byte layouts do not reproduce -- not even the
-  one over a plain transpose of a fixed byte pattern (test_qwen35.py:701-702) -- so they
-  are recorded as strict xfails, not used as pins.
+* the reference's FNV-1a goldens over its shared q8 vector (test_qwen35.py:694-703,
+  :890-903; pools_test.cpp:33-53): requant_q4_1, the exact split's hi and lo planes and a
+  plain transpose, each reproduced by the oracle byte for byte (the reference hashes from
+  its own offset basis, 1469598103934665603).
 """
 from __future__ import annotations
 
@@ -156,27 +157,36 @@ def _fnv(oracle, b):
     return oracle.fnv1a64(bytes(b))
 
 
-@pytest.mark.xfail(strict=True, reason="the reference's FNV-1a goldens do not reproduce, even this one over a "
-                   "plain transpose of a fixed byte pattern (test_qwen35.py:701-702); none is used as a pin")
 def test_reference_transpose_golden(oracle):
+    """test_qwen35.py:700-702: FNV-1a of a plain transpose of (i*37+11) & 0xFF."""
     t = np.frombuffer(bytes(((i * 37 + 11) & 0xFF) for i in range(32 * 64 * 2)), np.uint8)
     td = np.ascontiguousarray(t.reshape(32, 64, 2).transpose(1, 0, 2)).reshape(-1)
     assert _fnv(oracle, td) == 0xB27D0B6F7149FD83
 
 
-@pytest.mark.xfail(strict=True, reason="see test_reference_transpose_golden (test_qwen35.py:699)")
+def test_shared_q8_vector_follows_the_lcg(oracle):
+    """The vector both reference packers hash, checked by hand against its LCG for the
+    first chunk's first scale and code."""
+    v = oracle.shared_q8_vector(2)
+    s = 0x9E3779B9
+    s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+    assert int(v[0, :2].view(np.uint16)[0]) == 0x3B00 | (s >> 24)
+    for _ in range(256):
+        s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+    assert int(v[0, 512]) == s >> 24
+    assert v.shape == (2, 8704)
+
+
 def test_reference_requant_golden(oracle):
-    M32 = 0xFFFFFFFF
-    out = np.zeros((12, 8704), np.uint8)
-    for c in range(12):                                  # _shared_q8_vector (test_qwen35.py:668-684)
-        s = (0x9E3779B9 * (c + 1)) & M32
-        stream = []
-        for _ in range(256 + 8192):
-            s = (s * 1664525 + 1013904223) & M32
-            stream.append(s >> 24)
-        out[c, :512] = (0x3B00 | np.array(stream[:256], np.uint32)).astype(np.uint16).view(np.uint8)
-        out[c, 512:] = np.array(stream[256:], np.uint8)
-    assert _fnv(oracle, oracle.requant_q4_1(out)) == 0x4AC3BABAD266DD49
+    """test_qwen35.py:698-699 (and pools_test.cpp:37): requant_q4_1 of the shared vector."""
+    assert _fnv(oracle, oracle.requant_q4_1(oracle.shared_q8_vector(12))) == 0x4AC3BABAD266DD49
+
+
+def test_reference_split_goldens(oracle):
+    """test_qwen35.py:902-903: the exact q8 split's hi and lo chunks of the shared vector."""
+    v = oracle.shared_q8_vector(12)
+    assert _fnv(oracle, oracle.split_q8_chunks(v, 0)) == 0x011857DF63D905CE
+    assert _fnv(oracle, oracle.split_q8_chunks(v, 1)) == 0x1A95B8AE739769D2
 
 
 def test_q8_split_planes_sum_to_the_q8_values_exactly(oracle):
