@@ -86,14 +86,15 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     const CodeConsts kc = code_consts();
     const int64_t xrow = rows(token_of_row(i16));
-    // From NTL = 2 on (M > 4) only lanes whose data reaches a stored output load it: MFMA
-    // row i16 (a token slot) past M feeds only its own, discarded output row, and a lane
-    // of k-group kg holds tokens kg, kg + 4, ..., so it needs the scales only when kg < M.
-    // The others keep zeros. Measured on 8 Llama-3-8B layers: M = 8 236.4 -> 230.1 us,
-    // M = 16 288.8 -> 279.7 us, bit-identical; at M <= 4 it gained nothing (M = 1 194.9
-    // -> 196.2 us), so one-accumulator instances load in every lane.
+    // From NTL = 2 on (M > 4) only lanes whose activation row reaches a stored output load
+    // it: MFMA row i16 (a token slot) past M feeds only its own, discarded output row, so
+    // those lanes keep a zero fragment. Every lane loads the scales (a lane of k-group kg
+    // holds tokens kg, kg + 4, ..., and kg <= 3 < M). Measured on 8 Llama-3-8B layers:
+    // M = 8 236.4 -> 230.1 us, M = 16 288.8 -> 279.7 us, bit-identical; at M <= 4 it
+    // gained nothing (M = 1 194.9 -> 196.2 us), so one-accumulator instances load in
+    // every lane.
     constexpr bool kPred = NTL >= 2;
-    const bool need_x = !kPred || token_of_row(i16) < rows.M, need_s = !kPred || kg < rows.M;
+    const bool need_x = !kPred || token_of_row(i16) < rows.M;
     u32x4 s[kUnroll];
     bf16x8 xh[kUnroll], xl[kUnroll];
 #pragma unroll
@@ -110,7 +111,7 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
             const int t = min(kb + kWaves * u, kb1 - 1);
             const uint8_t* tp = gbase + (int64_t)t * kTileBytes;      // wave-uniform tile base
             c[u] = load_nt_u32x4(tp + coff);
-            if (need_s) s[u] = load_nt_u32x4(tp + soff);
+            s[u] = load_nt_u32x4(tp + soff);
             if (need_x) load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
         }
 #pragma unroll

@@ -76,6 +76,28 @@ def _ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
+def _buf(t, name: str, dtype, shape, dev: torch.device) -> torch.Tensor:
+    """A caller's output / in-place buffer, or a new one of ``shape``. The kernels write
+    through raw device pointers with no byte count, so a buffer of the wrong dtype, element
+    count, layout or device would be written (or read) out of bounds: refuse it here."""
+    numel = 1
+    for v in shape:
+        numel *= int(v)
+    if t is None:
+        return torch.empty(shape, dtype=dtype, device=dev)
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch tensor, got {type(t)}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.numel() != numel:
+        raise ValueError(f"{name} must hold {numel} elements {tuple(shape)}, got {t.numel()} {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.device != dev:
+        raise ValueError(f"{name} must be on {dev}, got {t.device}")
+    return t
+
+
 def packed_bytes(n: int, k: int) -> int:
     """Bytes of the mx layout for an [n, k] matrix (n % 64 == 0, k % 32 == 0)."""
     b = _lib_handle().q4_packed_bytes(n, k)
@@ -135,10 +157,7 @@ def pack_q4_1(blocks, device=None, out: torch.Tensor | None = None) -> PackedQ4:
     n, nb, w = src.shape
     k = nb * BLK
     nbytes = packed_bytes(n, k)
-    if out is None:
-        out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    elif out.numel() < nbytes or out.dtype != torch.uint8:
-        raise ValueError("out is too small or not uint8")
+    out = _buf(out, "out", torch.uint8, (nbytes,), dev)
     with torch.cuda.device(dev):
         check("q4_repack", _lib_handle().q4_repack(_ptr(src), w, _ptr(out), n, k, 0, _stream(dev)))
     return PackedQ4(out[:nbytes], n, k)
@@ -262,8 +281,7 @@ def pack_q4_k_chunks_native(chunks, n: int, k: int, rs: int = 1, device=None) ->
 def dequant_q4k(w: PackedQ4K, out: torch.Tensor | None = None) -> torch.Tensor:
     """Native Q4_K layout -> f32[n, k], w = fl32(q (d sc) + m mn), bit-exact."""
     dev = w.device
-    if out is None:
-        out = torch.empty((w.n, w.k), dtype=torch.float32, device=dev)
+    out = _buf(out, "out", torch.float32, (w.n, w.k), dev)
     with torch.cuda.device(dev):
         check("q4_dequant_q4k", _lib_handle().q4_dequant_q4k(_ptr(w.data), _ptr(out), w.n, w.k, _stream(dev)))
     return out
@@ -282,8 +300,7 @@ def gemm_q4k(w: PackedQ4K, x, y: torch.Tensor | None = None, workspace: torch.Te
         raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
     if not 1 <= M <= 16:
         raise ValueError(f"gemm_q4k takes 1..16 tokens, got {M}")
-    if y is None:
-        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    y = _buf(y, "y", torch.float32, (M, w.n), dev)
     if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
                                  or residual.numel() != M * w.n or residual.device != dev):
         raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
@@ -398,8 +415,7 @@ def pack_q8_native(src, n: int, k: int, fmt: str = "chunks", rs: int = 1, device
 def dequant_q8_native(w: PackedQ8N, out: torch.Tensor | None = None) -> torch.Tensor:
     """mx8 -> f32[n, k], w = s * q (exact)."""
     dev = w.device
-    if out is None:
-        out = torch.empty((w.n, w.k), dtype=torch.float32, device=dev)
+    out = _buf(out, "out", torch.float32, (w.n, w.k), dev)
     with torch.cuda.device(dev):
         check("q4_dequant_q8_native", _lib_handle().q4_dequant_q8_native(_ptr(w.data), _ptr(out), w.n, w.k,
                                                                          _stream(dev)))
@@ -419,8 +435,7 @@ def gemm_q8_native(w: PackedQ8N, x, y: torch.Tensor | None = None, workspace: to
         raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
     if not 1 <= M <= 16:
         raise ValueError(f"gemm_q8_native takes 1..16 tokens, got {M}")
-    if y is None:
-        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    y = _buf(y, "y", torch.float32, (M, w.n), dev)
     if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
                                  or residual.numel() != M * w.n or residual.device != dev):
         raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
@@ -465,8 +480,7 @@ def pack_chunks(chunks, fmt: str, n: int, k: int, rs: int = 1, device=None) -> P
 def dequant(w: PackedQ4, out: torch.Tensor | None = None) -> torch.Tensor:
     """mx layout -> f32[n, k], w = fl32(q*d + m), bit-exact with dequant_pool."""
     dev = w.device
-    if out is None:
-        out = torch.empty((w.n, w.k), dtype=torch.float32, device=dev)
+    out = _buf(out, "out", torch.float32, (w.n, w.k), dev)
     with torch.cuda.device(dev):
         check("q4_dequant", _lib_handle().q4_dequant(_ptr(w.data), _ptr(out), w.n, w.k, _stream(dev)))
     return out
@@ -497,6 +511,10 @@ def _ws_arg(dev, nbytes: int, op: str, workspace):
     if workspace is None:
         ws = _workspace(dev, nbytes, op)
         return (_ptr(ws), ws.numel()) if ws is not None else (None, 0)
+    if not isinstance(workspace, torch.Tensor):
+        raise TypeError(f"workspace must be a torch tensor, got {type(workspace)}")
+    if workspace.device != dev or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous tensor on {dev}, got {workspace.device}")
     if workspace.numel() * workspace.element_size() < nbytes:
         raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, {nbytes} needed")
     return _ptr(workspace), workspace.numel() * workspace.element_size()
@@ -551,8 +569,7 @@ def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tens
         raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
     if not 1 <= M <= 16:
         raise ValueError(f"gemm_q4 takes 1..16 tokens, got {M} (use gemm_q4_prefill)")
-    if y is None:
-        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    y = _buf(y, "y", torch.float32, (M, w.n), dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
@@ -581,8 +598,7 @@ def gemm_q8(w: PackedQ8, x, y: torch.Tensor | None = None, workspace: torch.Tens
         raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
     if not 1 <= M <= 16:
         raise ValueError(f"gemm_q8 takes 1..16 tokens, got {M}")
-    if y is None:
-        y = torch.empty((M, w.n), dtype=torch.float32, device=dev)
+    y = _buf(y, "y", torch.float32, (M, w.n), dev)
     if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
                                  or residual.numel() != M * w.n or residual.device != dev):
         raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
@@ -612,10 +628,7 @@ def swiglu_q4(gate: PackedQ4, up: PackedQ4, x, out_dtype=torch.float32, h: torch
         raise ValueError(f"x has K={K}, gate/up are [{gate.n}, {gate.k}]")
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise TypeError("out_dtype must be float32 or bfloat16")
-    if h is None:
-        h = torch.empty((M, gate.n), dtype=out_dtype, device=dev)
-    elif h.dtype != out_dtype or not h.is_contiguous() or h.numel() != M * gate.n:
-        raise ValueError(f"h must be a contiguous {out_dtype} [{M}, {gate.n}] tensor")
+    h = _buf(h, "h", out_dtype, (M, gate.n), dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_gemv_swiglu_workspace_bytes(M, gate.n, gate.k), "swiglu", workspace)
@@ -638,12 +651,17 @@ def rmsnorm_add(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None = Non
     if w.numel() != N or w.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError(f"w must be float32 or bfloat16 with {N} values")
     wt = w.to(dev).contiguous()
-    if add is not None and (add.shape != x.shape or add.dtype != torch.float32 or not add.is_contiguous()):
-        raise ValueError("add must be a contiguous float32 tensor shaped like x")
-    if y is None and add is not None:
-        y = torch.empty_like(x)
-    if xn is None:
-        xn = torch.empty(x.shape, dtype=out_dtype, device=dev)
+    if add is not None:
+        add = _buf(add, "add", torch.float32, tuple(x.shape), dev)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("out_dtype must be float32 or bfloat16")
+    if y is not None or add is not None:
+        y = _buf(y, "y", torch.float32, tuple(x.shape), dev)
+    if y is not None and N > 16384 and y.data_ptr() == x.data_ptr():
+        raise ValueError("y may alias x only for rows of <= 16384 values")
+    xn = _buf(xn, "xn", out_dtype if xn is None else xn.dtype, tuple(x.shape), dev)
+    if xn.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"xn must be float32 or bfloat16, got {xn.dtype}")
     with torch.cuda.device(dev):
         check("q4_rmsnorm_add", _lib_handle().q4_rmsnorm_add(
             _ptr(x), None if add is None else _ptr(add), _ptr(wt), Q4MI_BF16 if wt.dtype == torch.bfloat16 else Q4MI_F32,
@@ -657,7 +675,9 @@ def gemv_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tens
     xt = _acts(x, w.device)
     if xt.dim() != 1:
         raise ValueError("gemv_q4 takes one activation vector x[K]")
-    out = gemm_q4(w, xt.unsqueeze(0), None if y is None else y.view(1, -1), workspace)
+    if y is not None:
+        y = _buf(y, "y", torch.float32, (w.n,), w.device).view(1, -1)
+    out = gemm_q4(w, xt.unsqueeze(0), y, workspace)
     return out.view(-1)
 
 
@@ -675,14 +695,9 @@ def _topk_mode(mode) -> int:
 
 
 def _topk_outputs(M: int, k: int, dev, ids, vals):
-    if ids is None:
-        ids = torch.empty((M, k), dtype=torch.int32, device=dev)
-    if vals is None:
-        vals = torch.empty((M, k), dtype=torch.float32, device=dev)
-    if ids.dtype != torch.int32 or vals.dtype != torch.float32 or ids.numel() < M * k or vals.numel() < M * k \
-            or not ids.is_contiguous() or not vals.is_contiguous():
-        raise ValueError("ids must be int32 and vals float32, contiguous, M*k elements each")
-    return ids, vals
+    if not 1 <= k <= 64:
+        raise ValueError(f"k must be in 1..64, got {k}")
+    return _buf(ids, "ids", torch.int32, (M, k), dev), _buf(vals, "vals", torch.float32, (M, k), dev)
 
 
 def logits_topk(logits: torch.Tensor, k: int = 1, mode: str = "sampler", n_valid: int | None = None,
@@ -702,6 +717,8 @@ def logits_topk(logits: torch.Tensor, k: int = 1, mode: str = "sampler", n_valid
         raise ValueError("logits rows must be contiguous")
     M, N = lg.shape
     n = N if n_valid is None else int(n_valid)
+    if not 0 <= n <= N:
+        raise ValueError(f"n_valid must be in 0..{N}, got {n}")
     dev = lg.device
     ids, vals = _topk_outputs(M, k, dev, ids, vals)
     lib = _lib_handle()
@@ -726,10 +743,9 @@ def lm_head_topk(w: PackedQ4, x, k: int = 1, mode: str = "sampler", n_valid: int
     if K != w.k:
         raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
     n = w.n if n_valid is None else int(n_valid)
-    if logits is None:
-        logits = torch.empty((M, w.n), dtype=torch.float32, device=dev)
-    elif logits.dtype != torch.float32 or not logits.is_contiguous() or logits.numel() < M * w.n:
-        raise ValueError("logits must be a contiguous float32 [M, N] tensor")
+    if not 0 <= n <= w.n:
+        raise ValueError(f"n_valid must be in 0..{w.n}, got {n}")
+    logits = _buf(logits, "logits", torch.float32, (M, w.n), dev)
     ids, vals = _topk_outputs(M, k, dev, ids, vals)
     lib = _lib_handle()
     with torch.cuda.device(dev):
@@ -811,8 +827,9 @@ def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: st
     if xt.dim() != 2 or xt.shape[1] != w.k:
         raise ValueError(f"x must be [T, {w.k}], got {tuple(xt.shape)}")
     T = xt.shape[0]
-    if y is None:
-        y = torch.empty((T, w.n), dtype=torch.float32, device=dev)
+    if precision not in _PRECISION:
+        raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
+    y = _buf(y, "y", torch.float32, (T, w.n), dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_gemm_prefill_workspace_bytes(T, w.n, w.k), "prefill", workspace)
@@ -881,8 +898,7 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
     if ids.shape[0] != T or ids.shape != wts.shape:
         raise ValueError("topk_ids / topk_w must be [T, topk]")
     topk = ids.shape[1]
-    if out is None:
-        out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    out = _buf(out, "out", torch.float32, (T, H), dev)
     if (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w go together")
     for name, t_ in (("residual", residual), ("shared", shared)):

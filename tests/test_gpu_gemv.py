@@ -194,30 +194,61 @@ def test_repeated_calls_are_deterministic(gpu, pkg, oracle):
         assert pkg.gemv_q4(w, x).cpu().numpy().tobytes() == first.tobytes()
 
 
-@pytest.mark.parametrize("M", [1, 4])
-def test_grouped_gemv(gpu, pkg, oracle, M):
-    say(f"grouped gemv M={M}")
+# Every Llama-3-8B decode shape of config 1 but lm_head (q/o, k/v, gate/up, down, the
+# fused qkv and gate/up buffers), plus ragged small matrices: the grouped kernel's table
+# search crosses every kind of boundary.
+GROUP_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (6144, 4096), (64, 4096),
+                (128, 256), (28672, 4096)]
+_GROUP_CACHE: dict = {}
+
+
+def _group_weights(oracle, gpu, pkg):
+    """Blocks, f64 weights and packed matrices of GROUP_SHAPES, built once per session."""
+    if "w" not in _GROUP_CACHE:
+        rng = np.random.default_rng(300)
+        out = []
+        for (n, k) in GROUP_SHAPES:
+            blocks = oracle.baseline_q4_1_blocks(n, k, rng)
+            out.append((oracle.dequant_q4_1(blocks).astype(np.float64), pkg.pack_q4_1(blocks, gpu)))
+        _GROUP_CACHE["w"] = out
+    return _GROUP_CACHE["w"]
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("M", [1, 4, 5, 8, 13, 16])
+def test_grouped_gemv(gpu, pkg, oracle, M, xdt):
+    """The grouped kernel at every accumulator count (NTL = 1..4) the bench times, against
+    the fp64 reference, and each token row equal to that token run alone through the
+    single-matrix kernel up to fp32 summation order."""
+    say(f"grouped gemv M={M} x={xdt}")
     rng = np.random.default_rng(30 + M)
-    shapes = [(1024, 4096), (64, 4096), (4096, 14336), (128, 256), (14336, 4096)]
     items, refs = [], []
-    for (n, k) in shapes:
-        blocks = oracle.baseline_q4_1_blocks(n, k, rng)
-        X = _bf16(rng.standard_normal((M, k)))
-        w = pkg.pack_q4_1(blocks, gpu)
+    for (W, w) in _group_weights(oracle, gpu, pkg):
+        n, k = W.shape
+        X = rng.standard_normal((M, k)).astype(np.float32)
+        Xt = _bf16(X) if xdt == "bf16" else torch.from_numpy(X)
         y = torch.full((M, n), float("nan"), device=gpu)
-        items.append((w, X.to(gpu), y))
-        refs.append(oracle.gemv_reference(blocks, X.to(torch.float32).numpy()))
+        items.append((w, Xt.to(gpu), y))
+        refs.append(Xt.to(torch.float64).numpy() @ W.T)
     grp = pkg.GemvGroup(items)
     grp.run()
     torch.cuda.synchronize()
     for (w, X, y), ref in zip(items, refs):
         got = y.cpu().numpy()
         assert np.isfinite(got).all()
-        assert oracle.maxrel(got, ref) <= MAXREL
+        assert oracle.maxrel(got, ref) <= MAXREL, f"{w.shape}"
+        assert oracle.maxrel(got, ref) < REF_GATE and _cos(got, ref) > 0.9999999
     # the group agrees with single launches to fp32 summation-order noise
     for (w, X, y) in items:
         single = pkg.gemm_q4(w, X).cpu().numpy()
         assert oracle.maxrel(y.cpu().numpy(), single) < 1e-5
+    # a token row does not depend on the other tokens in the launch
+    if M > 1:
+        w, X, y = items[0]
+        lone = torch.full((1, w.n), float("nan"), device=gpu)
+        pkg.GemvGroup([(w, X[M - 1:M].contiguous(), lone)]).run()
+        torch.cuda.synchronize()
+        assert lone.cpu().numpy().tobytes() == y[M - 1:M].cpu().numpy().tobytes()
 
 
 def test_rejects_bad_shapes(gpu, pkg, oracle):

@@ -31,6 +31,7 @@ def _make(oracle, pkg, gpu, E, H, F, seed):
     (8, 256, 128, 3, 2, "bf16"),
     (128, 512, 256, 16, 8, "bf16"),      # config 4's routing (128 experts, top-8, 16 tokens), smaller matrices
     (16, 2048, 768, 16, 8, "bf16"),      # config 4's matrices (H=2048, F=768), 16 experts
+    (128, 2048, 768, 16, 8, "bf16"),     # config 4 exactly: 128 experts, top-8, 16 tokens, H=2048, F=768
     (4, 256, 192, 40, 2, "bf16"),        # ~20 tokens per expert: more than one 16-token chunk
     (8, 256, 128, 5, 3, "f32"),
     (8, 192, 128, 5, 2, "bf16"),         # H % 256 != 0: one 64-row group per down workgroup
@@ -116,7 +117,8 @@ def test_moe_few_pairs_path_with_popular_experts(gpu, pkg, oracle):
     assert oracle.rel_fro(out, ref) <= 5e-3
 
 
-@pytest.mark.parametrize("E,H,F,T,K,xdt", [(16, 512, 256, 6, 4, "bf16"), (8, 256, 128, 5, 3, "f32")])
+@pytest.mark.parametrize("E,H,F,T,K,xdt", [(16, 512, 256, 6, 4, "bf16"), (8, 256, 128, 5, 3, "f32"),
+                                            (128, 2048, 768, 16, 8, "bf16")])
 def test_moe_fin_residual_and_shared_expert(gpu, pkg, oracle, E, H, F, T, K, xdt):
     """The block's finish folded into the combine (moe_fin.py:1-4):
     out = (residual + routed sum) + sigmoid(x . sgw) * shared. Against fp64 of the same
