@@ -13,6 +13,14 @@
  * and keep no global state (calls that share one caller-owned workspace must
  * be ordered on one stream).
  *
+ * No entry point takes byte counts for its buffers: each pointer must cover the
+ * whole region its shape arguments name, in the dtype its enum names -- an
+ * activation X of M rows x K is M*K*4 bytes for Q4MI_F32 and M*K*2 for Q4MI_BF16,
+ * an f32 output Y[M][N] is M*N*4 bytes, a packed matrix q4_packed_bytes(N, K).
+ * A dtype enum that disagrees with the buffer reads or writes past its end (an
+ * f32 enum on a bf16 X reads 2*M*K bytes beyond it). The Python layer derives
+ * every enum from the tensor and checks every buffer before it calls in.
+ *
  * Weights live in the "mx" layout (see q4_packed_bytes): an [N, K] matrix,
  * N % 64 == 0, K % 32 == 0, cut into tiles of 64 rows x 32 K (one GGUF block
  * column) of 1280 bytes: 1024 B of 4-bit codes laid out as the B operand of a
