@@ -11,7 +11,8 @@
  * otherwise; the descriptors of q4_gemv_grouped are the caller's to check). Work is enqueued
  * on `stream` and is asynchronous to the host; the functions are re-entrant
  * and keep no global state (calls that share one caller-owned workspace must
- * be ordered on one stream).
+ * be ordered on one stream), except q4_gemv_noalloc, whose scratch is one
+ * static device array per device (see there).
  *
  * No entry point takes byte counts for its buffers: each pointer must cover the
  * whole region its shape arguments name, in the dtype its enum names -- an
@@ -200,6 +201,22 @@ size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K);
 int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
             int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
             void* stream);
+
+/* Bytes of the device array q4_gemv_noalloc keeps its K-split partial sums in (8 MiB per
+ * device that runs it, held until the process ends). */
+#define Q4MI_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* q4_gemv with no workspace argument and no allocation of any kind: its K-split partial
+ * sums go to a file-scope device array of Q4MI_NOALLOC_SCRATCH_BYTES, whose per-device
+ * address the library looks up on its first call on that device. Same shapes, kernels,
+ * split order and bits as q4_gemv. Q4MI_E_WORKSPACE when a shape's partials would not fit
+ * (none does under the current split policy: at most 8,380,416 bytes for M <= 16). Every
+ * call on one device shares that device's array: calls that overlap on one device (other
+ * streams or host threads) race, so order them on one stream. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). */
+int q4_gemv_noalloc(const uint8_t* packed, const void* x, int x_dtype, float* y,
+                    int M, int64_t N, int64_t K, void* stream);
 
 /* q4_gemv plus the residual: y = residual + X . W^T (residual f32 [M][N]; it may
  * be y itself, which then accumulates in place). Same workspace as q4_gemv. The

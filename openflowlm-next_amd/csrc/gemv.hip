@@ -10,6 +10,8 @@
 // invalidate the L2 of every XCD -- far slower than the extra launch.)
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "gemv_core.h"
 #include "q4mi_internal.h"
 
@@ -374,6 +376,58 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
 extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y, int M, int64_t N, int64_t K,
                        void* workspace, size_t workspace_bytes, void* stream) {
     return gemv_impl(packed, x, x_dtype, nullptr, y, M, N, K, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// q4_gemv_noalloc: q4_gemv with its K-split partial sums in a file-scope device array
+// instead of a caller workspace, for callers that cannot allocate device memory.
+//
+// The partials of a split call are [S][M][N] f32; the split policy (choose_splits) keeps
+// S * N/64 below 2048 for every N, so with M <= 16 they never exceed 2046 * 64 * 16 * 4 =
+// 8,380,416 bytes, and Q4MI_NOALLOC_SCRATCH_BYTES (8 MiB) covers every shape. The gemv
+// kernel writes every partial it later reduces, so nothing needs clearing between calls.
+// Each device holds its own copy of the array; its address is read once per device
+// (hipGetSymbolAddress, with that device current) and kept here. Calls that overlap on
+// one device (other streams, other host threads) share the array and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[Q4MI_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on its first use there.
+int scratch_for_current_device(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return Q4MI_E_LAUNCH;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return Q4MI_E_LAUNCH;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return Q4MI_OK;
+}
+
+}  // namespace
+
+extern "C" int q4_gemv_noalloc(const uint8_t* packed, const void* x, int x_dtype, float* y, int M, int64_t N,
+                               int64_t K, void* stream) {
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (M < 0 || M > 16) return Q4MI_E_RANGE;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    if (M == 0 || N == 0) return Q4MI_OK;
+    const size_t need = q4_gemv_workspace_bytes(M, N, K);
+    if (need > (size_t)Q4MI_NOALLOC_SCRATCH_BYTES) return Q4MI_E_WORKSPACE;
+    void* ws = nullptr;
+    if (need > 0) {
+        const int st = scratch_for_current_device(&ws);
+        if (st != Q4MI_OK) return st;
+    }
+    return gemv_impl(packed, x, x_dtype, nullptr, y, M, N, K, ws, need, stream);
 }
 
 extern "C" int q4_gemv_residual(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
