@@ -522,16 +522,19 @@ def extra_config3(torch, q4, dev):
     out = {}
     mats = {"gate_up": (14336, 4096), "down": (4096, 14336)}
     packed = {k: q4.pack_q4_1(gen_blocks(torch, n, kk, gen, dev), dev) for k, (n, kk) in mats.items()}
+    for w in packed.values():          # static weights: their fp16 prefill scales are made once
+        q4.prefill_scales(w)
     for T in (512, 2048):
         for name, (n, k) in mats.items():
             x = torch.randn(T, k, generator=gen, device=dev).to(torch.bfloat16)
             y = torch.empty(T, n, device=dev)
             ws = torch.empty(q4.prefill_workspace_bytes(T, n, k), dtype=torch.uint8, device=dev)
 
-            def run():
+            def run(prec="fp16"):
                 for _ in range(3):
-                    q4.gemm_q4_prefill(packed[name], x, y, workspace=ws)
+                    q4.gemm_q4_prefill(packed[name], x, y, precision=prec, workspace=ws)
             ms = graph_time(torch, run, [y], replays=5) / 3
+            ms_bf16 = graph_time(torch, lambda: run("bf16"), [y], replays=5) / 3
             tf = 2.0 * T * n * k / ms / 1e9
             # the vendor library's dense GEMM on the same shape (fp16 weights already
             # dequantized, [K, N] contiguous): the rate this box sustains for a plain
@@ -540,6 +543,7 @@ def extra_config3(torch, q4, dev):
             wd = (torch.randn(k, n, generator=gen, device=dev) * 0.01).to(torch.float16)
             _, dms = time_launches(torch, lambda: torch.matmul(xd, wd), 10, 3)
             out[f"T{T}_{name}"] = {"ms": ms, "tflops": tf, "frac_of_peak": tf / MFMA_PEAK_TFLOPS,
+                                   "bf16_tile_ms": ms_bf16, "bf16_tile_tflops": 2.0 * T * n * k / ms_bf16 / 1e9,
                                    "dense_fp16_matmul_ms": dms,
                                    "dense_fp16_matmul_tflops": 2.0 * T * n * k / dms / 1e9,
                                    "vs_dense_fp16_matmul": dms / ms}

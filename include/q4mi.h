@@ -338,9 +338,13 @@ size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K);
 
 /* Prefill GEMM: Y[T][N] = X[T][K] . W[N][K]^T with W dequantized into LDS
  * tiles feeding MFMA, fp32 accumulate, fp32 out. Any T >= 0, N % 64 == 0,
- * K % 32 == 0. precision 0 (default): each weight is rounded once to fp16
- * (11-bit significand; X bf16 -> fp16 exactly for |x| in fp16's range) and
- * fed to the fp16 MFMA, whose dense peak equals bf16's on CDNA4.
+ * K % 32 == 0. precision 0 (default): each weight row and each token row is
+ * scaled by a power of two into fp16's range (the weights' exponents and fp16
+ * scale words are the matrix's prefill scales, see q4_prefill_scales, computed
+ * into the workspace on every call), each weight is rounded once to fp16
+ * (11-bit significand; bf16 X converts exactly; f32 X goes through twice, as
+ * its fp16 rounding and the fp16 remainder) and fed to the fp16 MFMA, whose
+ * dense peak equals bf16's on CDNA4; the outputs are scaled back exactly.
  * precision 1: the reference's own tile, RNE_bf16(fl32(q*d+m)), into the
  * bf16 MFMA (gemm_q4_dequant.h:283-286; its rel_fro bar is 5e-3).
  * Replaces gemm_q4_prefill (gemm_q4_prefill.py:171-177: pool W, bf16 X,
@@ -349,6 +353,29 @@ size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K);
 int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype, float* y,
                     int T, int64_t N, int64_t K, int precision,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of an [N, K] matrix's prefill scales (0 for a shape the layout rejects). */
+size_t q4_prefill_scales_bytes(int64_t N, int64_t K);
+
+/* The prefill scales of an mx matrix, which precision 0 of the prefill GEMM reads instead of
+ * the tiles' bf16 scale words: per row n an exponent e_n with max over its 32-K blocks of
+ * (15 |d| + |m|) * 2^-e_n in [2^14, 2^15) (int32 [N]), and every block's (d, m) again as
+ * fp16(d 2^-e_n) << 16 | fp16(m 2^-e_n), in the tiles' scale-block word order (4 bytes per
+ * row and block). Every weight q d + m then fits fp16 with its 11-bit significand whatever
+ * its row's magnitude; the GEMM multiplies row n's outputs by 2^e_n back, exactly. `scales`
+ * (q4_prefill_scales_bytes) is caller-owned; weights are static, so compute it once per
+ * matrix. No counterpart in the reference, whose prefill tile is bf16
+ * (gemm_q4_dequant.h:283-286): it makes the fp16 tile exact in range. */
+int q4_prefill_scales(const uint8_t* packed, int64_t N, int64_t K, void* scales, size_t scales_bytes,
+                      void* stream);
+
+/* Workspace bytes q4_gemm_prefill_scaled needs (0 if none). */
+size_t q4_gemm_prefill_scaled_workspace_bytes(int T, int64_t N, int64_t K);
+
+/* q4_gemm_prefill at precision 0 with the matrix's prefill scales given (q4_prefill_scales),
+ * so a call does not compute them again. Same shapes, bits and bar. */
+int q4_gemm_prefill_scaled(const uint8_t* packed, const void* scales, const void* x, int x_dtype, float* y,
+                           int T, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes q4_moe_gemv needs. */
 size_t q4_moe_workspace_bytes(int T, int E, int topk, int H, int F);

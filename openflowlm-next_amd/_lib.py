@@ -61,6 +61,10 @@ SIGNATURES = {
     "q4_rmsnorm_add": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i64, C.c_float, _vp]),
     "q4_gemm_prefill_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemm_prefill": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _vp, _sz, _vp]),
+    "q4_prefill_scales_bytes": (_sz, [_i64, _i64]),
+    "q4_prefill_scales": (_i32, [_vp, _i64, _i64, _vp, _sz, _vp]),
+    "q4_gemm_prefill_scaled_workspace_bytes": (_sz, [_i32, _i64, _i64]),
+    "q4_gemm_prefill_scaled": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_topk_workspace_bytes": (_sz, [_i32, _i64, _i32]),
     "q4_logits_topk": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "q4_lm_head_workspace_bytes": (_sz, [_i32, _i64, _i64, _i32]),

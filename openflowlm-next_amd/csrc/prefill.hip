@@ -7,11 +7,21 @@
 // gemm_q4_prefill.py:198-203). Rounding each weight once to bf16 costs a
 // maxrel of ~1.8e-3 against the fp64 reference (gemm_q4_dequant.h:283-286),
 // over the 1e-3 bar. Two precisions are built from one kernel:
-//   PREC 0 (default): w16 = RNE_f16(q*d + m) (one v_pk_fma_f16 per pair, 11-bit
-//     significand), X -> fp16 (exact for bf16 inputs inside fp16's range; each
-//     token row is pre-scaled by a power of two when max|x| >= 2^15 and the
-//     output scaled back, both exact), fp16 MFMA. CDNA4's dense fp16 and bf16
-//     MFMA peaks are equal.
+//   PREC 0 (default): fp16 MFMA (CDNA4's dense fp16 and bf16 MFMA peaks are
+//     equal) on power-of-two-scaled operands, so fp16's narrow exponent range
+//     costs nothing: token row t is scaled by 2^-s_t so its max |x| lands in
+//     [2^14, 2^15) (bf16 -> fp16 is then exact: 8 significant bits, no
+//     overflow, no subnormal short of 2^-10 of the row max), and weight row n
+//     by 2^-e_n so its bound max_kb (15 |d| + |m|) >= max |w| lands there too:
+//     w16 = RNE_f16(q (d 2^-e) + m 2^-e) (one v_pk_fma_f16 per pair, 11-bit
+//     significand; d 2^-e and m 2^-e are exact in fp16 for every block within
+//     2^-24 of the row's bound). The output is ldexp(acc, s_t + e_n), exact.
+//     The token exponents come from the activation pre-pass. The weight rows'
+//     exponents and their scale words, scaled and in fp16, form the "prefill
+//     scales" of a matrix (q4_prefill_scales): a side plane laid out as the mx
+//     tiles' scale blocks (256 B per tile) from which the GEMM reads its scale
+//     words. Weights are static, so a caller computes them once per matrix
+//     (q4_gemm_prefill_scaled); q4_gemm_prefill computes them per call.
 //   PREC 1: the reference tile RNE_bf16(fl32(q*d + m)) with bf16 X, bf16 MFMA.
 // The exact-code alternative (4-bit codes on the MFMA, d and m applied per
 // 32-K block in fp32, as the decode kernel does) needs two VALU FMAs per
@@ -49,13 +59,15 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 
 // One codes dword + its row's scale word -> eight 16-bit weights (as u32x4),
-// element e = k offset e of the dword's k-group.
+// element e = k offset e of the dword's k-group. The scale word is (d << 16 | m):
+// PREC 0 reads it from the fp16 side plane (d and m already scaled by the row's
+// 2^-e), PREC 1 from the mx tile (bf16).
 template <int PREC>
 __device__ __forceinline__ u32x4 dequant8(uint32_t w, uint32_t s, uint32_t nib2, uint32_t magic) {
     u32x4 out;
     if constexpr (PREC == 0) {
-        const _Float16 dh = (_Float16)bf16_hi_to_f32(s), mh = (_Float16)bf16_lo_to_f32(s);
-        const f16x2 d2 = {dh, dh}, m2 = {mh, mh};
+        const f16x2 sv = __builtin_bit_cast(f16x2, s);                  // [0] m, [1] d
+        const f16x2 d2 = __builtin_shufflevector(sv, sv, 1, 1), m2 = __builtin_shufflevector(sv, sv, 0, 0);
         const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -76,14 +88,49 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, uint32_t s, uint32_t nib2,
     return out;
 }
 
+// Store a wave's FN x FT fragments of 16 x 16 (rows from wn0, tokens from wt0): the lane
+// holds D[n = 4 kg + r][t = i16] of each, 4 consecutive rows of one token, scaled back by
+// 2^(s_t + e_n) when the operands were scaled (texp / wexp not null), exactly; accum adds
+// the result to what y holds (the second pass of f32 activations).
+template <int FN, int FT, bool SCALED>
+__device__ __forceinline__ void store_tile(const f32x4 (&acc)[FN][FT], float* __restrict__ y,
+                                           const int* __restrict__ texp, const int* __restrict__ wexp, int T, int N,
+                                           int wt0, int wn0, int accum) {
+    const int lane = threadIdx.x & 63, i16 = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < FT; ++j) {
+        const int t = wt0 + j * 16 + i16;
+        if (t >= T) continue;
+        const int st = SCALED ? texp[t] : 0;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            const int n = wn0 + i * 16 + kg * 4;
+            if (n < N) {
+                f32x4 v = acc[i][j];
+                if constexpr (SCALED) {
+                    const int4 e = *(const int4*)(wexp + n);
+                    v[0] = ldexpf(v[0], st + e.x);
+                    v[1] = ldexpf(v[1], st + e.y);
+                    v[2] = ldexpf(v[2], st + e.z);
+                    v[3] = ldexpf(v[3], st + e.w);
+                }
+                if (SCALED && accum) v += *(const f32x4*)(y + (int64_t)t * N + n);   // PREC 0 only
+                *(f32x4*)(y + (int64_t)t * N + n) = v;
+            }
+        }
+    }
+}
+
 // BN x BT workgroup tile, WGN x WGT waves (wave tile BN/WGN x BT/WGT), KS
 // 32-K blocks per LDS stage.
 template <int BN, int BT, int WGN, int WGT, int KS, int PREC>
 __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* __restrict__ packed,
                                                                  const uint16_t* __restrict__ x16,
-                                                                 const float* __restrict__ tscale,
+                                                                 const int* __restrict__ texp,
+                                                                 const int* __restrict__ wexp,
+                                                                 const uint32_t* __restrict__ s16,
                                                                  float* __restrict__ y, int T, int N, int K,
-                                                                 int tiles_t) {
+                                                                 int tiles_t, int accum) {
     constexpr int NT = 64 * WGN * WGT, NW = WGN * WGT;
     constexpr int WN = BN / WGN, WT = BT / WGT;      // wave tile
     constexpr int FN = WN / 16, FT = WT / 16;        // 16-wide fragments per wave
@@ -113,6 +160,7 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
     // the per-lane offsets are fixed 32-bit values, so no address register is rewritten
     // inside the K loop (rewriting one that a pending load targets forces a vmcnt wait).
     const uint8_t* wbase[WPW];
+    const uint8_t* sbase[WPW];
     int wrow[WPW], wcol[WPW];
     bool wown[WPW];
 #pragma unroll
@@ -122,10 +170,12 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
         const int rgl = u % RG, kbl = u / RG;
         const int rg = min(n0 / 64 + rgl, G - 1);                       // clamp ragged N
         wbase[i] = packed + ((int64_t)rg * KB + kbl) * kTileBytes;
+        sbase[i] = PREC == 0 ? (const uint8_t*)s16 + ((int64_t)rg * KB + kbl) * 256 : wbase[i] + kCodeBytes;
         wrow[i] = rgl * 64 + i16;
         wcol[i] = kbl * 32 + kg * 8;
     }
-    const uint32_t coff = lane * 16, soff = kCodeBytes + i16 * 16;
+    const uint32_t coff = lane * 16, soff = i16 * 16;
+    constexpr int SSTR = PREC == 0 ? 256 : kTileBytes;               // scale block stride per 32-K block
     const uint16_t* xbase = x16 + (int64_t)t0 * K;                    // workgroup-uniform
     int xoff[XCH], xdst[XCH];
 #pragma unroll
@@ -154,7 +204,7 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
             if (wown[i]) {
                 const uint8_t* tp = wbase[i] + st * (KS * kTileBytes);  // uniform
                 wc[i] = load_nt_u32x4(tp + coff);
-                wsc[i] = load_nt_u32x4(tp + soff);
+                wsc[i] = load_nt_u32x4(sbase[i] + st * (KS * SSTR) + soff);
             }
         }
     };
@@ -198,22 +248,7 @@ __global__ __launch_bounds__(64 * WGN * WGT) void prefill_kernel(const uint8_t* 
         __syncthreads();
     }
 
-    // lane holds D[n = 4*kg + r][t = i16] of each 16x16 fragment: 4 consecutive n of one token
-#pragma unroll
-    for (int j = 0; j < FT; ++j) {
-        const int t = t0 + wt * WT + j * 16 + i16;
-        if (t >= T) continue;
-        const float sc = tscale ? tscale[t] : 1.0f;
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-            const int n = n0 + wn * WN + i * 16 + kg * 4;
-            if (n < N) {
-                f32x4 v = acc[i][j];
-                v = v * sc;
-                *(f32x4*)(y + (int64_t)t * N + n) = v;
-            }
-        }
-    }
+    store_tile<FN, FT, PREC == 0>(acc, y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN, accum);
 }
 
 // ---------------------------------------------------------------------------
@@ -277,9 +312,10 @@ __device__ __forceinline__ void vgpr_landed(u32x4& v) { asm volatile("" : "+v"(v
 // issues the same loads and the wait counts below hold for both.
 template <int PREC, int FN>
 __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict__ packed,
-                                         const uint16_t* __restrict__ x16, const float* __restrict__ tscale,
+                                         const uint16_t* __restrict__ x16, const int* __restrict__ texp,
+                                         const int* __restrict__ wexp, const uint32_t* __restrict__ s16,
                                          float* __restrict__ y, int T, int N, int K, int n0, int bt, int split,
-                                         int splits) {
+                                         int splits, int accum) {
     static_assert(FN == 8 || FN == 6, "256- or 192-row tiles");
     constexpr int WN = 16 * FN, WT = 64, FT = WT / 16, RG = FN / 2;
     typedef typename std::conditional<PREC == 0, f16x8, bf16x8>::type frag_t;
@@ -299,7 +335,11 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
     const int rgl = wave & 3, kbl = wave >> 2;
     const int rg = min(n0 / 64 + min(rgl, RG - 1), G - 1);              // clamp ragged N
     const uint8_t* const wsrc = packed + ((int64_t)rg * KB + kbl + 2 * st0) * kTileBytes;
-    const uint32_t coff = lane * 16, soff = kCodeBytes + i16 * 16;
+    // scale words: PREC 0 from the fp16 side plane (256 B per tile), PREC 1 from the tile
+    constexpr int SSTR = PREC == 0 ? 256 : kTileBytes;
+    const uint8_t* const ssrc = PREC == 0 ? (const uint8_t*)s16 + ((int64_t)rg * KB + kbl + 2 * st0) * 256
+                                          : wsrc + kCodeBytes;
+    const uint32_t coff = lane * 16, soff = i16 * 16;
     const uint32_t wst = kbl * kPlaneB + rgl * 64 * 64 + lane_row;     // + buffer + r * 1 KB
 
     // activations: pre-tiled as the LDS image of each stage (32 KB contiguous per token tile
@@ -332,9 +372,8 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
                 lds_dma16(src + kk * kPlaneB + h * 1024, xoff, dst + kk * kPlaneB + h * 1024);
     };
     auto issue_w = [&](int st, u32x4& c, u32x4& sc) {
-        const uint8_t* tp = wsrc + st * (2 * kTileBytes);               // uniform
-        load16_async(c, tp, coff);
-        load16_async(sc, tp, soff);
+        load16_async(c, wsrc + st * (2 * kTileBytes), coff);           // uniform bases
+        load16_async(sc, ssrc + st * (2 * SSTR), soff);
     };
     auto store_w = [&](int buf, const u32x4& c, const u32x4& sc, int r0, int r1) {
 #pragma unroll
@@ -436,22 +475,7 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
     if (st + 3 < NST) stage(I3{}, st + 3);
     if (st + 4 < NST) stage(I4{}, st + 4);
 
-    // lane holds D[n = 4*kg + r][t = i16] of each 16x16 fragment: 4 consecutive n of one token
-#pragma unroll
-    for (int j = 0; j < FT; ++j) {
-        const int t = t0 + wt * WT + j * 16 + i16;
-        if (t >= T) continue;
-        const float sc = tscale ? tscale[t] : 1.0f;
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-            const int n = n0 + wn * WN + i * 16 + kg * 4;
-            if (n < N) {
-                f32x4 v = acc[i][j];
-                v = v * sc;
-                *(f32x4*)(y + (int64_t)t * N + n) = v;
-            }
-        }
-    }
+    store_tile<FN, FT, PREC == 0>(acc, y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN, accum);
 }
 
 // Workgroups [0, wide_wgs) take the 256-row tiles of rows [0, narrow_row0), the rest the
@@ -462,25 +486,36 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
 template <int PREC, bool MIXED>
 __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restrict__ packed,
                                                           const uint16_t* __restrict__ x16,
-                                                          const float* __restrict__ tscale, float* __restrict__ y,
+                                                          const int* __restrict__ texp, const int* __restrict__ wexp,
+                                                          const uint32_t* __restrict__ s16, float* __restrict__ y,
                                                           int T, int N, int K, int tiles_t, int splits, int wide_wgs,
-                                                          int narrow_row0) {
+                                                          int narrow_row0, int accum) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
     const int b = blockIdx.x;
     if (!MIXED || b < wide_wgs) {
         const int tile = b / splits;
-        dma_tile<PREC, 8>(lds, packed, x16, tscale, y, T, N, K, (tile / tiles_t) * 256, tile % tiles_t, b % splits,
-                          splits);
+        dma_tile<PREC, 8>(lds, packed, x16, texp, wexp, s16, y, T, N, K, (tile / tiles_t) * 256, tile % tiles_t,
+                          b % splits, splits, accum);
     } else {
         const int i = b - wide_wgs, tile = i / splits;
-        dma_tile<PREC, 6>(lds, packed, x16, tscale, y, T, N, K, narrow_row0 + (tile / tiles_t) * 192,
-                          tile % tiles_t, i % splits, splits);
+        dma_tile<PREC, 6>(lds, packed, x16, texp, wexp, s16, y, T, N, K, narrow_row0 + (tile / tiles_t) * 192,
+                          tile % tiles_t, i % splits, splits, accum);
     }
 }
 
-// Activations -> the MFMA's 16-bit type, one workgroup per token row.
-// PREC 0: fp16, with the row scaled by 2^-s (s >= 0 the least that keeps
-// max|x| 2^-s < 2^15) and tscale[t] = 2^s; PREC 1: bf16 (RNE from f32).
+// The exponent that puts a positive finite magnitude v in [2^14, 2^15) after scaling by
+// 2^-e: v in [2^(x-1), 2^x) -> e = x - 15. 0 for zero, inf and NaN (those are passed
+// through unscaled).
+__device__ __forceinline__ int fp16_fit_exponent(float v) {
+    if (!(v > 0.0f) || v > 3.0e38f) return 0;
+    int x;
+    frexpf(v, &x);
+    return x - 15;
+}
+
+// Activations -> the MFMA's 16-bit type, one workgroup per token row (padded to whole
+// token tiles). PREC 0: fp16, token row t scaled by 2^-s_t with s_t = fp16_fit_exponent(max
+// |x_t|), and texp[t] = s_t. PREC 1: bf16 (RNE from f32), no exponents.
 // TILED: the 16-byte chunk i (k = 8i..8i+7) of token t goes to its place in the LDS image
 // of the pipelined kernel's activation tiles: [token tile][64-K stage][32-K plane][256 rows]
 // [4 chunks], chunk c of row r at slot c ^ ((r >> 1) & 3). Each stage of a token tile is then
@@ -490,9 +525,74 @@ __device__ __forceinline__ int64_t xchunk_dst(int t, int i, int K) {
     return ((((int64_t)(t >> 8) * (K >> 6) + st) * 2 + kk) * 256 + r) * 4 + (c ^ ((r >> 1) & 3));
 }
 
+// Block-wide max of a non-negative value over 256 threads (result in every thread).
+__device__ __forceinline__ float block_max256(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// The prefill scales of an [N, K] mx matrix, in two launches over (row group g, chunk c of
+// kScaleChunk 32-K blocks) workgroups, each of 64 rows x 4 parts (thread (part, row) takes
+// blocks part, part + 4, ... of the chunk):
+//   max pass:   cmax[n][c] = max over the chunk's blocks of 15 |d| + |m| for row n;
+//   write pass: wexp[n] = fp16_fit_exponent(max over c of cmax[n][c]) (chunk 0 stores it),
+//               s16 word (g KB + kb) * 64 + (n % 16) * 4 + (n % 64) / 16 = fp16(d 2^-e) << 16 |
+//               fp16(m 2^-e), the mx scale block's word order.
+constexpr int kScaleChunk = 32;
+
+__device__ __forceinline__ const uint8_t* scale_word_base(const uint8_t* packed, int64_t g, int KB, int row) {
+    return packed + g * KB * kTileBytes + kCodeBytes + ((row & 15) * 4 + (row >> 4)) * 4;
+}
+
+__global__ __launch_bounds__(256) void prefill_scale_max_kernel(const uint8_t* __restrict__ packed, int K, int nchunk,
+                                                                float* __restrict__ cmax) {
+    __shared__ float red[4][64];
+    const int64_t g = blockIdx.x / nchunk;
+    const int c = blockIdx.x % nchunk, row = threadIdx.x & 63, part = threadIdx.x >> 6;
+    const int KB = K >> 5, kb0 = c * kScaleChunk, kb1 = min(kb0 + kScaleChunk, KB);
+    const uint8_t* base = scale_word_base(packed, g, KB, row);
+    float b = 0.f;
+#pragma unroll 8
+    for (int kb = kb0 + part; kb < kb1; kb += 4) {
+        const uint32_t sw = load_global<uint32_t>(base + (int64_t)kb * kTileBytes);
+        b = fmaxf(b, __builtin_fmaf(15.0f, fabsf(bf16_hi_to_f32(sw)), fabsf(bf16_lo_to_f32(sw))));
+    }
+    red[part][row] = b;
+    __syncthreads();
+    if (part == 0)
+        cmax[(g * 64 + row) * nchunk + c] = fmaxf(fmaxf(red[0][row], red[1][row]), fmaxf(red[2][row], red[3][row]));
+}
+
+__global__ __launch_bounds__(256) void prefill_scale_write_kernel(const uint8_t* __restrict__ packed, int K,
+                                                                  int nchunk, const float* __restrict__ cmax,
+                                                                  int* __restrict__ wexp, uint32_t* __restrict__ s16) {
+    const int64_t g = blockIdx.x / nchunk;
+    const int c = blockIdx.x % nchunk, row = threadIdx.x & 63, part = threadIdx.x >> 6;
+    const int KB = K >> 5, kb0 = c * kScaleChunk, kb1 = min(kb0 + kScaleChunk, KB);
+    const float* cm = cmax + (g * 64 + row) * nchunk;
+    float m = 0.f;
+    for (int i = 0; i < nchunk; ++i) m = fmaxf(m, cm[i]);
+    const int e = fp16_fit_exponent(m);
+    if (c == 0 && part == 0) wexp[g * 64 + row] = e;
+    const uint8_t* base = scale_word_base(packed, g, KB, row);
+    uint32_t* out = s16 + g * KB * 64 + ((row & 15) * 4 + (row >> 4));
+#pragma unroll 8
+    for (int kb = kb0 + part; kb < kb1; kb += 4) {
+        const uint32_t sw = load_global<uint32_t>(base + (int64_t)kb * kTileBytes);
+        const uint32_t dh = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(bf16_hi_to_f32(sw), -e));
+        const uint32_t mh = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(bf16_lo_to_f32(sw), -e));
+        out[(int64_t)kb * 64] = (dh << 16) | mh;
+    }
+}
+
+// lo_pass (f32 activations, PREC 0): the fp16 remainder x 2^-s - fp16(x 2^-s) instead of the
+// rounded value; the two passes' products add up to the f32 activations' to ~2^-22.
 template <bool XF32, int PREC, bool TILED>
 __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x, uint16_t* __restrict__ x16,
-                                                     float* __restrict__ tscale, int T, int K) {
+                                                     int* __restrict__ texp, int T, int K, int lo_pass) {
     const int t = blockIdx.x, n8 = K >> 3;       // 8-element groups of the row (K % 32 == 0)
     const int64_t row = (int64_t)t * K;
     u32x4* const out = (u32x4*)x16;
@@ -525,7 +625,7 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
             if (i < n8) ld8(i, hv[c]);
         }
     }
-    float scale = 1.0f;
+    int s = 0;
     if constexpr (PREC == 0) {
         __shared__ float red[4];
         float mx = 0.f;
@@ -544,19 +644,8 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
                 for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
             }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-        __syncthreads();
-        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        int s = 0;
-        if (mx >= 32768.0f && mx <= 3.0e38f) {
-            int e;
-            frexpf(mx, &e);                      // mx in [2^(e-1), 2^e)
-            s = e - 15;                          // mx * 2^-s < 2^15
-        }
-        scale = ldexpf(1.0f, -s);
-        if (threadIdx.x == 0) tscale[t] = ldexpf(1.0f, s);
+        s = fp16_fit_exponent(block_max256(mx, red));
+        if (threadIdx.x == 0) texp[t] = s;
     }
     auto cvt8 = [&](const float (&v)[8]) -> u32x4 {
         u32x4 o;
@@ -564,8 +653,14 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
         for (int e = 0; e < 4; ++e) {
             uint32_t lo, hi;
             if constexpr (PREC == 0) {
-                lo = __builtin_bit_cast(uint16_t, (_Float16)(v[2 * e] * scale));
-                hi = __builtin_bit_cast(uint16_t, (_Float16)(v[2 * e + 1] * scale));
+                const float a = ldexpf(v[2 * e], -s), b = ldexpf(v[2 * e + 1], -s);
+                _Float16 ha = (_Float16)a, hb = (_Float16)b;
+                if (XF32 && lo_pass) {
+                    ha = (_Float16)(a - (float)ha);
+                    hb = (_Float16)(b - (float)hb);
+                }
+                lo = __builtin_bit_cast(uint16_t, ha);
+                hi = __builtin_bit_cast(uint16_t, hb);
             } else {
                 lo = f32_to_bf16_rne(v[2 * e]);
                 hi = f32_to_bf16_rne(v[2 * e + 1]);
@@ -631,41 +726,43 @@ int choose_cfg(int T, int N, int K) {
 }
 
 template <int C, int PREC>
-void launch_cfg(int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const float* ts, float* y,
-                int T, int N, int K, int tiles_t) {
+void launch_cfg(int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const int* te, const int* we,
+                const uint32_t* s16, float* y, int T, int N, int K, int tiles_t, int accum) {
     constexpr TileCfg c = kCfgs[C];
     hipLaunchKernelGGL((prefill_kernel<c.bn, c.bt, c.wgn, c.wgt, c.ks, PREC>), dim3((unsigned)grid),
-                       dim3(64 * c.wgn * c.wgt), 0, st, w, x16, ts, y, T, N, K, tiles_t);
+                       dim3(64 * c.wgn * c.wgt), 0, st, w, x16, te, we, s16, y, T, N, K, tiles_t, accum);
 }
 
 template <int PREC>
-void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const float* ts,
-                    float* y, int T, int N, int K, int tiles_t, int splits, int wide_wgs, int narrow_row0) {
+void launch_prefill(int cfg, int64_t grid, hipStream_t st, const uint8_t* w, const uint16_t* x16, const int* te,
+                    const int* we, const uint32_t* s16, float* y, int T, int N, int K, int tiles_t, int splits,
+                    int wide_wgs, int narrow_row0, int accum) {
     switch (cfg) {
-        case 0: launch_cfg<0, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
-        case 1: launch_cfg<1, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
-        case 2: launch_cfg<2, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
-        case 3: launch_cfg<3, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
-        case 4: launch_cfg<4, PREC>(grid, st, w, x16, ts, y, T, N, K, tiles_t); break;
+        case 0: launch_cfg<0, PREC>(grid, st, w, x16, te, we, s16, y, T, N, K, tiles_t, accum); break;
+        case 1: launch_cfg<1, PREC>(grid, st, w, x16, te, we, s16, y, T, N, K, tiles_t, accum); break;
+        case 2: launch_cfg<2, PREC>(grid, st, w, x16, te, we, s16, y, T, N, K, tiles_t, accum); break;
+        case 3: launch_cfg<3, PREC>(grid, st, w, x16, te, we, s16, y, T, N, K, tiles_t, accum); break;
+        case 4: launch_cfg<4, PREC>(grid, st, w, x16, te, we, s16, y, T, N, K, tiles_t, accum); break;
         default:
             if (wide_wgs < grid)
-                hipLaunchKernelGGL((prefill_dma_kernel<PREC, true>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, ts,
-                                   y, T, N, K, tiles_t, splits, wide_wgs, narrow_row0);
+                hipLaunchKernelGGL((prefill_dma_kernel<PREC, true>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, te,
+                                   we, s16, y, T, N, K, tiles_t, splits, wide_wgs, narrow_row0, accum);
             else
-                hipLaunchKernelGGL((prefill_dma_kernel<PREC, false>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, ts,
-                                   y, T, N, K, tiles_t, splits, wide_wgs, narrow_row0);
+                hipLaunchKernelGGL((prefill_dma_kernel<PREC, false>), dim3((unsigned)grid), dim3(512), 0, st, w, x16, te,
+                                   we, s16, y, T, N, K, tiles_t, splits, wide_wgs, narrow_row0, accum);
             break;
     }
 }
 
-// y = sum of the S partials in split order (deterministic), 4 floats per thread.
+// y = sum of the S partials in split order (deterministic), 4 floats per thread; accum adds
+// it to what y holds.
 __global__ __launch_bounds__(256) void prefill_reduce_kernel(const f32x4* __restrict__ part, f32x4* __restrict__ y,
-                                                             int64_t MN4, int S) {
+                                                             int64_t MN4, int S, int accum) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= MN4) return;
     f32x4 s = part[i];
     for (int q = 1; q < S; ++q) s += part[(int64_t)q * MN4 + i];
-    y[i] = s;
+    y[i] = accum ? y[i] + s : s;
 }
 
 // CUs of the current device (the MI355X's 256 when no device is visible, e.g. for a
@@ -795,18 +892,18 @@ PrefillPlan make_plan(int T, int64_t N, int64_t K) {
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 template <bool XF, int PR, bool TL>
-void launch_xprep_t(dim3 g, hipStream_t st, const void* x, uint16_t* x16, float* ts, int T, int K) {
-    hipLaunchKernelGGL((prefill_xprep<XF, PR, TL>), g, dim3(256), 0, st, x, x16, ts, T, K);
+void launch_xprep_t(dim3 g, hipStream_t st, const void* x, uint16_t* x16, int* te, int T, int K, int lo_pass) {
+    hipLaunchKernelGGL((prefill_xprep<XF, PR, TL>), g, dim3(256), 0, st, x, x16, te, T, K, lo_pass);
 }
 
-void launch_xprep(bool xf32, int prec, bool tiled, dim3 g, hipStream_t st, const void* x, uint16_t* x16, float* ts,
-                  int T, int K) {
-    typedef void (*fn_t)(dim3, hipStream_t, const void*, uint16_t*, float*, int, int);
+void launch_xprep(bool xf32, int prec, bool tiled, dim3 g, hipStream_t st, const void* x, uint16_t* x16, int* te,
+                  int T, int K, int lo_pass) {
+    typedef void (*fn_t)(dim3, hipStream_t, const void*, uint16_t*, int*, int, int, int);
     static const fn_t table[8] = {launch_xprep_t<false, 0, false>, launch_xprep_t<false, 0, true>,
                                   launch_xprep_t<false, 1, false>, launch_xprep_t<false, 1, true>,
                                   launch_xprep_t<true, 0, false>,  launch_xprep_t<true, 0, true>,
                                   launch_xprep_t<true, 1, false>,  launch_xprep_t<true, 1, true>};
-    table[(xf32 ? 4 : 0) + (prec ? 2 : 0) + (tiled ? 1 : 0)](g, st, x, x16, ts, T, K);
+    table[(xf32 ? 4 : 0) + (prec ? 2 : 0) + (tiled ? 1 : 0)](g, st, x, x16, te, T, K, lo_pass);
 }
 
 }  // namespace
@@ -814,50 +911,133 @@ void launch_xprep(bool xf32, int prec, bool tiled, dim3 g, hipStream_t st, const
 // Activation rows are padded with zeros to a multiple of 256 tokens (the widest token tile).
 static size_t padded_tokens(int T) { return ((size_t)T + 255) / 256 * 256; }
 
-// Workspace: activations in the kernel's 16-bit layout, per-token scales, and the K-split
-// partial sums when the plan splits K.
-static size_t xprep_bytes(int T, int64_t K) { return align256(padded_tokens(T) * K * 2) + align256((size_t)T * 4); }
+// The prefill scales of an [N, K] matrix: wexp int32[N], then the fp16 scale plane (4 bytes
+// per row and 32-K block), then the max pass's per-chunk maxima (f32 [N][chunks]).
+static int64_t scale_chunks(int64_t K) { return ceil_div(K / 32, kScaleChunk); }
+static size_t scales_wexp_bytes(int64_t N) { return align256((size_t)N * 4); }
+static size_t scales_plane_bytes(int64_t N, int64_t K) { return align256((size_t)N * (K / 32) * 4); }
+static size_t scales_bytes(int64_t N, int64_t K) {
+    return scales_wexp_bytes(N) + scales_plane_bytes(N, K) + align256((size_t)N * scale_chunks(K) * 4);
+}
 
-extern "C" size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K) {
-    if (T <= 0 || K <= 0 || N < 0 || N % 64 || K % 32) return 0;
+extern "C" size_t q4_prefill_scales_bytes(int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0 || N % 64 || K % 32) return 0;
+    return scales_bytes(N, K);
+}
+
+extern "C" int q4_prefill_scales(const uint8_t* packed, int64_t N, int64_t K, void* scales, size_t scales_bytes_,
+                                 void* stream) {
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    if (N > 0x7FFFFFFF || K > 0x7FFFFFFF) return Q4MI_E_RANGE;
+    if (N == 0) return Q4MI_OK;
+    if (!packed || !scales || misaligned16(packed) || misaligned16(scales)) return Q4MI_E_ARG;
+    if (scales_bytes_ < scales_bytes(N, K)) return Q4MI_E_WORKSPACE;
+    int* wexp = (int*)scales;
+    uint32_t* s16 = (uint32_t*)((char*)scales + scales_wexp_bytes(N));
+    float* cmax = (float*)((char*)s16 + scales_plane_bytes(N, K));
+    const int nchunk = (int)scale_chunks(K);
+    const dim3 grid((unsigned)((N / 64) * nchunk));
+    const hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(prefill_scale_max_kernel, grid, dim3(256), 0, st, packed, (int)K, nchunk, cmax);
+    if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    hipLaunchKernelGGL(prefill_scale_write_kernel, grid, dim3(256), 0, st, packed, (int)K, nchunk,
+                       (const float*)cmax, wexp, s16);
+    return launch_status();
+}
+
+// Workspace of the GEMM proper: activations in the kernel's 16-bit layout, the token
+// exponents, and the K-split partial sums when the plan splits K.
+static size_t x16_bytes(int T, int64_t K) { return align256(padded_tokens(T) * K * 2); }
+static size_t xprep_bytes(int T, int64_t K) { return x16_bytes(T, K) + align256((size_t)T * 4); }
+static size_t gemm_ws_bytes(int T, int64_t N, int64_t K) {
     const PrefillPlan p = make_plan(T, N, K);
     return xprep_bytes(T, K) + (p.splits > 1 ? align256((size_t)p.splits * T * N * 4) : 0);
 }
 
-extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype, float* y, int T, int64_t N,
-                               int64_t K, int precision, void* workspace, size_t workspace_bytes, void* stream) {
-    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
-    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
-    if (T < 0 || N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
-    if (N > 0x7FFFFFFF || K > 0x7FFFFFFF) return Q4MI_E_RANGE;
-    if (T == 0 || N == 0) return Q4MI_OK;
-    if (!packed || !x || !y) return Q4MI_E_ARG;
-    if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
-    const size_t need = q4_gemm_prefill_workspace_bytes(T, N, K);
-    if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
+extern "C" size_t q4_gemm_prefill_scaled_workspace_bytes(int T, int64_t N, int64_t K) {
+    if (T <= 0 || K <= 0 || N < 0 || N % 64 || K % 32) return 0;
+    return gemm_ws_bytes(T, N, K);
+}
+
+// q4_gemm_prefill's workspace also holds the matrix's prefill scales (precision 0).
+extern "C" size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K) {
+    if (T <= 0 || K <= 0 || N < 0 || N % 64 || K % 32) return 0;
+    return gemm_ws_bytes(T, N, K) + scales_bytes(N, K);
+}
+
+namespace {
+
+// The GEMM with the matrix's prefill scales (precision 0) given; workspace of gemm_ws_bytes.
+int prefill_impl(const uint8_t* packed, const void* scales, const void* x, int x_dtype, float* y, int T, int64_t N,
+                 int64_t K, int precision, void* workspace, hipStream_t st) {
     uint16_t* x16 = (uint16_t*)workspace;
-    float* ts = (float*)((char*)workspace + align256(padded_tokens(T) * K * 2));
+    int* te = (int*)((char*)workspace + x16_bytes(T, K));
+    const int* we = precision == 0 ? (const int*)scales : nullptr;
+    const uint32_t* s16 = precision == 0 ? (const uint32_t*)((const char*)scales + scales_wexp_bytes(N)) : nullptr;
     const PrefillPlan plan = make_plan(T, N, K);
-    const dim3 xgrid((unsigned)padded_tokens(T));
-    const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
     const int cfg = plan.cfg;
     const bool tiled = cfg == kDmaCfg;
-    launch_xprep(xf32, precision, tiled, xgrid, st, x, x16, ts, T, (int)K);
-    if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-    const float* tsp = precision == 0 ? ts : nullptr;
     float* out = plan.splits > 1 ? (float*)((char*)workspace + xprep_bytes(T, K)) : y;
-    if (precision == 0)
-        launch_prefill<0>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits,
-                          plan.wide_wgs, plan.narrow_row0);
-    else
-        launch_prefill<1>(cfg, plan.grid, st, packed, x16, tsp, out, T, (int)N, (int)K, plan.tiles_t, plan.splits,
-                          plan.wide_wgs, plan.narrow_row0);
-    if (plan.splits > 1) {
+    const dim3 xgrid((unsigned)padded_tokens(T));
+    // f32 activations in precision 0 take two passes: their fp16 rounding, then the fp16
+    // remainder, whose product the second pass adds to y.
+    const int passes = xf32 && precision == 0 ? 2 : 1;
+    for (int pass = 0; pass < passes; ++pass) {
+        launch_xprep(xf32, precision, tiled, xgrid, st, x, x16, te, T, (int)K, pass);
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-        const int64_t MN4 = (int64_t)T * N / 4;
-        hipLaunchKernelGGL(prefill_reduce_kernel, dim3((unsigned)ceil_div(MN4, 256)), dim3(256), 0, st,
-                           (const f32x4*)out, (f32x4*)y, MN4, plan.splits);
+        const int accum = plan.splits > 1 ? 0 : pass;
+        if (precision == 0)
+            launch_prefill<0>(cfg, plan.grid, st, packed, x16, te, we, s16, out, T, (int)N, (int)K, plan.tiles_t,
+                              plan.splits, plan.wide_wgs, plan.narrow_row0, accum);
+        else
+            launch_prefill<1>(cfg, plan.grid, st, packed, x16, nullptr, nullptr, nullptr, out, T, (int)N, (int)K,
+                              plan.tiles_t, plan.splits, plan.wide_wgs, plan.narrow_row0, accum);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        if (plan.splits > 1) {
+            const int64_t MN4 = (int64_t)T * N / 4;
+            hipLaunchKernelGGL(prefill_reduce_kernel, dim3((unsigned)ceil_div(MN4, 256)), dim3(256), 0, st,
+                               (const f32x4*)out, (f32x4*)y, MN4, plan.splits, pass);
+            if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        }
     }
     return launch_status();
+}
+
+int prefill_args(const uint8_t* packed, const void* x, int x_dtype, float* y, int T, int64_t N, int64_t K,
+                 void* workspace) {
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (T < 0 || N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    if (N > 0x7FFFFFFF || K > 0x7FFFFFFF) return Q4MI_E_RANGE;
+    if (T == 0 || N == 0) return 1;                              // nothing to compute
+    if (!packed || !x || !y) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
+    return Q4MI_OK;
+}
+
+}  // namespace
+
+extern "C" int q4_gemm_prefill(const uint8_t* packed, const void* x, int x_dtype, float* y, int T, int64_t N,
+                               int64_t K, int precision, void* workspace, size_t workspace_bytes, void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    const int a = prefill_args(packed, x, x_dtype, y, T, N, K, workspace);
+    if (a != Q4MI_OK) return a > 0 ? Q4MI_OK : a;
+    if (!workspace || workspace_bytes < q4_gemm_prefill_workspace_bytes(T, N, K)) return Q4MI_E_WORKSPACE;
+    const hipStream_t st = (hipStream_t)stream;
+    void* scales = (char*)workspace + gemm_ws_bytes(T, N, K);
+    if (precision == 0) {
+        const int rc = q4_prefill_scales(packed, N, K, scales, scales_bytes(N, K), stream);
+        if (rc != Q4MI_OK) return rc;
+    }
+    return prefill_impl(packed, scales, x, x_dtype, y, T, N, K, precision, workspace, st);
+}
+
+extern "C" int q4_gemm_prefill_scaled(const uint8_t* packed, const void* scales, const void* x, int x_dtype, float* y,
+                                      int T, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+    const int a = prefill_args(packed, x, x_dtype, y, T, N, K, workspace);
+    if (a != Q4MI_OK) return a > 0 ? Q4MI_OK : a;
+    if (!scales || misaligned16(scales)) return Q4MI_E_ARG;
+    if (!workspace || workspace_bytes < gemm_ws_bytes(T, N, K)) return Q4MI_E_WORKSPACE;
+    return prefill_impl(packed, scales, x, x_dtype, y, T, N, K, 0, workspace, (hipStream_t)stream);
 }

@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import ctypes as C
 import warnings
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
@@ -32,7 +32,7 @@ __all__ = [
     "PackedQ4", "PackedExperts", "packed_bytes", "pack_q4_1", "pack_q4_1_pool", "pack_q4_k", "pack_q4_k_chunks", "dequant",
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "logits_topk", "lm_head_topk",
-    "swiglu_q4", "rmsnorm_add", "pack_chunks", "PackedQ8", "pack_q8", "gemm_q8",
+    "swiglu_q4", "rmsnorm_add", "pack_chunks", "PackedQ8", "pack_q8", "gemm_q8", "prefill_scales",
 ]
 
 ROWS = 64          # rows per mx tile / row group
@@ -108,10 +108,13 @@ def packed_bytes(n: int, k: int) -> int:
 
 @dataclass
 class PackedQ4:
-    """One [n, k] Q4_1 weight matrix in the mx layout, resident on a GPU."""
+    """One [n, k] Q4_1 weight matrix in the mx layout, resident on a GPU. ``prefill_scales``
+    caches the matrix's fp16 prefill scales (q4_prefill_scales) once a prefill GEMM has
+    needed them; the weights are static, so they are computed once."""
     data: torch.Tensor        # uint8, packed_bytes(n, k)
     n: int
     k: int
+    prefill_scales: torch.Tensor | None = field(default=None, repr=False, compare=False)
 
     @property
     def shape(self):
@@ -816,12 +819,27 @@ class GemvGroup:
 _PRECISION = {"fp16": 0, "bf16": 1}
 
 
+def prefill_scales(w: PackedQ4) -> torch.Tensor:
+    """The matrix's fp16 prefill scales (per-row power-of-two exponents and the scale words
+    in fp16, q4_prefill_scales), computed on first use and kept on ``w``."""
+    if w.prefill_scales is None:
+        dev = w.device
+        lib = _lib_handle()
+        t = torch.empty(int(lib.q4_prefill_scales_bytes(w.n, w.k)), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            check("q4_prefill_scales", lib.q4_prefill_scales(_ptr(w.data), w.n, w.k, _ptr(t), t.numel(), _stream(dev)))
+        w.prefill_scales = t
+    return w.prefill_scales
+
+
 def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16",
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y[T, N] = X[T, K] @ W^T for a prefill block of T tokens, fp32 out.
 
-    precision "fp16": each weight rounded once to fp16 in LDS (fp16 MFMA);
-    "bf16": the reference tile RNE_bf16(fl32(q*d+m)) (gemm_q4_dequant.h:283-286)."""
+    precision "fp16": each weight rounded once to fp16 in LDS (fp16 MFMA), weight and token
+    rows scaled into fp16's range by powers of two (the matrix's prefill scales, computed
+    once and kept on ``w``); "bf16": the reference tile RNE_bf16(fl32(q*d+m))
+    (gemm_q4_dequant.h:283-286)."""
     dev = w.device
     xt = _acts(x, dev)
     if xt.dim() != 2 or xt.shape[1] != w.k:
@@ -831,6 +849,13 @@ def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: st
         raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
     y = _buf(y, "y", torch.float32, (T, w.n), dev)
     lib = _lib_handle()
+    if precision == "fp16" and T > 0 and w.n > 0:
+        sc = prefill_scales(w)
+        with torch.cuda.device(dev):
+            wp, wn = _ws_arg(dev, lib.q4_gemm_prefill_scaled_workspace_bytes(T, w.n, w.k), "prefill", workspace)
+            check("q4_gemm_prefill_scaled", lib.q4_gemm_prefill_scaled(
+                _ptr(w.data), _ptr(sc), _ptr(xt), _x_dtype(xt), _ptr(y), T, w.n, w.k, wp, wn, _stream(dev)))
+        return y
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_gemm_prefill_workspace_bytes(T, w.n, w.k), "prefill", workspace)
         check("q4_gemm_prefill", lib.q4_gemm_prefill(

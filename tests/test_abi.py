@@ -140,13 +140,36 @@ def test_argument_errors_before_any_launch(lib):
 
 def test_prefill_workspace_query(lib):
     """Activations in the kernel's layout (zero-padded to 256-token tiles) + per-token
-    scales, plus K-split partials when a grid of 256x256 tiles cannot fill the GPU."""
+    exponents, plus K-split partials when a grid of 256x256 tiles cannot fill the GPU."""
     x_only = lambda T, K: -(-((T + 255) // 256 * 256 * K * 2) // 256) * 256 + -(-(T * 4) // 256) * 256
     assert lib.q4_gemm_prefill_workspace_bytes(2048, 14336, 4096) >= x_only(2048, 4096)
     # 16 x 2 output tiles for 224 stages of K: split, partials [S][T][N] f32
     assert lib.q4_gemm_prefill_workspace_bytes(512, 4096, 14336) >= x_only(512, 14336) + 2 * 512 * 4096 * 4
     assert lib.q4_gemm_prefill_workspace_bytes(0, 4096, 4096) == 0
     assert lib.q4_gemm_prefill_workspace_bytes(64, 100, 4096) == 0
+    # the per-call path also holds the matrix's prefill scales: exponents, the fp16 plane
+    # (4 bytes per row and 32-K block) and the per-chunk maxima
+    sc = lib.q4_prefill_scales_bytes(14336, 4096)
+    assert sc >= 14336 * 4 + 14336 * 128 * 4
+    assert lib.q4_gemm_prefill_workspace_bytes(2048, 14336, 4096) == \
+        lib.q4_gemm_prefill_scaled_workspace_bytes(2048, 14336, 4096) + sc
+    assert lib.q4_prefill_scales_bytes(100, 4096) == 0 and lib.q4_prefill_scales_bytes(64, 48) == 0
+
+
+def test_prefill_scales_argument_errors(lib):
+    fake, odd = C.c_void_p(0x1000), C.c_void_p(0x1004)
+    need = lib.q4_prefill_scales_bytes(256, 1024)
+    assert lib.q4_prefill_scales(fake, 100, 1024, fake, need, None) == -1       # N % 64
+    assert lib.q4_prefill_scales(fake, 256, 1024, odd, need, None) == -2        # misaligned
+    assert lib.q4_prefill_scales(None, 256, 1024, fake, need, None) == -2       # NULL
+    assert lib.q4_prefill_scales(fake, 256, 1024, fake, need - 1, None) == -3   # short
+    assert lib.q4_prefill_scales(fake, 0, 1024, fake, 0, None) == 0             # nothing to do
+    ws = lib.q4_gemm_prefill_scaled_workspace_bytes(64, 256, 1024)
+    assert lib.q4_gemm_prefill_scaled(fake, None, fake, 1, fake, 64, 256, 1024, fake, ws, None) == -2
+    assert lib.q4_gemm_prefill_scaled(fake, odd, fake, 1, fake, 64, 256, 1024, fake, ws, None) == -2
+    assert lib.q4_gemm_prefill_scaled(fake, fake, fake, 1, fake, 64, 256, 1024, fake, ws - 1, None) == -3
+    assert lib.q4_gemm_prefill_scaled(fake, fake, fake, 5, fake, 64, 256, 1024, fake, ws, None) == -2
+    assert lib.q4_gemm_prefill_scaled(fake, fake, fake, 1, fake, 0, 256, 1024, None, 0, None) == 0
 
 
 def test_gemv_workspace_query(lib):

@@ -185,3 +185,103 @@ def test_prefill_config3_shapes(gpu, pkg, oracle, T, N, K, precision):
         for i, t in enumerate(toks):
             assert oracle.maxrel(Y[t], tile[i]) < 1e-5, int(t)
         assert oracle.rel_fro(Y[toks], ref) <= 5e-3
+
+
+def _wide_range_blocks(oracle, rng, N, K, lo_exp=-6.0, hi_exp=-2.0):
+    """Q4_1 blocks whose rows have d ~ 10^U(lo_exp, hi_exp) (one decade draw per row, a
+    +-50 % spread per block), m = -8 d U(0.9, 1.1), codes uniform; d and m rounded to fp16
+    as GGUF stores them (below 2^-14 they are fp16 subnormals, kept as stored)."""
+    nb = K // 32
+    dec = 10.0 ** rng.uniform(lo_exp, hi_exp, (N, 1))
+    d = (dec * rng.uniform(0.5, 1.5, (N, nb))).astype(np.float16)
+    m = (-8.0 * d.astype(np.float32) * rng.uniform(0.9, 1.1, (N, nb))).astype(np.float16)
+    q = rng.integers(0, 16, (N, nb, 32), dtype=np.uint8)
+    return oracle._assemble_q4_1(d, m, q)
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("T,N,K", [(300, 512, 1024), (64, 256, 2080)])
+def test_prefill_fp16_range_per_row(gpu, pkg, oracle, T, N, K, xdt):
+    """fp16's exponent range costs nothing: weight rows with d from 1e-6 (fp16 subnormals) to
+    ~5e3 (weights past fp16's 65504) and token rows from ~1e-6 to ~1e5 in magnitude, every
+    token row and every weight row held to maxrel <= 1e-3 against the fp64 oracle on its own
+    (per row, the bar the tiny rows would miss, and the large ones overflow, without their
+    power-of-two scaling). K = 2080 takes the generic kernel (K % 64 != 0), K = 1024 the
+    pipelined one."""
+    say(f"prefill fp16 range T={T} N={N} K={K} {xdt}")
+    rng = np.random.default_rng(T + N + K + (xdt == "f32"))
+    blocks = _wide_range_blocks(oracle, rng, N, K, -6.0, 3.5)
+    mag = 10.0 ** rng.uniform(-6.0, 5.0, (T, 1))
+    mag[0], mag[1] = 1e-6, 1e5
+    X = (rng.standard_normal((T, K)) * mag).astype(np.float32)
+    Xt = torch.from_numpy(X).to(torch.bfloat16) if xdt == "bf16" else torch.from_numpy(X)
+    w = pkg.pack_q4_1(blocks, gpu)
+    Y = pkg.gemm_q4_prefill(w, Xt.to(gpu)).cpu().numpy()
+    ref = oracle.prefill_reference(blocks, Xt.to(torch.float32).numpy())
+    assert np.isfinite(Y).all()
+    for t in range(T):
+        assert oracle.maxrel(Y[t], ref[t]) <= 1e-3, f"token row {t} (|x| ~ {float(mag[t, 0]):.1e})"
+    for n in range(N):
+        assert oracle.maxrel(Y[:, n], ref[:, n]) <= 1e-3, f"weight row {n}"
+
+
+def test_prefill_fp16_range_scaling_is_exact_on_powers_of_two(gpu, pkg, oracle):
+    """Scaling a token row by 2^40 or 2^-40 scales its output by exactly that (the row's
+    exponent absorbs it), bit for bit."""
+    say("prefill fp16 range: power-of-two invariance")
+    rng = np.random.default_rng(41)
+    N, K, T = 256, 512, 16
+    blocks = _wide_range_blocks(oracle, rng, N, K)
+    X = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(torch.bfloat16)
+    w = pkg.pack_q4_1(blocks, gpu)
+    base = pkg.gemm_q4_prefill(w, X.to(gpu))
+    for p in (40, -40):
+        got = pkg.gemm_q4_prefill(w, (X.to(torch.float32) * 2.0 ** p).to(torch.bfloat16).to(gpu))
+        assert torch.equal(got, base * 2.0 ** p), p
+
+
+def _prefill_scales_numpy(oracle, blocks):
+    """(wexp int32[N], fp16 scale words uint32[N/64, KB, 64]) of a matrix, restated on the CPU:
+    e_n puts max_kb (15 |d| + |m|) (f32, bf16 d and m) in [2^14, 2^15) after 2^-e_n; each word
+    is fp16(d 2^-e) << 16 | fp16(m 2^-e) at (row % 16) * 4 + (row % 64) / 16 of its tile."""
+    b = np.asarray(blocks)
+    N, KB, _ = b.shape
+    d = oracle.bf16_to_f32(oracle.f32_to_bf16(np.ascontiguousarray(b[..., 0:2]).view(np.float16)[..., 0].astype(np.float32)))
+    m = oracle.bf16_to_f32(oracle.f32_to_bf16(np.ascontiguousarray(b[..., 2:4]).view(np.float16)[..., 0].astype(np.float32)))
+    bound = (np.float32(15) * np.abs(d) + np.abs(m)).astype(np.float32).max(axis=1)
+    _, ex = np.frexp(bound)
+    e = np.where((bound > 0) & (bound <= 3.0e38), ex - 15, 0).astype(np.int32)
+    dh = np.ldexp(d, -e[:, None]).astype(np.float16).view(np.uint16).astype(np.uint32)
+    mh = np.ldexp(m, -e[:, None]).astype(np.float16).view(np.uint16).astype(np.uint32)
+    words = (dh << 16) | mh                                           # [N, KB]
+    rows = np.arange(N)
+    slot = (rows % 16) * 4 + (rows % 64) // 16
+    plane = np.zeros((N // 64, KB, 64), np.uint32)
+    plane[rows // 64, :, slot] = words
+    return e, plane
+
+
+def test_prefill_scales_match_numpy_and_paths_agree(gpu, pkg, oracle):
+    """q4_prefill_scales bit for bit against a numpy restatement (over wide-range weights,
+    fp16 subnormal d included), and the per-call path (q4_gemm_prefill) equal to the cached
+    one (q4_gemm_prefill_scaled) bit for bit."""
+    say("prefill scales")
+    rng = np.random.default_rng(77)
+    N, K, T = 320, 1536, 100
+    blocks = _wide_range_blocks(oracle, rng, N, K, -6.0, 3.5)
+    w = pkg.pack_q4_1(blocks, gpu)
+    sc = pkg.prefill_scales(w).cpu().numpy()
+    e, plane = _prefill_scales_numpy(oracle, blocks)
+    assert np.array_equal(sc[:N * 4].view(np.int32), e)
+    off = (N * 4 + 255) // 256 * 256
+    got = sc[off:off + plane.size * 4].view(np.uint32).reshape(plane.shape)
+    assert np.array_equal(got, plane)
+    X = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    lib = pkg.load_library()
+    y_call = torch.empty(T, N, device=gpu)
+    ws = torch.empty(lib.q4_gemm_prefill_workspace_bytes(T, N, K), dtype=torch.uint8, device=gpu)
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    assert lib.q4_gemm_prefill(w.data.data_ptr(), X.data_ptr(), 1, y_call.data_ptr(), T, N, K, 0, ws.data_ptr(),
+                               ws.numel(), st) == 0
+    y_cached = pkg.gemm_q4_prefill(w, X)
+    assert torch.equal(y_call, y_cached)
