@@ -216,7 +216,10 @@ def graph_time(torch, fn, outputs, replays: int = 20, reset=None) -> float:
 # process so the BLAS thread count can be set before numpy loads
 # --------------------------------------------------------------------------
 
-def cpu_baseline_child(threads: int, passes: int) -> dict:
+def cpu_baseline_child(threads: int, passes: int, runs: int = 5) -> dict:
+    """One CPU worker: the oracle's restatement of the reference CPU path over one Llama-3-8B
+    layer in pool-chunk form, `runs` timed runs of `passes` passes each (after building the
+    layer, untimed). Returns the seconds of each run and the Q4_1 bytes one run streams."""
     import numpy as np
     from oracle import q4_oracle as O
     rng = np.random.default_rng(SEED)
@@ -230,39 +233,74 @@ def cpu_baseline_child(threads: int, passes: int) -> dict:
         chunks[:, 512:1024] = O.f32_to_bf16(m).view(np.uint8).reshape(nch, 512)
         layer.append((n, k, chunks, rng.standard_normal(k).astype(np.float32)))
     chunk_slice = 2048                                   # 10 MB of chunks -> 64 MB of f32 at a time
-    total_bytes, t = 0, time.perf_counter()
-    for _ in range(passes):
-        for n, k, chunks, x in layer:
-            per_row = k // 256                           # chunk c: rows 32 (c // per_row), k-tile c % per_row
-            xs = x.reshape(per_row, 256)
-            y = np.zeros((n // 32, 32), np.float32)
-            for c0 in range(0, chunks.shape[0], chunk_slice):
-                c1 = min(chunks.shape[0], c0 + chunk_slice)
-                w = O.dq_chunks_q4_1(chunks[c0:c1]).reshape(c1 - c0, 32, 256)
-                cc = np.arange(c0, c1)
-                part = np.matmul(w, xs[cc % per_row][:, :, None])[..., 0]
-                np.add.at(y, cc // per_row, part)
-            total_bytes += chunks.nbytes
-    secs = time.perf_counter() - t
-    return {"seconds": secs, "bytes": total_bytes, "gbs": total_bytes / secs / 1e9, "threads": threads,
-            "passes": passes}
+    run_bytes = passes * sum(c.nbytes for _, _, c, _ in layer)
+    secs = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        for _ in range(passes):
+            for n, k, chunks, x in layer:
+                per_row = k // 256                       # chunk c: rows 32 (c // per_row), k-tile c % per_row
+                xs = x.reshape(per_row, 256)
+                y = np.zeros((n // 32, 32), np.float32)
+                for c0 in range(0, chunks.shape[0], chunk_slice):
+                    c1 = min(chunks.shape[0], c0 + chunk_slice)
+                    w = O.dq_chunks_q4_1(chunks[c0:c1]).reshape(c1 - c0, 32, 256)
+                    cc = np.arange(c0, c1)
+                    part = np.matmul(w, xs[cc % per_row][:, :, None])[..., 0]
+                    np.add.at(y, cc // per_row, part)
+        secs.append(time.perf_counter() - t)
+    return {"run_seconds": secs, "run_bytes": run_bytes, "threads": threads, "passes": passes, "runs": runs}
 
 
-def cpu_baseline(threads: int, passes: int) -> dict | None:
+def cpu_model_name() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20)
+        for line in r.stdout.splitlines():
+            if line.strip().lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(workers: int, passes: int, runs: int = 5) -> dict | None:
+    """`workers` concurrent single-thread CPU workers (OPENBLAS_NUM_THREADS=1 each, the
+    reference harness's setting), each timing `runs` runs of `passes` passes over one layer.
+    A worker's rate is its median run; the leg's rate is the sum over workers (they run the
+    same work side by side), with the wall time of the whole parallel phase beside it."""
     env = dict(os.environ)
     for v in ("OPENBLAS_NUM_THREADS", "OMP_NUM_THREADS", "MKL_NUM_THREADS"):
-        env[v] = str(threads)
+        env[v] = "1"
     env["HIP_VISIBLE_DEVICES"] = ""      # the CPU leg never touches the GPU
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-child", "1", "--cpu-passes", str(passes),
+           "--cpu-runs", str(runs)]
+    t0 = time.perf_counter()
     try:
-        r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-child", str(threads),
-                            "--cpu-passes", str(passes)], capture_output=True, text=True, env=env, timeout=900)
-        if r.returncode != 0:
-            log(f"cpu baseline failed: {r.stderr[-500:]}")
-            return None
-        return json.loads(r.stdout.strip().splitlines()[-1])
+        procs = [subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, env=env)
+                 for _ in range(workers)]
+        outs = []
+        for p in procs:
+            so, se = p.communicate(timeout=900)
+            if p.returncode != 0:
+                log(f"cpu baseline worker failed: {se[-500:]}")
+                return None
+            outs.append(json.loads(so.strip().splitlines()[-1]))
     except Exception as e:  # the baseline is reported, never required
         log(f"cpu baseline skipped: {e}")
         return None
+    import statistics
+    med = [statistics.median(o["run_seconds"]) for o in outs]
+    rates = [o["run_bytes"] / m / 1e9 for o, m in zip(outs, med)]
+    return {"gbs": sum(rates), "workers": workers, "median_run_seconds": statistics.median(med),
+            "run_bytes": outs[0]["run_bytes"], "passes": passes, "runs": runs,
+            "wall_seconds": time.perf_counter() - t0, "worker_gbs_min": min(rates), "worker_gbs_max": max(rates)}
 
 
 # --------------------------------------------------------------------------
@@ -656,7 +694,8 @@ def main() -> int:
     ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks",
                     help="comma list (staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-passes", type=int, default=15, help="passes over one layer in the CPU baseline")
+    ap.add_argument("--cpu-passes", type=int, default=3, help="passes over one layer per timed CPU run")
+    ap.add_argument("--cpu-runs", type=int, default=5, help="timed runs per CPU worker (the median is reported)")
     ap.add_argument("--cpu-baseline-child", type=int, default=None, help=argparse.SUPPRESS)
     ap.add_argument("--only-extras", action="store_true",
                     help="skip the headline sweep; run the --extras list and print them (profiling runs)")
@@ -671,7 +710,7 @@ def main() -> int:
     a = ap.parse_args()
 
     if a.cpu_baseline_child is not None:
-        print(json.dumps(cpu_baseline_child(a.cpu_baseline_child, a.cpu_passes)))
+        print(json.dumps(cpu_baseline_child(a.cpu_baseline_child, a.cpu_passes, a.cpu_runs)))
         return 0
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or ws != 1:
@@ -760,20 +799,27 @@ def main() -> int:
 
     cpu = None
     if not a.no_cpu:
-        log(f"CPU baseline: numpy restatement, 1 thread, {a.cpu_passes} passes over one layer ...")
-        c1 = cpu_baseline(1, a.cpu_passes)
+        model_name = cpu_model_name()
+        log(f"CPU baseline ({model_name}): numpy restatement, 1 worker, {a.cpu_runs} runs of {a.cpu_passes} "
+            "passes over one layer ...")
+        c1 = cpu_baseline(1, a.cpu_passes, a.cpu_runs)
         cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-        log(f"CPU baseline: all {cores} cores ...")
-        call = cpu_baseline(cores, max(3, a.cpu_passes // 3))
+        log(f"CPU baseline: {cores} workers, one per core ...")
+        call = cpu_baseline(cores, 1, a.cpu_runs)
         if c1:
             cpu = {"value": round(c1["gbs"], 4), "unit": "GB/s", "cores": 1, "kind": "port",
-                   "sample": f"{c1['passes']} passes over one Llama-3-8B layer (q,k,v,o,gate,up,down; "
-                             f"{c1['bytes'] / c1['passes'] / 1e6:.1f} MB of Q4_1 each): pool-chunk dequant "
-                             "(q4nx.dq_chunks_q4_1 restated) + f32 matvec, OPENBLAS_NUM_THREADS=1",
-                   "seconds": round(c1["seconds"], 2)}
+                   "sample": f"median of {c1['runs']} runs, each {c1['passes']} passes over one Llama-3-8B layer "
+                             f"(q,k,v,o,gate,up,down; {c1['run_bytes'] / c1['passes'] / 1e6:.1f} MB of Q4_1 per "
+                             "pass): pool-chunk dequant (q4nx.dq_chunks_q4_1 restated) + f32 matvec, "
+                             "OPENBLAS_NUM_THREADS=1",
+                   "seconds_per_run": round(c1["median_run_seconds"], 3), "cpu_model": model_name}
             if call:
-                cpu["all_cores"] = {"value": round(call["gbs"], 4), "cores": cores,
-                                    "seconds": round(call["seconds"], 2), "passes": call["passes"]}
+                cpu["all_cores"] = {"value": round(call["gbs"], 4), "cores": cores, "workers": call["workers"],
+                                    "how": f"{cores} single-thread worker processes side by side, each the median "
+                                           f"of {call['runs']} runs of one pass; the sum of their rates",
+                                    "worker_gbs_range": [round(call["worker_gbs_min"], 4),
+                                                         round(call["worker_gbs_max"], 4)],
+                                    "wall_seconds": round(call["wall_seconds"], 2)}
 
     line = {
         "metric": "Q4_1 decode GEMV HBM GB/s (% of peak) at M=1; prefill GEMM TFLOP/s",
