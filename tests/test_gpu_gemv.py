@@ -259,3 +259,44 @@ def test_rejects_bad_shapes(gpu, pkg, oracle):
         pkg.gemm_q4(w, torch.zeros(17, 64, dtype=torch.bfloat16, device=gpu))
     with pytest.raises(ValueError):
         pkg.gemv_q4(w, torch.zeros(96, dtype=torch.bfloat16, device=gpu))
+
+
+def test_split_calls_share_one_workspace(gpu, pkg, oracle):
+    """K-split GEMVs back to back on ONE workspace: 60 calls alternating shapes, token counts
+    and operators (plain, residual, SwiGLU), every result bit-identical to the first call of
+    its kind and within the bar of the fp64 oracle."""
+    say("gemv splits: shared workspace")
+    rng = np.random.default_rng(61)
+    shapes = [(4096, 4096, 1), (1024, 4096, 3), (4096, 14336, 16), (6144, 4096, 5), (256, 2048, 2)]
+    cases = []
+    for n, k, M in shapes:
+        blocks = oracle.baseline_q4_1_blocks(n, k, rng)
+        X = _bf16(rng.standard_normal((M, k)))
+        w = pkg.pack_q4_1(blocks, gpu)
+        res = torch.from_numpy(rng.standard_normal((M, n)).astype(np.float32)).to(gpu)
+        cases.append((w, X.to(gpu), res, oracle.gemv_reference(blocks, X.to(torch.float32).numpy())))
+    gate = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(1024, 4096, rng), gpu)
+    up = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(1024, 4096, rng), gpu)
+    xs = _bf16(rng.standard_normal((2, 4096))).to(gpu)
+    need = max([pkg.gemv_workspace_bytes(X.shape[0], w.n, w.k) for w, X, _, _ in cases] +
+               [pkg.load_library().q4_gemv_swiglu_workspace_bytes(2, 1024, 4096)])
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    first = {}
+    for it in range(60):
+        i = it % (len(cases) + 1)
+        if i == len(cases):
+            got = pkg.swiglu_q4(gate, up, xs, workspace=ws)
+        elif (it // (len(cases) + 1)) % 2:            # alternate rounds: residual, plain
+            w, X, res, _ = cases[i]
+            got = pkg.gemm_q4(w, X, workspace=ws, residual=res)
+            i = -1 - i
+        else:
+            w, X, _, _ = cases[i]
+            got = pkg.gemm_q4(w, X, workspace=ws)
+        b = got.cpu().numpy().tobytes()
+        assert first.setdefault(i, b) == b, f"call {it} ({i}) differs from its first run"
+    for i, (w, X, res, ref) in enumerate(cases):
+        assert oracle.maxrel(np.frombuffer(first[i], np.float32).reshape(ref.shape), ref) <= MAXREL
+        if -1 - i in first:
+            r = np.frombuffer(first[-1 - i], np.float32).reshape(ref.shape)
+            assert oracle.maxrel(r, ref + res.cpu().numpy()) <= MAXREL
