@@ -50,9 +50,11 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
     y[i] = res ? res[i] + s : s;
 }
 
-template <int NTL, bool XF32>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
-    __shared__ float red[kWaves][4][NTL][64];
+// WAVES waves per workgroup (4, 8 or 16): more waves put more tiles of a row group in
+// flight, so fewer K splits fill the memory system.
+template <int NTL, bool XF32, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
+    __shared__ float red[WAVES][4][NTL][64];
     const int64_t item = blockIdx.x;
     const int S = P.S;
     const int64_t g = item / S;
@@ -64,9 +66,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
-    gemv_rows<NTL, XF32>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
-    if (S == 1) gemv_finish<NTL>(acc, red, P.M, P.y, P.N, g, P.res);
-    else gemv_finish<NTL>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
+    gemv_rows<NTL, XF32, DenseRows, WAVES>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
+    if (S == 1) gemv_finish<NTL, WAVES>(acc, red, P.M, P.y, P.N, g, P.res);
+    else gemv_finish<NTL, WAVES>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
 
 // The GEMV over the native Q4_K layout: split s takes super-blocks [sb0, sb1) of K / 256
@@ -230,25 +232,64 @@ __global__ __launch_bounds__(256) void swiglu_reduce_kernel(const float* __restr
 }
 
 // Workgroups to aim for when a matrix has few row groups.
-int64_t target_workgroups() {
+// Q4MI_GEMV_TARGET_WGS (experiments): the workgroup count to split toward, else 0.
+int64_t forced_target() {
     static int64_t t = [] {
         const char* e = getenv("Q4MI_GEMV_TARGET_WGS");
         const long v = e ? atol(e) : 0;
-        return (int64_t)(v > 0 ? v : 1024);
+        return (int64_t)(v > 0 ? v : 0);
     }();
     return t;
 }
 
 constexpr int64_t kMaxSplitGroups = 4096;                 // row groups a split call may have
 
-int choose_splits(int64_t N, int64_t K) {
+// Splits that bring N/64 row groups toward `target` workgroups (keeping >= 8 blocks, two
+// tiles per wave, per split).
+int splits_toward(int64_t N, int64_t K, int64_t target) {
     const int64_t G = N / 64, KB = K / 32;
-    const int64_t target = target_workgroups();
     if (G >= target || G > kMaxSplitGroups) return 1;
     int64_t S = ceil_div(target, G);
-    const int64_t max_s = KB / 8;           // keep >= 8 blocks (2 tiles per wave) per split
+    const int64_t max_s = KB / 8;
     if (S > max_s) S = max_s;
     return (int)(S < 1 ? 1 : S);
+}
+
+// The q8 pair, native q8 and SwiGLU kernels (4 waves): about 1024 workgroups.
+int choose_splits(int64_t N, int64_t K) {
+    const int64_t t = forced_target();
+    return splits_toward(N, K, t ? t : 1024);
+}
+
+// The plain GEMV's plan: K splits and waves per workgroup. Measured per Llama-3-8B shape in
+// a same-process A/B (M = 1, graph replays over rotating copies, bit-identical outputs
+// across plans up to the split order's fp32 rounding), against 1024 workgroups of 4 waves:
+//   28672 x 4096 (448 row groups): unsplit, 8 waves       19.1 -> 15.9 us
+//   14336 x 4096 (224):            unsplit, 16 waves      12.7 ->  9.6 us
+//    6144 x 4096 (96):             unsplit, 16 waves       8.6 ->  8.4 us
+//    4096 x 4096 (64):             4 splits, 8 waves       7.3 ->  7.0 us
+//    1024 x 4096 (16):             16 splits, 8 waves      5.6 ->  5.2 us
+//    4096 x 14336 (64):            16 splits, 4 waves (kept; 4 splits of 8 waves 12.9 us)
+// More waves keep more of a row group's tiles in flight, so fewer splits (and reduce
+// traffic) fill the memory system. From 1024 row groups on (lm_head) nothing changes.
+// Q4MI_GEMV_TARGET_WGS and Q4MI_GEMV_WAVES override, for experiments.
+struct GemvPlan {
+    int S, waves;
+};
+
+GemvPlan plan_gemv(int64_t N, int64_t K) {
+    static const int forced_waves = [] {
+        const char* e = getenv("Q4MI_GEMV_WAVES");
+        const int v = e ? atoi(e) : 0;
+        return v == 4 || v == 8 || v == 16 ? v : 0;
+    }();
+    const int64_t G = N / 64, t = forced_target();
+    if (t || forced_waves) return {splits_toward(N, K, t ? t : 1024), forced_waves ? forced_waves : 4};
+    if (G >= 1024) return {1, 4};
+    if (G >= 384) return {1, 8};
+    if (K <= 8192 && G >= 96) return {1, 16};
+    if (K <= 8192) return {splits_toward(N, K, 256), 8};
+    return {splits_toward(N, K, 1024), 4};
 }
 
 // Native Q4_K: split on whole super-blocks. A wave takes whole super-blocks, so S is the
@@ -260,7 +301,7 @@ constexpr int64_t kQ4kNoSplitGroups = 256;
 
 int q4k_splits(int64_t N, int64_t K) {
     const int64_t G = N / 64, SB = K / 256;
-    const int64_t target = target_workgroups();
+    const int64_t t = forced_target(), target = t ? t : 1024;
     if (G >= target || G >= kQ4kNoSplitGroups || SB < 8) return 1;
     const int64_t want = ceil_div(target, G), per_wave = SB / 4;
     for (int64_t S = 1; S <= per_wave; ++S)
@@ -294,11 +335,20 @@ void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, cons
     else hipLaunchKernelGGL((gemv_pair_kernel<NTL, false>), grid, dim3(256), 0, st, P, lo);
 }
 
-template <int NTL>
-void launch_gemv(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
-    if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true>), grid, dim3(256), 0, st, P);
-    else hipLaunchKernelGGL((gemv_kernel<NTL, false>), grid, dim3(256), 0, st, P);
+template <int NTL, int WAVES>
+void launch_gemv_w(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, WAVES>), grid, dim3(64 * WAVES), 0, st, P);
+    else hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES>), grid, dim3(64 * WAVES), 0, st, P);
 }
+
+template <int NTL>
+void launch_gemv(bool xf32, int waves, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (waves == 16) launch_gemv_w<NTL, 16>(xf32, grid, st, P);
+    else if (waves == 8) launch_gemv_w<NTL, 8>(xf32, grid, st, P);
+    else launch_gemv_w<NTL, 4>(xf32, grid, st, P);
+}
+
+
 
 template <int NTL>
 void launch_q4k(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
@@ -314,9 +364,11 @@ void launch_q8n(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
 
 }  // namespace
 
+// The plain GEMV and the q8 pair kernel share this query: it covers both plans.
 extern "C" size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K) {
     if (M < 1 || M > 16 || N <= 0 || K <= 0 || N % 64 || K % 32) return 0;
-    return workspace_for(M, N, K, choose_splits(N, K));
+    const size_t a = workspace_for(M, N, K, plan_gemv(N, K).S), b = workspace_for(M, N, K, choose_splits(N, K));
+    return a > b ? a : b;
 }
 
 namespace {
@@ -329,7 +381,8 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
     if (!packed || !x || !y) return Q4MI_E_ARG;
     if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
-    const int S = choose_splits(N, K);
+    const GemvPlan plan = lo ? GemvPlan{choose_splits(N, K), 4} : plan_gemv(N, K);
+    const int S = plan.S;
     GemvParams P{};
     P.packed = packed;
     P.x = x;
@@ -339,9 +392,8 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     P.N = N;
     P.K = K;
     P.res = res;
-    if (S > 1) {
-        const size_t need = workspace_for(M, N, K, S);
-        if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
+    if (S > 1) {   // the documented contract: at least what the query reports
+        if (!workspace || workspace_bytes < q4_gemv_workspace_bytes(M, N, K)) return Q4MI_E_WORKSPACE;
         P.part = (float*)workspace;
     }
     const dim3 grid((unsigned)((N / 64) * S));
@@ -355,11 +407,12 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
             default: launch_pair<4>(xf32, grid, st, P, lo); break;
         }
     } else {
+        const int waves = plan.waves;
         switch ((M + 3) / 4) {
-            case 1: launch_gemv<1>(xf32, grid, st, P); break;
-            case 2: launch_gemv<2>(xf32, grid, st, P); break;
-            case 3: launch_gemv<3>(xf32, grid, st, P); break;
-            default: launch_gemv<4>(xf32, grid, st, P); break;
+            case 1: launch_gemv<1>(xf32, waves, grid, st, P); break;
+            case 2: launch_gemv<2>(xf32, waves, grid, st, P); break;
+            case 3: launch_gemv<3>(xf32, waves, grid, st, P); break;
+            default: launch_gemv<4>(xf32, waves, grid, st, P); break;
         }
     }
     if (S > 1) {
@@ -382,8 +435,8 @@ extern "C" int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float*
 // q4_gemv_noalloc: q4_gemv with its K-split partial sums in a file-scope device array
 // instead of a caller workspace, for callers that cannot allocate device memory.
 //
-// The partials of a split call are [S][M][N] f32; the split policy (choose_splits) keeps
-// S * N/64 below 2048 for every N, so with M <= 16 they never exceed 2046 * 64 * 16 * 4 =
+// The partials of a split call are [S][M][N] f32; both split plans (plan_gemv, choose_splits)
+// keep S * N/64 below 2048 for every N, so with M <= 16 they never exceed 2046 * 64 * 16 * 4 =
 // 8,380,416 bytes, and Q4MI_NOALLOC_SCRATCH_BYTES (8 MiB) covers every shape. The gemv
 // kernel writes every partial it later reduces, so nothing needs clearing between calls.
 // Each device holds its own copy of the array; its address is read once per device

@@ -67,11 +67,12 @@ __device__ __forceinline__ void load_xfrag(const void* __restrict__ x, int64_t K
     }
 }
 
-// Accumulate this wave's share of tiles [kb0, kb1) of row group g.
+// Accumulate this wave's share of tiles [kb0, kb1) of row group g: with WAVES waves in
+// the workgroup, wave w takes tiles kb0 + w, kb0 + w + WAVES, ...
 // Loads are unconditional (a tile index past kb1 is clamped to kb1 - 1 and
 // its data skipped) so the compiler can count them statically and wait for
 // each tile's loads only, keeping kUnroll tiles in flight per wave.
-template <int NTL, bool XF32, class Rows>
+template <int NTL, bool XF32, class Rows, int WAVES = kWaves>
 __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, const void* __restrict__ x, Rows rows,
                                           int64_t K, int64_t g, int kb0, int kb1, float (&acc)[4][NTL]) {
     const int lane = threadIdx.x & 63;
@@ -104,11 +105,11 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
         xl[u] = xh[u];
     }
 
-    for (int kb = kb0 + wave; kb < kb1; kb += kWaves * kUnroll) {
+    for (int kb = kb0 + wave; kb < kb1; kb += WAVES * kUnroll) {
         u32x4 c[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            const int t = min(kb + kWaves * u, kb1 - 1);
+            const int t = min(kb + WAVES * u, kb1 - 1);
             const uint8_t* tp = gbase + (int64_t)t * kTileBytes;      // wave-uniform tile base
             c[u] = load_nt_u32x4(tp + coff);
             s[u] = load_nt_u32x4(tp + soff);
@@ -116,7 +117,7 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            if (kb + kWaves * u < kb1) {
+            if (kb + WAVES * u < kb1) {
                 f32x4 ns = mfma_bf16(xh[u], neg128, zero4);
                 if constexpr (XF32) ns = mfma_bf16(xl[u], neg128, ns);
                 f32x4 p[4];
@@ -339,10 +340,11 @@ __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG
     }
 }
 
-// Sum the four waves' accumulators through LDS. Afterwards thread t owns
+// Sum the WAVES waves' accumulators through LDS. Afterwards thread t < 256 owns
 // row 16 r + lane % 16 of the row group (r = t >> 6, lane = t & 63) for the
-// tokens token_of(lane / 16, j), j < NTL: v[j].
-template <int NTL>
+// tokens token_of(lane / 16, j), j < NTL: v[j] (the waves' sums pairwise, in a
+// fixed order). Threads from 256 on own nothing.
+template <int NTL, int WAVES = kWaves>
 __device__ __forceinline__ void wave_sum(float (&acc)[4][NTL], float (*red)[4][NTL][64], float (&v)[NTL]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 #pragma unroll
@@ -350,22 +352,32 @@ __device__ __forceinline__ void wave_sum(float (&acc)[4][NTL], float (*red)[4][N
 #pragma unroll
         for (int j = 0; j < NTL; ++j) red[wave][r][j][lane] = acc[r][j];
     __syncthreads();
+    if (wave >= 4) return;
     const int r = wave;
 #pragma unroll
-    for (int j = 0; j < NTL; ++j)
-        v[j] = (red[0][r][j][lane] + red[1][r][j][lane]) + (red[2][r][j][lane] + red[3][r][j][lane]);
+    for (int j = 0; j < NTL; ++j) {
+        float t[WAVES];
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) t[w] = red[w][r][j][lane];
+#pragma unroll
+        for (int h = WAVES / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int w = 0; w < h; ++w) t[w] = t[2 * w] + t[2 * w + 1];
+        v[j] = t[0];
+    }
 }
 
 // Store the row group's result (S == 1, plus the residual when one is given) or this
 // split's partial sums (res null).
-template <int NTL>
+template <int NTL, int WAVES = kWaves>
 __device__ __forceinline__ void gemv_finish(float (&acc)[4][NTL], float (*red)[4][NTL][64], int M,
                                             float* y, int64_t N, int64_t g, const float* res = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int64_t n = g * 64 + r * 16 + i16;
     float v[NTL];
-    wave_sum<NTL>(acc, red, v);
+    wave_sum<NTL, WAVES>(acc, red, v);
+    if (r >= 4) return;
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
         const int tok = token_of(kg, j);
