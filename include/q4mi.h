@@ -388,7 +388,8 @@ size_t q4_moe_workspace_bytes(int T, int E, int topk, int H, int F);
  *   gate / up (64 gate rows, then the same 64 rows of up, ...);
  * down: E experts, each an mx matrix [H, F];
  * x: [T][H] in x_dtype; topk_ids int32 [T][topk] in [0, E); topk_w f32.
- * H % 64 == 0, F % 64 == 0, 1 <= T*topk <= 4096, topk <= 16.
+ * H % 64 == 0, F % 64 == 0, 1 <= T*topk <= 4096, topk <= 16, E <= 8192; ids outside
+ * [0, E) contribute nothing.
  * Replaces moe_batch (moe_batch.py:145-281, per-slot
  * y = down(silu(gate x) * (up x))) with the host gather/scatter of
  * Core::moe_block (core.cpp:5150-5245) moved onto the device. */

@@ -19,6 +19,11 @@
 // and M tokens need only NTL = ceil(M / 4) accumulators per row (M <= 4: one,
 // as for a single token). f32 activations are split x = hi + lo (two bf16s,
 // |residual| <= 2^-18 |x|) and both halves go through the MFMA.
+//
+// gemv_rows_multi streams several row groups per K position with compiler-tracked
+// loads; gemv_rows_pipe is the same arithmetic as a rolling pipeline of inline-asm loads
+// with explicit waits, so a wave always has UNR K positions in flight (the routed-expert
+// kernels, whose workgroups stream short row-group spans and gain most from it).
 #pragma once
 
 #include "q4mi_device.h"
@@ -277,10 +282,43 @@ __device__ __forceinline__ void q8n_rows(const uint8_t* __restrict__ packed, con
     }
 }
 
+// The MFMAs and scale FMAs of one K position (32 K) of NG row groups: c / s the tiles' code
+// and scale words of this lane, xh / xl the activation fragment (xl only for f32 x).
+template <int NTL, bool XF32, int NG>
+__device__ __forceinline__ void multi_tile(const u32x4 (&c)[NG], const u32x4 (&s)[NG], bf16x8 xh, bf16x8 xl,
+                                           CodeConsts kc, float (&acc)[NG][4][NTL]) {
+    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ns = mfma_bf16(xh, neg128, zero4);
+    if constexpr (XF32) ns = mfma_bf16(xl, neg128, ns);
+    float sx[NTL];
+#pragma unroll
+    for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        f32x4 p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bf16x8 b = codes_to_bf16(c[i][r], kc);
+            p[r] = mfma_bf16(xh, b, ns);
+            if constexpr (XF32) p[r] = mfma_bf16(xl, b, p[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float d = bf16_hi_to_f32(s[i][r]), m = bf16_lo_to_f32(s[i][r]);
+#pragma unroll
+            for (int j = 0; j < NTL; ++j) {
+                acc[i][r][j] = __builtin_fmaf(d, p[r][j], acc[i][r][j]);
+                acc[i][r][j] = __builtin_fmaf(m, sx[j], acc[i][r][j]);
+            }
+        }
+    }
+}
+
 // gemv_rows over NG row groups at once (tile bases gbase[i], same K range and
 // activations): per K position the activation fragment and the -128 sum x
 // MFMA are shared by the NG groups, and NG x UNR tiles are in flight per wave.
-template <int NTL, bool XF32, int NG, int UNR, class Rows>
+template <int NTL, bool XF32, int NG, int UNR, int WAVES = kWaves, class Rows>
 __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG], const void* __restrict__ x, Rows rows,
                                                 int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL]) {
     const int lane = threadIdx.x & 63;
@@ -289,17 +327,15 @@ __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG
     kb1 = __builtin_amdgcn_readfirstlane(kb1);
     const int i16 = lane & 15, kg = lane >> 4;
     const int coff = lane * 16, soff = kCodeBytes + i16 * 16;
-    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
-    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     const CodeConsts kc = code_consts();
     const int64_t xrow = rows(token_of_row(i16));
 
-    for (int kb = kb0 + wave; kb < kb1; kb += kWaves * UNR) {
+    for (int kb = kb0 + wave; kb < kb1; kb += WAVES * UNR) {
         u32x4 c[UNR][NG], s[UNR][NG];
         bf16x8 xh[UNR], xl[UNR];
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
-            const int t = min(kb + kWaves * u, kb1 - 1);
+            const int t = min(kb + WAVES * u, kb1 - 1);
 #pragma unroll
             for (int i = 0; i < NG; ++i) {
                 const uint8_t* tp = gbase[i] + (int64_t)t * kTileBytes;
@@ -309,34 +345,106 @@ __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG
             load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
         }
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            if (kb + kWaves * u < kb1) {
-                f32x4 ns = mfma_bf16(xh[u], neg128, zero4);
-                if constexpr (XF32) ns = mfma_bf16(xl[u], neg128, ns);
-                float sx[NTL];
+        for (int u = 0; u < UNR; ++u)
+            if (kb + WAVES * u < kb1) multi_tile<NTL, XF32, NG>(c[u], s[u], xh[u], xl[u], kc, acc);
+    }
+}
+
+// 16 bytes per lane into registers, streaming, that the compiler does not track: the caller
+// waits for it (s_waitcnt vmcnt, in issue order) and passes the registers through
+// pipe_landed before any use. Weights: wave-uniform base + 32-bit lane offset.
+__device__ __forceinline__ void pipe_load_w(u32x4& dst, const void* gbase, uint32_t goff) {
+    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(dst) : "v"(goff), "s"(gbase) : "memory");
+}
+// Activations: a per-lane 64-bit address (gathered rows), cached.
+__device__ __forceinline__ void pipe_load_x(u32x4& dst, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst) : "v"(p) : "memory");
+}
+__device__ __forceinline__ void pipe_landed(u32x4& v) { asm volatile("" : "+v"(v)); }
+
+constexpr int pipe_wait_imm(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// gemv_rows_multi as a rolling pipeline with explicit waits: a wave keeps UNR K positions of
+// loads (NG tiles' codes and scales plus the activation fragment each) in flight at all
+// times. Its K positions are kb0 + wave + WAVES b, b = 0 .. cnt - 1; position b + UNR is
+// issued into the registers of position b as soon as b has been used, so the wait before
+// each position is always "all but the (UNR - 1) younger positions' loads". Positions past
+// cnt load the wave's last tile again (cache hits) and are not accumulated; the wave drains
+// them before it returns.
+template <int NTL, bool XF32, int NG, int UNR, int WAVES, class Rows>
+__device__ __forceinline__ void gemv_rows_pipe(const uint8_t* const (&gbase)[NG], const void* __restrict__ x, Rows rows,
+                                               int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL]) {
+    constexpr int XL = XF32 ? 2 : 1;                // activation loads per K position
+    constexpr int L = 2 * NG + XL;                  // loads per K position
+    static_assert((UNR - 1) * L <= 63, "vmcnt holds 6 bits");
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kb0 = __builtin_amdgcn_readfirstlane(kb0);
+    kb1 = __builtin_amdgcn_readfirstlane(kb1);
+    const int first = kb0 + wave;
+    if (first >= kb1) return;
+    const int cnt = (kb1 - first + WAVES - 1) / WAVES;
+    const int i16 = lane & 15, kg = lane >> 4;
+    const uint32_t coff = lane * 16, soff = kCodeBytes + i16 * 16;
+    const CodeConsts kc = code_consts();
+    const int64_t es = XF32 ? 4 : 2;
+    const uint8_t* xp = (const uint8_t*)x + (rows(token_of_row(i16)) * K + kg * 8) * es;
+    u32x4 c[UNR][NG], s[UNR][NG], xr[UNR][XL];
+    auto issue = [&](int b, int slot) {
+        const int t = first + WAVES * min(b, cnt - 1);
+        const uint32_t toff = (uint32_t)t * kTileBytes;
 #pragma unroll
-                for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
-#pragma unroll
-                for (int i = 0; i < NG; ++i) {
-                    f32x4 p[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const bf16x8 b = codes_to_bf16(c[u][i][r], kc);
-                        p[r] = mfma_bf16(xh[u], b, ns);
-                        if constexpr (XF32) p[r] = mfma_bf16(xl[u], b, p[r]);
-                    }
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float d = bf16_hi_to_f32(s[u][i][r]), m = bf16_lo_to_f32(s[u][i][r]);
-#pragma unroll
-                        for (int j = 0; j < NTL; ++j) {
-                            acc[i][r][j] = __builtin_fmaf(d, p[r][j], acc[i][r][j]);
-                            acc[i][r][j] = __builtin_fmaf(m, sx[j], acc[i][r][j]);
-                        }
-                    }
-                }
-            }
+        for (int i = 0; i < NG; ++i) {
+            pipe_load_w(c[slot][i], gbase[i], toff + coff);
+            pipe_load_w(s[slot][i], gbase[i], toff + soff);
         }
+        const uint8_t* xa = xp + (int64_t)t * 32 * es;
+#pragma unroll
+        for (int h = 0; h < XL; ++h) pipe_load_x(xr[slot][h], xa + 16 * h);
+    };
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) issue(u, u);
+    for (int b0 = 0; b0 < cnt; b0 += UNR) {
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            __builtin_amdgcn_s_waitcnt(pipe_wait_imm((UNR - 1) * L));
+#pragma unroll
+            for (int i = 0; i < NG; ++i) {
+                pipe_landed(c[u][i]);
+                pipe_landed(s[u][i]);
+            }
+#pragma unroll
+            for (int h = 0; h < XL; ++h) pipe_landed(xr[u][h]);
+            if (b0 + u < cnt) {
+                bf16x8 xh, xl;
+                if constexpr (XF32) {
+                    const f32x4 a = __builtin_bit_cast(f32x4, xr[u][0]), bb = __builtin_bit_cast(f32x4, xr[u][1]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const __bf16 ha = (__bf16)a[e], hb = (__bf16)bb[e];
+                        xh[e] = ha;
+                        xh[e + 4] = hb;
+                        xl[e] = (__bf16)(a[e] - (float)ha);
+                        xl[e + 4] = (__bf16)(bb[e] - (float)hb);
+                    }
+                } else {
+                    xh = __builtin_bit_cast(bf16x8, xr[u][0]);
+                }
+                multi_tile<NTL, XF32, NG>(c[u], s[u], xh, xl, kc, acc);
+            }
+            issue(b0 + u + UNR, u);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(pipe_wait_imm(0));
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            pipe_landed(c[u][i]);
+            pipe_landed(s[u][i]);
+        }
+#pragma unroll
+        for (int h = 0; h < XL; ++h) pipe_landed(xr[u][h]);
     }
 }
 

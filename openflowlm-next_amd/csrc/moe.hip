@@ -6,14 +6,15 @@
 // after the host gathers tokens per expert and before it scatters y with the
 // router weights (Core::moe_block, core.cpp:5150-5245). Here the gather and
 // the scatter run on the device, in three launches:
-//   1. gate/up: workgroup (expert e, 64-row group of F). It finds the (token,
-//      slot) pairs routed to e by a ballot compaction of ids (pair order, so
-//      the result is deterministic), streams e's 64 gate rows and the 64 up
+//   1. gate/up: workgroup (a, 64-row group of F), for the a-th routed expert e in
+//      ascending order (found from an LDS bitmap of ids, so the workgroups of the
+//      routed experts lead the grid and the rest leave at once). It finds the
+//      (token, slot) pairs routed to e by a ballot compaction of ids (pair order,
+//      so the result is deterministic), streams e's 64 gate rows and the 64 up
 //      rows next to them once for all those tokens (gemv_core.h, activations
 //      gathered by row index), and writes h = silu(g) * u in fp32 per pair.
-//      Workgroups of experts no token picked leave after the scan.
-//   2. down: workgroup (expert e, 64-row group of H): y_pair = down_e h_pair,
-//      h read as fp32 (split into two bf16 halves for the MFMA).
+//   2. down: workgroup (a, 64-row groups of H): y_pair = down_e h_pair, h read
+//      as fp32 (split into two bf16 halves for the MFMA).
 //   3. combine: out[t] = sum_j w[t][j] y_pair[t][j] in slot order j.
 // h stays fp32 (the fp64 replica's semantics, model/replica.py:131-140); the
 // reference kernel's bf16 rounding of h would cost ~2^-9 relative.
@@ -25,16 +26,68 @@ using namespace q4mi;
 namespace {
 
 constexpr int kMaxPairs = 4096;     // T * topk per call
+constexpr int kMaxExperts = 8192;   // one bit each in LDS, one 32-expert word per thread
 
-// The pairs p = t * topk + j with ids[p] == e, ascending, into `list`; returns
-// their count (all 256 threads call it; barriers inside).
+// Waves per workgroup, K positions in flight per wave and 64-row groups of H per down
+// workgroup. Measured at config 4 (128 experts, top-8 of 16 tokens, H 2048, F 768, bf16 x;
+// 84 routed experts, graph replays over 4 expert pools), per call: 4 waves, 2 positions (up),
+// 4 waves, 2 positions, 4 groups (down) 56.9 us; 4 positions in up 58.5 us; 3 in down
+// 59.6 us; 8 waves per workgroup 73 us; 2 row-group pairs per up workgroup 65 us; 2 or 1
+// groups per down workgroup 64 / 71 us.
+constexpr int kUpWaves = 4, kUpUnr = 2;
+constexpr int kDnWaves = 4, kDnUnr = 2, kDnGroups = 4;
+
+// The a-th expert, in ascending order, that at least one pair is routed to; -1 when fewer
+// than a + 1 are. Every thread of the workgroup calls it (barriers inside) and gets the
+// same answer: the routed experts are marked in an LDS bitmap, each thread counts one
+// 32-expert word, and a block-wide prefix sum of the counts finds the word and bit. The
+// expert kernels map their workgroups onto this list, so the workgroups of routed experts
+// come first in the grid and the rest leave at once.
+template <int WAVES>
+__device__ int active_expert(const int32_t* __restrict__ ids, int P, int E, int a) {
+    __shared__ uint32_t bits[kMaxExperts / 32];
+    __shared__ int wsum[WAVES];
+    __shared__ int found;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (E + 31) >> 5;
+    for (int i = tid; i < nw; i += 64 * WAVES) bits[i] = 0u;
+    if (tid == 0) found = -1;
+    __syncthreads();
+    for (int p = tid; p < P; p += 64 * WAVES) {
+        const int e = ids[p];
+        if (e >= 0 && e < E) atomicOr(&bits[e >> 5], 1u << (e & 31));
+    }
+    __syncthreads();
+    const uint32_t w = tid < nw ? bits[tid] : 0u;
+    const int c = __popc(w);
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int excl = incl - c;
+    for (int i = 0; i < wave; ++i) excl += wsum[i];
+    if (a >= excl && a < excl + c) {
+        uint32_t m = w;
+        for (int i = excl; i < a; ++i) m &= m - 1u;     // drop the lower set bits
+        found = tid * 32 + __builtin_ctz(m);
+    }
+    __syncthreads();
+    return found;
+}
+
+// The pairs p = t * topk + j with ids[p] == e, ascending, into `list`; returns their count
+// (every thread calls it; barriers inside).
+template <int WAVES>
 __device__ int collect_pairs(const int32_t* __restrict__ ids, int P, int e, int* list) {
-    __shared__ int wave_cnt[4];
+    __shared__ int wave_cnt[WAVES];
     __shared__ int base;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) base = 0;
     __syncthreads();
-    for (int p0 = 0; p0 < P; p0 += 256) {
+    for (int p0 = 0; p0 < P; p0 += 64 * WAVES) {
         const int p = p0 + tid;
         const bool hit = p < P && ids[p] == e;
         const uint64_t mask = __ballot(hit);
@@ -45,7 +98,8 @@ __device__ int collect_pairs(const int32_t* __restrict__ ids, int P, int e, int*
         for (int w = 0; w < wave; ++w) off += wave_cnt[w];
         if (hit) list[off + within] = p;
         __syncthreads();
-        if (tid == 0) base += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+        if (tid == 0)
+            for (int w = 0; w < WAVES; ++w) base += wave_cnt[w];
         __syncthreads();
     }
     return base;
@@ -53,9 +107,9 @@ __device__ int collect_pairs(const int32_t* __restrict__ ids, int P, int e, int*
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-template <int NTL, bool XF32>
+template <int NTL, bool XF32, int WAVES, int UNR>
 __device__ __forceinline__ void up_chunk(const uint8_t* wexp, const void* x, int H, int F, int rgp, const int* rows,
-                                         const int* pairs, int M, float (*red)[4][4][64], float* __restrict__ hbuf) {
+                                         const int* pairs, int M, float* red, float* __restrict__ hbuf) {
     // the gate rows (row group 2 rgp) and the up rows next to them (2 rgp + 1) in one stream
     float acc[2][4][NTL];
 #pragma unroll
@@ -67,13 +121,14 @@ __device__ __forceinline__ void up_chunk(const uint8_t* wexp, const void* x, int
     const int KB = H >> 5;
     const uint8_t* const gb[2] = {wexp + (int64_t)(2 * rgp) * KB * kTileBytes,
                                   wexp + (int64_t)(2 * rgp + 1) * KB * kTileBytes};
-    gemv_rows_multi<NTL, XF32, 2, 4>(gb, x, GatherRows{rows, M}, H, 0, KB, acc);
+    gemv_rows_pipe<NTL, XF32, 2, UNR, WAVES>(gb, x, GatherRows{rows, M}, H, 0, KB, acc);
     float (*rd)[4][NTL][64] = (float (*)[4][NTL][64])red;
     float vg[NTL], vu[NTL];
-    wave_sum<NTL>(acc[0], rd, vg);
+    wave_sum<NTL, WAVES>(acc[0], rd, vg);
     __syncthreads();
-    wave_sum<NTL>(acc[1], rd, vu);
+    wave_sum<NTL, WAVES>(acc[1], rd, vu);
     const int tid = threadIdx.x, lane = tid & 63, r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
+    if (r >= 4) return;
     const int64_t f = (int64_t)rgp * 64 + r * 16 + i16;
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
@@ -82,45 +137,48 @@ __device__ __forceinline__ void up_chunk(const uint8_t* wexp, const void* x, int
     }
 }
 
-// MAXNTL: accumulators per row (chunks of 4 * MAXNTL routed tokens). The register
-// allocation follows the largest instance a kernel holds: MAXNTL = 1 needs 132 VGPRs for
-// gate/up and 156 for down (3 waves per SIMD), MAXNTL = 4 188 and 224 (2 waves). An expert
-// with more than 4 * MAXNTL tokens streams its rows once per chunk.
+// Workgroup (a, rgp): the a-th routed expert's gate/up row-group pair rgp, for all the
+// pairs routed to it. MAXNTL: accumulators per row (chunks of 4 * MAXNTL routed tokens);
+// the register allocation follows the largest instance a kernel holds, so batches of at
+// most 2 pairs per expert on average take the one-accumulator instance. An expert with
+// more than 4 * MAXNTL pairs streams its rows once per chunk.
 template <bool XF32, int MAXNTL>
-__global__ __launch_bounds__(256) void moe_up_kernel(const uint8_t* __restrict__ gate_up, const void* __restrict__ x,
-                                                     const int32_t* __restrict__ ids, int P, int topk, int H, int F,
-                                                     float* __restrict__ hbuf) {
+__global__ __launch_bounds__(64 * kUpWaves) void moe_up_kernel(const uint8_t* __restrict__ gate_up,
+                                                               const void* __restrict__ x,
+                                                               const int32_t* __restrict__ ids, int P, int E,
+                                                               int topk, int H, int F, float* __restrict__ hbuf) {
     __shared__ int list[kMaxPairs];
     __shared__ int rows[16];
-    __shared__ float red[4][4][4][64];
+    __shared__ float red[kUpWaves * 4 * MAXNTL * 64];
     const int fg = F >> 6;
-    const int e = blockIdx.x / fg, rgp = blockIdx.x % fg;
-    const int cnt = collect_pairs(ids, P, e, list);
-    if (cnt == 0) return;
+    const int e = active_expert<kUpWaves>(ids, P, E, blockIdx.x / fg);
+    if (e < 0) return;
+    const int rgp = blockIdx.x % fg;
+    const int cnt = collect_pairs<kUpWaves>(ids, P, e, list);
     const uint8_t* wexp = gate_up + (int64_t)e * (2 * F / 64) * (H / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 4 * MAXNTL) {
         const int M = min(4 * MAXNTL, cnt - c0);
         if (threadIdx.x < 16) rows[threadIdx.x] = list[c0 + min((int)threadIdx.x, M - 1)] / topk;
         __syncthreads();
         if constexpr (MAXNTL == 1) {
-            up_chunk<1, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf);
+            up_chunk<1, XF32, kUpWaves, kUpUnr>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf);
         } else {
             switch ((M + 3) / 4) {
-                case 1: up_chunk<1, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
-                case 2: up_chunk<2, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
-                case 3: up_chunk<3, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
-                default: up_chunk<4, XF32>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
+                case 1: up_chunk<1, XF32, kUpWaves, kUpUnr>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
+                case 2: up_chunk<2, XF32, kUpWaves, kUpUnr>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
+                case 3: up_chunk<3, XF32, kUpWaves, kUpUnr>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
+                default: up_chunk<4, XF32, kUpWaves, kUpUnr>(wexp, x, H, F, rgp, rows, list + c0, M, red, hbuf); break;
             }
         }
         __syncthreads();
     }
 }
 
-// NG 64-row groups of H per down workgroup (4 when H % 256 == 0, else 1): K = F is short,
-// so one group alone is latency-bound.
-template <int NTL, int NG>
+// NG 64-row groups of H per down workgroup: K = F is short, so one group alone is
+// latency-bound.
+template <int NTL, int NG, int WAVES, int UNR>
 __device__ __forceinline__ void down_chunk(const uint8_t* wexp, const float* hbuf, int H, int F, int rg0,
-                                           const int* pairs, int M, float (*red)[4][4][64], float* __restrict__ ypair) {
+                                           const int* pairs, int M, float* red, float* __restrict__ ypair) {
     float acc[NG][4][NTL];
 #pragma unroll
     for (int i = 0; i < NG; ++i)
@@ -132,65 +190,81 @@ __device__ __forceinline__ void down_chunk(const uint8_t* wexp, const float* hbu
     const uint8_t* gb[NG];
 #pragma unroll
     for (int i = 0; i < NG; ++i) gb[i] = wexp + (int64_t)(rg0 + i) * KB * kTileBytes;
-    gemv_rows_multi<NTL, true, NG, NG == 1 ? 4 : 2>(gb, hbuf, GatherRows{pairs, M}, F, 0, KB, acc);
+    gemv_rows_pipe<NTL, true, NG, UNR, WAVES>(gb, hbuf, GatherRows{pairs, M}, F, 0, KB, acc);
     float (*rd)[4][NTL][64] = (float (*)[4][NTL][64])red;
     const int tid = threadIdx.x, lane = tid & 63, r = tid >> 6, i16 = lane & 15, kg = lane >> 4;
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
         float v[NTL];
         if (i) __syncthreads();
-        wave_sum<NTL>(acc[i], rd, v);
+        wave_sum<NTL, WAVES>(acc[i], rd, v);
         const int64_t n = (int64_t)(rg0 + i) * 64 + r * 16 + i16;
+        if (r < 4) {
 #pragma unroll
-        for (int j = 0; j < NTL; ++j) {
-            const int tok = token_of(kg, j);
-            if (tok < M) ypair[(int64_t)pairs[tok] * H + n] = v[j];
+            for (int j = 0; j < NTL; ++j) {
+                const int tok = token_of(kg, j);
+                if (tok < M) ypair[(int64_t)pairs[tok] * H + n] = v[j];
+            }
         }
     }
 }
 
+// Workgroup (a, g): NG row groups of H from g * NG of the a-th routed expert's down matrix.
 template <int NG, int MAXNTL>
-__global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t* __restrict__ down,
-                                                       const float* __restrict__ hbuf,
-                                                       const int32_t* __restrict__ ids, int P, int H, int F,
-                                                       float* __restrict__ ypair) {
+__global__ __launch_bounds__(64 * kDnWaves) void moe_down_kernel(const uint8_t* __restrict__ down,
+                                                                 const float* __restrict__ hbuf,
+                                                                 const int32_t* __restrict__ ids, int P, int E, int H,
+                                                                 int F, float* __restrict__ ypair) {
     __shared__ int list[kMaxPairs];
-    __shared__ float red[4][4][4][64];
-    const int hg = H >> 6, wg_per_e = hg / NG;
-    const int e = blockIdx.x / wg_per_e, rg0 = (blockIdx.x % wg_per_e) * NG;
-    const int cnt = collect_pairs(ids, P, e, list);
-    if (cnt == 0) return;
+    __shared__ float red[kDnWaves * 4 * MAXNTL * 64];
+    const int wg_per_e = (H >> 6) / NG;
+    const int e = active_expert<kDnWaves>(ids, P, E, blockIdx.x / wg_per_e);
+    if (e < 0) return;
+    const int rg0 = (blockIdx.x % wg_per_e) * NG;
+    const int cnt = collect_pairs<kDnWaves>(ids, P, e, list);
     const uint8_t* wexp = down + (int64_t)e * (H / 64) * (F / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 4 * MAXNTL) {
         const int M = min(4 * MAXNTL, cnt - c0);
         if constexpr (MAXNTL == 1) {
-            down_chunk<1, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair);
+            down_chunk<1, NG, kDnWaves, kDnUnr>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair);
         } else {
             switch ((M + 3) / 4) {
-                case 1: down_chunk<1, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
-                case 2: down_chunk<2, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
-                case 3: down_chunk<3, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
-                default: down_chunk<4, NG>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
+                case 1: down_chunk<1, NG, kDnWaves, kDnUnr>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
+                case 2: down_chunk<2, NG, kDnWaves, kDnUnr>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
+                case 3: down_chunk<3, NG, kDnWaves, kDnUnr>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
+                default: down_chunk<4, NG, kDnWaves, kDnUnr>(wexp, hbuf, H, F, rg0, list + c0, M, red, ypair); break;
             }
         }
         __syncthreads();
     }
 }
 
+// out[t][n..n+3] = sum_j w[t][j] y_pair[t][j][n..n+3], slot order j (H % 4 == 0). Workgroup
+// (chunk of 1024 n, token t): the token's ids and weights are uniform, and the slots' y loads
+// are all issued before the sum.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ ypair,
                                                           const int32_t* __restrict__ ids,
-                                                          const float* __restrict__ w, int T, int topk, int E, int H,
+                                                          const float* __restrict__ w, int topk, int E, int H,
                                                           float* __restrict__ out) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)T * H) return;
-    const int64_t t = idx / H, n = idx % H;
-    float s = 0.f;
-    for (int j = 0; j < topk; ++j) {
-        const int64_t p = t * topk + j;
-        const int e = ids[p];
-        if (e >= 0 && e < E) s += w[p] * ypair[p * H + n];
+    const int64_t t = blockIdx.y, n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (n >= H) return;
+    f32x4 y[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < topk) y[j] = load_global<f32x4>(ypair + (t * topk + j) * H + n);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < topk) {
+            const int e = ids[t * topk + j];
+            if (e >= 0 && e < E) {
+                const float wp = w[t * topk + j];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) s[c] += wp * y[j][c];
+            }
+        }
     }
-    out[idx] = s;
+    *(f32x4*)(out + t * H + n) = s;
 }
 
 // The block output with the residual and the gated shared expert folded into the combine,
@@ -255,7 +329,8 @@ static int moe_impl(const uint8_t* gate_up, const uint8_t* down, const void* x, 
     if (fin && (!shared) != (!shared_gate_w)) return Q4MI_E_ARG;
     if (H <= 0 || F <= 0 || H % 64 || F % 64) return Q4MI_E_SHAPE;
     if (H > (1 << 24) || F > (1 << 24)) return Q4MI_E_RANGE;
-    if (T < 0 || E <= 0 || topk <= 0 || topk > 16 || (int64_t)T * topk > kMaxPairs) return Q4MI_E_RANGE;
+    if (T < 0 || E <= 0 || E > kMaxExperts || topk <= 0 || topk > 16 || (int64_t)T * topk > kMaxPairs)
+        return Q4MI_E_RANGE;
     if (T == 0) return Q4MI_OK;
     if (!gate_up || !down || !x || !topk_ids || !topk_w || !out) return Q4MI_E_ARG;
     if (misaligned16(gate_up) || misaligned16(down) || misaligned16(x) || misaligned16(out) || misaligned16(workspace))
@@ -266,42 +341,45 @@ static int moe_impl(const uint8_t* gate_up, const uint8_t* down, const void* x, 
     float* hbuf = (float*)workspace;
     float* ypair = (float*)((char*)workspace + align256((size_t)P * F * 4));
     const hipStream_t st = (hipStream_t)stream;
-    const int ng = H % 256 == 0 ? 4 : 1;
-    const dim3 gu((unsigned)(E * (F / 64))), dn((unsigned)(E * (H / (64 * ng))));
+    // Workgroups for every expert that could be routed (at most min(E, P)); those past the
+    // routed count leave at once.
+    const int64_t routed_max = E < P ? E : P;
+    const int ng = H % (64 * kDnGroups) == 0 ? kDnGroups : 1;
+    const dim3 gu((unsigned)(routed_max * (F / 64))), dn((unsigned)(routed_max * (H / (64 * ng))));
+    const dim3 bu(64 * kUpWaves), bd(64 * kDnWaves);
     // At most 2 routed pairs per expert on average (decode batches): the one-accumulator
-    // instances, whose lower register use runs 3 waves per SIMD (config 4, 16 tokens x top-8
-    // of 128 experts: 66.7 -> 63.7 us, bit-identical). Larger batches stream each expert's
-    // rows once per 16 tokens instead of once per 4.
+    // instances, whose lower register use keeps more waves per SIMD. Larger batches stream
+    // each expert's rows once per 16 tokens instead of once per 4.
     const bool few = P <= 2 * E;
     if (x_dtype == Q4MI_F32) {
         if (few)
-            hipLaunchKernelGGL((moe_up_kernel<true, 1>), gu, dim3(256), 0, st, gate_up, x, topk_ids, P, topk, (int)H,
+            hipLaunchKernelGGL((moe_up_kernel<true, 1>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
                                (int)F, hbuf);
         else
-            hipLaunchKernelGGL((moe_up_kernel<true, 4>), gu, dim3(256), 0, st, gate_up, x, topk_ids, P, topk, (int)H,
+            hipLaunchKernelGGL((moe_up_kernel<true, 4>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
                                (int)F, hbuf);
     } else {
         if (few)
-            hipLaunchKernelGGL((moe_up_kernel<false, 1>), gu, dim3(256), 0, st, gate_up, x, topk_ids, P, topk,
-                               (int)H, (int)F, hbuf);
+            hipLaunchKernelGGL((moe_up_kernel<false, 1>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
+                               (int)F, hbuf);
         else
-            hipLaunchKernelGGL((moe_up_kernel<false, 4>), gu, dim3(256), 0, st, gate_up, x, topk_ids, P, topk,
-                               (int)H, (int)F, hbuf);
+            hipLaunchKernelGGL((moe_up_kernel<false, 4>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
+                               (int)F, hbuf);
     }
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-    if (ng == 4) {
+    if (ng == kDnGroups) {
         if (few)
-            hipLaunchKernelGGL((moe_down_kernel<4, 1>), dn, dim3(256), 0, st, down, hbuf, topk_ids, P, (int)H, (int)F,
-                               ypair);
+            hipLaunchKernelGGL((moe_down_kernel<kDnGroups, 1>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H,
+                               (int)F, ypair);
         else
-            hipLaunchKernelGGL((moe_down_kernel<4, 4>), dn, dim3(256), 0, st, down, hbuf, topk_ids, P, (int)H, (int)F,
-                               ypair);
+            hipLaunchKernelGGL((moe_down_kernel<kDnGroups, 4>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H,
+                               (int)F, ypair);
     } else {
         if (few)
-            hipLaunchKernelGGL((moe_down_kernel<1, 1>), dn, dim3(256), 0, st, down, hbuf, topk_ids, P, (int)H, (int)F,
+            hipLaunchKernelGGL((moe_down_kernel<1, 1>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H, (int)F,
                                ypair);
         else
-            hipLaunchKernelGGL((moe_down_kernel<1, 4>), dn, dim3(256), 0, st, down, hbuf, topk_ids, P, (int)H, (int)F,
+            hipLaunchKernelGGL((moe_down_kernel<1, 4>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H, (int)F,
                                ypair);
     }
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
@@ -314,9 +392,8 @@ static int moe_impl(const uint8_t* gate_up, const uint8_t* down, const void* x, 
                                topk, E, (int)H, x, shared_gate_w, shared, residual, out);
         return launch_status();
     }
-    const int64_t tot = (int64_t)T * H;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st, ypair, topk_ids,
-                       topk_w, T, topk, E, (int)H, out);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)ceil_div(H / 4, 256), (unsigned)T), dim3(256), 0, st, ypair,
+                       topk_ids, topk_w, topk, E, (int)H, out);
     return launch_status();
 }
 

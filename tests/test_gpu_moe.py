@@ -117,6 +117,25 @@ def test_moe_few_pairs_path_with_popular_experts(gpu, pkg, oracle):
     assert oracle.rel_fro(out, ref) <= 5e-3
 
 
+def test_moe_routed_experts_past_the_first_words(gpu, pkg, oracle):
+    """The expert kernels map their workgroups onto the routed experts in ascending order
+    (a bitmap of 32-expert words): with E = 300 and every token routed into experts
+    250..299, the routed experts sit in words 7..9 and the last word is partial. Also a
+    single token (8 workgroup rows of routed experts, the rest of the grid idle)."""
+    E, H, F = 300, 128, 64
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 4242)
+    for T, K in ((12, 4), (1, 8)):
+        say(f"moe E={E} T={T} top{K}, experts 250..299")
+        x = rng.standard_normal((T, H)).astype(np.float32)
+        xt = torch.from_numpy(x).to(torch.bfloat16)
+        ids = np.stack([rng.choice(np.arange(250, 300), K, replace=False) for _ in range(T)]).astype(np.int32)
+        w = rng.uniform(0.5, 1.5, (T, K)).astype(np.float32)
+        out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w).cpu().numpy()
+        ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy(), ids, w)
+        assert np.isfinite(out).all()
+        assert oracle.maxrel(out, ref) <= 1e-3, oracle.maxrel(out, ref)
+
+
 @pytest.mark.parametrize("E,H,F,T,K,xdt", [(16, 512, 256, 6, 4, "bf16"), (8, 256, 128, 5, 3, "f32"),
                                             (128, 2048, 768, 16, 8, "bf16")])
 def test_moe_fin_residual_and_shared_expert(gpu, pkg, oracle, E, H, F, T, K, xdt):

@@ -40,7 +40,8 @@ def inner_loops(asm: list[str]) -> list[list[str]]:
     for h, line in enumerate(asm):
         if "Loop Header" not in line or (inner and "Inner" not in line):
             continue
-        label = line.split(":")[0].strip()
+        # the header comment may sit on its own line under the block's label
+        label = (asm[h - 1] if line.lstrip().startswith(";") and h else line).split(":")[0].strip()
         name = label[2:] if label.startswith(".L") else label.lstrip(".")   # ".LBB0_1" -> "BB0_1"
         members = {label} | {l.split(":")[0].strip() for l in asm if f"in Loop: Header={name} " in l + " "}
         first = min(i for i, l in enumerate(asm) if l.split(":")[0].strip() in members and ":" in l)
@@ -109,6 +110,33 @@ def test_prefill_loop_waits_cover_every_asm_load(tmp_path):
                 n, bad = early_uses_in(body)
                 assert n >= 6, f"{what}: expected the weight loads of the unrolled loop, found {n}"
                 assert not bad, f"{what}: registers used before their load's wait: {bad[:3]}"
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+def test_moe_pipelined_loops_wait_for_every_asm_load(tmp_path):
+    """The routed-expert kernels stream through gemv_rows_pipe, whose loads are inline asm
+    with explicit waits: in every instance's K loop, each load's registers are touched only
+    after a wait that covers it (the loads of the next positions stay in flight)."""
+    src = SRC.parent / "moe.hip"
+    out = tmp_path / "moe.s"
+    cmd = ["hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{ROOT / 'include'}", f"-I{SRC.parent}", "--cuda-device-only", "-S",
+           str(src), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    text = out.read_text().splitlines()
+    kernels = [l.split(":")[0] for l in text if re.match(r"_ZN12_GLOBAL__N_1\w*moe_(up|down)_kernel\w*:", l)]
+    assert len(kernels) == 8
+    for k in kernels:
+        start = next(i for i, l in enumerate(text) if l.startswith(k + ":"))
+        stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
+        checked = 0
+        for body in inner_loops(text[start:stop]):
+            if sum(1 for l in body if re.match(r"\s*global_load_dwordx4", l)) < 4:
+                continue                        # the routing scans: compiler-tracked loads
+            n, bad = early_uses_in(body)
+            assert not bad, f"{k}: registers used before their load's wait: {bad[:3]}"
+            checked += n
+        assert checked >= 5, f"{k}: no pipelined K loop found"
 
 
 def test_checker_flags_an_early_use():
