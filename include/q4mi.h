@@ -194,9 +194,10 @@ int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stre
 size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K);
 
 /* Decode GEMV / skinny GEMM: Y[M][N] = X[M][K] . W[N][K]^T, fp32 accumulate,
- * fp32 out. 1 <= M <= 16. x_dtype Q4MI_F32 or Q4MI_BF16, X row-major [M][K].
+ * fp32 out. 1 <= M <= 24 (17..24: two 16-token blocks share each weight tile's loads).
+ * x_dtype Q4MI_F32 or Q4MI_BF16, X row-major [M][K].
  * Replaces gemv_q4 (M = 1; gemv_q4.py:118-123: pool in, bf16 x in, f32 y out)
- * and gemm_q4 (M = 1..24; gemm_q4.py:164-197); Y is the logical [M][N] order
+ * and gemm_q4 (M = 1..24; gemm_q4.py:9-13, :164-197); Y is the logical [M][N] order
  * (the reference's device order is core-interleaved, check.py:59-79). */
 int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
             int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
@@ -208,9 +209,10 @@ int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
 
 /* q4_gemv with no workspace argument and no allocation of any kind: its K-split partial
  * sums go to a file-scope device array of Q4MI_NOALLOC_SCRATCH_BYTES, whose per-device
- * address the library looks up on its first call on that device. Same shapes, kernels,
- * split order and bits as q4_gemv. Q4MI_E_WORKSPACE when a shape's partials would not fit
- * (none does under the current split policy: at most 8,380,416 bytes for M <= 16). Every
+ * address the library looks up on its first call on that device. Same kernels, split
+ * order and bits as q4_gemv, for 1 <= M <= 16 (Q4MI_E_RANGE above). Q4MI_E_WORKSPACE when
+ * a shape's partials would not fit (none does under the current split policy: at most
+ * 8,380,416 bytes for M <= 16). Every
  * call on one device shares that device's array: calls that overlap on one device (other
  * streams or host threads) race, so order them on one stream. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP graph
@@ -229,7 +231,8 @@ int q4_gemv_residual(const uint8_t* packed, const void* x, int x_dtype, const fl
 /* The q8 GEMV (the reference's gemv_q8 sibling, designs/gemv_q4's q8 twin): Y[M][N] =
  * X . (HI + LO)^T for a q8 matrix split by q4_repack_q8_split, exact in the weights;
  * both planes stream in one launch with shared activation fragments. residual (f32
- * [M][N], may be y) is added when not NULL. Same shapes and workspace as q4_gemv. */
+ * [M][N], may be y) is added when not NULL. Same shapes (1 <= M <= 16) and workspace as
+ * q4_gemv. */
 int q4_gemv_q8(const uint8_t* hi, const uint8_t* lo, const void* x, int x_dtype,
                const float* residual, float* y, int M, int64_t N, int64_t K,
                void* workspace, size_t workspace_bytes, void* stream);

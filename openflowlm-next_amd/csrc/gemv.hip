@@ -71,6 +71,35 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     else gemv_finish<NTL, WAVES>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
 
+// gemv_kernel for 17..24 tokens: two 16-token blocks (gemv_rows_tb2) over the same work
+// items and splits; block 1's rows are stored from y + 16 N (its partials from the split's
+// token row 16).
+template <int NTL2, bool XF32, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_tb2_kernel(GemvParams P) {
+    __shared__ float red[WAVES][4][4][64];
+    const int64_t item = blockIdx.x;
+    const int S = P.S;
+    const int64_t g = item / S;
+    const int s = (int)(item % S);
+    const int KB = (int)(P.K >> 5);
+    const int kb0 = (int)((int64_t)s * KB / S), kb1 = (int)((int64_t)(s + 1) * KB / S);
+    float acc0[4][4], acc1[4][NTL2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc0[r][j] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NTL2; ++j) acc1[r][j] = 0.f;
+    }
+    gemv_rows_tb2<NTL2, XF32, WAVES>(P.packed, P.x, P.M, P.K, g, kb0, kb1, acc0, acc1);
+    float* y = S == 1 ? P.y : P.part + (int64_t)s * P.M * P.N;
+    const float* res = S == 1 ? P.res : nullptr;
+    gemv_finish<4, WAVES>(acc0, red, 16, y, P.N, g, res);
+    __syncthreads();
+    gemv_finish<NTL2, WAVES>(acc1, (float (*)[4][NTL2][64])red, P.M - 16, y + 16 * P.N, P.N, g,
+                             res ? res + 16 * P.N : nullptr);
+}
+
 // The GEMV over the native Q4_K layout: split s takes super-blocks [sb0, sb1) of K / 256
 // (each wave whole super-blocks), then stores as gemv_kernel.
 template <int NTL, bool XF32>
@@ -242,6 +271,7 @@ int64_t forced_target() {
     return t;
 }
 
+constexpr int kMaxGemvTokens = 24;    // the plain GEMV; the q8 pair, SwiGLU, q8 and Q4_K kernels take 16
 constexpr int64_t kMaxSplitGroups = 4096;                 // row groups a split call may have
 
 // Splits that bring N/64 row groups toward `target` workgroups (keeping >= 8 blocks, two
@@ -348,6 +378,19 @@ void launch_gemv(bool xf32, int waves, dim3 grid, hipStream_t st, const GemvPara
     else launch_gemv_w<NTL, 4>(xf32, grid, st, P);
 }
 
+template <int NTL2, int WAVES>
+void launch_tb2_w(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (xf32) hipLaunchKernelGGL((gemv_tb2_kernel<NTL2, true, WAVES>), grid, dim3(64 * WAVES), 0, st, P);
+    else hipLaunchKernelGGL((gemv_tb2_kernel<NTL2, false, WAVES>), grid, dim3(64 * WAVES), 0, st, P);
+}
+
+template <int NTL2>
+void launch_tb2(bool xf32, int waves, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (waves == 16) launch_tb2_w<NTL2, 16>(xf32, grid, st, P);
+    else if (waves == 8) launch_tb2_w<NTL2, 8>(xf32, grid, st, P);
+    else launch_tb2_w<NTL2, 4>(xf32, grid, st, P);
+}
+
 
 
 template <int NTL>
@@ -366,7 +409,7 @@ void launch_q8n(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
 
 // The plain GEMV and the q8 pair kernel share this query: it covers both plans.
 extern "C" size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K) {
-    if (M < 1 || M > 16 || N <= 0 || K <= 0 || N % 64 || K % 32) return 0;
+    if (M < 1 || M > kMaxGemvTokens || N <= 0 || K <= 0 || N % 64 || K % 32) return 0;
     const size_t a = workspace_for(M, N, K, plan_gemv(N, K).S), b = workspace_for(M, N, K, choose_splits(N, K));
     return a > b ? a : b;
 }
@@ -376,7 +419,7 @@ namespace {
 int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* res, float* y, int M, int64_t N,
               int64_t K, void* workspace, size_t workspace_bytes, void* stream, const uint8_t* lo = nullptr) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
-    if (M < 0 || M > 16) return Q4MI_E_RANGE;
+    if (M < 0 || M > (lo ? 16 : kMaxGemvTokens)) return Q4MI_E_RANGE;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
     if (!packed || !x || !y) return Q4MI_E_ARG;
@@ -412,7 +455,9 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
             case 1: launch_gemv<1>(xf32, waves, grid, st, P); break;
             case 2: launch_gemv<2>(xf32, waves, grid, st, P); break;
             case 3: launch_gemv<3>(xf32, waves, grid, st, P); break;
-            default: launch_gemv<4>(xf32, waves, grid, st, P); break;
+            case 4: launch_gemv<4>(xf32, waves, grid, st, P); break;
+            case 5: launch_tb2<1>(xf32, waves, grid, st, P); break;
+            default: launch_tb2<2>(xf32, waves, grid, st, P); break;
         }
     }
     if (S > 1) {

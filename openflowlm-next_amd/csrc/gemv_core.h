@@ -282,6 +282,84 @@ __device__ __forceinline__ void q8n_rows(const uint8_t* __restrict__ packed, con
     }
 }
 
+// gemv_rows for 17 to 32 tokens (M > 16): two 16-token blocks share each tile's code and
+// scale loads. Block 0 holds tokens 0..15 (four accumulators per row, acc0), block 1 tokens
+// 16..M-1 (NTL2 accumulators, acc1); each block is the 16-token case above with its own
+// activation fragment, -128 sum and MFMAs. Lanes of block 1 whose token slot is past M keep
+// a zero fragment (their MFMA rows feed only discarded outputs).
+template <int NTL2, bool XF32, int WAVES = kWaves>
+__device__ __forceinline__ void gemv_rows_tb2(const uint8_t* __restrict__ packed, const void* __restrict__ x, int M,
+                                              int64_t K, int64_t g, int kb0, int kb1, float (&acc0)[4][4],
+                                              float (&acc1)[4][NTL2]) {
+    constexpr int UNR = 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kb0 = __builtin_amdgcn_readfirstlane(kb0);
+    kb1 = __builtin_amdgcn_readfirstlane(kb1);
+    const int i16 = lane & 15, kg = lane >> 4;
+    const int64_t KB = K >> 5;
+    const uint8_t* gbase = packed + g * KB * kTileBytes;
+    const int coff = lane * 16, soff = kCodeBytes + i16 * 16;
+    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const CodeConsts kc = code_consts();
+    const int64_t row0 = token_of_row(i16), tok1 = 16 + token_of_row(i16);
+    const bool need1 = tok1 < M;
+    const bf16x8 zx = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    bf16x8 xh1[UNR], xl1[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) xh1[u] = xl1[u] = zx;
+
+    for (int kb = kb0 + wave; kb < kb1; kb += WAVES * UNR) {
+        u32x4 c[UNR], s[UNR];
+        bf16x8 xh0[UNR], xl0[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int t = min(kb + WAVES * u, kb1 - 1);
+            const uint8_t* tp = gbase + (int64_t)t * kTileBytes;
+            c[u] = load_nt_u32x4(tp + coff);
+            s[u] = load_nt_u32x4(tp + soff);
+            load_xfrag<XF32>(x, K, row0, (int64_t)t * 32 + kg * 8, xh0[u], xl0[u]);
+            if (need1) load_xfrag<XF32>(x, K, tok1, (int64_t)t * 32 + kg * 8, xh1[u], xl1[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            if (kb + WAVES * u < kb1) {
+                f32x4 ns0 = mfma_bf16(xh0[u], neg128, zero4), ns1 = mfma_bf16(xh1[u], neg128, zero4);
+                if constexpr (XF32) {
+                    ns0 = mfma_bf16(xl0[u], neg128, ns0);
+                    ns1 = mfma_bf16(xl1[u], neg128, ns1);
+                }
+                f32x4 p0[4], p1[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bf16x8 b = codes_to_bf16(c[u][r], kc);
+                    p0[r] = mfma_bf16(xh0[u], b, ns0);
+                    p1[r] = mfma_bf16(xh1[u], b, ns1);
+                    if constexpr (XF32) {
+                        p0[r] = mfma_bf16(xl0[u], b, p0[r]);
+                        p1[r] = mfma_bf16(xl1[u], b, p1[r]);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float d = bf16_hi_to_f32(s[u][r]), m = bf16_lo_to_f32(s[u][r]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc0[r][j] = __builtin_fmaf(d, p0[r][j], acc0[r][j]);
+                        acc0[r][j] = __builtin_fmaf(m, ns0[j] * (-1.0f / 128.0f), acc0[r][j]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < NTL2; ++j) {
+                        acc1[r][j] = __builtin_fmaf(d, p1[r][j], acc1[r][j]);
+                        acc1[r][j] = __builtin_fmaf(m, ns1[j] * (-1.0f / 128.0f), acc1[r][j]);
+                    }
+                }
+            }
+        }
+    }
+}
+
 // The MFMAs and scale FMAs of one K position (32 K) of NG row groups: c / s the tiles' code
 // and scale words of this lane, xh / xl the activation fragment (xl only for f32 x).
 template <int NTL, bool XF32, int NG>

@@ -7,7 +7,7 @@ weights in, bf16 or fp32 activations in, fp32 out:
 * ``dequant``                          dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:173-180,
                                        model/q4nx.py:105-126), bit-exact
 * ``gemv_q4``                          designs/gemv_q4 (gemv_q4.py:118-123): y[N] = W x
-* ``gemm_q4``                          designs/gemm_q4 (gemm_q4.py:164-197): Y[M,N], M <= 16
+* ``gemm_q4``                          designs/gemm_q4 (gemm_q4.py:164-197): Y[M,N], M <= 24
 * ``gemm_q4_prefill``                  designs/gemm_q4_prefill (gemm_q4_prefill.py:171-177)
 * ``moe_batch``                        designs/moe_batch + Core::moe_block's gather/scatter
                                        (moe_batch.py:145-281, core.cpp:5150-5245)
@@ -558,8 +558,9 @@ def _acts(x, dev: torch.device) -> torch.Tensor:
 
 def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
             residual: torch.Tensor | None = None) -> torch.Tensor:
-    """Y[M, N] = X[M, K] @ W^T for 1 <= M <= 16 decode tokens, fp32 out
-    (gemm_q4.py:164-197's operator, logical [M, N] order). ``workspace``
+    """Y[M, N] = X[M, K] @ W^T for 1 <= M <= 24 decode tokens, fp32 out
+    (gemm_q4.py:164-197's operator, logical [M, N] order; the reference's blocked dataflow
+    covers M = 1..24, gemm_q4.py:9-13). ``workspace``
     (>= gemv_workspace_bytes) avoids the cached one, e.g. under graph capture.
     ``residual`` (f32 [M, N]) is added in the epilogue -- the x_res + W h of
     model/replica.py:81 -- and may be ``y`` itself to accumulate in place."""
@@ -570,8 +571,8 @@ def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tens
     M, K = xt.shape
     if K != w.k:
         raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
-    if not 1 <= M <= 16:
-        raise ValueError(f"gemm_q4 takes 1..16 tokens, got {M} (use gemm_q4_prefill)")
+    if not 1 <= M <= 24:
+        raise ValueError(f"gemm_q4 takes 1..24 tokens, got {M} (use gemm_q4_prefill)")
     y = _buf(y, "y", torch.float32, (M, w.n), dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):

@@ -86,7 +86,9 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_dequant(fake, None, 64, 32, None) == -2
     assert lib.q4_dequant(None, None, 0, 32, None) == 0
     assert lib.q4_gemv(fake, fake, 2, fake, 1, 64, 32, None, 0, None) == -2    # dtype
-    assert lib.q4_gemv(fake, fake, 1, fake, 17, 64, 32, None, 0, None) == -5   # M > 16
+    assert lib.q4_gemv(fake, fake, 1, fake, 25, 64, 32, None, 0, None) == -5   # M > 24
+    assert lib.q4_gemv_q8(fake, fake, fake, 1, None, fake, 17, 64, 32, None, 0, None) == -5   # pair: M > 16
+    assert lib.q4_gemv_noalloc(fake, fake, 1, fake, 17, 64, 32, None) == -5     # no-alloc: M > 16
     assert lib.q4_gemv(fake, fake, 1, fake, 1, 100, 32, None, 0, None) == -1   # N % 64
     assert lib.q4_gemv(None, None, 1, None, 0, 64, 32, None, 0, None) == 0     # M = 0
     # a short matrix is split along K and needs the workspace the query reports

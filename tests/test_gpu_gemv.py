@@ -119,7 +119,7 @@ def test_gemv_matches_oracle(gpu, pkg, oracle, xdt, n, k):
     assert mr < REF_GATE and _cos(y, ref) > 0.9999999, (mr, _cos(y, ref))
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 13, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 13, 16, 17, 20, 21, 24])
 def test_skinny_gemm_distinct_tokens(gpu, pkg, oracle, M):
     say(f"gemm_q4 M={M}")
     rng = np.random.default_rng(100 + M)
@@ -134,9 +134,32 @@ def test_skinny_gemm_distinct_tokens(gpu, pkg, oracle, M):
     assert oracle.maxrel(Y, ref) <= MAXREL
     # every token row of the batch equals that token run alone, bit for bit
     # (MFMA rows are independent and the epilogue is per token)
-    for t in (0, M - 1):
+    for t in sorted({0, min(15, M - 1), min(16, M - 1), M - 1}):
         y1 = pkg.gemv_q4(w, X[t].to(gpu)).cpu().numpy()
         assert y1.tobytes() == Y[t].tobytes()
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336)])
+def test_two_token_blocks_on_plan_shapes(gpu, pkg, oracle, xdt, n, k):
+    """M = 17..24 runs two 16-token blocks over one weight stream (block 1 from token 16).
+    On an unsplit 16-wave shape (6144 x 4096) and a split one (4096 x 14336, 16 K splits),
+    with the residual epilogue: within the bar of the oracle, and every token row equal, bit
+    for bit, to that token run alone."""
+    M = 23
+    say(f"gemm_q4 two token blocks M={M} {n}x{k} {xdt}")
+    rng = np.random.default_rng(n + k + M)
+    blocks = oracle.baseline_q4_1_blocks(n, k, rng)
+    xf = rng.standard_normal((M, k)).astype(np.float32)
+    X = _bf16(xf) if xdt == "bf16" else torch.from_numpy(xf)
+    res = rng.standard_normal((M, n)).astype(np.float32)
+    w = pkg.pack_q4_1(blocks, gpu)
+    Y = pkg.gemm_q4(w, X.to(gpu), residual=torch.from_numpy(res).to(gpu)).cpu().numpy()
+    ref = oracle.gemv_reference(blocks, X.to(torch.float32).numpy()) + res
+    assert oracle.maxrel(Y, ref) <= MAXREL
+    for t in (0, 3, 15, 16, 19, 22):
+        y1 = pkg.gemm_q4(w, X[t:t + 1].to(gpu), residual=torch.from_numpy(res[t:t + 1]).to(gpu)).cpu().numpy()
+        assert y1.tobytes() == Y[t:t + 1].tobytes(), t
 
 
 @pytest.mark.parametrize("xdt", ["bf16", "f32"])
@@ -256,7 +279,7 @@ def test_rejects_bad_shapes(gpu, pkg, oracle):
     rng = np.random.default_rng(40)
     w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(64, 64, rng), gpu)
     with pytest.raises(ValueError):
-        pkg.gemm_q4(w, torch.zeros(17, 64, dtype=torch.bfloat16, device=gpu))
+        pkg.gemm_q4(w, torch.zeros(25, 64, dtype=torch.bfloat16, device=gpu))
     with pytest.raises(ValueError):
         pkg.gemv_q4(w, torch.zeros(96, dtype=torch.bfloat16, device=gpu))
 
