@@ -458,6 +458,48 @@ def extra_q8(torch, q4, dev):
     return out
 
 
+def extra_q40(torch, q4, dev):
+    """The Q4_0-native GEMV (mx0, 0.5625 B per weight) against the widened Q4_1 layout of
+    the same GGUF Q4_0 blocks (mx, 0.625 B per weight) at M=1 on Llama-3-8B shapes,
+    graph-timed over rotating copies; outputs bit-identical."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 17)
+    out = {}
+    for name, n, k in (("o", 4096, 4096), ("down", 4096, 14336), ("gate_up", 28672, 4096),
+                       ("lm_head", 128256, 4096)):
+        blocks = torch.empty((n, k // 32, 18), dtype=torch.uint8, device=dev)
+        d = (torch.randn(n, k // 32, generator=gen, device=dev).abs() * 0.002 + 1e-4).to(torch.float16)
+        blocks[..., 0:2] = d.view(torch.uint8).view(n, k // 32, 2)
+        blocks[..., 2:] = torch.randint(0, 256, (n, k // 32, 16), generator=gen, device=dev, dtype=torch.uint8)
+        copies = max(2, min(32, int(1.2e9 // (n * k))))
+        w0 = [q4.pack_q4_0_native(blocks, n, k, "q4_0", device=dev) for _ in range(copies)]
+        w1 = [q4.pack_q4_1(blocks, dev) for _ in range(copies)]
+        del blocks
+        x = torch.randn(1, k, generator=gen, device=dev).to(torch.bfloat16)
+        y0 = torch.empty(1, n, dtype=torch.float32, device=dev)
+        y1 = torch.empty(1, n, dtype=torch.float32, device=dev)
+        wsp = torch.empty(max(q4.gemv_workspace_bytes(1, n, k), 256), dtype=torch.uint8, device=dev)
+
+        def run0():
+            for w in w0:
+                q4.gemm_q4_0_native(w, x, y0, workspace=wsp)
+
+        def run1():
+            for w in w1:
+                q4.gemm_q4(w, x, y1, workspace=wsp)
+        ms0 = graph_time(torch, run0, [y0], replays=10) / copies
+        ms1 = graph_time(torch, run1, [y1], replays=10) / copies
+        if not torch.equal(y0, y1):
+            raise RuntimeError(f"{name}: the Q4_0-native GEMV differs from the widened layout's")
+        io = k * 2 + n * 4
+        out[name] = {"N": n, "K": k, "native_us": round(ms0 * 1e3, 2),
+                     "native_gbs": round((w0[0].nbytes + io) / ms0 / 1e6, 1),
+                     "widened_us": round(ms1 * 1e3, 2), "widened_gbs": round((w1[0].nbytes + io) / ms1 / 1e6, 1)}
+        del w0, w1
+        torch.cuda.empty_cache()
+    return out
+
+
 def extra_q4k(torch, q4, dev):
     """GGUF Q4_K weights at M=1 on the Llama-3-8B gate_up, down and lm_head shapes: the
     native Q4_K kernel (the super-block's integers, 0.594 B/weight, exact) against the
@@ -691,7 +733,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks",
+    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,q8,q4k,q40,peaks",
                     help="comma list (staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=3, help="passes over one layer per timed CPU run")
@@ -753,6 +795,8 @@ def main() -> int:
                 out["q8_gemv"] = extra_q8(torch, q4, dev)
             elif cfg == "q4k":
                 out["q4k_native_gemv"] = extra_q4k(torch, q4, dev)
+            elif cfg == "q40":
+                out["q4_0_native_gemv"] = extra_q40(torch, q4, dev)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -792,6 +836,8 @@ def main() -> int:
                 extras["q8_gemv"] = extra_q8(torch, q4, dev)
             elif cfg == "q4k":
                 extras["q4k_native_gemv"] = extra_q4k(torch, q4, dev)
+            elif cfg == "q40":
+                extras["q4_0_native_gemv"] = extra_q40(torch, q4, dev)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
         log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")

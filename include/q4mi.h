@@ -253,6 +253,34 @@ int q4_repack_q8_native(const uint8_t* src, int src_format, int rs, uint8_t* pac
 /* mx8 -> f32 [N][K] row-major, w = s * q (exact). */
 int q4_dequant_q8_native(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
 
+/* Q4_0-native ("mx0" layout): Q4_0 stores no min, so the 64-row x 32-K tile is the mx
+ * codes plus one bf16 d per row, 1152 bytes (0.5625 bytes per weight against the widened
+ * Q4_1's 0.625). Weight = fl32(q d + m) with m = -8 d, exact: the same values as q4_repack of
+ * the same 18-byte blocks. The counterpart of the reference's Q4_0-native chunk
+ * (open_kernels/q4_1_pack.py:145-152, 4608 B: the d plane and the codes, no m plane) and of
+ * its GEMV build that reads it (designs/gemv_q4/gemv_q4.h:66-82, GEMV_Q4_0_NATIVE, m = -8 d).
+ * Bytes of an [N, K] matrix (N % 64 == 0, K % 32 == 0), or -1: */
+int64_t q4_q40_packed_bytes(int64_t N, int64_t K);
+
+/* Q4_0 -> mx0, on the device. src_format 0: GGUF Q4_0 blocks (18 B, row-major [N][K/32]),
+ * d narrowed fp16 -> bf16 by RNE as pack_q4_1_pool narrows it (q4_1_pack.py:129-130);
+ * 1: the reference's 4608 B Q4_0-native chunks in pool order with row split rs
+ * (pack_q4_0_native_pool, q4_1_pack.py:148-152; K % 256 == 0, N % (32 rs) == 0), bytes
+ * carried over. */
+int q4_repack_q40(const uint8_t* src, int src_format, int rs, uint8_t* packed, int64_t N, int64_t K,
+                  void* stream);
+
+/* mx0 -> f32 [N][K] row-major, w = fl32(q d - 8 d) (bit-exact with the reference's
+ * dequant_chunk of the same Q4_0 values, q4_1_pack.py:155-170). */
+int q4_dequant_q40(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
+
+/* Y[M][N] = X[M][K] . W^T over an mx0 matrix, 1 <= M <= 16, plus residual (f32 [M][N], may
+ * be y) when not NULL. q4_gemv's work items, split plan and workspace
+ * (q4_gemv_workspace_bytes); bit-identical to q4_gemv over q4_repack of the same Q4_0
+ * blocks. Replaces gemv_q4 built with GEMV_Q4_0_NATIVE (gemv_q4.h:66-82, :235-238). */
+int q4_gemv_q40(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
+                int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes q4_gemv_q8_native needs (0 if none; the same as q4_gemv's). */
 size_t q4_gemv_q8_native_workspace_bytes(int M, int64_t N, int64_t K);
 

@@ -44,6 +44,10 @@ SIGNATURES = {
     "q4_q8_native_packed_bytes": (_i64, [_i64, _i64]),
     "q4_repack_q8_native": (_i32, [_vp, _i32, _i32, _vp, _i64, _i64, _vp]),
     "q4_dequant_q8_native": (_i32, [_vp, _vp, _i64, _i64, _vp]),
+    "q4_q40_packed_bytes": (_i64, [_i64, _i64]),
+    "q4_repack_q40": (_i32, [_vp, _i32, _i32, _vp, _i64, _i64, _vp]),
+    "q4_dequant_q40": (_i32, [_vp, _vp, _i64, _i64, _vp]),
+    "q4_gemv_q40": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_gemv_q8_native_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemv_q8_native": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_repack_pool_signed": (_i32, [_vp, _i32, _vp, _i64, _i64, _vp]),

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 
 // WAVES waves per workgroup (4, 8 or 16): more waves put more tiles of a row group in
 // flight, so fewer K splits fill the memory system.
-template <int NTL, bool XF32, int WAVES>
+template <int NTL, bool XF32, int WAVES, bool Q40 = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     __shared__ float red[WAVES][4][NTL][64];
     const int64_t item = blockIdx.x;
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
-    gemv_rows<NTL, XF32, DenseRows, WAVES>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
+    gemv_rows<NTL, XF32, DenseRows, WAVES, Q40>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
     if (S == 1) gemv_finish<NTL, WAVES>(acc, red, P.M, P.y, P.N, g, P.res);
     else gemv_finish<NTL, WAVES>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
@@ -365,17 +365,17 @@ void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, cons
     else hipLaunchKernelGGL((gemv_pair_kernel<NTL, false>), grid, dim3(256), 0, st, P, lo);
 }
 
-template <int NTL, int WAVES>
+template <int NTL, int WAVES, bool Q40>
 void launch_gemv_w(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
-    if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, WAVES>), grid, dim3(64 * WAVES), 0, st, P);
-    else hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES>), grid, dim3(64 * WAVES), 0, st, P);
+    if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, WAVES, Q40>), grid, dim3(64 * WAVES), 0, st, P);
+    else hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, Q40>), grid, dim3(64 * WAVES), 0, st, P);
 }
 
-template <int NTL>
+template <int NTL, bool Q40 = false>
 void launch_gemv(bool xf32, int waves, dim3 grid, hipStream_t st, const GemvParams& P) {
-    if (waves == 16) launch_gemv_w<NTL, 16>(xf32, grid, st, P);
-    else if (waves == 8) launch_gemv_w<NTL, 8>(xf32, grid, st, P);
-    else launch_gemv_w<NTL, 4>(xf32, grid, st, P);
+    if (waves == 16) launch_gemv_w<NTL, 16, Q40>(xf32, grid, st, P);
+    else if (waves == 8) launch_gemv_w<NTL, 8, Q40>(xf32, grid, st, P);
+    else launch_gemv_w<NTL, 4, Q40>(xf32, grid, st, P);
 }
 
 template <int NTL2, int WAVES>
@@ -417,9 +417,10 @@ extern "C" size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K) {
 namespace {
 
 int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* res, float* y, int M, int64_t N,
-              int64_t K, void* workspace, size_t workspace_bytes, void* stream, const uint8_t* lo = nullptr) {
+              int64_t K, void* workspace, size_t workspace_bytes, void* stream, const uint8_t* lo = nullptr,
+              bool q40 = false) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
-    if (M < 0 || M > (lo ? 16 : kMaxGemvTokens)) return Q4MI_E_RANGE;
+    if (M < 0 || M > (lo || q40 ? 16 : kMaxGemvTokens)) return Q4MI_E_RANGE;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
     if (!packed || !x || !y) return Q4MI_E_ARG;
@@ -448,6 +449,14 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
             case 2: launch_pair<2>(xf32, grid, st, P, lo); break;
             case 3: launch_pair<3>(xf32, grid, st, P, lo); break;
             default: launch_pair<4>(xf32, grid, st, P, lo); break;
+        }
+    } else if (q40) {
+        const int waves = plan.waves;
+        switch ((M + 3) / 4) {
+            case 1: launch_gemv<1, true>(xf32, waves, grid, st, P); break;
+            case 2: launch_gemv<2, true>(xf32, waves, grid, st, P); break;
+            case 3: launch_gemv<3, true>(xf32, waves, grid, st, P); break;
+            default: launch_gemv<4, true>(xf32, waves, grid, st, P); break;
         }
     } else {
         const int waves = plan.waves;
@@ -539,6 +548,12 @@ extern "C" int q4_gemv_q8(const uint8_t* hi, const uint8_t* lo, const void* x, i
                           void* stream) {
     if (M > 0 && N > 0 && (!lo || misaligned16(lo))) return Q4MI_E_ARG;
     return gemv_impl(hi, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream, lo);
+}
+
+// The mx0 (Q4_0-native) GEMV: q4_gemv's work items, plan and workspace over 1152 B tiles.
+extern "C" int q4_gemv_q40(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y, int M,
+                           int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+    return gemv_impl(packed, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream, nullptr, true);
 }
 
 extern "C" size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K) {

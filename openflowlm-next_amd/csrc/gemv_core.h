@@ -77,17 +77,19 @@ __device__ __forceinline__ void load_xfrag(const void* __restrict__ x, int64_t K
 // Loads are unconditional (a tile index past kb1 is clamped to kb1 - 1 and
 // its data skipped) so the compiler can count them statically and wait for
 // each tile's loads only, keeping kUnroll tiles in flight per wave.
-template <int NTL, bool XF32, class Rows, int WAVES = kWaves>
+// Q40: the mx0 layout (1152 B tiles, bf16 d only; m = -8 d), else the mx layout.
+template <int NTL, bool XF32, class Rows, int WAVES = kWaves, bool Q40 = false>
 __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, const void* __restrict__ x, Rows rows,
                                           int64_t K, int64_t g, int kb0, int kb1, float (&acc)[4][NTL]) {
+    constexpr int TB = Q40 ? kQ0TileBytes : kTileBytes;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
     kb0 = __builtin_amdgcn_readfirstlane(kb0);
     kb1 = __builtin_amdgcn_readfirstlane(kb1);
     const int i16 = lane & 15, kg = lane >> 4;
     const int64_t KB = K >> 5;
-    const uint8_t* gbase = packed + g * KB * kTileBytes;
-    const int coff = lane * 16, soff = kCodeBytes + i16 * 16;   // per-lane byte offsets in a tile
+    const uint8_t* gbase = packed + g * KB * TB;
+    const int coff = lane * 16, soff = kCodeBytes + i16 * (Q40 ? 8 : 16);   // per-lane byte offsets in a tile
     const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     const CodeConsts kc = code_consts();
@@ -115,9 +117,14 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int t = min(kb + WAVES * u, kb1 - 1);
-            const uint8_t* tp = gbase + (int64_t)t * kTileBytes;      // wave-uniform tile base
+            const uint8_t* tp = gbase + (int64_t)t * TB;              // wave-uniform tile base
             c[u] = load_nt_u32x4(tp + coff);
-            s[u] = load_nt_u32x4(tp + soff);
+            if constexpr (Q40) {
+                const u32x2 d2 = load_nt_u32x2(tp + soff);
+                s[u] = u32x4{d2[0], d2[1], 0u, 0u};
+            } else {
+                s[u] = load_nt_u32x4(tp + soff);
+            }
             if (need_x) load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
         }
 #pragma unroll
@@ -137,7 +144,14 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
                 for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float d = bf16_hi_to_f32(s[u][r]), m = bf16_lo_to_f32(s[u][r]);
+                    float d, m;
+                    if constexpr (Q40) {
+                        d = bf16_hi_to_f32(r & 1 ? s[u][r >> 1] : s[u][r >> 1] << 16);
+                        m = -8.0f * d;
+                    } else {
+                        d = bf16_hi_to_f32(s[u][r]);
+                        m = bf16_lo_to_f32(s[u][r]);
+                    }
 #pragma unroll
                     for (int j = 0; j < NTL; ++j) {
                         acc[r][j] = __builtin_fmaf(d, p[r][j], acc[r][j]);

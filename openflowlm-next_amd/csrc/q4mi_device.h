@@ -42,6 +42,16 @@ constexpr int kKScOff = 8192, kKDOff = 9216, kKMOff = 9472;
 constexpr int kQ8TileBytes = 2176;
 constexpr int kQ8ScaleOff = 2048;
 
+// The Q4_0-native ("mx0") layout of an [N, K] matrix (N % 64 == 0, K % 32 == 0): tile
+// (g, kb) = 64 rows x 32 K, 1152 B, at byte (g * K/32 + kb) * 1152:
+//   codes [0, 1024): as the mx layout;
+//   d     [1024, 1152): bf16 d of row 16 r + i16 at 1024 + i16 * 8 + r * 2.
+// Q4_0 stores no min: weight = fl32(q d + m) with m = -8 d, exact in bf16 and f32, so the
+// values equal the mx layout's for the same blocks at 0.5625 B per weight against 0.625
+// (the reference's 4608 B Q4_0-native chunk, open_kernels/q4_1_pack.py:145-152, read by
+// designs/gemv_q4/gemv_q4.h:66-82 with m = -8 d).
+constexpr int kQ0TileBytes = 1152;
+
 constexpr int kRows = 64;        // rows per tile / row group
 constexpr int kBlk = 32;         // K per tile (one GGUF block)
 constexpr int kTileBytes = 1280;

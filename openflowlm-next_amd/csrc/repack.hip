@@ -473,6 +473,78 @@ __global__ __launch_bounds__(256) void dequant_mx8_kernel(const uint8_t* __restr
     dst[1] = f32x4{o[4], o[5], o[6], o[7]};
 }
 
+// Q4_0 -> mx0 (no m plane). Thread per (row n, 32-K block kb). src_format 0: GGUF Q4_0
+// blocks (18 B: fp16 d | 16 code bytes, row-major [N][K/32]), d narrowed to bf16 by RNE as
+// q4_1_pack.py:129-130 narrows it; 1: the reference's 4608 B Q4_0-native chunks in pool
+// order with row split rs (q4_1_pack.py:145-152: the 5120 B chunk's d plane at 0, its codes
+// at 512), bytes carried over.
+__global__ __launch_bounds__(256) void repack_q40_kernel(const uint8_t* __restrict__ src, int src_format, int rs,
+                                                         uint8_t* __restrict__ packed, int64_t N, int64_t KB) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * KB) return;
+    const int64_t tile = idx >> 6;
+    const int64_t n = (tile / KB) * 64 + (idx & 63);
+    const int64_t kb = tile % KB;
+    uint8_t code[32];
+    uint32_t d16;
+    if (src_format == 0) {
+        const uint8_t* b = src + (n * KB + kb) * 18;
+        d16 = f32_to_bf16_rne(f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8)));
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            code[j] = b[2 + j] & 0xF;
+            code[j + 16] = b[2 + j] >> 4;
+        }
+    } else {
+        const int64_t per_band = (int64_t)rs * KB / 8;
+        const int64_t band = n / (32 * rs);
+        const int64_t ci = (kb / 8) * rs + (n % (32 * rs)) / 32;
+        const uint8_t* ch = src + (band * per_band + ci) * 4608;
+        const int r = (int)(n & 31), kbl = (int)(kb & 7);
+        d16 = ((const uint16_t*)ch)[kbl * 32 + r];
+        const uint8_t* nib = ch + 512 + (r >> 4) * 2048 + (r & 15) / 2;
+        const int sh = 4 * (r & 1);
+#pragma unroll
+        for (int v = 0; v < 32; ++v) code[v] = (nib[(32 * kbl + v) * 8] >> sh) & 0xF;
+    }
+    const int i = (int)(n & 63), r = i >> 4, i16 = i & 15;
+    uint8_t* t = packed + ((n >> 6) * KB + kb) * kQ0TileBytes;
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            w |= (uint32_t)code[8 * kg + e] << (16 * (e & 1) + 4 * (e >> 1));
+        *(uint32_t*)(t + (kg * 16 + i16) * 16 + r * 4) = w;
+    }
+    *(uint16_t*)(t + kCodeBytes + i16 * 8 + r * 2) = (uint16_t)d16;
+}
+
+// mx0 -> f32 [N][K]: fl32(q d + m), m = -8 d. Thread per (row n, 8-wide k group).
+__global__ __launch_bounds__(256) void dequant_mx0_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
+                                                          int64_t N, int64_t K) {
+    const int64_t K8 = K >> 3;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= N * K8) return;
+    const int64_t n = idx / K8, k8 = idx % K8;
+    const int64_t KB = K >> 5;
+    const int64_t g = n >> 6, kb = k8 >> 2;
+    const int i = (int)(n & 63), r = i >> 4, i16 = i & 15, kg = (int)(k8 & 3);
+    const uint8_t* tile = packed + (g * KB + kb) * kQ0TileBytes;
+    const uint32_t c = *(const uint32_t*)(tile + (kg * 16 + i16) * 16 + r * 4);
+    const float d = bf16_hi_to_f32((uint32_t)*(const uint16_t*)(tile + kCodeBytes + i16 * 8 + r * 2) << 16);
+    const float m = -8.0f * d;
+    f32x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        lo[e] = __builtin_fmaf((float)((c >> (16 * (e & 1) + 4 * (e >> 1))) & 0xF), d, m);
+        hi[e] = __builtin_fmaf((float)((c >> (16 * ((e + 4) & 1) + 4 * ((e + 4) >> 1))) & 0xF), d, m);
+    }
+    f32x4* out = (f32x4*)(w + n * K + k8 * 8);
+    out[0] = lo;
+    out[1] = hi;
+}
+
 // Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats.
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
                                                       int64_t N, int64_t K) {
@@ -687,6 +759,39 @@ extern "C" int q4_dequant_q8_native(const uint8_t* packed, float* w, int64_t N, 
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     const int64_t total = N * (K / 8);
     hipLaunchKernelGGL(dequant_mx8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       packed, w, N, K);
+    return launch_status();
+}
+
+extern "C" int64_t q4_q40_packed_bytes(int64_t N, int64_t K) {
+    if (N == 0 && K > 0 && K % 32 == 0) return 0;
+    if (N <= 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    return (N / 64) * (K / 32) * (int64_t)kQ0TileBytes;
+}
+
+extern "C" int q4_repack_q40(const uint8_t* src, int src_format, int rs, uint8_t* packed, int64_t N, int64_t K,
+                             void* stream) {
+    if (src_format != 0 && src_format != 1) return Q4MI_E_ARG;
+    if (src_format == 1 && rs <= 0) return Q4MI_E_ARG;
+    const int64_t kmul = src_format == 1 ? 256 : 32;
+    if (N == 0 && K > 0 && K % kmul == 0) return Q4MI_OK;
+    if (!src || !packed) return Q4MI_E_ARG;
+    if (misaligned16(packed)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % kmul) return Q4MI_E_SHAPE;
+    if (src_format == 1 && (N % (32 * rs) || ((uintptr_t)src & 1))) return N % (32 * rs) ? Q4MI_E_SHAPE : Q4MI_E_ARG;
+    const int64_t KB = K / 32, total = N * KB;
+    hipLaunchKernelGGL(repack_q40_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       src, src_format, rs, packed, N, KB);
+    return launch_status();
+}
+
+extern "C" int q4_dequant_q40(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
+    if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;
+    if (!packed || !w) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(w)) return Q4MI_E_ARG;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    const int64_t total = N * (K / 8);
+    hipLaunchKernelGGL(dequant_mx0_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        packed, w, N, K);
     return launch_status();
 }

@@ -451,6 +451,90 @@ def gemm_q8_native(w: PackedQ8N, x, y: torch.Tensor | None = None, workspace: to
     return y
 
 
+@dataclass
+class PackedQ40:
+    """A Q4_0 matrix [n, k] in the Q4_0-native mx0 layout: the mx codes plus one bf16 d per
+    row and 32-K block, weight q d - 8 d (0.5625 B per weight; the reference's 4608 B
+    Q4_0-native chunk, q4_1_pack.py:145-152)."""
+    data: torch.Tensor
+    n: int
+    k: int
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+
+def pack_q4_0_native(src, n: int, k: int, fmt: str = "q4_0", rs: int = 1, device=None) -> PackedQ40:
+    """Q4_0 weights -> the mx0 layout on the GPU. ``fmt`` "q4_0": GGUF Q4_0 blocks (18 B,
+    [n, k/32, 18] or flat); "chunks": the reference's 4608 B Q4_0-native chunks in pool
+    order with row split ``rs`` (pack_q4_0_native_pool, q4_1_pack.py:148-152)."""
+    if fmt not in ("q4_0", "chunks"):
+        raise ValueError(f"fmt must be 'q4_0' or 'chunks', got {fmt!r}")
+    dev = _device(device if device is not None else (src.device if isinstance(src, torch.Tensor)
+                                                     and src.is_cuda else None))
+    t = _to_dev(src, dev, torch.uint8).reshape(-1)
+    if fmt == "chunks":
+        want = (n // 32) * (k // 256) * 4608 if n % 32 == 0 and k % 256 == 0 else -1
+    else:
+        want = n * (k // 32) * 18 if k % 32 == 0 else -1
+    if t.numel() != want:
+        raise ValueError(f"{fmt} source holds {t.numel()} bytes, [{n}, {k}] needs {want}")
+    lib = _lib_handle()
+    nbytes = lib.q4_q40_packed_bytes(n, k)
+    if nbytes < 0:
+        raise ValueError(f"[{n}, {k}] does not fit the mx0 layout (n % 64 == 0, k % 32 == 0)")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check("q4_repack_q40", lib.q4_repack_q40(_ptr(t), 0 if fmt == "q4_0" else 1, rs, _ptr(out), n, k,
+                                                 _stream(dev)))
+    return PackedQ40(out, n, k)
+
+
+def dequant_q4_0_native(w: PackedQ40, out: torch.Tensor | None = None) -> torch.Tensor:
+    """mx0 -> f32[n, k], w = fl32(q d - 8 d), bit-exact."""
+    dev = w.device
+    out = _buf(out, "out", torch.float32, (w.n, w.k), dev)
+    with torch.cuda.device(dev):
+        check("q4_dequant_q40", _lib_handle().q4_dequant_q40(_ptr(w.data), _ptr(out), w.n, w.k, _stream(dev)))
+    return out
+
+
+def gemm_q4_0_native(w: PackedQ40, x, y: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                     residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Y[M, N] = X[M, K] @ W^T over a Q4_0-native matrix, 1 <= M <= 16: gemm_q4 on the mx0
+    layout (gemv_q4.h:66-82's GEMV_Q4_0_NATIVE build), bit-identical to gemm_q4 over
+    pack_q4_1 of the same Q4_0 blocks; ``residual`` as in gemm_q4."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != w.k:
+        raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q4_0_native takes 1..16 tokens, got {M}")
+    y = _buf(y, "y", torch.float32, (M, w.n), dev)
+    if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
+                                 or residual.numel() != M * w.n or residual.device != dev):
+        raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        check("q4_gemv_q40", lib.q4_gemv_q40(_ptr(w.data), _ptr(xt), _x_dtype(xt),
+                                             None if residual is None else _ptr(residual), _ptr(y),
+                                             M, w.n, w.k, wp, wn, _stream(dev)))
+    return y
+
+
 _CHUNK_ENTRY = {   # chunk format -> (chunk bytes, C entry point)
     "q4_1": (5120, "q4_repack_pool"),
     "q4_f32": (6144, "q4_repack_pool_f32"),

@@ -27,6 +27,8 @@ this hot path (``/root/reference`` is read as text, never imported):
                                   open_kernels/designs/gemv_q4/gemv_q8.h
 * native Q4_K values              open_kernels/designs/gemm_q4/gemm_q4.h:456-507
   (value d sc nib + mcoef mn of the container chunk; d sc q - dmin min of GGUF)
+* the 4608 B Q4_0-native chunk    open_kernels/q4_1_pack.py:145-152 (read with
+  m = -8 d by designs/gemv_q4/gemv_q4.h:66-82, :235-238)
 
 ``ml_dtypes`` (which the reference uses for its bf16 casts) is absent here; the
 bf16 conversions are restated as IEEE round-to-nearest-even on the f32 bits.
@@ -493,6 +495,60 @@ def pack_mx_from_parts(d16: np.ndarray, m16: np.ndarray, q: np.ndarray) -> np.nd
     out[:, :, :MX_CODES] = np.ascontiguousarray(codes).reshape(G, nb, 256).view(np.uint8).reshape(G, nb, MX_CODES)
     out[:, :, MX_CODES:] = np.ascontiguousarray(sc).reshape(G, nb, 64).view(np.uint8).reshape(G, nb, 256)
     return out.reshape(-1)
+
+
+# --------------------------------------------------------------------------
+# Q4_0-native: the reference's 4608 B chunk and the MI355X mx0 tile
+# --------------------------------------------------------------------------
+# mx0 tile (g, kb), 1152 B: the mx codes [0, 1024), then bf16 d of row 16 r + i at
+# 1024 + 8 i + 2 r. Q4_0 stores no min: weight = fl32(q d + m), m = -8 d (exact).
+CH_Q4_0 = 4608
+MX0_TILE = 1152
+
+
+def pack_q4_0_native_pool(blocks: np.ndarray, rs: int) -> np.ndarray:
+    """GGUF Q4_0 blocks -> 4608 B Q4_0-native chunks in pool order: the 5120 B chunk of
+    pack_q4_1_pool with its m plane [512, 1024) left out (q4_1_pack.py:145-152)."""
+    assert blocks.shape[2] == Q4_0_BYTES, "a Q4_0-native pool holds Q4_0 blocks only"
+    full = pack_q4_1_pool(blocks, rs).reshape(-1, CH)
+    return np.concatenate([full[:, :512], full[:, 1024:]], axis=1).reshape(-1)
+
+
+def mx0_bytes(n: int, k: int) -> int:
+    assert n % MX_ROWS == 0 and k % BLK == 0
+    return (n // MX_ROWS) * (k // BLK) * MX0_TILE
+
+
+def pack_mx0(blocks: np.ndarray) -> np.ndarray:
+    """GGUF Q4_0 blocks [N, K/32, 18] -> mx0 bytes: pack_mx's codes with the bf16 d alone."""
+    assert blocks.shape[2] == Q4_0_BYTES
+    d, _, q = unpack_q4_1_blocks(blocks)
+    n, nb = d.shape
+    G = n // MX_ROWS
+    full = pack_mx_from_parts(f32_to_bf16(d), np.zeros_like(f32_to_bf16(d)), q).reshape(G, nb, MX_TILE)
+    dd = f32_to_bf16(d).reshape(G, 4, 16, nb).transpose(0, 3, 2, 1)          # [G, kb, i, r]
+    out = np.empty((G, nb, MX0_TILE), np.uint8)
+    out[:, :, :MX_CODES] = full[:, :, :MX_CODES]
+    out[:, :, MX_CODES:] = np.ascontiguousarray(dd).view(np.uint8).reshape(G, nb, 128)
+    return out.reshape(-1)
+
+
+def unpack_mx0(packed: np.ndarray, n: int, k: int):
+    """mx0 bytes -> (d16 uint16[n, k/32], codes uint8[n, k])."""
+    nb, G = k // BLK, n // MX_ROWS
+    t = np.asarray(packed, np.uint8).reshape(G, nb, MX0_TILE)
+    as_mx = np.zeros((G, nb, MX_TILE), np.uint8)
+    as_mx[:, :, :MX_CODES] = t[:, :, :MX_CODES]
+    _, _, q = unpack_mx(as_mx.reshape(-1), n, k)
+    d16 = np.ascontiguousarray(t[:, :, MX_CODES:]).view(np.uint16).reshape(G, nb, 16, 4).transpose(0, 3, 2, 1)
+    return d16.reshape(n, nb), q
+
+
+def dequant_mx0(packed: np.ndarray, n: int, k: int) -> np.ndarray:
+    """mx0 -> f32[n, k] = fl32(q d + m), m = -8 d from the stored bf16 d."""
+    d16, q = unpack_mx0(packed, n, k)
+    d = np.repeat(bf16_to_f32(d16), BLK, axis=1)
+    return (q.astype(np.float32) * d + np.float32(-8.0) * d).astype(np.float32)
 
 
 # --------------------------------------------------------------------------

@@ -72,6 +72,14 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_repack_q4k_chunks(fake, 0, fake, 64, 256, None) == -2  # rs
     assert lib.q4_repack_q4k_chunks(fake, 4, fake, 64, 256, None) == -1  # N % (32 rs)
     assert lib.q4_repack_q8_split(fake, 3, 1, 0, fake, 64, 256, None) == -2   # source format
+    assert lib.q4_repack_q40(fake, 2, 1, fake, 64, 256, None) == -2          # source format
+    assert lib.q4_repack_q40(fake, 1, 0, fake, 64, 256, None) == -2          # chunks: rs
+    assert lib.q4_repack_q40(fake, 1, 1, fake, 64, 128, None) == -1          # chunks: K % 256
+    assert lib.q4_repack_q40(fake, 0, 1, fake, 96, 32, None) == -1           # N % 64
+    assert lib.q4_repack_q40(None, 0, 1, None, 0, 32, None) == 0             # empty is a no-op
+    assert lib.q4_q40_packed_bytes(64, 32) == 1152 and lib.q4_q40_packed_bytes(96, 32) < 0
+    assert lib.q4_gemv_q40(fake, fake, 1, None, fake, 17, 64, 32, None, 0, None) == -5   # M > 16
+    assert lib.q4_dequant_q40(fake, None, 64, 32, None) == -2
     assert lib.q4_repack_pool_f32(fake, 1, fake, 64, 128, None) == -1          # K % 256
     assert lib.q4_repack_pool_f32(C.c_void_p(0x1002), 1, fake, 64, 256, None) == -2   # f32 scales misaligned
     assert lib.q4_repack_q8_split(fake, 0, 1, 2, fake, 64, 256, None) == -2   # part
