@@ -668,6 +668,55 @@ def extra_config4(torch, q4, dev):
             "tflops": 2.0 * T * K8 * 3 * H * F / ms / 1e9}
 
 
+def extra_moe_prefill(torch, q4, dev):
+    """Config 4's experts (128 x Qwen3-MoE-style gate/up [1536, 2048] and down [2048, 768],
+    top-8 of a seeded softmax) at prefill scale: T = 512 and 2048 tokens through the prefill
+    path (q4_moe_prefill, fp16 and bf16 tiles) and, at T = 512 (4096 pairs), the decode path
+    beside it. Graph-timed; one expert pool (each expert's weights are read once per token
+    tile that routes to it)."""
+    import numpy as np
+    E, K8, H, F = 128, 8, 2048, 768
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 23)
+    gb, db = q4.packed_bytes(2 * F, H), q4.packed_bytes(H, F)
+    gu = torch.empty(E * gb, dtype=torch.uint8, device=dev)
+    dn = torch.empty(E * db, dtype=torch.uint8, device=dev)
+    for e in range(E):
+        q4.pack_q4_1(gen_blocks(torch, 2 * F, H, gen, dev), dev, out=gu[e * gb:(e + 1) * gb])
+        q4.pack_q4_1(gen_blocks(torch, H, F, gen, dev), dev, out=dn[e * db:(e + 1) * db])
+    gup, dnp = q4.PackedExperts(gu, E, 2 * F, H), q4.PackedExperts(dn, E, H, F)
+    out = {}
+    for T in (512, 2048):
+        rng = np.random.default_rng(SEED + T)
+        logits = rng.standard_normal((T, E))
+        pr = np.exp(logits - logits.max(1, keepdims=True))
+        pr /= pr.sum(1, keepdims=True)
+        ids = np.argsort(-pr, axis=1, kind="stable")[:, :K8]
+        w = np.take_along_axis(pr, ids, 1)
+        w /= w.sum(1, keepdims=True)
+        ids_t = torch.from_numpy(ids.astype(np.int32)).to(dev)
+        w_t = torch.from_numpy(w.astype(np.float32)).to(dev)
+        x = torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty(T, H, device=dev)
+        flops = 2.0 * T * K8 * 3 * H * F
+        wbytes = len(np.unique(ids)) * (gb + db)
+        rec = {"pairs": T * K8, "distinct_experts": int(len(np.unique(ids)))}
+        paths = [("prefill_fp16", "prefill", "fp16"), ("prefill_bf16", "prefill", "bf16")]
+        if T * K8 <= q4.MOE_DECODE_MAX_PAIRS:
+            paths.append(("decode", "decode", "fp16"))
+        for name, path, prec in paths:
+            ws = torch.empty(max(q4.moe_prefill_workspace_bytes(T, E, K8, H, F) if path == "prefill"
+                                 else q4.moe_workspace_bytes(T, E, K8, H, F), 256), dtype=torch.uint8, device=dev)
+            q4.moe_batch(gup, dnp, x, ids_t, w_t, y, workspace=ws, path=path, precision=prec)   # scales, once
+            ms = graph_time(torch, lambda: q4.moe_batch(gup, dnp, x, ids_t, w_t, y, workspace=ws, path=path,
+                                                        precision=prec), [y], replays=10)
+            rec[name] = {"us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1),
+                         "weight_gbs": round(wbytes / ms / 1e6, 1)}
+            del ws
+        out[f"T{T}"] = rec
+    return out
+
+
 # --------------------------------------------------------------------------
 
 def q4nx_decode_harness(model_dir, tensor: str, shape=None, reps: int = 10) -> dict:
@@ -733,7 +782,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="staged,0,2,3,4,lm_head,ffn,q8,q4k,q40,peaks",
+    ap.add_argument("--extras", default="staged,0,2,3,4,moe_prefill,lm_head,ffn,q8,q4k,q40,peaks",
                     help="comma list (staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=3, help="passes over one layer per timed CPU run")
@@ -797,6 +846,8 @@ def main() -> int:
                 out["q4k_native_gemv"] = extra_q4k(torch, q4, dev)
             elif cfg == "q40":
                 out["q4_0_native_gemv"] = extra_q40(torch, q4, dev)
+            elif cfg == "moe_prefill":
+                out["moe_prefill"] = extra_moe_prefill(torch, q4, dev)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -838,6 +889,8 @@ def main() -> int:
                 extras["q4k_native_gemv"] = extra_q4k(torch, q4, dev)
             elif cfg == "q40":
                 extras["q4_0_native_gemv"] = extra_q40(torch, q4, dev)
+            elif cfg == "moe_prefill":
+                extras["moe_prefill"] = extra_moe_prefill(torch, q4, dev)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
         log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")

@@ -429,6 +429,26 @@ int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const void* x, int 
                 int T, int E, int topk, int64_t H, int64_t F,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes q4_moe_prefill needs (sized for any routing of T tokens x topk). */
+size_t q4_moe_prefill_workspace_bytes(int T, int E, int topk, int H, int F);
+
+/* The routed MoE block at prefill scale (any T; the same formula and operand layouts as
+ * q4_moe_gemv): the pairs routed to each expert are batched into 256-token tiles on the
+ * device and every expert's gate/up and down run as tiles of the prefill GEMM, one launch
+ * each over all experts; then out[t] = sum_j topk_w[t][j] y[t][j] in slot order j.
+ * precision 0: fp16 tiles with power-of-two scaling as q4_gemm_prefill precision 0, with
+ * gate_up_scales / down_scales = q4_prefill_scales of the stacked matrices ([E 2F, H] and
+ * [E H, F]); f32 x and h go in two passes (value and remainder). precision 1: the reference's
+ * bf16 tile RNE(q d + m), x and h rounded to bf16 (scales may be NULL).
+ * H % 256 == 0, F % 128 == 0, 1 <= topk <= 16, T * topk <= 2^22, E <= 8192.
+ * Replaces the host loop over expert dispatches of 256 slots (Core::moe_block,
+ * core.cpp:5163-5178; moe_batch.h:98-172 mb_step_parity / mb_step_tile, h in bf16 as
+ * moe_batch.h:181-202). */
+int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const void* gate_up_scales,
+                   const void* down_scales, const void* x, int x_dtype, const int32_t* topk_ids,
+                   const float* topk_w, float* out, int T, int E, int topk, int64_t H, int64_t F,
+                   int precision, void* workspace, size_t workspace_bytes, void* stream);
+
 /* The same block with the residual and a gated shared expert folded into the combine:
  *   out[t] = (residual[t] + sum_j topk_w[t][j] * y[t][j]) + sigmoid(x[t] . sgw) * shared[t],
  * residual f32 [T][H] (may be NULL, may alias out), shared f32 [T][H] (the shared expert's

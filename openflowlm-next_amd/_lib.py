@@ -75,6 +75,9 @@ SIGNATURES = {
     "q4_lm_head_topk": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _sz,
                                _vp]),
     "q4_moe_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "q4_moe_prefill_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "q4_moe_prefill": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i32, _vp,
+                              _sz, _vp]),
     "q4_moe_gemv": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_moe_gemv_fin": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp,
                                _sz, _vp]),

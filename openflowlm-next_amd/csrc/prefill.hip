@@ -590,29 +590,20 @@ __global__ __launch_bounds__(256) void prefill_scale_write_kernel(const uint8_t*
 
 // lo_pass (f32 activations, PREC 0): the fp16 remainder x 2^-s - fp16(x 2^-s) instead of the
 // rounded value; the two passes' products add up to the f32 activations' to ~2^-22.
-template <bool XF32, int PREC, bool TILED>
-__global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x, uint16_t* __restrict__ x16,
-                                                     int* __restrict__ texp, int T, int K, int lo_pass) {
-    const int t = blockIdx.x, n8 = K >> 3;       // 8-element groups of the row (K % 32 == 0)
+// One token row of prefill_xprep (all 256 threads): ld8(i, v) loads the row's 8-element
+// group i as f32 (zero: a padding row, written as zeros). F32SRC: the source is f32, so the
+// lo pass of PREC 0 writes the fp16 remainder.
+template <bool F32SRC, int PREC, bool TILED, class Load>
+__device__ __forceinline__ void xprep_row(Load ld8, bool zero, uint16_t* __restrict__ x16, int* __restrict__ texp,
+                                          int t, int K, int lo_pass) {
+    const int n8 = K >> 3;                       // 8-element groups of the row (K % 32 == 0)
     const int64_t row = (int64_t)t * K;
     u32x4* const out = (u32x4*)x16;
     auto dst = [&](int i) -> int64_t { return TILED ? xchunk_dst(t, i, K) : row / 8 + i; };
-    if (t >= T) {                                // padding rows of the last token tile
+    if (zero) {
         for (int i = threadIdx.x; i < n8; i += 256) out[dst(i)] = u32x4{0u, 0u, 0u, 0u};
         return;
     }
-    auto ld8 = [&](int i, float (&v)[8]) {
-        if constexpr (XF32) {
-            const f32x4* p = (const f32x4*)((const float*)x + row) + 2 * i;
-            const f32x4 a = p[0], b = p[1];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = a[e], v[e + 4] = b[e];
-        } else {
-            const u32x4 w = ((const u32x4*)((const uint16_t*)x + row))[i];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[2 * e] = bf16_lo_to_f32(w[e]), v[2 * e + 1] = bf16_hi_to_f32(w[e]);
-        }
-    };
     // Rows of up to 2048 chunks (K <= 16384) are read once and held in registers for both
     // the max and the conversion; longer rows are read twice.
     constexpr int kHeld = 8;
@@ -655,7 +646,7 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
             if constexpr (PREC == 0) {
                 const float a = ldexpf(v[2 * e], -s), b = ldexpf(v[2 * e + 1], -s);
                 _Float16 ha = (_Float16)a, hb = (_Float16)b;
-                if (XF32 && lo_pass) {
+                if (F32SRC && lo_pass) {
                     ha = (_Float16)(a - (float)ha);
                     hb = (_Float16)(b - (float)hb);
                 }
@@ -682,6 +673,30 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
             out[dst(i)] = cvt8(v);
         }
     }
+}
+
+// The 8 activations of group i of a row, as f32.
+template <bool XF32>
+__device__ __forceinline__ void load_x8(const void* __restrict__ xrow, int i, float (&v)[8]) {
+    if constexpr (XF32) {
+        const f32x4* p = (const f32x4*)xrow + 2 * i;
+        const f32x4 a = p[0], b = p[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = a[e], v[e + 4] = b[e];
+    } else {
+        const u32x4 w = ((const u32x4*)xrow)[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[2 * e] = bf16_lo_to_f32(w[e]), v[2 * e + 1] = bf16_hi_to_f32(w[e]);
+    }
+}
+
+template <bool XF32, int PREC, bool TILED>
+__global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x, uint16_t* __restrict__ x16,
+                                                     int* __restrict__ texp, int T, int K, int lo_pass) {
+    const int t = blockIdx.x;
+    const void* xrow = (const uint8_t*)x + (int64_t)t * K * (XF32 ? 4 : 2);
+    xprep_row<XF32, PREC, TILED>([&](int i, float (&v)[8]) { load_x8<XF32>(xrow, i, v); }, t >= T, x16, texp, t,
+                                 K, lo_pass);
 }
 
 // Kernel variants: (BN, BT, waves along N, waves along T, 32-K blocks per stage).
@@ -1040,4 +1055,430 @@ extern "C" int q4_gemm_prefill_scaled(const uint8_t* packed, const void* scales,
     if (!scales || misaligned16(scales)) return Q4MI_E_ARG;
     if (!workspace || workspace_bytes < gemm_ws_bytes(T, N, K)) return Q4MI_E_WORKSPACE;
     return prefill_impl(packed, scales, x, x_dtype, y, T, N, K, 0, workspace, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Routed MoE at prefill scale: out[t] = sum_j w[t][j] down_e(silu(gate_e x_t) (up_e x_t)).
+//
+// The reference batches an expert's tokens into slots and runs them through its expert
+// GEMM dispatch by dispatch (moe_batch.h:98-172, a host loop over dispatches in
+// Core::moe_block, core.cpp:5163-5178). Here the batching is on the device and the expert
+// GEMMs are the pipelined prefill tiles (dma_tile) over all experts in one launch each:
+//   1. route (one workgroup): tokens per expert from an LDS histogram of ids; expert e's
+//      slots are [off_e, off_e + n_e), padded to whole 256-token tiles, experts in
+//      ascending order; per tile its expert and the end of that expert's slots.
+//   2. slots (a workgroup per expert): the pairs routed to e, in pair order, get the slots
+//      off_e, off_e + 1, ...; slot -> token row (pads -1) and pair -> slot.
+//   3. the token rows gathered into the slots in the GEMM's tiled 16-bit layout (pads 0);
+//   4. gate/up: workgroup (tile, 256-row tile) runs dma_tile on expert e's [2F, H] matrix
+//      into G[slot][2F] (f32);
+//   5. h = silu(g) u from G (gate and up row groups alternate), into the 16-bit layout;
+//   6. down: as 4 on the [H, F] matrices into Y[slot][H];
+//   7. combine: out[t] = sum_j w[t][j] Y[slot(t, j)] in slot order j.
+// Precision 0 (fp16 tiles with power-of-two scaling, the matrices' prefill scales given)
+// takes f32 activations and h in two passes (fp16 value + remainder), as q4_gemm_prefill
+// does; precision 1 (the reference's bf16 tile, RNE(q d + m)) rounds x and h to bf16, as
+// the reference's moe_batch rounds h (moe_batch.h:181-202). A token row's result does not
+// depend on its slot (MFMA rows are independent), and the combine sums in slot order, so
+// results are deterministic.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kMoePfMaxExperts = 8192;
+constexpr int64_t kMoePfMaxPairs = (int64_t)1 << 22;
+
+__global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t* __restrict__ ids, int P, int E,
+                                                         int* __restrict__ cnt, int* __restrict__ off,
+                                                         int* __restrict__ tile_e, int* __restrict__ tile_end,
+                                                         int* __restrict__ meta) {
+    __shared__ int hist[kMoePfMaxExperts];
+    __shared__ int wsum[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += 1024) hist[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += 1024) {
+        const int e = ids[p];
+        if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+    }
+    __syncthreads();
+    const int per = (E + 1023) / 1024;               // experts per thread, consecutive
+    int tiles = 0;
+    for (int j = 0; j < per; ++j) {
+        const int e = tid * per + j;
+        if (e < E) tiles += (hist[e] + 255) >> 8;
+    }
+    int incl = tiles;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int tp = incl - tiles;
+    for (int w = 0; w < wave; ++w) tp += wsum[w];
+    for (int j = 0; j < per; ++j) {
+        const int e = tid * per + j;
+        if (e >= E) break;
+        const int n = hist[e], nt = (n + 255) >> 8;
+        cnt[e] = n;
+        off[e] = tp * 256;
+        for (int i = 0; i < nt; ++i) {
+            tile_e[tp + i] = e;
+            tile_end[tp + i] = tp * 256 + n;
+        }
+        tp += nt;
+    }
+    if (tid == 1023) meta[0] = tp;
+}
+
+__global__ __launch_bounds__(256) void moe_slots_kernel(const int32_t* __restrict__ ids, int P, int topk,
+                                                        const int* __restrict__ cnt, const int* __restrict__ off,
+                                                        int* __restrict__ slot_of_pair, int* __restrict__ rowmap) {
+    constexpr int kBatch = 4096, kPer = kBatch / 256;
+    __shared__ int buf[kBatch];
+    __shared__ int wsum[4];
+    const int e = blockIdx.x, n = cnt[e];
+    if (n == 0) return;
+    const int o = off[e];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int base = 0;                                   // slots given out before this batch
+    for (int b0 = 0; b0 < P && base < n; b0 += kBatch) {
+        const int nb = min(kBatch, P - b0);
+        for (int i = tid; i < nb; i += 256) buf[i] = ids[b0 + i];          // coalesced
+        __syncthreads();
+        int c = 0;                                  // this thread's pairs: kPer consecutive
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = tid * kPer + j;
+            c += i < nb && buf[i] == e;
+        }
+        int incl = c;
+#pragma unroll
+        for (int sft = 1; sft < 64; sft <<= 1) {
+            const int v = __shfl_up(incl, sft);
+            if (lane >= sft) incl += v;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int r = base + incl - c;
+        for (int w = 0; w < wave; ++w) r += wsum[w];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = tid * kPer + j;
+            if (i < nb && buf[i] == e) {
+                const int p = b0 + i;
+                slot_of_pair[p] = o + r;
+                rowmap[o + r] = p / topk;
+                ++r;
+            }
+        }
+        base += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        __syncthreads();                            // buf and wsum are rewritten next batch
+    }
+    const int pad = ((n + 255) >> 8) << 8;
+    for (int i = n + tid; i < pad; i += 256) rowmap[o + i] = -1;
+}
+
+// One slot row per wave (4 per workgroup) of the MoE activation preps: xprep_row's
+// conversion with the row max reduced within the wave. ld8(i, v) loads 8-element group i
+// of the row as f32; zero writes a padding row. Rows of up to 512 groups (K <= 4096) are
+// held in registers, longer ones read twice.
+template <bool F32SRC, int PREC, class Load>
+__device__ __forceinline__ void xprep_row_wave(Load ld8, bool zero, uint16_t* __restrict__ x16,
+                                               int* __restrict__ texp, int t, int K, int lo_pass) {
+    const int n8 = K >> 3, lane = threadIdx.x & 63;
+    u32x4* const out = (u32x4*)x16;
+    if (zero) {
+        for (int i = lane; i < n8; i += 64) out[xchunk_dst(t, i, K)] = u32x4{0u, 0u, 0u, 0u};
+        return;
+    }
+    constexpr int kHeld = 8;
+    const bool held = n8 <= 64 * kHeld;
+    float hv[kHeld][8];
+    if (held) {
+#pragma unroll
+        for (int c = 0; c < kHeld; ++c) {
+            const int i = lane + 64 * c;
+            if (i < n8) ld8(i, hv[c]);
+        }
+    }
+    int s = 0;
+    if constexpr (PREC == 0) {
+        float mx = 0.f;
+        if (held) {
+#pragma unroll
+            for (int c = 0; c < kHeld; ++c)
+                if (lane + 64 * c < n8) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(hv[c][e]));
+                }
+        } else {
+            for (int i = lane; i < n8; i += 64) {
+                float v[8];
+                ld8(i, v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        s = fp16_fit_exponent(mx);
+        if (lane == 0) texp[t] = s;
+    }
+    auto cvt8 = [&](const float (&v)[8]) -> u32x4 {
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t lo, hi;
+            if constexpr (PREC == 0) {
+                const float a = ldexpf(v[2 * e], -s), b = ldexpf(v[2 * e + 1], -s);
+                _Float16 ha = (_Float16)a, hb = (_Float16)b;
+                if (F32SRC && lo_pass) {
+                    ha = (_Float16)(a - (float)ha);
+                    hb = (_Float16)(b - (float)hb);
+                }
+                lo = __builtin_bit_cast(uint16_t, ha);
+                hi = __builtin_bit_cast(uint16_t, hb);
+            } else {
+                lo = f32_to_bf16_rne(v[2 * e]);
+                hi = f32_to_bf16_rne(v[2 * e + 1]);
+            }
+            o[e] = lo | (hi << 16);
+        }
+        return o;
+    };
+    if (held) {
+#pragma unroll
+        for (int c = 0; c < kHeld; ++c) {
+            const int i = lane + 64 * c;
+            if (i < n8) out[xchunk_dst(t, i, K)] = cvt8(hv[c]);
+        }
+    } else {
+        for (int i = lane; i < n8; i += 64) {
+            float v[8];
+            ld8(i, v);
+            out[xchunk_dst(t, i, K)] = cvt8(v);
+        }
+    }
+}
+
+template <bool XF32, int PREC>
+__global__ __launch_bounds__(256) void moe_xprep_kernel(const void* __restrict__ x, const int* __restrict__ rowmap,
+                                                        const int* __restrict__ meta, uint16_t* __restrict__ x16,
+                                                        int* __restrict__ texp, int K, int lo_pass) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= meta[0] * 256) return;
+    const int row = rowmap[t];
+    const void* xrow = (const uint8_t*)x + (int64_t)(row < 0 ? 0 : row) * K * (XF32 ? 4 : 2);
+    xprep_row_wave<XF32, PREC>([&](int i, float (&v)[8]) { load_x8<XF32>(xrow, i, v); }, row < 0, x16, texp, t, K,
+                               lo_pass);
+}
+
+// h[f] = silu(g[f]) u[f] of slot t from G[t][2F], where the 64 gate rows of row group j are
+// columns 128 j .. 128 j + 63 and its up rows the next 64.
+template <int PREC>
+__global__ __launch_bounds__(256) void moe_hprep_kernel(const float* __restrict__ G, const int* __restrict__ rowmap,
+                                                        const int* __restrict__ meta, uint16_t* __restrict__ x16,
+                                                        int* __restrict__ texp, int F, int lo_pass) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= meta[0] * 256) return;
+    const float* g = G + (int64_t)t * 2 * F;
+    auto ld8 = [&](int i, float (&v)[8]) {
+        const int f = 8 * i, c = (f >> 6) * 128 + (f & 63);
+        const f32x4 g0 = *(const f32x4*)(g + c), g1 = *(const f32x4*)(g + c + 4);
+        const f32x4 u0 = *(const f32x4*)(g + c + 64), u1 = *(const f32x4*)(g + c + 68);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = g0[e] / (1.0f + expf(-g0[e])) * u0[e];
+            v[e + 4] = g1[e] / (1.0f + expf(-g1[e])) * u1[e];
+        }
+    };
+    xprep_row_wave<true, PREC>(ld8, rowmap[t] < 0, x16, texp, t, F, lo_pass);
+}
+
+// Workgroup (token tile tt, 256-row tile rt) of a grouped expert GEMM: dma_tile on tile tt's
+// expert's matrix (N rows, ebytes each expert), slots [256 tt, tile_end) valid.
+template <int PREC>
+__global__ __launch_bounds__(512) void moe_dma_kernel(const uint8_t* __restrict__ packed, int64_t ebytes,
+                                                      const uint16_t* __restrict__ x16,
+                                                      const int* __restrict__ texp, const int* __restrict__ wexp,
+                                                      const uint32_t* __restrict__ s16, int64_t s16_words,
+                                                      float* __restrict__ y, const int* __restrict__ tile_e,
+                                                      const int* __restrict__ tile_end, const int* __restrict__ meta,
+                                                      int N, int K, int tiles_n, int accum) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
+    const int b = blockIdx.x, tt = b / tiles_n, rt = b % tiles_n;
+    if (tt >= meta[0]) return;
+    const int e = tile_e[tt];
+    dma_tile<PREC, 8>(lds, packed + e * ebytes, x16, texp, PREC == 0 ? wexp + (int64_t)e * N : nullptr,
+                      PREC == 0 ? s16 + e * s16_words : nullptr, y, tile_end[tt], N, K, rt * 256, tt, 0, 1, accum);
+}
+
+// out[t][n..n+3] = sum_j w[t][j] Y[slot(t, j)][n..n+3], slot order j.
+__global__ __launch_bounds__(256) void moe_prefill_combine_kernel(const float* __restrict__ Y,
+                                                                  const int* __restrict__ slot_of_pair,
+                                                                  const int32_t* __restrict__ ids,
+                                                                  const float* __restrict__ w, int topk, int E,
+                                                                  int H, float* __restrict__ out) {
+    const int64_t t = blockIdx.y, n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (n >= H) return;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < topk; ++j) {
+        const int64_t p = t * topk + j;
+        const int e = ids[p];
+        if (e >= 0 && e < E) {
+            const float wp = w[p];
+            const f32x4 v = *(const f32x4*)(Y + (int64_t)slot_of_pair[p] * H + n);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] += wp * v[c];
+        }
+    }
+    *(f32x4*)(out + t * H + n) = s;
+}
+
+struct MoePfWs {
+    size_t cnt, off, meta, tile_e, tile_end, sop, rowmap, texp, x16, gy, total;
+    int64_t tiles_max;
+};
+
+// Workspace layout for T tokens x topk over E experts (slots: every tile an expert could use).
+MoePfWs moe_pf_ws(int T, int E, int topk, int64_t H, int64_t F) {
+    MoePfWs w{};
+    const int64_t P = (int64_t)T * topk;
+    w.tiles_max = ceil_div(P, 256) + (E < P ? E : P);
+    const size_t S = (size_t)w.tiles_max * 256;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o += align256(bytes);
+        return at;
+    };
+    w.cnt = take((size_t)E * 4);
+    w.off = take((size_t)E * 4);
+    w.meta = take(16);
+    w.tile_e = take((size_t)w.tiles_max * 4);
+    w.tile_end = take((size_t)w.tiles_max * 4);
+    w.sop = take((size_t)P * 4);
+    w.rowmap = take(S * 4);
+    w.texp = take(S * 4);
+    const size_t x16a = S * H * 2, x16b = 2 * S * F * 2;
+    w.x16 = take(x16a > x16b ? x16a : x16b);       // x, then h (value and remainder planes)
+    w.gy = take(S * (2 * F > H ? 2 * F : H) * 4);  // G, then Y
+    w.total = o;
+    return w;
+}
+
+}  // namespace
+
+extern "C" size_t q4_moe_prefill_workspace_bytes(int T, int E, int topk, int H, int F) {
+    if (T <= 0 || E <= 0 || topk <= 0 || H <= 0 || F <= 0) return 0;
+    return moe_pf_ws(T, E, topk, H, F).total;
+}
+
+extern "C" int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const void* gate_up_scales,
+                              const void* down_scales, const void* x, int x_dtype, const int32_t* topk_ids,
+                              const float* topk_w, float* out, int T, int E, int topk, int64_t H, int64_t F,
+                              int precision, void* workspace, size_t workspace_bytes, void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (H <= 0 || F <= 0 || H % 256 || F % 128) return Q4MI_E_SHAPE;
+    if (H > (1 << 20) || F > (1 << 20)) return Q4MI_E_RANGE;
+    if (T < 0 || E <= 0 || E > kMoePfMaxExperts || topk <= 0 || topk > 16 || (int64_t)T * topk > kMoePfMaxPairs)
+        return Q4MI_E_RANGE;
+    if (T == 0) return Q4MI_OK;
+    if (!gate_up || !down || !x || !topk_ids || !topk_w || !out) return Q4MI_E_ARG;
+    if (misaligned16(gate_up) || misaligned16(down) || misaligned16(x) || misaligned16(out) || misaligned16(workspace))
+        return Q4MI_E_ARG;
+    if (precision == 0 && (!gate_up_scales || !down_scales || misaligned16(gate_up_scales) ||
+                           misaligned16(down_scales)))
+        return Q4MI_E_ARG;
+    const MoePfWs w = moe_pf_ws(T, E, topk, H, F);
+    if (!workspace || workspace_bytes < w.total) return Q4MI_E_WORKSPACE;
+    char* ws = (char*)workspace;
+    int* cnt = (int*)(ws + w.cnt);
+    int* off = (int*)(ws + w.off);
+    int* meta = (int*)(ws + w.meta);
+    int* tile_e = (int*)(ws + w.tile_e);
+    int* tile_end = (int*)(ws + w.tile_end);
+    int* sop = (int*)(ws + w.sop);
+    int* rowmap = (int*)(ws + w.rowmap);
+    int* texp = (int*)(ws + w.texp);
+    uint16_t* x16 = (uint16_t*)(ws + w.x16);
+    float* gy = (float*)(ws + w.gy);
+    const int P = T * topk;
+    const hipStream_t st = (hipStream_t)stream;
+    const unsigned S = (unsigned)(w.tiles_max * 256), SP = S / 4;
+    const bool xf32 = x_dtype == Q4MI_F32;
+
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), 0, st, topk_ids, P, E, cnt, off, tile_e, tile_end, meta);
+    if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    hipLaunchKernelGGL(moe_slots_kernel, dim3((unsigned)E), dim3(256), 0, st, topk_ids, P, topk, cnt, off, sop, rowmap);
+    if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+
+    // the prefill scales: wexp int32[N], then the fp16 plane, per stacked matrix
+    auto plane = [](const void* sc, int64_t N) {
+        return (const uint32_t*)((const char*)sc + align256((size_t)N * 4));
+    };
+    const int64_t N1 = 2 * F, N2 = H;
+    const int64_t eb1 = (N1 / 64) * (H / 32) * kTileBytes, eb2 = (N2 / 64) * (F / 32) * kTileBytes;
+    const int64_t sw1 = (N1 / 64) * (H / 32) * 64, sw2 = (N2 / 64) * (F / 32) * 64;
+    const int* we1 = precision == 0 ? (const int*)gate_up_scales : nullptr;
+    const int* we2 = precision == 0 ? (const int*)down_scales : nullptr;
+    const uint32_t* s1 = precision == 0 ? plane(gate_up_scales, (int64_t)E * N1) : nullptr;
+    const uint32_t* s2 = precision == 0 ? plane(down_scales, (int64_t)E * N2) : nullptr;
+    const unsigned g1 = (unsigned)(w.tiles_max * (N1 / 256)), g2 = (unsigned)(w.tiles_max * (N2 / 256));
+
+    // gate/up: G = X . [gate; up]^T per expert
+    const int xpasses = precision == 0 && xf32 ? 2 : 1;
+    for (int pass = 0; pass < xpasses; ++pass) {
+        if (xf32) {
+            if (precision == 0)
+                hipLaunchKernelGGL((moe_xprep_kernel<true, 0>), dim3(SP), dim3(256), 0, st, x, rowmap, meta, x16, texp,
+                                   (int)H, pass);
+            else
+                hipLaunchKernelGGL((moe_xprep_kernel<true, 1>), dim3(SP), dim3(256), 0, st, x, rowmap, meta, x16, texp,
+                                   (int)H, pass);
+        } else {
+            if (precision == 0)
+                hipLaunchKernelGGL((moe_xprep_kernel<false, 0>), dim3(SP), dim3(256), 0, st, x, rowmap, meta, x16,
+                                   texp, (int)H, pass);
+            else
+                hipLaunchKernelGGL((moe_xprep_kernel<false, 1>), dim3(SP), dim3(256), 0, st, x, rowmap, meta, x16,
+                                   texp, (int)H, pass);
+        }
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        if (precision == 0)
+            hipLaunchKernelGGL((moe_dma_kernel<0>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1, sw1,
+                               gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), pass);
+        else
+            hipLaunchKernelGGL((moe_dma_kernel<1>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1, sw1,
+                               gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), 0);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    }
+    // h = silu(g) u into the 16-bit layout (precision 0: value and remainder planes, both
+    // made before the down GEMM overwrites G with Y)
+    const int hpasses = precision == 0 ? 2 : 1;
+    uint16_t* h16[2] = {x16, x16 + (size_t)S * F};
+    for (int pass = 0; pass < hpasses; ++pass) {
+        if (precision == 0)
+            hipLaunchKernelGGL((moe_hprep_kernel<0>), dim3(SP), dim3(256), 0, st, gy, rowmap, meta, h16[pass], texp,
+                               (int)F, pass);
+        else
+            hipLaunchKernelGGL((moe_hprep_kernel<1>), dim3(SP), dim3(256), 0, st, gy, rowmap, meta, h16[pass], texp,
+                               (int)F, pass);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    }
+    for (int pass = 0; pass < hpasses; ++pass) {
+        if (precision == 0)
+            hipLaunchKernelGGL((moe_dma_kernel<0>), dim3(g2), dim3(512), 0, st, down, eb2, h16[pass], texp, we2, s2,
+                               sw2, gy, tile_e, tile_end, meta, (int)N2, (int)F, (int)(N2 / 256), pass);
+        else
+            hipLaunchKernelGGL((moe_dma_kernel<1>), dim3(g2), dim3(512), 0, st, down, eb2, h16[pass], texp, we2, s2,
+                               sw2, gy, tile_e, tile_end, meta, (int)N2, (int)F, (int)(N2 / 256), 0);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    }
+    hipLaunchKernelGGL(moe_prefill_combine_kernel, dim3((unsigned)ceil_div(H / 4, 256), (unsigned)T), dim3(256), 0, st,
+                       gy, sop, topk_ids, topk_w, topk, E, (int)H, out);
+    return launch_status();
 }

@@ -131,11 +131,14 @@ class PackedQ4:
 
 @dataclass
 class PackedExperts:
-    """E experts' matrices of one shape [n, k], back to back in the mx layout."""
+    """E experts' matrices of one shape [n, k], back to back in the mx layout (one [E n, k]
+    mx matrix). ``prefill_scales`` caches that matrix's fp16 prefill scales once the
+    prefill-scale MoE path has needed them."""
     data: torch.Tensor
     experts: int
     n: int
     k: int
+    prefill_scales: torch.Tensor | None = field(default=None, repr=False, compare=False)
 
     @property
     def expert_bytes(self) -> int:
@@ -616,6 +619,10 @@ def prefill_workspace_bytes(t: int, n: int, k: int) -> int:
     return int(_lib_handle().q4_gemm_prefill_workspace_bytes(t, n, k))
 
 
+def moe_prefill_workspace_bytes(t: int, e: int, topk: int, h: int, f: int) -> int:
+    return int(_lib_handle().q4_moe_prefill_workspace_bytes(t, e, topk, h, f))
+
+
 def moe_workspace_bytes(t: int, e: int, topk: int, h: int, f: int) -> int:
     return int(_lib_handle().q4_moe_workspace_bytes(t, e, topk, h, f))
 
@@ -904,15 +911,17 @@ class GemvGroup:
 _PRECISION = {"fp16": 0, "bf16": 1}
 
 
-def prefill_scales(w: PackedQ4) -> torch.Tensor:
+def prefill_scales(w) -> torch.Tensor:
     """The matrix's fp16 prefill scales (per-row power-of-two exponents and the scale words
-    in fp16, q4_prefill_scales), computed on first use and kept on ``w``."""
+    in fp16, q4_prefill_scales), computed on first use and kept on ``w`` (a PackedQ4, or a
+    PackedExperts as its stacked [E n, k] matrix)."""
     if w.prefill_scales is None:
-        dev = w.device
+        dev = w.data.device
+        n = w.n * w.experts if isinstance(w, PackedExperts) else w.n
         lib = _lib_handle()
-        t = torch.empty(int(lib.q4_prefill_scales_bytes(w.n, w.k)), dtype=torch.uint8, device=dev)
+        t = torch.empty(int(lib.q4_prefill_scales_bytes(n, w.k)), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
-            check("q4_prefill_scales", lib.q4_prefill_scales(_ptr(w.data), w.n, w.k, _ptr(t), t.numel(), _stream(dev)))
+            check("q4_prefill_scales", lib.q4_prefill_scales(_ptr(w.data), n, w.k, _ptr(t), t.numel(), _stream(dev)))
         w.prefill_scales = t
     return w.prefill_scales
 
@@ -980,10 +989,13 @@ def pack_moe_experts(gate_blocks, up_blocks, down_blocks, device=None):
     return PackedExperts(gu, E, 2 * F, H), PackedExperts(dn, E, H, F)
 
 
+MOE_DECODE_MAX_PAIRS = 4096        # T * topk the decode kernels take (q4_moe_gemv)
+
+
 def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
               out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
               residual: torch.Tensor | None = None, shared: torch.Tensor | None = None,
-              shared_gate_w=None) -> torch.Tensor:
+              shared_gate_w=None, path: str = "auto", precision: str = "fp16") -> torch.Tensor:
     """out[t] = sum_j w[t,j] * down_e(silu(gate_e x_t) * (up_e x_t)), e = ids[t,j]; fp32 h,
     fp32 out [T, H] (moe_batch.py's per-slot product plus core.cpp:5150-5245's
     gather/scatter, done on the device).
@@ -991,7 +1003,13 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
     With ``residual`` (f32 [T, H], may be ``out``) and/or ``shared`` (the shared expert's
     f32 [T, H] output) with ``shared_gate_w`` (sgw, [H], rounded to bf16 if given wider),
     the block's finish is folded into the combine, as moe_fin does
-    (designs/moe_combine/moe_fin.py:1-4): out = (residual + routed sum) + sigmoid(x . sgw) * shared."""
+    (designs/moe_combine/moe_fin.py:1-4): out = (residual + routed sum) + sigmoid(x . sgw) * shared.
+
+    ``path``: "decode" (q4_moe_gemv: routed-expert GEMVs, T * topk <= 4096), "prefill"
+    (q4_moe_prefill: the experts' tokens batched into 256-token tiles of the prefill GEMM,
+    any T; ``precision`` "fp16" or "bf16" as gemm_q4_prefill, h rounded to bf16 in "bf16" as
+    the reference's moe_batch does), or "auto" (decode up to 4096 pairs, then prefill). The
+    prefill path takes no residual / shared expert."""
     dev = gate_up.data.device
     xt = _acts(x, dev)
     if xt.dim() == 1:
@@ -1023,7 +1041,26 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
         sgw = sgw.contiguous().reshape(-1)
         if sgw.numel() != H:
             raise ValueError(f"shared_gate_w must have {H} values, got {sgw.numel()}")
+    if path not in ("auto", "decode", "prefill"):
+        raise ValueError(f"path must be 'auto', 'decode' or 'prefill', got {path!r}")
+    if path == "auto":
+        path = "decode" if T * topk <= MOE_DECODE_MAX_PAIRS else "prefill"
     lib = _lib_handle()
+    if path == "prefill":
+        if residual is not None or shared is not None:
+            raise ValueError("the prefill MoE path takes no residual or shared expert")
+        if precision not in _PRECISION:
+            raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
+        if T == 0:
+            return out
+        sc = (prefill_scales(gate_up), prefill_scales(down)) if precision == "fp16" else (None, None)
+        with torch.cuda.device(dev):
+            wp, wn = _ws_arg(dev, lib.q4_moe_prefill_workspace_bytes(T, E, topk, H, F), "moe_prefill", workspace)
+            check("q4_moe_prefill", lib.q4_moe_prefill(
+                _ptr(gate_up.data), _ptr(down.data), None if sc[0] is None else _ptr(sc[0]),
+                None if sc[1] is None else _ptr(sc[1]), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts), _ptr(out),
+                T, E, topk, H, F, _PRECISION[precision], wp, wn, _stream(dev)))
+        return out
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_moe_workspace_bytes(T, E, topk, H, F), "moe", workspace)
         if residual is None and shared is None:

@@ -95,7 +95,11 @@ def test_moe_empty_and_limits(gpu, pkg, oracle):
     assert out.shape == (0, H)
     with pytest.raises(Exception):
         pkg.moe_batch(gu, dn, torch.zeros(600, H, dtype=torch.bfloat16, device=gpu),
-                      np.zeros((600, 8), np.int32), np.zeros((600, 8), np.float32))   # 4800 pairs > 4096
+                      np.zeros((600, 8), np.int32), np.zeros((600, 8), np.float32),
+                      path="decode")                                           # 4800 pairs > 4096
+    with pytest.raises(Exception):                                             # prefill path: H % 256
+        pkg.moe_batch(gu, dn, torch.zeros(600, H, dtype=torch.bfloat16, device=gpu),
+                      np.zeros((600, 8), np.int32), np.zeros((600, 8), np.float32))
 
 
 def test_moe_few_pairs_path_with_popular_experts(gpu, pkg, oracle):

@@ -1,0 +1,103 @@
+"""GPU parity of the routed MoE block at prefill scale (q4_moe_prefill: each expert's tokens
+batched into 256-token tiles of the prefill GEMM, as the reference batches them into slots
+of its expert dispatches, moe_batch.h:98-172 and core.cpp:5163-5178).
+
+Bars: precision "fp16" against the fp64 oracle with the exact weights and fp32 h
+(moe_reference): maxrel <= 1e-3 per the north star, and the reference's moe_batch gate
+rel_fro <= 5e-3 (designs/moe_batch/compare.py:20). Precision "bf16" (the reference's tile,
+RNE_bf16(q d + m), h rounded to bf16 as moe_batch.h:181-202 does) against the oracle over
+the same bf16-rounded weights with h_bf16: maxrel <= 1e-3. At config 4's matrices and
+T = 2048 (16384 pairs) the oracle runs on sampled tokens (the routing of one token does not
+involve the others)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _make(oracle, pkg, gpu, E, H, F, seed, bf16_weights=False):
+    rng = np.random.default_rng(seed)
+    gates = [oracle.baseline_q4_1_blocks(F, H, rng) for _ in range(E)]
+    ups = [oracle.baseline_q4_1_blocks(F, H, rng) for _ in range(E)]
+    downs = [oracle.baseline_q4_1_blocks(H, F, rng) for _ in range(E)]
+    gu, dn = pkg.pack_moe_experts(gates, ups, downs, gpu)
+    if bf16_weights:
+        deq = lambda blocks: (lambda e: oracle.bf16_round(oracle.dequant_q4_1(blocks[e])))
+    else:
+        deq = lambda blocks: (lambda e: oracle.dequant_q4_1(blocks[e]))
+    return rng, gu, dn, deq(gates), deq(ups), deq(downs)
+
+
+@pytest.mark.parametrize("E,H,F,T,K,xdt,prec", [
+    (8, 256, 128, 300, 2, "bf16", "fp16"),        # several token tiles per expert
+    (8, 256, 128, 300, 2, "f32", "fp16"),         # f32 x: value and remainder passes
+    (16, 512, 256, 97, 4, "bf16", "fp16"),        # ragged tiles, some experts empty
+    (8, 256, 128, 300, 2, "bf16", "bf16"),
+    (16, 512, 256, 97, 4, "f32", "bf16"),
+])
+def test_moe_prefill_matches_oracle(gpu, pkg, oracle, E, H, F, T, K, xdt, prec):
+    say(f"moe prefill E={E} H={H} F={F} T={T} top{K} {xdt} {prec}")
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, E + H + T, bf16_weights=prec == "bf16")
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xt = torch.from_numpy(x).to(torch.bfloat16) if xdt == "bf16" else torch.from_numpy(x)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill", precision=prec).cpu().numpy()
+    xr = xt.to(torch.float32).numpy()
+    if prec == "bf16":
+        xr = oracle.bf16_round(xr)
+    ref = oracle.moe_reference(g_of, u_of, d_of, xr, ids, w, h_bf16=prec == "bf16")
+    assert out.shape == (T, H) and np.isfinite(out).all()
+    assert oracle.maxrel(out, ref) <= 1e-3, oracle.maxrel(out, ref)
+    assert oracle.rel_fro(out, ref) <= 5e-3
+
+
+def test_moe_prefill_deterministic_and_equal_to_decode_path(gpu, pkg, oracle):
+    """Same bits on every call; within fp32-level noise of the decode path (fp32 h) at a
+    batch both paths take."""
+    say("moe prefill determinism / decode agreement")
+    E, H, F, T, K = 16, 512, 256, 200, 4
+    rng, gu, dn, *_ = _make(oracle, pkg, gpu, E, H, F, 31)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    a = pkg.moe_batch(gu, dn, x, ids, w, path="prefill").cpu().numpy()
+    for _ in range(2):
+        assert pkg.moe_batch(gu, dn, x, ids, w, path="prefill").cpu().numpy().tobytes() == a.tobytes()
+    d = pkg.moe_batch(gu, dn, x, ids, w, path="decode").cpu().numpy()
+    assert oracle.maxrel(a, d) <= 1e-3
+
+
+def test_moe_prefill_one_expert_takes_every_token(gpu, pkg, oracle):
+    """All pairs on one expert (many full tiles), the rest empty; ids outside [0, E) add nothing."""
+    say("moe prefill, one popular expert")
+    E, H, F, T = 6, 256, 128, 700
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 77)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    ids = np.stack([np.full(T, 4), np.full(T, -1)], axis=1).astype(np.int32)
+    w = np.stack([np.ones(T), np.full(T, 3.0)], axis=1).astype(np.float32)
+    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill").cpu().numpy()
+    ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy(), ids[:, :1], w[:, :1])
+    assert oracle.maxrel(out, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("T", [512, 2048])
+def test_moe_prefill_config4_matrices_sampled_tokens(gpu, pkg, oracle, T):
+    """Config 4's experts (128 x [1536, 2048] gate/up, [2048, 768] down, top-8 routing) at
+    prefill scale: T * 8 = 4096 and 16384 pairs through the prefill path; sampled tokens held
+    to the fp64 oracle."""
+    E, H, F, K = 128, 2048, 768, 8
+    say(f"moe prefill config-4 matrices T={T}")
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 4000 + T)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill").cpu().numpy()
+    assert np.isfinite(out).all()
+    pick = np.sort(rng.choice(T, 12, replace=False))
+    ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy()[pick], ids[pick], w[pick])
+    assert oracle.maxrel(out[pick], ref) <= 1e-3, oracle.maxrel(out[pick], ref)
