@@ -616,6 +616,21 @@ def extra_config3(torch, q4, dev):
             ms = graph_time(torch, run, [y], replays=5) / 3
             ms_bf16 = graph_time(torch, lambda: run("bf16"), [y], replays=5) / 3
             tf = 2.0 * T * n * k / ms / 1e9
+            # the activation pre-pass and the GEMM apart: activations prepared once
+            # (q4_prefill_prepare) are what a model hands its projections (gate and up
+            # share one; the SwiGLU producer can write down's)
+            prep = q4.prefill_prepare(x)
+            wsp = torch.empty(max(q4.prefill_workspace_bytes(T, n, k), 256), dtype=torch.uint8, device=dev)
+
+            def run_prepared():
+                for _ in range(3):
+                    q4.gemm_q4_prefill(packed[name], prep, y, workspace=wsp)
+
+            def run_prepare():
+                for _ in range(3):
+                    q4.prefill_prepare(x, out=prep.data)
+            ms_gemm = graph_time(torch, run_prepared, [y], replays=5) / 3
+            ms_prep = graph_time(torch, run_prepare, [], replays=5) / 3   # (padding bytes are not written)
             # the vendor library's dense GEMM on the same shape (fp16 weights already
             # dequantized, [K, N] contiguous): the rate this box sustains for a plain
             # GEMM of this problem, as a yardstick for the dequant GEMM
@@ -623,11 +638,32 @@ def extra_config3(torch, q4, dev):
             wd = (torch.randn(k, n, generator=gen, device=dev) * 0.01).to(torch.float16)
             _, dms = time_launches(torch, lambda: torch.matmul(xd, wd), 10, 3)
             out[f"T{T}_{name}"] = {"ms": ms, "tflops": tf, "frac_of_peak": tf / MFMA_PEAK_TFLOPS,
+                                   "prepared_gemm_ms": ms_gemm, "prepared_gemm_tflops": 2.0 * T * n * k / ms_gemm / 1e9,
+                                   "prepared_gemm_frac_of_peak": 2.0 * T * n * k / ms_gemm / 1e9 / MFMA_PEAK_TFLOPS,
+                                   "prepare_ms": ms_prep,
                                    "bf16_tile_ms": ms_bf16, "bf16_tile_tflops": 2.0 * T * n * k / ms_bf16 / 1e9,
                                    "dense_fp16_matmul_ms": dms,
                                    "dense_fp16_matmul_tflops": 2.0 * T * n * k / dms / 1e9,
                                    "vs_dense_fp16_matmul": dms / ms}
-            del xd, wd
+            del xd, wd, prep, wsp
+    # Llama-3-8B's gate and up as one [28672, 4096] matrix (row groups concatenated) over
+    # one prepared X: the FFN's first GEMM as a model issues it
+    gu = q4.pack_q4_1(gen_blocks(torch, 28672, 4096, gen, dev), dev)
+    q4.prefill_scales(gu)
+    for T in (512, 2048):
+        x = torch.randn(T, 4096, generator=gen, device=dev).to(torch.bfloat16)
+        prep = q4.prefill_prepare(x)
+        y = torch.empty(T, 28672, device=dev)
+        wsp = torch.empty(max(q4.prefill_workspace_bytes(T, 28672, 4096), 256), dtype=torch.uint8, device=dev)
+
+        def run_fused():
+            for _ in range(3):
+                q4.gemm_q4_prefill(gu, prep, y, workspace=wsp)
+        msf = graph_time(torch, run_fused, [y], replays=5) / 3
+        tff = 2.0 * T * 28672 * 4096 / msf / 1e9
+        out[f"T{T}_gate_up_fused_prepared"] = {"N": 28672, "K": 4096, "ms": msf, "tflops": tff,
+                                               "frac_of_peak": tff / MFMA_PEAK_TFLOPS}
+        del prep, wsp, y
     return out
 
 

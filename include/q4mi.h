@@ -408,6 +408,27 @@ size_t q4_gemm_prefill_scaled_workspace_bytes(int T, int64_t N, int64_t K);
 int q4_gemm_prefill_scaled(const uint8_t* packed, const void* scales, const void* x, int x_dtype, float* y,
                            int T, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Prepared activations: q4_gemm_prefill's activation pre-pass on its own, so one producer
+ * output is converted once and read by several projections (gate and up of an FFN; Q, K
+ * and V), or written in this layout by the producer itself. The buffer holds the GEMM's
+ * 16-bit activation planes (one; two for f32 x in precision 0: value and fp16 remainder) in
+ * the pipelined kernel's tiled image (K % 64 == 0; rows [T][K] otherwise), then the
+ * per-token exponents (precision 0). The reference's prefill design likewise takes X
+ * pre-tiled for its B operand, the tiling being the host's job (gemm_q4_prefill.py:19-22,
+ * :68-70). Bytes, or 0 for bad arguments: */
+size_t q4_prefill_prepared_bytes(int T, int64_t K, int x_dtype, int precision);
+int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, int precision,
+                       void* prepared, size_t prepared_bytes, void* stream);
+
+/* Workspace of q4_gemm_prefill_prepared: the K-split partials only (0 when unsplit). */
+size_t q4_gemm_prefill_prepared_workspace_bytes(int T, int64_t N, int64_t K);
+
+/* q4_gemm_prefill over prepared activations (x_dtype and precision as prepared; precision 0
+ * takes the matrix's prefill scales). Same bits as q4_gemm_prefill / _scaled on the same X. */
+int q4_gemm_prefill_prepared(const uint8_t* packed, const void* scales, const void* prepared, int x_dtype,
+                             float* y, int T, int64_t N, int64_t K, int precision, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* Workspace bytes q4_moe_gemv needs. */
 size_t q4_moe_workspace_bytes(int T, int E, int topk, int H, int F);
 

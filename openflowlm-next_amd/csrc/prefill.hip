@@ -983,38 +983,50 @@ extern "C" size_t q4_gemm_prefill_workspace_bytes(int T, int64_t N, int64_t K) {
 namespace {
 
 // The GEMM with the matrix's prefill scales (precision 0) given; workspace of gemm_ws_bytes.
+// One GEMM pass over activation plane x16 (exponents te): pass 0 writes y, later passes add
+// their products to it (f32 activations' remainder). part: the split partials, when the plan
+// splits K; the in-order reduce then writes (or adds to) y.
+int gemm_pass(const uint8_t* packed, const void* scales, const uint16_t* x16, const int* te, float* y, int T,
+              int64_t N, int64_t K, int precision, float* part, int pass, hipStream_t st) {
+    const int* we = precision == 0 ? (const int*)scales : nullptr;
+    const uint32_t* s16 = precision == 0 ? (const uint32_t*)((const char*)scales + scales_wexp_bytes(N)) : nullptr;
+    const PrefillPlan plan = make_plan(T, N, K);
+    float* out = plan.splits > 1 ? part : y;
+    const int accum = plan.splits > 1 ? 0 : pass;
+    if (precision == 0)
+        launch_prefill<0>(plan.cfg, plan.grid, st, packed, x16, te, we, s16, out, T, (int)N, (int)K, plan.tiles_t,
+                          plan.splits, plan.wide_wgs, plan.narrow_row0, accum);
+    else
+        launch_prefill<1>(plan.cfg, plan.grid, st, packed, x16, nullptr, nullptr, nullptr, out, T, (int)N, (int)K,
+                          plan.tiles_t, plan.splits, plan.wide_wgs, plan.narrow_row0, accum);
+    if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    if (plan.splits > 1) {
+        const int64_t MN4 = (int64_t)T * N / 4;
+        hipLaunchKernelGGL(prefill_reduce_kernel, dim3((unsigned)ceil_div(MN4, 256)), dim3(256), 0, st,
+                           (const f32x4*)out, (f32x4*)y, MN4, plan.splits, pass);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    }
+    return Q4MI_OK;
+}
+
+// f32 activations in precision 0 take two passes: their fp16 rounding, then the fp16
+// remainder, whose product the second pass adds to y.
+int activation_passes(int x_dtype, int precision) { return x_dtype == Q4MI_F32 && precision == 0 ? 2 : 1; }
+
+// The GEMM with the matrix's prefill scales (precision 0) given; workspace of gemm_ws_bytes:
+// one activation plane, prepared and consumed pass by pass.
 int prefill_impl(const uint8_t* packed, const void* scales, const void* x, int x_dtype, float* y, int T, int64_t N,
                  int64_t K, int precision, void* workspace, hipStream_t st) {
     uint16_t* x16 = (uint16_t*)workspace;
     int* te = (int*)((char*)workspace + x16_bytes(T, K));
-    const int* we = precision == 0 ? (const int*)scales : nullptr;
-    const uint32_t* s16 = precision == 0 ? (const uint32_t*)((const char*)scales + scales_wexp_bytes(N)) : nullptr;
-    const PrefillPlan plan = make_plan(T, N, K);
-    const bool xf32 = x_dtype == Q4MI_F32;
-    const int cfg = plan.cfg;
-    const bool tiled = cfg == kDmaCfg;
-    float* out = plan.splits > 1 ? (float*)((char*)workspace + xprep_bytes(T, K)) : y;
-    const dim3 xgrid((unsigned)padded_tokens(T));
-    // f32 activations in precision 0 take two passes: their fp16 rounding, then the fp16
-    // remainder, whose product the second pass adds to y.
-    const int passes = xf32 && precision == 0 ? 2 : 1;
-    for (int pass = 0; pass < passes; ++pass) {
-        launch_xprep(xf32, precision, tiled, xgrid, st, x, x16, te, T, (int)K, pass);
+    float* part = (float*)((char*)workspace + xprep_bytes(T, K));
+    const bool tiled = make_plan(T, N, K).cfg == kDmaCfg;
+    for (int pass = 0; pass < activation_passes(x_dtype, precision); ++pass) {
+        launch_xprep(x_dtype == Q4MI_F32, precision, tiled, dim3((unsigned)padded_tokens(T)), st, x, x16, te, T,
+                     (int)K, pass);
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-        const int accum = plan.splits > 1 ? 0 : pass;
-        if (precision == 0)
-            launch_prefill<0>(cfg, plan.grid, st, packed, x16, te, we, s16, out, T, (int)N, (int)K, plan.tiles_t,
-                              plan.splits, plan.wide_wgs, plan.narrow_row0, accum);
-        else
-            launch_prefill<1>(cfg, plan.grid, st, packed, x16, nullptr, nullptr, nullptr, out, T, (int)N, (int)K,
-                              plan.tiles_t, plan.splits, plan.wide_wgs, plan.narrow_row0, accum);
-        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-        if (plan.splits > 1) {
-            const int64_t MN4 = (int64_t)T * N / 4;
-            hipLaunchKernelGGL(prefill_reduce_kernel, dim3((unsigned)ceil_div(MN4, 256)), dim3(256), 0, st,
-                               (const f32x4*)out, (f32x4*)y, MN4, plan.splits, pass);
-            if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-        }
+        const int rc = gemm_pass(packed, scales, x16, te, y, T, N, K, precision, part, pass, st);
+        if (rc != Q4MI_OK) return rc;
     }
     return launch_status();
 }
@@ -1055,6 +1067,73 @@ extern "C" int q4_gemm_prefill_scaled(const uint8_t* packed, const void* scales,
     if (!scales || misaligned16(scales)) return Q4MI_E_ARG;
     if (!workspace || workspace_bytes < gemm_ws_bytes(T, N, K)) return Q4MI_E_WORKSPACE;
     return prefill_impl(packed, scales, x, x_dtype, y, T, N, K, 0, workspace, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Prepared activations: the pre-pass on its own, so a producer's output is converted once
+// and read by several projections (gate and up of an FFN, Q, K and V), or written in this
+// layout by the producer itself. Layout: the activation planes of the GEMM's passes (two for
+// f32 x in precision 0: value and remainder), each x16_bytes(T, K), then the token exponents.
+// The pipelined kernel's tiled image when K % 64 == 0, else rows [T][K].
+// ---------------------------------------------------------------------------
+namespace {
+size_t prepared_bytes(int T, int64_t K, int x_dtype, int precision) {
+    return (size_t)activation_passes(x_dtype, precision) * x16_bytes(T, K) + align256((size_t)T * 4);
+}
+}  // namespace
+
+extern "C" size_t q4_prefill_prepared_bytes(int T, int64_t K, int x_dtype, int precision) {
+    if (T <= 0 || K <= 0 || K % 32 || (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) || (precision != 0 && precision != 1))
+        return 0;
+    return prepared_bytes(T, K, x_dtype, precision);
+}
+
+extern "C" int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, int precision, void* prepared,
+                                  size_t prepared_bytes_, void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (T < 0 || K <= 0 || K % 32) return Q4MI_E_SHAPE;
+    if (K > 0x7FFFFFFF) return Q4MI_E_RANGE;
+    if (T == 0) return Q4MI_OK;
+    if (!x || !prepared || misaligned16(x) || misaligned16(prepared)) return Q4MI_E_ARG;
+    if (prepared_bytes_ < prepared_bytes(T, K, x_dtype, precision)) return Q4MI_E_WORKSPACE;
+    const int passes = activation_passes(x_dtype, precision);
+    int* te = (int*)((char*)prepared + passes * x16_bytes(T, K));
+    for (int pass = 0; pass < passes; ++pass) {
+        launch_xprep(x_dtype == Q4MI_F32, precision, K % 64 == 0, dim3((unsigned)padded_tokens(T)),
+                     (hipStream_t)stream, x, (uint16_t*)((char*)prepared + pass * x16_bytes(T, K)), te, T, (int)K,
+                     pass);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+    }
+    return Q4MI_OK;
+}
+
+extern "C" size_t q4_gemm_prefill_prepared_workspace_bytes(int T, int64_t N, int64_t K) {
+    if (T <= 0 || K <= 0 || N < 0 || N % 64 || K % 32) return 0;
+    const PrefillPlan p = make_plan(T, N, K);
+    return p.splits > 1 ? align256((size_t)p.splits * T * N * 4) : 0;
+}
+
+extern "C" int q4_gemm_prefill_prepared(const uint8_t* packed, const void* scales, const void* prepared, int x_dtype,
+                                        float* y, int T, int64_t N, int64_t K, int precision, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    const int a = prefill_args(packed, prepared, x_dtype, y, T, N, K, workspace);
+    if (a != Q4MI_OK) return a > 0 ? Q4MI_OK : a;
+    if (precision == 0 && (!scales || misaligned16(scales))) return Q4MI_E_ARG;
+    const PrefillPlan plan = make_plan(T, N, K);
+    if ((plan.cfg == kDmaCfg) != (K % 64 == 0)) return Q4MI_E_ARG;   // a forced generic variant reads rows
+    if (plan.splits > 1 && (!workspace || workspace_bytes < q4_gemm_prefill_prepared_workspace_bytes(T, N, K)))
+        return Q4MI_E_WORKSPACE;
+    const int passes = activation_passes(x_dtype, precision);
+    const int* te = (const int*)((const char*)prepared + passes * x16_bytes(T, K));
+    for (int pass = 0; pass < passes; ++pass) {
+        const uint16_t* x16 = (const uint16_t*)((const char*)prepared + pass * x16_bytes(T, K));
+        const int rc = gemm_pass(packed, scales, x16, te, y, T, N, K, precision, (float*)workspace, pass,
+                                 (hipStream_t)stream);
+        if (rc != Q4MI_OK) return rc;
+    }
+    return Q4MI_OK;
 }
 
 // ---------------------------------------------------------------------------

@@ -926,6 +926,40 @@ def prefill_scales(w) -> torch.Tensor:
     return w.prefill_scales
 
 
+@dataclass
+class PreparedActs:
+    """Activations [t, k] converted once for the prefill GEMM (q4_prefill_prepare): the
+    GEMM's 16-bit tiled image (fp16 scaled per token row by a power of two, or bf16), so
+    several projections of the same input (gate and up, Q / K / V) read it without
+    converting it again."""
+    data: torch.Tensor
+    t: int
+    k: int
+    x_dtype: int
+    precision: str
+
+
+def prefill_prepare(x, precision: str = "fp16", out: torch.Tensor | None = None) -> PreparedActs:
+    """Convert X [T, K] (bf16 or f32) for gemm_q4_prefill once (its activation pre-pass)."""
+    if precision not in _PRECISION:
+        raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
+    dev = _device(x.device if isinstance(x, torch.Tensor) and x.is_cuda else None)
+    xt = _acts(x, dev)
+    if xt.dim() != 2:
+        raise ValueError(f"x must be [T, K], got {tuple(xt.shape)}")
+    T, K = xt.shape
+    lib = _lib_handle()
+    nbytes = int(lib.q4_prefill_prepared_bytes(T, K, _x_dtype(xt), _PRECISION[precision])) if T else 0
+    if T and nbytes == 0:
+        raise ValueError(f"[{T}, {K}] cannot be prepared (K % 32 == 0)")
+    data = _buf(out, "out", torch.uint8, (nbytes,), dev)
+    if T:
+        with torch.cuda.device(dev):
+            check("q4_prefill_prepare", lib.q4_prefill_prepare(_ptr(xt), _x_dtype(xt), T, K, _PRECISION[precision],
+                                                               _ptr(data), nbytes, _stream(dev)))
+    return PreparedActs(data, T, K, _x_dtype(xt), precision)
+
+
 def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16",
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y[T, N] = X[T, K] @ W^T for a prefill block of T tokens, fp32 out.
@@ -933,8 +967,25 @@ def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: st
     precision "fp16": each weight rounded once to fp16 in LDS (fp16 MFMA), weight and token
     rows scaled into fp16's range by powers of two (the matrix's prefill scales, computed
     once and kept on ``w``); "bf16": the reference tile RNE_bf16(fl32(q*d+m))
-    (gemm_q4_dequant.h:283-286)."""
+    (gemm_q4_dequant.h:283-286). ``x`` may be a PreparedActs (its own precision is used)."""
     dev = w.device
+    if isinstance(x, PreparedActs):
+        if x.k != w.k:
+            raise ValueError(f"prepared activations have K={x.k}, W is [{w.n}, {w.k}]")
+        if x.data.device != dev:
+            raise ValueError(f"prepared activations are on {x.data.device}, W on {dev}")
+        T, prec = x.t, _PRECISION[x.precision]
+        y = _buf(y, "y", torch.float32, (T, w.n), dev)
+        if T == 0 or w.n == 0:
+            return y
+        lib = _lib_handle()
+        sc = prefill_scales(w) if x.precision == "fp16" else None
+        with torch.cuda.device(dev):
+            wp, wn = _ws_arg(dev, lib.q4_gemm_prefill_prepared_workspace_bytes(T, w.n, w.k), "prefill", workspace)
+            check("q4_gemm_prefill_prepared", lib.q4_gemm_prefill_prepared(
+                _ptr(w.data), None if sc is None else _ptr(sc), _ptr(x.data), x.x_dtype, _ptr(y), T, w.n, w.k, prec,
+                wp, wn, _stream(dev)))
+        return y
     xt = _acts(x, dev)
     if xt.dim() != 2 or xt.shape[1] != w.k:
         raise ValueError(f"x must be [T, {w.k}], got {tuple(xt.shape)}")

@@ -285,3 +285,26 @@ def test_prefill_scales_match_numpy_and_paths_agree(gpu, pkg, oracle):
                                ws.numel(), st) == 0
     y_cached = pkg.gemm_q4_prefill(w, X)
     assert torch.equal(y_call, y_cached)
+
+
+@pytest.mark.parametrize("T,N,K,xdt,precision", [
+    (300, 256, 512, "bf16", "fp16"),       # one token tile + a ragged one, unsplit
+    (300, 256, 512, "f32", "fp16"),        # value and remainder planes
+    (512, 4096, 14336, "bf16", "fp16"),    # config 3's down at T = 512: K split and reduce
+    (200, 192, 96, "bf16", "fp16"),        # K % 64 != 0: rows [T][K], the generic kernel
+    (300, 256, 512, "f32", "bf16"),        # the reference tile
+])
+def test_prefill_prepared_activations_equal_the_one_call_path(gpu, pkg, oracle, T, N, K, xdt, precision):
+    """Activations prepared once (q4_prefill_prepare) and read by two projections give the
+    bits the one-call path gives for each."""
+    say(f"prefill prepared T={T} N={N} K={K} {xdt} {precision}")
+    rng = np.random.default_rng(T + N + K)
+    w1 = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(N, K, rng), gpu)
+    w2 = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(N, K, rng), gpu)
+    xf = rng.standard_normal((T, K)).astype(np.float32)
+    x = (torch.from_numpy(xf).to(torch.bfloat16) if xdt == "bf16" else torch.from_numpy(xf)).to(gpu)
+    prep = pkg.prefill_prepare(x, precision)
+    for w in (w1, w2):
+        a = pkg.gemm_q4_prefill(w, prep).cpu().numpy()
+        b = pkg.gemm_q4_prefill(w, x, precision=precision).cpu().numpy()
+        assert a.tobytes() == b.tobytes()
