@@ -334,6 +334,61 @@ def extra_staged(torch, q4, model, acts, xhead):
     return {"ms": ms, "gbs": nbytes / ms / 1e6, "calls": len(calls), "bytes": nbytes}
 
 
+def extra_decode_step(torch, q4, model, acts, xhead):
+    """A decode step's weight traffic in order with its own epilogues (attention itself
+    left out: its output is a fixed bf16 vector): per layer RMSNorm -> fused qkv -> o with
+    the residual -> RMSNorm -> SwiGLU gate/up (bf16 h) -> down with the residual; then the
+    final RMSNorm and lm_head, one HIP graph. Bytes: the weights streamed (qkv, o, gate, up,
+    down per layer, lm_head)."""
+    dev = model.head.device
+    H, F = 4096, 14336
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 29)
+    xres0 = torch.randn(1, H, generator=gen, device=dev)
+    xres = xres0.clone()
+    nw = (1 + 0.1 * torch.randn(H, generator=gen, device=dev)).to(torch.bfloat16)
+    xn = torch.empty(1, H, dtype=torch.bfloat16, device=dev)
+    qkv = torch.empty(1, 6144, device=dev)
+    h = torch.empty(1, F, dtype=torch.bfloat16, device=dev)
+    logits = torch.empty(1, model.head.n, device=dev)
+    ws = torch.empty(1 << 24, dtype=torch.uint8, device=dev)
+    attn = [xs["o"] for xs in acts]
+    nbytes = sum(p[n].nbytes for p in model.layers for n in ("qkv", "o", "gate", "up", "down")) + model.head.nbytes
+
+    def step():
+        for i, p in enumerate(model.layers):
+            q4.rmsnorm_add(xres, nw, xn=xn)
+            q4.gemm_q4(p["qkv"], xn, y=qkv, workspace=ws)
+            q4.gemm_q4(p["o"], attn[i], y=xres, residual=xres, workspace=ws)
+            q4.rmsnorm_add(xres, nw, xn=xn)
+            q4.swiglu_q4(p["gate"], p["up"], xn, out_dtype=torch.bfloat16, h=h, workspace=ws)
+            q4.gemm_q4(p["down"], h, y=xres, residual=xres, workspace=ws)
+        q4.rmsnorm_add(xres, nw, xn=xn)
+        q4.gemm_q4(model.head, xn, y=logits, workspace=ws)
+
+    def step_fused():           # the two norms inside the GEMVs that consume them
+        for i, p in enumerate(model.layers):
+            q4.gemm_q4_rmsnorm(p["qkv"], xres, nw, y=qkv, workspace=ws)
+            q4.gemm_q4(p["o"], attn[i], y=xres, residual=xres, workspace=ws)
+            q4.swiglu_q4(p["gate"], p["up"], xres, out_dtype=torch.bfloat16, h=h, workspace=ws, norm_w=nw)
+            q4.gemm_q4(p["down"], h, y=xres, residual=xres, workspace=ws)
+        q4.gemm_q4_rmsnorm(model.head, xres, nw, y=logits, workspace=ws)
+
+    def reset():
+        xres.copy_(xres0)
+    out = {"bytes": nbytes}
+    for name, fn in (("separate_norms", step), ("norms_in_gemv", step_fused)):
+        ms = graph_time(torch, fn, [logits, xres], replays=10, reset=reset)
+        out[name] = {"ms": ms, "gbs": nbytes / ms / 1e6}
+    reset()
+    step()
+    a = logits.clone()
+    reset()
+    step_fused()
+    out["same_logits"] = bool(torch.equal(a, logits))
+    return out
+
+
 def extra_lm_head(torch, q4, dev, head=None, xhead=None):
     """lm_head at vocabulary scale (128256 x 4096, M=1) with its sampling epilogue:
     the GEMV alone, then GEMV + greedy argmax and GEMV + top-40 (the sampler's
@@ -818,7 +873,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--extras", default="staged,0,2,3,4,moe_prefill,lm_head,ffn,q8,q4k,q40,peaks",
+    ap.add_argument("--extras", default="staged,step,0,2,3,4,moe_prefill,lm_head,ffn,q8,q4k,q40,peaks",
                     help="comma list (staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=3, help="passes over one layer per timed CPU run")
@@ -907,6 +962,8 @@ def main() -> int:
                 extras["measured_peaks"] = extra_peaks(torch, dev)
             elif cfg == "staged":
                 extras["config1_staged_decode_order"] = extra_staged(torch, q4, model, acts, xhead)
+            elif cfg == "step":
+                extras["config1_decode_step"] = extra_decode_step(torch, q4, model, acts, xhead)
             elif cfg == "0":
                 extras["config0_gemv_4096_f32x"] = extra_config0(torch, q4, dev)
             elif cfg == "2":

@@ -220,6 +220,16 @@ int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
 int q4_gemv_noalloc(const uint8_t* packed, const void* x, int x_dtype, float* y,
                     int M, int64_t N, int64_t K, void* stream);
 
+/* The GEMV with its RMSNorm inside: Y = X . W^T with X = bf16(RMSNorm(x) * norm_w), formed per
+ * tile from the f32 residual stream x [M][K] (1 <= M <= 16, K <= 16384, norm_w [K] bf16 or
+ * f32). Same bits as q4_rmsnorm_add (bf16 out, no add) then q4_gemv: every workgroup first
+ * computes the rows' 1/rms with q4_rmsnorm_add's arithmetic. Saves the norm's launch and its
+ * bf16 copy in a decode step (the reference's ln design ahead of a projection,
+ * designs/ln/ln.py:1-6). Workspace as q4_gemv. */
+int q4_gemv_rmsnorm(const uint8_t* packed, const float* x, const void* norm_w, int norm_w_dtype, float eps,
+                    float* y, int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* q4_gemv plus the residual: y = residual + X . W^T (residual f32 [M][N]; it may
  * be y itself, which then accumulates in place). Same workspace as q4_gemv. The
  * residual adds the reference makes after a projection: x_res + o_proj / down
@@ -302,6 +312,12 @@ size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K);
 int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void* x, int x_dtype,
                    void* h, int h_dtype, int M, int64_t F, int64_t K,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* q4_gemv_swiglu with its RMSNorm inside, as q4_gemv_rmsnorm (x the f32 residual stream,
+ * 1 <= M <= 16, K <= 16384): the bits of q4_rmsnorm_add then q4_gemv_swiglu. */
+int q4_gemv_swiglu_rmsnorm(const uint8_t* gate, const uint8_t* up, const float* x, const void* norm_w,
+                           int norm_w_dtype, float eps, void* h, int h_dtype, int M, int64_t F, int64_t K,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* The activation producer: per row m < M of N values,
  *   y = x + add (add may be NULL; y may be NULL, or x itself when N <= 16384),

@@ -60,6 +60,9 @@ SIGNATURES = {
     "q4_gemv_noalloc": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "q4_gemv_grouped": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp]),
     "q4_gemv_residual": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
+    "q4_gemv_rmsnorm": (_i32, [_vp, _vp, _vp, _i32, C.c_float, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
+    "q4_gemv_swiglu_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i32, C.c_float, _vp, _i32, _i32, _i64, _i64, _vp, _sz,
+                                      _vp]),
     "q4_gemv_swiglu_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemv_swiglu": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_rmsnorm_add": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i64, C.c_float, _vp]),

@@ -28,6 +28,9 @@ struct GemvParams {
     int64_t N, K;
     float* part;      // [S][M][N] partial sums (S > 1)
     const float* res; // residual added to the result ([M][N], may alias y), or null
+    const void* nw;   // NORM kernels: the RMSNorm weight [K] (x is the f32 residual stream)
+    int nw_bf16;
+    float eps;
 };
 
 
@@ -52,9 +55,14 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 
 // WAVES waves per workgroup (4, 8 or 16): more waves put more tiles of a row group in
 // flight, so fewer K splits fill the memory system.
-template <int NTL, bool XF32, int WAVES, bool Q40 = false>
+// NORM: X = bf16(RMSNorm(x) * nw) formed per tile from the f32 row x (every workgroup
+// first computes the rows' 1/rms exactly as q4_rmsnorm_add does), so the norm needs no
+// launch and no bf16 copy of its own.
+template <int NTL, bool XF32, int WAVES, bool Q40 = false, bool NORM = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     __shared__ float red[WAVES][4][NTL][64];
+    __shared__ float rrow[NORM ? 4 * NTL : 1];
+    if constexpr (NORM) rms_inv_rows<4 * NTL>((const float*)P.x, P.M, P.K, P.eps, rrow);
     const int64_t item = blockIdx.x;
     const int S = P.S;
     const int64_t g = item / S;
@@ -66,7 +74,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
-    gemv_rows<NTL, XF32, DenseRows, WAVES, Q40>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc);
+    gemv_rows<NTL, XF32, DenseRows, WAVES, Q40, NORM>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc,
+                                                       NormIn{P.nw, P.nw_bf16, rrow});
     if (S == 1) gemv_finish<NTL, WAVES>(acc, red, P.M, P.y, P.N, g, P.res);
     else gemv_finish<NTL, WAVES>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
@@ -184,6 +193,9 @@ struct SwigluParams {
     int S;
     int64_t F, K;
     float* part;
+    const void* nw;   // NORM: the RMSNorm weight [K] (x is the f32 residual stream)
+    int nw_bf16;
+    float eps;
 };
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -193,9 +205,11 @@ __device__ __forceinline__ void store_h(void* h, bool bf16, int64_t i, float v) 
     else ((float*)h)[i] = v;
 }
 
-template <int NTL, bool XF32>
+template <int NTL, bool XF32, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_swiglu_kernel(SwigluParams P) {
     __shared__ float red[kWaves][4][NTL][64];
+    __shared__ float rrow[NORM ? 4 * NTL : 1];
+    if constexpr (NORM) rms_inv_rows<4 * NTL>((const float*)P.x, P.M, P.K, P.eps, rrow);
     const int64_t item = blockIdx.x;
     const int S = P.S;
     const int64_t g = item / S;
@@ -210,7 +224,8 @@ __global__ __launch_bounds__(256) void gemv_swiglu_kernel(SwigluParams P) {
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int j = 0; j < NTL; ++j) acc[i][r][j] = 0.f;
-    gemv_rows_multi<NTL, XF32, 2, 4>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc);
+    gemv_rows_multi<NTL, XF32, 2, 4, kWaves, NORM>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc,
+                                                  NormIn{P.nw, P.nw_bf16, rrow});
     float vg[NTL], vu[NTL];
     wave_sum<NTL>(acc[0], red, vg);
     __syncthreads();
@@ -355,7 +370,8 @@ size_t workspace_for(int M, int64_t N, int64_t K, int S) {
 
 template <int NTL>
 void launch_swiglu(bool xf32, dim3 grid, hipStream_t st, const SwigluParams& P) {
-    if (xf32) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, true>), grid, dim3(256), 0, st, P);
+    if (P.nw) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false, true>), grid, dim3(256), 0, st, P);
+    else if (xf32) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, true>), grid, dim3(256), 0, st, P);
     else hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false>), grid, dim3(256), 0, st, P);
 }
 
@@ -367,6 +383,12 @@ void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, cons
 
 template <int NTL, int WAVES, bool Q40>
 void launch_gemv_w(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if constexpr (!Q40) {
+        if (P.nw) {
+            hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, false, true>), grid, dim3(64 * WAVES), 0, st, P);
+            return;
+        }
+    }
     if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, WAVES, Q40>), grid, dim3(64 * WAVES), 0, st, P);
     else hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, Q40>), grid, dim3(64 * WAVES), 0, st, P);
 }
@@ -416,9 +438,15 @@ extern "C" size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K) {
 
 namespace {
 
+struct NormSpec {
+    const void* w = nullptr;   // RMSNorm weight [K]; null: x is the GEMV's input as given
+    int w_bf16 = 0;
+    float eps = 0.f;
+};
+
 int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* res, float* y, int M, int64_t N,
               int64_t K, void* workspace, size_t workspace_bytes, void* stream, const uint8_t* lo = nullptr,
-              bool q40 = false) {
+              bool q40 = false, NormSpec nrm = {}) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
     if (M < 0 || M > (lo || q40 ? 16 : kMaxGemvTokens)) return Q4MI_E_RANGE;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
@@ -436,6 +464,9 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     P.N = N;
     P.K = K;
     P.res = res;
+    P.nw = nrm.w;
+    P.nw_bf16 = nrm.w_bf16;
+    P.eps = nrm.eps;
     if (S > 1) {   // the documented contract: at least what the query reports
         if (!workspace || workspace_bytes < q4_gemv_workspace_bytes(M, N, K)) return Q4MI_E_WORKSPACE;
         P.part = (float*)workspace;
@@ -556,15 +587,40 @@ extern "C" int q4_gemv_q40(const uint8_t* packed, const void* x, int x_dtype, co
     return gemv_impl(packed, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream, nullptr, true);
 }
 
+// Norm-fused forms: X = bf16(RMSNorm(x) * norm_w) from the f32 residual stream x, the same
+// bits as q4_rmsnorm_add (bf16 out, no add) followed by q4_gemv / q4_gemv_swiglu.
+static int norm_args(const float* x, const void* norm_w, int norm_w_dtype, float eps, int M, int64_t K,
+                     NormSpec* out) {
+    if (norm_w_dtype != Q4MI_F32 && norm_w_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (!(eps >= 0.0f)) return Q4MI_E_ARG;
+    if (M > 16) return Q4MI_E_RANGE;
+    if (K > 16384) return Q4MI_E_RANGE;
+    if (M > 0 && (!x || !norm_w || misaligned16(norm_w))) return Q4MI_E_ARG;
+    out->w = norm_w;
+    out->w_bf16 = norm_w_dtype == Q4MI_BF16;
+    out->eps = eps;
+    return Q4MI_OK;
+}
+
+extern "C" int q4_gemv_rmsnorm(const uint8_t* packed, const float* x, const void* norm_w, int norm_w_dtype, float eps,
+                               float* y, int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+    NormSpec nrm;
+    const int a = norm_args(x, norm_w, norm_w_dtype, eps, M, K, &nrm);
+    if (a != Q4MI_OK) return a;
+    return gemv_impl(packed, x, Q4MI_F32, nullptr, y, M, N, K, workspace, workspace_bytes, stream, nullptr, false,
+                     nrm);
+}
+
 extern "C" size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K) {
     if (M < 1 || M > 16 || F <= 0 || K <= 0 || F % 64 || K % 32) return 0;
     const int S = swiglu_splits(F, K);
     return S > 1 ? (size_t)S * M * 2 * F * sizeof(float) : 0;
 }
 
-extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void* x, int x_dtype, void* h,
-                              int h_dtype, int M, int64_t F, int64_t K, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, int x_dtype, void* h, int h_dtype,
+                       int M, int64_t F, int64_t K, void* workspace, size_t workspace_bytes, void* stream,
+                       NormSpec nrm = {}) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
     if (h_dtype != Q4MI_F32 && h_dtype != Q4MI_BF16) return Q4MI_E_ARG;
     if (M < 0 || M > 16) return Q4MI_E_RANGE;
@@ -584,6 +640,9 @@ extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void
     P.S = S;
     P.F = F;
     P.K = K;
+    P.nw = nrm.w;
+    P.nw_bf16 = nrm.w_bf16;
+    P.eps = nrm.eps;
     if (S > 1) {
         if (!workspace || workspace_bytes < (size_t)S * M * 2 * F * sizeof(float)) return Q4MI_E_WORKSPACE;
         P.part = (float*)workspace;
@@ -604,6 +663,21 @@ extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void
                            P.h_bf16, M, F, S);
     }
     return launch_status();
+}
+
+extern "C" int q4_gemv_swiglu(const uint8_t* gate, const uint8_t* up, const void* x, int x_dtype, void* h,
+                              int h_dtype, int M, int64_t F, int64_t K, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+    return swiglu_impl(gate, up, x, x_dtype, h, h_dtype, M, F, K, workspace, workspace_bytes, stream);
+}
+
+extern "C" int q4_gemv_swiglu_rmsnorm(const uint8_t* gate, const uint8_t* up, const float* x, const void* norm_w,
+                                      int norm_w_dtype, float eps, void* h, int h_dtype, int M, int64_t F, int64_t K,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    NormSpec nrm;
+    const int a = norm_args(x, norm_w, norm_w_dtype, eps, M, K, &nrm);
+    if (a != Q4MI_OK) return a;
+    return swiglu_impl(gate, up, x, Q4MI_F32, h, h_dtype, M, F, K, workspace, workspace_bytes, stream, nrm);
 }
 
 extern "C" size_t q4_gemv_q4k_workspace_bytes(int M, int64_t N, int64_t K) {

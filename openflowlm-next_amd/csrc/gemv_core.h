@@ -26,6 +26,7 @@
 // kernels, whose workgroups stream short row-group spans and gain most from it).
 #pragma once
 
+#include "norm_core.h"
 #include "q4mi_device.h"
 
 namespace q4mi {
@@ -77,10 +78,20 @@ __device__ __forceinline__ void load_xfrag(const void* __restrict__ x, int64_t K
 // Loads are unconditional (a tile index past kb1 is clamped to kb1 - 1 and
 // its data skipped) so the compiler can count them statically and wait for
 // each tile's loads only, keeping kUnroll tiles in flight per wave.
+// The activation row normalised in the GEMV (RMSNorm, norm_core.h): x is the f32 residual
+// stream, w the norm weight (bf16 or f32), r the rows' 1/rms (LDS, per activation row).
+struct NormIn {
+    const void* w;
+    int w_bf16;
+    const float* r;
+};
+
 // Q40: the mx0 layout (1152 B tiles, bf16 d only; m = -8 d), else the mx layout.
-template <int NTL, bool XF32, class Rows, int WAVES = kWaves, bool Q40 = false>
+// NORM: x is f32 and normalised on the fly (nrm), rounded to bf16 as q4_rmsnorm_add rounds it.
+template <int NTL, bool XF32, class Rows, int WAVES = kWaves, bool Q40 = false, bool NORM = false>
 __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, const void* __restrict__ x, Rows rows,
-                                          int64_t K, int64_t g, int kb0, int kb1, float (&acc)[4][NTL]) {
+                                          int64_t K, int64_t g, int kb0, int kb1, float (&acc)[4][NTL],
+                                          NormIn nrm = {}) {
     constexpr int TB = Q40 ? kQ0TileBytes : kTileBytes;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
@@ -125,7 +136,14 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ packed, co
             } else {
                 s[u] = load_nt_u32x4(tp + soff);
             }
-            if (need_x) load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
+            if (need_x) {
+                if constexpr (NORM)
+                    xh[u] = norm_bf16x8((const float*)x + xrow * K + (int64_t)t * 32 + kg * 8,
+                                        (const uint8_t*)nrm.w + ((int64_t)t * 32 + kg * 8) * (nrm.w_bf16 ? 2 : 4),
+                                        nrm.w_bf16, nrm.r[xrow]);
+                else
+                    load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
+            }
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -410,9 +428,10 @@ __device__ __forceinline__ void multi_tile(const u32x4 (&c)[NG], const u32x4 (&s
 // gemv_rows over NG row groups at once (tile bases gbase[i], same K range and
 // activations): per K position the activation fragment and the -128 sum x
 // MFMA are shared by the NG groups, and NG x UNR tiles are in flight per wave.
-template <int NTL, bool XF32, int NG, int UNR, int WAVES = kWaves, class Rows>
+template <int NTL, bool XF32, int NG, int UNR, int WAVES = kWaves, bool NORM = false, class Rows>
 __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG], const void* __restrict__ x, Rows rows,
-                                                int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL]) {
+                                                int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL],
+                                                NormIn nrm = {}) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     kb0 = __builtin_amdgcn_readfirstlane(kb0);
@@ -434,7 +453,12 @@ __device__ __forceinline__ void gemv_rows_multi(const uint8_t* const (&gbase)[NG
                 c[u][i] = load_nt_u32x4(tp + coff);
                 s[u][i] = load_nt_u32x4(tp + soff);
             }
-            load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
+            if constexpr (NORM)
+                xh[u] = norm_bf16x8((const float*)x + xrow * K + (int64_t)t * 32 + kg * 8,
+                                    (const uint8_t*)nrm.w + ((int64_t)t * 32 + kg * 8) * (nrm.w_bf16 ? 2 : 4),
+                                    nrm.w_bf16, nrm.r[xrow]);
+            else
+                load_xfrag<XF32>(x, K, xrow, (int64_t)t * 32 + kg * 8, xh[u], xl[u]);
         }
 #pragma unroll
         for (int u = 0; u < UNR; ++u)

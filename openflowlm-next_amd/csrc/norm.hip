@@ -11,7 +11,7 @@
 // One 256-thread workgroup per row. Rows up to 16384 values are read once into
 // registers (the loads issue together; y is stored only after all of x is read, so y
 // may be x); longer rows take a two-pass kernel.
-#include "q4mi_device.h"
+#include "norm_core.h"
 #include "q4mi_internal.h"
 
 using namespace q4mi;
@@ -22,24 +22,6 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
     return v;
-}
-
-// Wave sum of an f32 in every lane: DPP steps within rows (xor 1, xor 2 quad permutes,
-// the half-row and row mirrors), row broadcasts into lane 63, then readlane. Every lane's
-// addends arrive in the same tree order, so the result is deterministic.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add(float v) {
-    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
-                                                                    0xF, false));
-}
-__device__ __forceinline__ float wave_sum_f32(float v) {
-    v = dpp_add<0xB1, 0xF>(v);        // quad_perm [1,0,3,2]
-    v = dpp_add<0x4E, 0xF>(v);        // quad_perm [2,3,0,1]
-    v = dpp_add<0x141, 0xF>(v);       // row_half_mirror
-    v = dpp_add<0x140, 0xF>(v);       // row_mirror
-    v = dpp_add<0x142, 0xA>(v);       // row_bcast:15 -> rows 1, 3
-    v = dpp_add<0x143, 0xC>(v);       // row_bcast:31 -> rows 2, 3
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // PER: values each thread keeps in registers (N <= 256 PER); the row is read once, and
@@ -65,9 +47,8 @@ __global__ __launch_bounds__(256) void rmsnorm_add_kernel(const float* x, const 
     }
 #pragma unroll
     for (int j = 0; j < PER; ++j) ss += (double)v[j] * (double)v[j];
-    // the lane sums are exact in f64; the wave tree adds them as two f32 halves (hi + lo)
-    const float hi = (float)ss, lo = (float)(ss - (double)hi);
-    const double ws = (double)wave_sum_f32(hi) + (double)wave_sum_f32(lo);
+    // the wave tree adds the lane sums as two f32 halves (hi + lo)
+    const double ws = wave_sum_ss(ss);
     if ((tid & 63) == 0) part[tid >> 6] = ws;
     __syncthreads();
     if (y) {
@@ -78,8 +59,7 @@ __global__ __launch_bounds__(256) void rmsnorm_add_kernel(const float* x, const 
             if (i < N) yr[i] = v[j];
         }
     }
-    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
-    const float r = (float)(1.0 / sqrt(tot / (double)N + (double)eps));
+    const float r = inv_rms(part, N, eps);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int64_t i = tid + 256 * j;

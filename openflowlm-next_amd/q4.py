@@ -706,15 +706,70 @@ def gemm_q8(w: PackedQ8, x, y: torch.Tensor | None = None, workspace: torch.Tens
     return y
 
 
+def _norm_w(norm_w, K: int, dev) -> tuple[torch.Tensor, int]:
+    if not isinstance(norm_w, torch.Tensor) or norm_w.numel() != K or norm_w.dtype not in (torch.float32,
+                                                                                            torch.bfloat16):
+        raise ValueError(f"norm_w must be a float32 or bfloat16 tensor of {K} values")
+    wt = norm_w.to(dev).contiguous()
+    return wt, Q4MI_BF16 if wt.dtype == torch.bfloat16 else Q4MI_F32
+
+
+def _norm_x(x, K: int, dev) -> torch.Tensor:
+    if not isinstance(x, torch.Tensor) or x.dtype != torch.float32 or x.device != dev or not x.is_contiguous():
+        raise TypeError(f"x must be the contiguous float32 residual stream on {dev}")
+    xt = x.view(-1, x.shape[-1])
+    if xt.shape[1] != K:
+        raise ValueError(f"x has K={xt.shape[1]}, W has K={K}")
+    return xt
+
+
+def gemm_q4_rmsnorm(w: PackedQ4, x: torch.Tensor, norm_w: torch.Tensor, eps: float = 1e-6,
+                    y: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Y = bf16(RMSNorm(x) * norm_w) @ W^T with the norm formed inside the GEMV from the f32
+    residual stream x [M, K] (1 <= M <= 16, K <= 16384): the bits of rmsnorm_add (bf16 out)
+    followed by gemm_q4, with no launch and no copy for the norm."""
+    dev = w.device
+    xt = _norm_x(x, w.k, dev)
+    M = xt.shape[0]
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q4_rmsnorm takes 1..16 tokens, got {M}")
+    wt, wd = _norm_w(norm_w, w.k, dev)
+    y = _buf(y, "y", torch.float32, (M, w.n), dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        check("q4_gemv_rmsnorm", lib.q4_gemv_rmsnorm(_ptr(w.data), _ptr(xt), _ptr(wt), wd, float(eps), _ptr(y),
+                                                     M, w.n, w.k, wp, wn, _stream(dev)))
+    return y
+
+
 def swiglu_q4(gate: PackedQ4, up: PackedQ4, x, out_dtype=torch.float32, h: torch.Tensor | None = None,
-              workspace: torch.Tensor | None = None) -> torch.Tensor:
+              workspace: torch.Tensor | None = None, norm_w: torch.Tensor | None = None,
+              eps: float = 1e-6) -> torch.Tensor:
     """h[M, F] = silu(X @ G^T) * (X @ U^T) for 1 <= M <= 16 tokens in one launch (two
     when K is split): the gate/up GEMVs with the silu_mul design fused as their
     epilogue (designs/silu_mul/silu_mul.cc). ``out_dtype`` float32 or bfloat16 (RNE),
-    the down projection's input."""
+    the down projection's input. With ``norm_w``, x is the f32 residual stream and
+    X = bf16(RMSNorm(x) * norm_w) is formed inside the kernel (rmsnorm_add's bits)."""
     if gate.n != up.n or gate.k != up.k or gate.device != up.device:
         raise ValueError(f"gate {gate.shape} and up {up.shape} must match")
     dev = gate.device
+    if norm_w is not None:
+        xt = _norm_x(x, gate.k, dev)
+        M = xt.shape[0]
+        if not 1 <= M <= 16:
+            raise ValueError(f"swiglu_q4 with a norm takes 1..16 tokens, got {M}")
+        wt, wd = _norm_w(norm_w, gate.k, dev)
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("out_dtype must be float32 or bfloat16")
+        h = _buf(h, "h", out_dtype, (M, gate.n), dev)
+        lib = _lib_handle()
+        with torch.cuda.device(dev):
+            wp, wn = _ws_arg(dev, lib.q4_gemv_swiglu_workspace_bytes(M, gate.n, gate.k), "swiglu", workspace)
+            check("q4_gemv_swiglu_rmsnorm", lib.q4_gemv_swiglu_rmsnorm(
+                _ptr(gate.data), _ptr(up.data), _ptr(xt), _ptr(wt), wd, float(eps), _ptr(h),
+                Q4MI_BF16 if out_dtype == torch.bfloat16 else Q4MI_F32, M, gate.n, gate.k, wp, wn, _stream(dev)))
+        return h
     xt = _acts(x, dev)
     if xt.dim() == 1:
         xt = xt.unsqueeze(0)

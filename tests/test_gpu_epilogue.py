@@ -181,3 +181,37 @@ def test_fused_ffn_block_end_to_end(gpu, pkg, oracle):
     _bf16_bars(hb.astype(np.float64), rh)
     ref = xres.astype(np.float64) + oracle.gemv_reference(db, hb).astype(np.float64)
     assert oracle.maxrel(xr.cpu().numpy(), ref) <= MAXREL
+
+
+@pytest.mark.parametrize("wdt", ["bf16", "f32"])
+@pytest.mark.parametrize("N,K,M", [(6144, 4096, 1), (4096, 4096, 3), (1024, 4096, 16), (512, 14336, 2), (256, 96, 5)])
+def test_gemv_with_its_rmsnorm_inside(gpu, pkg, oracle, N, K, M, wdt):
+    """q4_gemv_rmsnorm: the norm formed per tile inside the GEMV gives the bits of
+    q4_rmsnorm_add (bf16 out) followed by q4_gemv, on split and unsplit plans, 1..16 rows."""
+    say(f"gemv with its rmsnorm N={N} K={K} M={M} w={wdt}")
+    rng = np.random.default_rng(N + K + M)
+    w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(N, K, rng), gpu)
+    x = torch.from_numpy((rng.standard_normal((M, K)) * 3).astype(np.float32)).to(gpu)
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(gpu)
+    if wdt == "bf16":
+        nw = nw.to(torch.bfloat16)
+    _, xn = pkg.rmsnorm_add(x, nw, eps=1e-5)
+    ref = pkg.gemm_q4(w, xn)
+    y = pkg.gemm_q4_rmsnorm(w, x, nw, eps=1e-5)
+    assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("M", [1, 4, 9])
+def test_swiglu_with_its_rmsnorm_inside(gpu, pkg, oracle, M):
+    say(f"swiglu with its rmsnorm M={M}")
+    F, K = 14336, 4096
+    rng = np.random.default_rng(700 + M)
+    g = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(F, K, rng), gpu)
+    u = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(F, K, rng), gpu)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(gpu)
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    _, xn = pkg.rmsnorm_add(x, nw)
+    for dt in (torch.bfloat16, torch.float32):
+        ref = pkg.swiglu_q4(g, u, xn, out_dtype=dt)
+        h = pkg.swiglu_q4(g, u, x, out_dtype=dt, norm_w=nw)
+        assert torch.equal(h, ref)
