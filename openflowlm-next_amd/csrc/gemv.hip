@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // NORM: X = bf16(RMSNorm(x) * nw) formed per tile from the f32 row x (every workgroup
 // first computes the rows' 1/rms exactly as q4_rmsnorm_add does), so the norm needs no
 // launch and no bf16 copy of its own.
-template <int NTL, bool XF32, int WAVES, bool Q40 = false, bool NORM = false>
+template <int NTL, bool XF32, int WAVES, bool Q40 = false, bool NORM = false, bool STREAM = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     __shared__ float red[WAVES][4][NTL][64];
     __shared__ float rrow[NORM ? 4 * NTL : 1];
@@ -74,8 +74,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
-    gemv_rows<NTL, XF32, DenseRows, WAVES, Q40, NORM>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc,
-                                                       NormIn{P.nw, P.nw_bf16, rrow});
+    if constexpr (STREAM) {
+        const NormIn nrm{P.nw, P.nw_bf16, rrow};
+        if constexpr (NORM) {
+            if (P.nw_bf16)
+                gemv_rows_stream<NTL, false, DenseRows, WAVES, Q40, 1, 4>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0,
+                                                                          kb1, acc, nrm);
+            else
+                gemv_rows_stream<NTL, false, DenseRows, WAVES, Q40, 2, 3>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0,
+                                                                          kb1, acc, nrm);
+        } else {
+            gemv_rows_stream<NTL, XF32, DenseRows, WAVES, Q40, 0, 4>(P.packed, P.x, DenseRows{P.M}, P.K, g,
+                                                                                kb0, kb1, acc);
+        }
+    } else {
+        gemv_rows<NTL, XF32, DenseRows, WAVES, Q40, NORM>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc,
+                                                           NormIn{P.nw, P.nw_bf16, rrow});
+    }
     if (S == 1) gemv_finish<NTL, WAVES>(acc, red, P.M, P.y, P.N, g, P.res);
     else gemv_finish<NTL, WAVES>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
@@ -381,16 +396,33 @@ void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, cons
     else hipLaunchKernelGGL((gemv_pair_kernel<NTL, false>), grid, dim3(256), 0, st, P, lo);
 }
 
-template <int NTL, int WAVES, bool Q40>
-void launch_gemv_w(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+// Q4MI_GEMV_STREAM=0 selects the batched loop (gemv_rows) instead of the rolling
+// pipeline (gemv_rows_stream), for experiments.
+bool gemv_stream() {
+    static const bool on = [] {
+        const char* e = getenv("Q4MI_GEMV_STREAM");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+template <int NTL, int WAVES, bool Q40, bool STREAM>
+void launch_gemv_ws(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
     if constexpr (!Q40) {
         if (P.nw) {
-            hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, false, true>), grid, dim3(64 * WAVES), 0, st, P);
+            hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, false, true, STREAM>), grid, dim3(64 * WAVES), 0, st,
+                               P);
             return;
         }
     }
-    if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, WAVES, Q40>), grid, dim3(64 * WAVES), 0, st, P);
-    else hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, Q40>), grid, dim3(64 * WAVES), 0, st, P);
+    if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, WAVES, Q40, false, STREAM>), grid, dim3(64 * WAVES), 0, st, P);
+    else hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, Q40, false, STREAM>), grid, dim3(64 * WAVES), 0, st, P);
+}
+
+template <int NTL, int WAVES, bool Q40>
+void launch_gemv_w(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if (gemv_stream()) launch_gemv_ws<NTL, WAVES, Q40, true>(xf32, grid, st, P);
+    else launch_gemv_ws<NTL, WAVES, Q40, false>(xf32, grid, st, P);
 }
 
 template <int NTL, bool Q40 = false>

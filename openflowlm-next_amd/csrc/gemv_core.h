@@ -26,6 +26,8 @@
 // kernels, whose workgroups stream short row-group spans and gain most from it).
 #pragma once
 
+#include <type_traits>
+
 #include "norm_core.h"
 #include "q4mi_device.h"
 
@@ -562,6 +564,161 @@ __device__ __forceinline__ void gemv_rows_pipe(const uint8_t* const (&gbase)[NG]
 #pragma unroll
         for (int h = 0; h < XL; ++h) pipe_landed(xr[u][h]);
     }
+}
+
+// f(std::integral_constant<int, I>{}) for I = B .. E - 1, so f can use I as a constant.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// One tile's arithmetic (gemv_rows' per-tile body): codes c, scale words s (mx: d<<16 | m
+// per row sub-tile; mx0: four bf16 d in s[0..1]), activation fragment xh (+ xl for f32 x).
+template <int NTL, bool XF32, bool Q40>
+__device__ __forceinline__ void tile_math(u32x4 c, u32x4 s, bf16x8 xh, bf16x8 xl, CodeConsts kc,
+                                          float (&acc)[4][NTL]) {
+    const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ns = mfma_bf16(xh, neg128, zero4);
+    if constexpr (XF32) ns = mfma_bf16(xl, neg128, ns);
+    f32x4 p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const bf16x8 b = codes_to_bf16(c[r], kc);
+        p[r] = mfma_bf16(xh, b, ns);
+        if constexpr (XF32) p[r] = mfma_bf16(xl, b, p[r]);
+    }
+    float sx[NTL];
+#pragma unroll
+    for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float d, m;
+        if constexpr (Q40) {
+            d = bf16_hi_to_f32(r & 1 ? s[r >> 1] : s[r >> 1] << 16);
+            m = -8.0f * d;
+        } else {
+            d = bf16_hi_to_f32(s[r]);
+            m = bf16_lo_to_f32(s[r]);
+        }
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) {
+            acc[r][j] = __builtin_fmaf(d, p[r][j], acc[r][j]);
+            acc[r][j] = __builtin_fmaf(m, sx[j], acc[r][j]);
+        }
+    }
+}
+
+// gemv_rows as a rolling pipeline with explicit waits: a wave issues its first UNR K
+// positions (codes, scales and activation fragment; NW: the f32 row and the norm weight,
+// bf16 (NW 1) or f32 (NW 2)), then per position b waits for "all but the positions issued
+// after b", runs the tile and, while b + UNR lies before the last chunk of UNR positions,
+// issues b + UNR into b's registers. Every issue is unconditional (an asm load issued under
+// a branch merges with the slot's old value, and the register allocator may then copy the
+// asm output before its wait): the last chunk's positions past the wave's count re-load its
+// last tile (at most UNR - 1 of them, cache hits) and are not accumulated. Positions are
+// visited in the same order as gemv_rows, with the same per-tile arithmetic, so the sums are
+// bit-identical to it.
+template <int NTL, bool XF32, class Rows, int WAVES, bool Q40, int NW, int UNR>
+__device__ __forceinline__ void gemv_rows_stream(const uint8_t* __restrict__ packed, const void* __restrict__ x,
+                                                 Rows rows, int64_t K, int64_t g, int kb0, int kb1,
+                                                 float (&acc)[4][NTL], NormIn nrm = {}) {
+    constexpr int TB = Q40 ? kQ0TileBytes : kTileBytes;
+    constexpr int XL = NW == 0 ? (XF32 ? 2 : 1) : (NW == 1 ? 3 : 4);   // activation-side loads
+    constexpr int L = 2 + XL;                                          // loads per K position
+    static_assert((UNR - 1) * L <= 63, "vmcnt holds 6 bits");
+    static_assert(NW == 0 || !XF32, "a normalised row feeds the MFMA as one bf16 fragment");
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kb0 = __builtin_amdgcn_readfirstlane(kb0);
+    kb1 = __builtin_amdgcn_readfirstlane(kb1);
+    const int first = kb0 + wave;
+    if (first >= kb1) return;
+    const int cnt = (kb1 - first + WAVES - 1) / WAVES;
+    const int i16 = lane & 15, kg = lane >> 4;
+    const uint8_t* gbase = packed + g * (K >> 5) * TB;
+    // mx0: the 16 aligned bytes holding this lane's 8 scale bytes and its neighbour's (an asm
+    // load into a register pair drew compiler copies ahead of its wait)
+    const uint32_t coff = lane * 16, soff = kCodeBytes + (Q40 ? (i16 & ~1) * 8 : i16 * 16);
+    const bool odd = Q40 && (i16 & 1);
+    const CodeConsts kc = code_consts();
+    const int64_t xrow = rows(token_of_row(i16));
+    constexpr int64_t es = (XF32 || NW) ? 4 : 2;                       // activation element bytes
+    const uint8_t* xp = (const uint8_t*)x + (xrow * K + kg * 8) * es;
+    constexpr int64_t ws = NW == 1 ? 2 : 4;                            // norm weight element bytes
+    const uint8_t* wp = NW ? (const uint8_t*)nrm.w + kg * 8 * ws : nullptr;
+    const float rr = NW ? nrm.r[xrow] : 0.f;
+    u32x4 c[UNR], s[UNR], xr[UNR][XL];
+    auto issue = [&](int b, int slot) {
+        const int t = first + WAVES * min(b, cnt - 1);
+        const uint32_t toff = (uint32_t)t * TB;
+        pipe_load_w(c[slot], gbase, toff + coff);
+        pipe_load_w(s[slot], gbase, toff + soff);
+        const uint8_t* xa = xp + (int64_t)t * 32 * es;
+        pipe_load_x(xr[slot][0], xa);
+        if constexpr (XF32 || NW) pipe_load_x(xr[slot][1], xa + 16);
+        if constexpr (NW) {
+            const uint8_t* wa = wp + (int64_t)t * 32 * ws;
+            pipe_load_x(xr[slot][2], wa);
+            if constexpr (NW == 2) pipe_load_x(xr[slot][3], wa + 16);
+        }
+    };
+    auto land = [&](int slot) {
+        pipe_landed(c[slot]);
+        pipe_landed(s[slot]);
+#pragma unroll
+        for (int h = 0; h < XL; ++h) pipe_landed(xr[slot][h]);
+    };
+    auto run = [&](int u) {
+        bf16x8 xh, xl;
+        if constexpr (NW) {
+            float wv[8];
+            if constexpr (NW == 1) {
+                norm_w_of_bf16(xr[u][2], wv);
+            } else {
+                const f32x4 w0 = __builtin_bit_cast(f32x4, xr[u][2]), w1 = __builtin_bit_cast(f32x4, xr[u][3]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wv[e] = w0[e], wv[e + 4] = w1[e];
+            }
+            xh = norm_bf16x8_of(__builtin_bit_cast(f32x4, xr[u][0]), __builtin_bit_cast(f32x4, xr[u][1]), wv, rr);
+        } else if constexpr (XF32) {
+            const f32x4 a = __builtin_bit_cast(f32x4, xr[u][0]), bb = __builtin_bit_cast(f32x4, xr[u][1]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const __bf16 ha = (__bf16)a[e], hb = (__bf16)bb[e];
+                xh[e] = ha;
+                xh[e + 4] = hb;
+                xl[e] = (__bf16)(a[e] - (float)ha);
+                xl[e + 4] = (__bf16)(bb[e] - (float)hb);
+            }
+        } else {
+            xh = __builtin_bit_cast(bf16x8, xr[u][0]);
+        }
+        u32x4 sw = s[u];
+        if constexpr (Q40) sw = odd ? u32x4{sw[2], sw[3], 0u, 0u} : u32x4{sw[0], sw[1], 0u, 0u};
+        tile_math<NTL, XF32, Q40>(c[u], sw, xh, xl, kc, acc);
+    };
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) issue(u, u);
+    int b0 = 0;
+    for (; b0 + UNR < cnt; b0 += UNR) {
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            __builtin_amdgcn_s_waitcnt(pipe_wait_imm((UNR - 1) * L));
+            land(u);
+            run(u);
+            issue(b0 + u + UNR, u);
+        }
+    }
+    static_for<0, UNR>([&](auto U) {      // the last chunk: nothing more to issue
+        constexpr int u = decltype(U)::value;
+        __builtin_amdgcn_s_waitcnt(pipe_wait_imm((UNR - 1 - u) * L));
+        land(u);
+        if (b0 + u < cnt) run(u);
+    });
 }
 
 // Sum the WAVES waves' accumulators through LDS. Afterwards thread t < 256 owns

@@ -68,20 +68,9 @@ __device__ __forceinline__ void rms_inv_rows(const float* __restrict__ x, int M,
     __syncthreads();
 }
 
-// The normalised bf16 of 8 consecutive activations: ((x * r) * w) rounded to bf16.
-__device__ __forceinline__ bf16x8 norm_bf16x8(const float* __restrict__ x, const void* __restrict__ w, int w_bf16,
-                                              float r) {
-    const f32x4 a = load_global<f32x4>(x), b = load_global<f32x4>(x + 4);
-    float wv[8];
-    if (w_bf16) {
-        const u32x4 ww = load_global<u32x4>(w);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wv[2 * e] = bf16_lo_to_f32(ww[e]), wv[2 * e + 1] = bf16_hi_to_f32(ww[e]);
-    } else {
-        const f32x4 c = load_global<f32x4>(w), d = load_global<f32x4>((const float*)w + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wv[e] = c[e], wv[e + 4] = d[e];
-    }
+// The normalised bf16 of 8 consecutive activations a[0..3], b[0..3] with weights wv:
+// ((x * r) * w) rounded to bf16.
+__device__ __forceinline__ bf16x8 norm_bf16x8_of(f32x4 a, f32x4 b, const float (&wv)[8], float r) {
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -89,6 +78,27 @@ __device__ __forceinline__ bf16x8 norm_bf16x8(const float* __restrict__ x, const
         o[e] = f32_to_bf16_rne(v0 * r * wv[2 * e]) | (f32_to_bf16_rne(v1 * r * wv[2 * e + 1]) << 16);
     }
     return __builtin_bit_cast(bf16x8, o);
+}
+
+// 8 bf16 norm weights (one 16-byte word) as f32.
+__device__ __forceinline__ void norm_w_of_bf16(u32x4 ww, float (&wv)[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[2 * e] = bf16_lo_to_f32(ww[e]), wv[2 * e + 1] = bf16_hi_to_f32(ww[e]);
+}
+
+// The normalised bf16 of 8 consecutive activations: ((x * r) * w) rounded to bf16.
+__device__ __forceinline__ bf16x8 norm_bf16x8(const float* __restrict__ x, const void* __restrict__ w, int w_bf16,
+                                              float r) {
+    const f32x4 a = load_global<f32x4>(x), b = load_global<f32x4>(x + 4);
+    float wv[8];
+    if (w_bf16) {
+        norm_w_of_bf16(load_global<u32x4>(w), wv);
+    } else {
+        const f32x4 c = load_global<f32x4>(w), d = load_global<f32x4>((const float*)w + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[e] = c[e], wv[e + 4] = d[e];
+    }
+    return norm_bf16x8_of(a, b, wv, r);
 }
 
 }  // namespace q4mi

@@ -147,6 +147,34 @@ def test_moe_pipelined_loops_wait_for_every_asm_load(tmp_path):
         assert checked >= 5, f"{k}: no pipelined K loop found"
 
 
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
+    """The dense GEMV streams through gemv_rows_stream (inline-asm loads, a runtime-chosen
+    explicit wait per K position): in every instance's K loop each load's registers are
+    touched only after a wait that covers it."""
+    src = SRC.parent / "gemv.hip"
+    out = tmp_path / "gemv.s"
+    cmd = ["hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{ROOT / 'include'}", f"-I{SRC.parent}", "--cuda-device-only", "-S",
+           str(src), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=900)
+    text = out.read_text().splitlines()
+    kernels = [l.split(":")[0] for l in text
+               if re.match(r"_ZN12_GLOBAL__N_111gemv_kernelILi\dELb\dELi\d+ELb\dELb\dELb1EE\w*:", l)]
+    assert len(kernels) == 4 * 3 * (2 + 2 + 1)     # NTL x waves x (f32 / bf16 x, mx0 f32 / bf16 x, norm)
+    for k in kernels:
+        start = next(i for i, l in enumerate(text) if l.startswith(k + ":"))
+        stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
+        checked = 0
+        for body in inner_loops(text[start:stop]):
+            if sum(1 for l in body if re.match(r"\s*global_load_dwordx4 .* nt$", l)) < 6:
+                continue                        # the norm prelude: compiler-tracked loads
+            n, bad = early_uses_in(body)
+            assert not bad, f"{k}: registers used before their load's wait: {bad[:3]}"
+            checked += n
+        assert checked >= 9, f"{k}: no pipelined K loop found"
+
+
 def test_checker_flags_an_early_use():
     """Plant the mistake: a use of the loaded registers before any covering wait."""
     asm = [".LBB0_1: ; Loop Header: Depth=1",
