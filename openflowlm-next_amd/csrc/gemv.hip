@@ -10,6 +10,7 @@
 // invalidate the L2 of every XCD -- far slower than the extra launch.)
 #include <stdlib.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "gemv_core.h"
@@ -69,30 +70,31 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     const int s = (int)(item % S);
     const int KB = (int)(P.K >> 5);
     const int kb0 = (int)((int64_t)s * KB / S), kb1 = (int)((int64_t)(s + 1) * KB / S);
-    float acc[4][NTL];
+    float acc[1][4][NTL];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
+        for (int j = 0; j < NTL; ++j) acc[0][r][j] = 0.f;
     if constexpr (STREAM) {
+        // K positions in flight: 4, or 3 where 16 waves (128 VGPRs each) hold 3-4 accumulator sets
+        constexpr int kUnr = WAVES == 16 && NTL >= 3 ? 3 : 4;
+        const uint8_t* const gb[1] = {P.packed + g * KB * (Q40 ? kQ0TileBytes : kTileBytes)};
         const NormIn nrm{P.nw, P.nw_bf16, rrow};
         if constexpr (NORM) {
             if (P.nw_bf16)
-                gemv_rows_stream<NTL, false, DenseRows, WAVES, Q40, 1, 4>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0,
-                                                                          kb1, acc, nrm);
+                gemv_rows_stream<NTL, false, 1, kUnr, WAVES, Q40, 1>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc,
+                                                                     nrm);
             else
-                gemv_rows_stream<NTL, false, DenseRows, WAVES, Q40, 2, 3>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0,
-                                                                          kb1, acc, nrm);
+                gemv_rows_stream<NTL, false, 1, 3, WAVES, Q40, 2>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc, nrm);
         } else {
-            gemv_rows_stream<NTL, XF32, DenseRows, WAVES, Q40, 0, 4>(P.packed, P.x, DenseRows{P.M}, P.K, g,
-                                                                                kb0, kb1, acc);
+            gemv_rows_stream<NTL, XF32, 1, kUnr, WAVES, Q40, 0>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc);
         }
     } else {
-        gemv_rows<NTL, XF32, DenseRows, WAVES, Q40, NORM>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc,
+        gemv_rows<NTL, XF32, DenseRows, WAVES, Q40, NORM>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc[0],
                                                            NormIn{P.nw, P.nw_bf16, rrow});
     }
-    if (S == 1) gemv_finish<NTL, WAVES>(acc, red, P.M, P.y, P.N, g, P.res);
-    else gemv_finish<NTL, WAVES>(acc, red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
+    if (S == 1) gemv_finish<NTL, WAVES>(acc[0], red, P.M, P.y, P.N, g, P.res);
+    else gemv_finish<NTL, WAVES>(acc[0], red, P.M, P.part + (int64_t)s * P.M * P.N, P.N, g);
 }
 
 // gemv_kernel for 17..24 tokens: two 16-token blocks (gemv_rows_tb2) over the same work
@@ -220,9 +222,9 @@ __device__ __forceinline__ void store_h(void* h, bool bf16, int64_t i, float v) 
     else ((float*)h)[i] = v;
 }
 
-template <int NTL, bool XF32, bool NORM = false>
-__global__ __launch_bounds__(256) void gemv_swiglu_kernel(SwigluParams P) {
-    __shared__ float red[kWaves][4][NTL][64];
+template <int NTL, bool XF32, bool NORM = false, int WAVES = kWaves, bool STREAM = false>
+__global__ __launch_bounds__(64 * WAVES) void gemv_swiglu_kernel(SwigluParams P) {
+    __shared__ float red[WAVES][4][NTL][64];
     __shared__ float rrow[NORM ? 4 * NTL : 1];
     if constexpr (NORM) rms_inv_rows<4 * NTL>((const float*)P.x, P.M, P.K, P.eps, rrow);
     const int64_t item = blockIdx.x;
@@ -239,13 +241,27 @@ __global__ __launch_bounds__(256) void gemv_swiglu_kernel(SwigluParams P) {
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int j = 0; j < NTL; ++j) acc[i][r][j] = 0.f;
-    gemv_rows_multi<NTL, XF32, 2, 4, kWaves, NORM>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc,
-                                                  NormIn{P.nw, P.nw_bf16, rrow});
+    const NormIn nrm{P.nw, P.nw_bf16, rrow};
+    constexpr int kUnr = NTL >= 3 ? 3 : 4;   // K positions in flight (two tiles each)
+    if constexpr (STREAM) {
+        if constexpr (NORM) {
+            if (P.nw_bf16)
+                gemv_rows_stream<NTL, false, 2, kUnr, WAVES, false, 1>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc,
+                                                                       nrm);
+            else
+                gemv_rows_stream<NTL, false, 2, 2, WAVES, false, 2>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc, nrm);
+        } else {
+            gemv_rows_stream<NTL, XF32, 2, kUnr, WAVES, false, 0>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc);
+        }
+    } else {
+        gemv_rows_multi<NTL, XF32, 2, 4, WAVES, NORM>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc, nrm);
+    }
     float vg[NTL], vu[NTL];
-    wave_sum<NTL>(acc[0], red, vg);
+    wave_sum<NTL, WAVES>(acc[0], red, vg);
     __syncthreads();
-    wave_sum<NTL>(acc[1], red, vu);
+    wave_sum<NTL, WAVES>(acc[1], red, vu);
     const int tid = threadIdx.x, lane = tid & 63;
+    if (tid >= 256) return;               // threads 0..255 own the row group's 64 rows
     const int64_t f = g * 64 + (tid >> 6) * 16 + (lane & 15);
 #pragma unroll
     for (int j = 0; j < NTL; ++j) {
@@ -369,6 +385,12 @@ int q4k_splits(int64_t N, int64_t K) {
     return (int)per_wave;
 }
 
+// The SwiGLU kernel's plan. On the rolling pipeline (the default) it is the plain GEMV's
+// plan for the 2F rows it streams (gate and up row groups side by side per work item), at
+// most 8 waves; on the batched loop, swiglu_splits with 4 waves.
+bool gemv_stream();
+GemvPlan swiglu_plan(int64_t F, int64_t K);
+
 // The SwiGLU kernel streams two row groups per work item, so it takes half the splits
 // a plain GEMV of F rows would (measured on Llama-3-8B's 14336 x 4096 pair: 2 splits
 // 1.10 ms per 32 layers, 5 splits 1.15, 3 splits 1.14, none 1.22).
@@ -377,23 +399,17 @@ int swiglu_splits(int64_t F, int64_t K) {
     return s < 1 ? 1 : s;
 }
 
+GemvPlan swiglu_plan(int64_t F, int64_t K) {
+    if (!gemv_stream()) return {swiglu_splits(F, K), 4};
+    GemvPlan p = plan_gemv(2 * F, K);
+    p.waves = std::min(p.waves, 8);   // two row groups per position: 16 waves would spill
+    return p;
+}
+
 size_t workspace_for(int M, int64_t N, int64_t K, int S) {
     (void)K;
     if (S <= 1) return 0;
     return (size_t)S * M * N * sizeof(float);
-}
-
-template <int NTL>
-void launch_swiglu(bool xf32, dim3 grid, hipStream_t st, const SwigluParams& P) {
-    if (P.nw) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false, true>), grid, dim3(256), 0, st, P);
-    else if (xf32) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, true>), grid, dim3(256), 0, st, P);
-    else hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false>), grid, dim3(256), 0, st, P);
-}
-
-template <int NTL>
-void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, const uint8_t* lo) {
-    if (xf32) hipLaunchKernelGGL((gemv_pair_kernel<NTL, true>), grid, dim3(256), 0, st, P, lo);
-    else hipLaunchKernelGGL((gemv_pair_kernel<NTL, false>), grid, dim3(256), 0, st, P, lo);
 }
 
 // Q4MI_GEMV_STREAM=0 selects the batched loop (gemv_rows) instead of the rolling
@@ -404,6 +420,27 @@ bool gemv_stream() {
         return !(e && e[0] == '0');
     }();
     return on;
+}
+
+template <int NTL, int WAVES, bool STREAM>
+void launch_swiglu_ws(bool xf32, dim3 grid, hipStream_t st, const SwigluParams& P) {
+    const dim3 block(64 * WAVES);
+    if (P.nw) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false, true, WAVES, STREAM>), grid, block, 0, st, P);
+    else if (xf32) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, true, false, WAVES, STREAM>), grid, block, 0, st, P);
+    else hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false, false, WAVES, STREAM>), grid, block, 0, st, P);
+}
+
+template <int NTL>
+void launch_swiglu(bool xf32, bool stream, int waves, dim3 grid, hipStream_t st, const SwigluParams& P) {
+    if (!stream) launch_swiglu_ws<NTL, 4, false>(xf32, grid, st, P);
+    else if (waves >= 8) launch_swiglu_ws<NTL, 8, true>(xf32, grid, st, P);
+    else launch_swiglu_ws<NTL, 4, true>(xf32, grid, st, P);
+}
+
+template <int NTL>
+void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, const uint8_t* lo) {
+    if (xf32) hipLaunchKernelGGL((gemv_pair_kernel<NTL, true>), grid, dim3(256), 0, st, P, lo);
+    else hipLaunchKernelGGL((gemv_pair_kernel<NTL, false>), grid, dim3(256), 0, st, P, lo);
 }
 
 template <int NTL, int WAVES, bool Q40, bool STREAM>
@@ -646,7 +683,7 @@ extern "C" int q4_gemv_rmsnorm(const uint8_t* packed, const float* x, const void
 
 extern "C" size_t q4_gemv_swiglu_workspace_bytes(int M, int64_t F, int64_t K) {
     if (M < 1 || M > 16 || F <= 0 || K <= 0 || F % 64 || K % 32) return 0;
-    const int S = swiglu_splits(F, K);
+    const int S = std::max(swiglu_splits(F, K), swiglu_plan(F, K).S);   // either loop's plan
     return S > 1 ? (size_t)S * M * 2 * F * sizeof(float) : 0;
 }
 
@@ -661,7 +698,8 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     if (!gate || !up || !x || !h) return Q4MI_E_ARG;
     if (misaligned16(gate) || misaligned16(up) || misaligned16(x) || misaligned16(workspace)) return Q4MI_E_ARG;
     if (((uintptr_t)h & (h_dtype == Q4MI_BF16 ? 1 : 3)) != 0) return Q4MI_E_ARG;
-    const int S = swiglu_splits(F, K);
+    const GemvPlan plan = swiglu_plan(F, K);
+    const int S = plan.S;
     SwigluParams P{};
     P.gate = gate;
     P.up = up;
@@ -682,11 +720,12 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     const dim3 grid((unsigned)((F / 64) * S));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
+    const bool sm = gemv_stream();
     switch ((M + 3) / 4) {
-        case 1: launch_swiglu<1>(xf32, grid, st, P); break;
-        case 2: launch_swiglu<2>(xf32, grid, st, P); break;
-        case 3: launch_swiglu<3>(xf32, grid, st, P); break;
-        default: launch_swiglu<4>(xf32, grid, st, P); break;
+        case 1: launch_swiglu<1>(xf32, sm, plan.waves, grid, st, P); break;
+        case 2: launch_swiglu<2>(xf32, sm, plan.waves, grid, st, P); break;
+        case 3: launch_swiglu<3>(xf32, sm, plan.waves, grid, st, P); break;
+        default: launch_swiglu<4>(xf32, sm, plan.waves, grid, st, P); break;
     }
     if (S > 1) {
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;

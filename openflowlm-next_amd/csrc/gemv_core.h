@@ -575,60 +575,66 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// One tile's arithmetic (gemv_rows' per-tile body): codes c, scale words s (mx: d<<16 | m
-// per row sub-tile; mx0: four bf16 d in s[0..1]), activation fragment xh (+ xl for f32 x).
-template <int NTL, bool XF32, bool Q40>
-__device__ __forceinline__ void tile_math(u32x4 c, u32x4 s, bf16x8 xh, bf16x8 xl, CodeConsts kc,
-                                          float (&acc)[4][NTL]) {
+// One K position's arithmetic over NG row groups (gemv_rows' per-tile body; multi_tile's
+// for NG > 1): codes c[i], scale words s[i] (mx: d<<16 | m per row sub-tile; mx0: four
+// bf16 d in s[i][0..1]), activation fragment xh (+ xl for f32 x) shared by the groups.
+template <int NTL, bool XF32, bool Q40, int NG>
+__device__ __forceinline__ void tile_math(const u32x4 (&c)[NG], const u32x4 (&s)[NG], bf16x8 xh, bf16x8 xl,
+                                          CodeConsts kc, float (&acc)[NG][4][NTL]) {
     const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     f32x4 ns = mfma_bf16(xh, neg128, zero4);
     if constexpr (XF32) ns = mfma_bf16(xl, neg128, ns);
-    f32x4 p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const bf16x8 b = codes_to_bf16(c[r], kc);
-        p[r] = mfma_bf16(xh, b, ns);
-        if constexpr (XF32) p[r] = mfma_bf16(xl, b, p[r]);
-    }
     float sx[NTL];
 #pragma unroll
     for (int j = 0; j < NTL; ++j) sx[j] = ns[j] * (-1.0f / 128.0f);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        float d, m;
-        if constexpr (Q40) {
-            d = bf16_hi_to_f32(r & 1 ? s[r >> 1] : s[r >> 1] << 16);
-            m = -8.0f * d;
-        } else {
-            d = bf16_hi_to_f32(s[r]);
-            m = bf16_lo_to_f32(s[r]);
+    for (int i = 0; i < NG; ++i) {
+        f32x4 p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bf16x8 b = codes_to_bf16(c[i][r], kc);
+            p[r] = mfma_bf16(xh, b, ns);
+            if constexpr (XF32) p[r] = mfma_bf16(xl, b, p[r]);
         }
 #pragma unroll
-        for (int j = 0; j < NTL; ++j) {
-            acc[r][j] = __builtin_fmaf(d, p[r][j], acc[r][j]);
-            acc[r][j] = __builtin_fmaf(m, sx[j], acc[r][j]);
+        for (int r = 0; r < 4; ++r) {
+            float d, m;
+            if constexpr (Q40) {
+                d = bf16_hi_to_f32(r & 1 ? s[i][r >> 1] : s[i][r >> 1] << 16);
+                m = -8.0f * d;
+            } else {
+                d = bf16_hi_to_f32(s[i][r]);
+                m = bf16_lo_to_f32(s[i][r]);
+            }
+#pragma unroll
+            for (int j = 0; j < NTL; ++j) {
+                acc[i][r][j] = __builtin_fmaf(d, p[r][j], acc[i][r][j]);
+                acc[i][r][j] = __builtin_fmaf(m, sx[j], acc[i][r][j]);
+            }
         }
     }
 }
 
-// gemv_rows as a rolling pipeline with explicit waits: a wave issues its first UNR K
-// positions (codes, scales and activation fragment; NW: the f32 row and the norm weight,
-// bf16 (NW 1) or f32 (NW 2)), then per position b waits for "all but the positions issued
-// after b", runs the tile and, while b + UNR lies before the last chunk of UNR positions,
-// issues b + UNR into b's registers. Every issue is unconditional (an asm load issued under
-// a branch merges with the slot's old value, and the register allocator may then copy the
-// asm output before its wait): the last chunk's positions past the wave's count re-load its
-// last tile (at most UNR - 1 of them, cache hits) and are not accumulated. Positions are
-// visited in the same order as gemv_rows, with the same per-tile arithmetic, so the sums are
-// bit-identical to it.
-template <int NTL, bool XF32, class Rows, int WAVES, bool Q40, int NW, int UNR>
-__device__ __forceinline__ void gemv_rows_stream(const uint8_t* __restrict__ packed, const void* __restrict__ x,
-                                                 Rows rows, int64_t K, int64_t g, int kb0, int kb1,
-                                                 float (&acc)[4][NTL], NormIn nrm = {}) {
+// gemv_rows (NG = 1) and gemv_rows_multi (NG row groups with tile bases gbase[i], the same
+// K range and activations) as a rolling pipeline with explicit waits: a wave issues its
+// first UNR K positions (per group the codes and scales, and the activation fragment; NW:
+// the f32 row and the norm weight, bf16 (NW 1) or f32 (NW 2)), then per position b waits
+// for "all but the positions issued after b", runs the position and, while b + UNR lies
+// before the last chunk of UNR positions, issues b + UNR into b's registers. Every issue is
+// unconditional (an asm load issued under a branch merges with the slot's old value, and the
+// register allocator may then copy the asm output before its wait): the last chunk's
+// positions past the wave's count re-load its last tile (at most UNR - 1 of them, cache
+// hits) and are not accumulated. Positions are visited in the same order as the batched
+// loops, with the same arithmetic, so the sums are bit-identical to theirs for the same
+// waves and K range.
+template <int NTL, bool XF32, int NG, int UNR, int WAVES, bool Q40, int NW, class Rows>
+__device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[NG], const void* __restrict__ x,
+                                                 Rows rows, int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL],
+                                                 NormIn nrm = {}) {
     constexpr int TB = Q40 ? kQ0TileBytes : kTileBytes;
     constexpr int XL = NW == 0 ? (XF32 ? 2 : 1) : (NW == 1 ? 3 : 4);   // activation-side loads
-    constexpr int L = 2 + XL;                                          // loads per K position
+    constexpr int L = 2 * NG + XL;                                     // loads per K position
     static_assert((UNR - 1) * L <= 63, "vmcnt holds 6 bits");
     static_assert(NW == 0 || !XF32, "a normalised row feeds the MFMA as one bf16 fragment");
     const int lane = threadIdx.x & 63;
@@ -639,7 +645,6 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* __restrict__ pac
     if (first >= kb1) return;
     const int cnt = (kb1 - first + WAVES - 1) / WAVES;
     const int i16 = lane & 15, kg = lane >> 4;
-    const uint8_t* gbase = packed + g * (K >> 5) * TB;
     // mx0: the 16 aligned bytes holding this lane's 8 scale bytes and its neighbour's (an asm
     // load into a register pair drew compiler copies ahead of its wait)
     const uint32_t coff = lane * 16, soff = kCodeBytes + (Q40 ? (i16 & ~1) * 8 : i16 * 16);
@@ -651,12 +656,15 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* __restrict__ pac
     constexpr int64_t ws = NW == 1 ? 2 : 4;                            // norm weight element bytes
     const uint8_t* wp = NW ? (const uint8_t*)nrm.w + kg * 8 * ws : nullptr;
     const float rr = NW ? nrm.r[xrow] : 0.f;
-    u32x4 c[UNR], s[UNR], xr[UNR][XL];
+    u32x4 c[UNR][NG], s[UNR][NG], xr[UNR][XL];
     auto issue = [&](int b, int slot) {
         const int t = first + WAVES * min(b, cnt - 1);
         const uint32_t toff = (uint32_t)t * TB;
-        pipe_load_w(c[slot], gbase, toff + coff);
-        pipe_load_w(s[slot], gbase, toff + soff);
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            pipe_load_w(c[slot][i], gbase[i], toff + coff);
+            pipe_load_w(s[slot][i], gbase[i], toff + soff);
+        }
         const uint8_t* xa = xp + (int64_t)t * 32 * es;
         pipe_load_x(xr[slot][0], xa);
         if constexpr (XF32 || NW) pipe_load_x(xr[slot][1], xa + 16);
@@ -667,8 +675,11 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* __restrict__ pac
         }
     };
     auto land = [&](int slot) {
-        pipe_landed(c[slot]);
-        pipe_landed(s[slot]);
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            pipe_landed(c[slot][i]);
+            pipe_landed(s[slot][i]);
+        }
 #pragma unroll
         for (int h = 0; h < XL; ++h) pipe_landed(xr[slot][h]);
     };
@@ -697,9 +708,13 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* __restrict__ pac
         } else {
             xh = __builtin_bit_cast(bf16x8, xr[u][0]);
         }
-        u32x4 sw = s[u];
-        if constexpr (Q40) sw = odd ? u32x4{sw[2], sw[3], 0u, 0u} : u32x4{sw[0], sw[1], 0u, 0u};
-        tile_math<NTL, XF32, Q40>(c[u], sw, xh, xl, kc, acc);
+        u32x4 sw[NG];
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            sw[i] = s[u][i];
+            if constexpr (Q40) sw[i] = odd ? u32x4{sw[i][2], sw[i][3], 0u, 0u} : u32x4{sw[i][0], sw[i][1], 0u, 0u};
+        }
+        tile_math<NTL, XF32, Q40, NG>(c[u], sw, xh, xl, kc, acc);
     };
 #pragma unroll
     for (int u = 0; u < UNR; ++u) issue(u, u);

@@ -149,8 +149,8 @@ def test_moe_pipelined_loops_wait_for_every_asm_load(tmp_path):
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
 def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
-    """The dense GEMV streams through gemv_rows_stream (inline-asm loads, a runtime-chosen
-    explicit wait per K position): in every instance's K loop each load's registers are
+    """The dense GEMV and the SwiGLU pair stream through gemv_rows_stream (inline-asm loads,
+    an explicit wait per K position): in every instance's K loop each load's registers are
     touched only after a wait that covers it."""
     src = SRC.parent / "gemv.hip"
     out = tmp_path / "gemv.s"
@@ -159,9 +159,13 @@ def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
            str(src), "-o", str(out)]
     subprocess.run(cmd, check=True, capture_output=True, timeout=900)
     text = out.read_text().splitlines()
-    kernels = [l.split(":")[0] for l in text
-               if re.match(r"_ZN12_GLOBAL__N_111gemv_kernelILi\dELb\dELi\d+ELb\dELb\dELb1EE\w*:", l)]
-    assert len(kernels) == 4 * 3 * (2 + 2 + 1)     # NTL x waves x (f32 / bf16 x, mx0 f32 / bf16 x, norm)
+    dense = [l.split(":")[0] for l in text
+             if re.match(r"_ZN12_GLOBAL__N_111gemv_kernelILi\dELb\dELi\d+ELb\dELb\dELb1EE\w*:", l)]
+    assert len(dense) == 4 * 3 * (2 + 2 + 1)       # NTL x waves x (f32 / bf16 x, mx0 f32 / bf16 x, norm)
+    swiglu = [l.split(":")[0] for l in text
+              if re.match(r"_ZN12_GLOBAL__N_118gemv_swiglu_kernelILi\dELb\dELb\dELi\d+ELb1EE\w*:", l)]
+    assert len(swiglu) == 4 * 2 * 3                # NTL x waves x (f32 x, bf16 x, norm)
+    kernels = dense + swiglu
     for k in kernels:
         start = next(i for i, l in enumerate(text) if l.startswith(k + ":"))
         stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
