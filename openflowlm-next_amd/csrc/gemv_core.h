@@ -482,13 +482,23 @@ __device__ __forceinline__ void pipe_landed(u32x4& v) { asm volatile("" : "+v"(v
 
 constexpr int pipe_wait_imm(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// f(std::integral_constant<int, I>{}) for I = B .. E - 1, so f can use I as a constant.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 // gemv_rows_multi as a rolling pipeline with explicit waits: a wave keeps UNR K positions of
 // loads (NG tiles' codes and scales plus the activation fragment each) in flight at all
-// times. Its K positions are kb0 + wave + WAVES b, b = 0 .. cnt - 1; position b + UNR is
-// issued into the registers of position b as soon as b has been used, so the wait before
-// each position is always "all but the (UNR - 1) younger positions' loads". Positions past
-// cnt load the wave's last tile again (cache hits) and are not accumulated; the wave drains
-// them before it returns.
+// times. Its K positions are kb0 + wave + WAVES b, b = 0 .. cnt - 1; while b + UNR lies
+// before the last chunk of UNR positions, position b + UNR is issued into the registers of
+// position b as soon as b has been used, so the wait before each position is "all but the
+// (UNR - 1) younger positions' loads"; the last chunk waits down to zero. Positions of the
+// last chunk past cnt load the wave's last tile again (at most UNR - 1, cache hits) and
+// are not accumulated.
 template <int NTL, bool XF32, int NG, int UNR, int WAVES, class Rows>
 __device__ __forceinline__ void gemv_rows_pipe(const uint8_t* const (&gbase)[NG], const void* __restrict__ x, Rows rows,
                                                int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL]) {
@@ -520,59 +530,50 @@ __device__ __forceinline__ void gemv_rows_pipe(const uint8_t* const (&gbase)[NG]
 #pragma unroll
         for (int h = 0; h < XL; ++h) pipe_load_x(xr[slot][h], xa + 16 * h);
     };
+    auto land = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            pipe_landed(c[slot][i]);
+            pipe_landed(s[slot][i]);
+        }
+#pragma unroll
+        for (int h = 0; h < XL; ++h) pipe_landed(xr[slot][h]);
+    };
+    auto run = [&](int u) {
+        bf16x8 xh, xl;
+        if constexpr (XF32) {
+            const f32x4 a = __builtin_bit_cast(f32x4, xr[u][0]), bb = __builtin_bit_cast(f32x4, xr[u][1]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const __bf16 ha = (__bf16)a[e], hb = (__bf16)bb[e];
+                xh[e] = ha;
+                xh[e + 4] = hb;
+                xl[e] = (__bf16)(a[e] - (float)ha);
+                xl[e + 4] = (__bf16)(bb[e] - (float)hb);
+            }
+        } else {
+            xh = __builtin_bit_cast(bf16x8, xr[u][0]);
+        }
+        multi_tile<NTL, XF32, NG>(c[u], s[u], xh, xl, kc, acc);
+    };
 #pragma unroll
     for (int u = 0; u < UNR; ++u) issue(u, u);
-    for (int b0 = 0; b0 < cnt; b0 += UNR) {
+    int b0 = 0;
+    for (; b0 + UNR < cnt; b0 += UNR) {
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
             __builtin_amdgcn_s_waitcnt(pipe_wait_imm((UNR - 1) * L));
-#pragma unroll
-            for (int i = 0; i < NG; ++i) {
-                pipe_landed(c[u][i]);
-                pipe_landed(s[u][i]);
-            }
-#pragma unroll
-            for (int h = 0; h < XL; ++h) pipe_landed(xr[u][h]);
-            if (b0 + u < cnt) {
-                bf16x8 xh, xl;
-                if constexpr (XF32) {
-                    const f32x4 a = __builtin_bit_cast(f32x4, xr[u][0]), bb = __builtin_bit_cast(f32x4, xr[u][1]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const __bf16 ha = (__bf16)a[e], hb = (__bf16)bb[e];
-                        xh[e] = ha;
-                        xh[e + 4] = hb;
-                        xl[e] = (__bf16)(a[e] - (float)ha);
-                        xl[e + 4] = (__bf16)(bb[e] - (float)hb);
-                    }
-                } else {
-                    xh = __builtin_bit_cast(bf16x8, xr[u][0]);
-                }
-                multi_tile<NTL, XF32, NG>(c[u], s[u], xh, xl, kc, acc);
-            }
+            land(u);
+            run(u);
             issue(b0 + u + UNR, u);
         }
     }
-    __builtin_amdgcn_s_waitcnt(pipe_wait_imm(0));
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-#pragma unroll
-        for (int i = 0; i < NG; ++i) {
-            pipe_landed(c[u][i]);
-            pipe_landed(s[u][i]);
-        }
-#pragma unroll
-        for (int h = 0; h < XL; ++h) pipe_landed(xr[u][h]);
-    }
-}
-
-// f(std::integral_constant<int, I>{}) for I = B .. E - 1, so f can use I as a constant.
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
+    static_for<0, UNR>([&](auto U) {      // the last chunk: nothing more to issue
+        constexpr int u = decltype(U)::value;
+        __builtin_amdgcn_s_waitcnt(pipe_wait_imm((UNR - 1 - u) * L));
+        land(u);
+        if (b0 + u < cnt) run(u);
+    });
 }
 
 // One K position's arithmetic over NG row groups (gemv_rows' per-tile body; multi_tile's
