@@ -5,6 +5,8 @@
 // per-source flags): here that measured faster (the Llama-3-8B sweep at M = 1: 197.1 ->
 // 193.6 us for 8 layers), while the same flag on the single-matrix kernels of gemv.hip
 // measured slower (native Q4_K gate_up 14.9 -> 21.0 us).
+#include <stdlib.h>
+
 #include "gemv_core.h"
 #include "q4mi_internal.h"
 
@@ -12,7 +14,13 @@ using namespace q4mi;
 
 namespace {
 
-template <int NTL, bool XF32>
+// K positions in flight per wave on the rolling loop. Same-process A/B over the 225
+// Llama-3-8B matrices (graph-free back-to-back launches, bit-identical outputs), µs:
+//   M = 1: batched 685.8, depth 4 684.6, 6 698.8, 8 680.1
+//   M = 4: 741.0, 740.2, 753.0, 732.9;  M = 16: 1066.7, 1067.6, 1109.3, 1055.6
+constexpr int kGroupedUnr = 8;
+
+template <int NTL, bool XF32, bool STREAM>
 __global__ __launch_bounds__(256) void gemv_grouped_kernel(const q4_gemv_desc* __restrict__ descs, int count, int M) {
     __shared__ float red[kWaves][4][NTL][64];
     const int64_t item = blockIdx.x;
@@ -30,14 +38,41 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(const q4_gemv_desc* _
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[r][j] = 0.f;
-    gemv_rows<NTL, XF32>(D.packed, D.x, DenseRows{M}, D.K, g, 0, (int)(D.K >> 5), acc);
-    gemv_finish<NTL>(acc, red, M, D.y, D.N, g);
+    if constexpr (STREAM) {
+        float acc1[1][4][NTL];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < NTL; ++j) acc1[0][r][j] = 0.f;
+        const uint8_t* const gb[1] = {D.packed + g * (D.K >> 5) * kTileBytes};
+        gemv_rows_stream<NTL, XF32, 1, kGroupedUnr, kWaves, false, 0>(gb, D.x, DenseRows{M}, D.K, 0, (int)(D.K >> 5),
+                                                                      acc1);
+        gemv_finish<NTL>(acc1[0], red, M, D.y, D.N, g);
+    } else {
+        gemv_rows<NTL, XF32>(D.packed, D.x, DenseRows{M}, D.K, g, 0, (int)(D.K >> 5), acc);
+        gemv_finish<NTL>(acc, red, M, D.y, D.N, g);
+    }
+}
+
+// Q4MI_GROUPED_STREAM=0 keeps the batched loop (experiments).
+bool grouped_stream() {
+    static const bool on = [] {
+        const char* e = getenv("Q4MI_GROUPED_STREAM");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+template <int NTL, bool STREAM>
+void launch_grouped_s(bool xf32, dim3 grid, hipStream_t st, const q4_gemv_desc* d, int count, int M) {
+    if (xf32) hipLaunchKernelGGL((gemv_grouped_kernel<NTL, true, STREAM>), grid, dim3(256), 0, st, d, count, M);
+    else hipLaunchKernelGGL((gemv_grouped_kernel<NTL, false, STREAM>), grid, dim3(256), 0, st, d, count, M);
 }
 
 template <int NTL>
 void launch_grouped(bool xf32, dim3 grid, hipStream_t st, const q4_gemv_desc* d, int count, int M) {
-    if (xf32) hipLaunchKernelGGL((gemv_grouped_kernel<NTL, true>), grid, dim3(256), 0, st, d, count, M);
-    else hipLaunchKernelGGL((gemv_grouped_kernel<NTL, false>), grid, dim3(256), 0, st, d, count, M);
+    if (grouped_stream()) launch_grouped_s<NTL, true>(xf32, grid, st, d, count, M);
+    else launch_grouped_s<NTL, false>(xf32, grid, st, d, count, M);
 }
 
 }  // namespace

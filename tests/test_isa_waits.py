@@ -179,6 +179,34 @@ def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
         assert checked >= 9, f"{k}: no pipelined K loop found"
 
 
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+def test_grouped_stream_loops_wait_for_every_asm_load(tmp_path):
+    """The grouped GEMV (one launch over many matrices) streams through gemv_rows_stream,
+    built with its own per-source flags: every instance's K loop waits before each use."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("q4mi_build", ROOT / "openflowlm-next_amd" / "build.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    path = SRC.parent / "gemv_grouped.hip"
+    out = tmp_path / "grouped.s"
+    subprocess.run(["hipcc", *b.flags(path), "--cuda-device-only", "-S", str(path), "-o", str(out)], check=True,
+                   capture_output=True, timeout=600)
+    text = out.read_text().splitlines()
+    kernels = [l.split(":")[0] for l in text if re.match(r"_ZN12_GLOBAL__N_119gemv_grouped_kernelILi\dELb\dELb1EE\w*:", l)]
+    assert len(kernels) == 8                       # NTL x (f32 / bf16 x)
+    for k in kernels:
+        start = next(i for i, l in enumerate(text) if l.startswith(k + ":"))
+        stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
+        checked = 0
+        for body in inner_loops(text[start:stop]):
+            if sum(1 for l in body if re.match(r"\s*global_load_dwordx4 .* nt$", l)) < 6:
+                continue
+            n, bad = early_uses_in(body)
+            assert not bad, f"{k}: registers used before their load's wait: {bad[:3]}"
+            checked += n
+        assert checked >= 24, f"{k}: no pipelined K loop found"
+
+
 def test_checker_flags_an_early_use():
     """Plant the mistake: a use of the loaded registers before any covering wait."""
     asm = [".LBB0_1: ; Loop Header: Depth=1",
