@@ -169,8 +169,9 @@ def time_launches(torch, fn, steps: int, warmup: int):
 
 def graph_time(torch, fn, outputs, replays: int = 20, reset=None) -> float:
     """Capture fn() in a HIP graph, check one replay against the eager run
-    (bit for bit: every kernel here is deterministic), then time `replays`
-    replays with events. Returns mean ms per replay. `reset` restores the state
+    (bit for bit: every kernel here is deterministic), replay it untimed for
+    about 25 ms (clocks settle under load), then time `replays` replays with
+    events. Returns mean ms per replay. `reset` restores the state
     of an fn that updates its inputs in place (a residual stream) before the
     eager run and before the checked replay."""
     if reset:
@@ -198,11 +199,17 @@ def graph_time(torch, fn, outputs, replays: int = 20, reset=None) -> float:
     for o, e in zip(outputs, eager):
         if not torch.equal(o, e):
             raise RuntimeError("graph replay differs from the eager run")
-    for _ in range(2):
-        g.replay()
-    torch.cuda.synchronize()
+    # untimed replays until ~25 ms of load (at least 2): the clocks settle before the timing
     st = torch.cuda.current_stream()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    g.replay()
+    b.record(st)
+    torch.cuda.synchronize()
+    one = max(a.elapsed_time(b), 1e-3)
+    for _ in range(max(2, min(2000, int(25.0 / one)))):
+        g.replay()
+    torch.cuda.synchronize()
     a.record(st)
     for _ in range(replays):
         g.replay()
