@@ -76,8 +76,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[0][r][j] = 0.f;
     if constexpr (STREAM) {
-        // K positions in flight: 4, or 3 where 16 waves (128 VGPRs each) hold 3-4 accumulator sets
-        constexpr int kUnr = WAVES == 16 && NTL >= 3 ? 3 : 4;
+        // K positions in flight: 4, or 3 where 16 waves (128 VGPRs each) hold 3-4 accumulator
+        // sets or 2 with the f32 activation's two fragments (an in-flight register must not be
+        // spilled)
+        constexpr int kUnr = WAVES == 16 && (NTL >= 3 || (NTL == 2 && XF32)) ? 3 : 4;
         const uint8_t* const gb[1] = {P.packed + g * KB * (Q40 ? kQ0TileBytes : kTileBytes)};
         const NormIn nrm{P.nw, P.nw_bf16, rrow};
         if constexpr (NORM) {

@@ -166,7 +166,11 @@ def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
               if re.match(r"_ZN12_GLOBAL__N_118gemv_swiglu_kernelILi\dELb\dELb\dELi\d+ELb1EE\w*:", l)]
     assert len(swiglu) == 4 * 2 * 3                # NTL x waves x (f32 x, bf16 x, norm)
     kernels = dense + swiglu
+    meta = "\n".join(text)
     for k in kernels:
+        # a spilled register may be one whose asm load is still in flight
+        m = re.search(r"\.name:\s+" + re.escape(k) + r"\n.*?\.vgpr_spill_count:\s+(\d+)", meta, re.S)
+        assert m and int(m.group(1)) == 0, f"{k}: {m.group(1) if m else '?'} VGPRs spilled"
         start = next(i for i, l in enumerate(text) if l.startswith(k + ":"))
         stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
         checked = 0
