@@ -381,11 +381,41 @@ def extra_decode_step(torch, q4, model, acts, xhead):
             q4.gemm_q4(p["down"], h, y=xres, residual=xres, workspace=ws)
         q4.gemm_q4_rmsnorm(model.head, xres, nw, y=logits, workspace=ws)
 
+    xalt = torch.empty(1, H, device=dev)
+
+    def deferred(so, sd):
+        """The norms inside the GEMVs and the o / down K-split sums deferred into them: o and
+        down leave partial planes, the next norm GEMV adds them to the residual stream (written
+        to the other of two buffers) in its prelude; no reduce launches."""
+        po = torch.empty(so, 1, H, device=dev)
+        pd = torch.empty(sd, 1, H, device=dev)
+
+        def fn():
+            cur, nxt = xres, xalt
+            for i, p in enumerate(model.layers):
+                if i == 0:
+                    q4.gemm_q4_rmsnorm(p["qkv"], cur, nw, y=qkv, workspace=ws)
+                else:
+                    q4.gemm_q4_rmsnorm_acc(p["qkv"], cur, pd, nw, x_out=nxt, y=qkv, workspace=ws)
+                    cur, nxt = nxt, cur
+                q4.gemm_q4_partials(p["o"], attn[i], splits=so, part=po)
+                q4.swiglu_q4_acc(p["gate"], p["up"], cur, po, nw, out_dtype=torch.bfloat16, x_out=nxt, h=h,
+                                 workspace=ws)
+                cur, nxt = nxt, cur
+                q4.gemm_q4_partials(p["down"], h, splits=sd, part=pd)
+            q4.gemm_q4_rmsnorm_acc(model.head, cur, pd, nw, x_out=nxt, y=logits, workspace=ws)
+        return fn
+
+    l0 = model.layers[0]
+    so, sd = q4.gemv_split_count(l0["o"]), q4.gemv_split_count(l0["down"])
+
     def reset():
         xres.copy_(xres0)
     out = {"bytes": nbytes}
-    for name, fn in (("separate_norms", step), ("norms_in_gemv", step_fused)):
-        ms = graph_time(torch, fn, [logits, xres], replays=10, reset=reset)
+    variants = (("separate_norms", step), ("norms_in_gemv", step_fused),
+                (f"deferred_sums_o{so}_d{sd}", deferred(so, sd)), ("deferred_sums_o4_d4", deferred(4, 4)))
+    for name, fn in variants:
+        ms = graph_time(torch, fn, [logits, xres, xalt], replays=10, reset=reset)
         out[name] = {"ms": ms, "gbs": nbytes / ms / 1e6}
     reset()
     step()
@@ -393,6 +423,12 @@ def extra_decode_step(torch, q4, model, acts, xhead):
     reset()
     step_fused()
     out["same_logits"] = bool(torch.equal(a, logits))
+    reset()
+    variants[2][1]()
+    out["deferred_same_logits"] = bool(torch.equal(a, logits))
+    reset()
+    variants[3][1]()
+    out["deferred_o4_d4_maxrel"] = float(((logits - a).abs().max() / a.abs().max()).item())
     return out
 
 

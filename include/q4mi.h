@@ -319,6 +319,38 @@ int q4_gemv_swiglu_rmsnorm(const uint8_t* gate, const uint8_t* up, const float* 
                            int norm_w_dtype, float eps, void* h, int h_dtype, int M, int64_t F, int64_t K,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* The K-split reduction deferred into the next norm-fused GEMV (a decode step's o and down
+ * projections feed the residual stream that the next RMSNorm reads). In the reference the
+ * split GEMV's partials are summed by the kernel's own reduction (split_reduce in the
+ * gemv design, open_kernels/designs/gemv_q4/gemv_q4.py) and the residual add and norm
+ * follow as separate steps (model/replica.py:81, :144; designs/ln/ln.py:1-6); here the
+ * three become the prelude of the GEMV that consumes the norm. */
+
+/* The split count q4_gemv plans for an N x K matrix (1: unsplit; 0: invalid shape). */
+int q4_gemv_split_count(int64_t N, int64_t K);
+
+/* The partial sums of a K-split GEMV, left unreduced: part[s][M][N] (f32) is X . W^T over
+ * the s-th of S contiguous K ranges (1 <= S <= 16, S <= K / 32, 1 <= M <= 16). With S =
+ * q4_gemv_split_count(N, K) the planes added in split order are q4_gemv's Y bit for bit. */
+int q4_gemv_partials(const uint8_t* packed, const void* x, int x_dtype, float* part, int S, int M,
+                     int64_t N, int64_t K, void* stream);
+
+/* q4_gemv_rmsnorm of x = res + ((0 + part[0]) + part[1] + ...) (S planes of [M][K], in
+ * split order; S = 0: x = res; S = 1: res + part[0]), which is also stored to x_out [M][K]
+ * (the residual stream's next value: q4_gemv_residual's bits for the GEMV that made the
+ * planes). x_out must not overlap res or part. M = 1 with K <= 4096 reduces inside the
+ * GEMV's workgroups; other shapes add one reduce launch first. Workspace as q4_gemv. */
+int q4_gemv_rmsnorm_acc(const uint8_t* packed, const float* res, const float* part, int S,
+                        const void* norm_w, int norm_w_dtype, float eps, float* x_out, float* y, int M,
+                        int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+
+/* q4_gemv_swiglu_rmsnorm of the same x = res + partials, stored to x_out, as
+ * q4_gemv_rmsnorm_acc. */
+int q4_gemv_swiglu_rmsnorm_acc(const uint8_t* gate, const uint8_t* up, const float* res, const float* part,
+                               int S, const void* norm_w, int norm_w_dtype, float eps, float* x_out, void* h,
+                               int h_dtype, int M, int64_t F, int64_t K, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* The activation producer: per row m < M of N values,
  *   y = x + add (add may be NULL; y may be NULL, or x itself when N <= 16384),
  *   xn = (y * r) * w, r = 1 / sqrt(mean(y^2) + eps) with the sum in fp64,

@@ -63,6 +63,12 @@ SIGNATURES = {
     "q4_gemv_rmsnorm": (_i32, [_vp, _vp, _vp, _i32, C.c_float, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_gemv_swiglu_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i32, C.c_float, _vp, _i32, _i32, _i64, _i64, _vp, _sz,
                                       _vp]),
+    "q4_gemv_split_count": (_i32, [_i64, _i64]),
+    "q4_gemv_partials": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i64, _i64, _vp]),
+    "q4_gemv_rmsnorm_acc": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, C.c_float, _vp, _vp, _i32, _i64, _i64, _vp, _sz,
+                                   _vp]),
+    "q4_gemv_swiglu_rmsnorm_acc": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, C.c_float, _vp, _vp, _i32, _i32,
+                                          _i64, _i64, _vp, _sz, _vp]),
     "q4_gemv_swiglu_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemv_swiglu": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_rmsnorm_add": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i64, C.c_float, _vp]),

@@ -32,6 +32,9 @@ struct GemvParams {
     const void* nw;   // NORM kernels: the RMSNorm weight [K] (x is the f32 residual stream)
     int nw_bf16;
     float eps;
+    const float* acc_part;   // XN kernels: x = res (P.x) + the S planes of a split GEMV's partials
+    int acc_S;
+    float* x_out;            // XN kernels: that x, written by workgroup 0
 };
 
 
@@ -59,11 +62,20 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // NORM: X = bf16(RMSNorm(x) * nw) formed per tile from the f32 row x (every workgroup
 // first computes the rows' 1/rms exactly as q4_rmsnorm_add does), so the norm needs no
 // launch and no bf16 copy of its own.
-template <int NTL, bool XF32, int WAVES, bool Q40 = false, bool NORM = false, bool STREAM = false>
+// XN (NORM on the rolling loop, one row of K <= 256 kAccRowJ): x is res (P.x) plus a split
+// GEMV's partial-sum planes (P.acc_part, P.acc_S); each workgroup reduces them in
+// split_reduce's order, normalises the row into LDS once, and workgroup 0 writes x to
+// P.x_out, so the producer needs no reduce launch.
+constexpr int kXnElems = 256 * kAccRowJ;
+
+template <int NTL, bool XF32, int WAVES, bool Q40 = false, bool NORM = false, bool STREAM = false, bool XN = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
+    static_assert(!XN || (NORM && STREAM && NTL == 1 && !Q40), "XN: one row, norm, rolling loop");
     __shared__ float red[WAVES][4][NTL][64];
     __shared__ float rrow[NORM ? 4 * NTL : 1];
-    if constexpr (NORM) rms_inv_rows<4 * NTL>((const float*)P.x, P.M, P.K, P.eps, rrow);
+    __shared__ __attribute__((aligned(16))) __bf16 xs[XN ? kXnElems : 8];
+    __shared__ float xf[XN ? kXnElems : 1];
+    if constexpr (NORM && !XN) rms_inv_rows<4 * NTL>((const float*)P.x, P.M, P.K, P.eps, rrow);
     const int64_t item = blockIdx.x;
     const int S = P.S;
     const int64_t g = item / S;
@@ -75,7 +87,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int j = 0; j < NTL; ++j) acc[0][r][j] = 0.f;
-    if constexpr (STREAM) {
+    if constexpr (XN) {
+        const uint8_t* const gb[1] = {P.packed + g * KB * kTileBytes};
+        const int kr = (kb1 - kb0) * 32;
+        float* xo = blockIdx.x == 0 ? P.x_out : nullptr;
+        if (P.nw_bf16)
+            stage_norm_acc_row<1, 64 * WAVES>((const float*)P.x, P.acc_part, P.acc_S, P.K, P.K, P.eps, P.nw, (int64_t)kb0 * 32, kr,
+                                  xs, xo, xf);
+        else
+            stage_norm_acc_row<2, 64 * WAVES>((const float*)P.x, P.acc_part, P.acc_S, P.K, P.K, P.eps, P.nw, (int64_t)kb0 * 32, kr,
+                                  xs, xo, xf);
+        gemv_rows_stream<1, false, 1, 4, WAVES, false, 0, DenseRows, true>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc,
+                                                                          NormIn{}, xs, kr);
+    } else if constexpr (STREAM) {
         // K positions in flight: 4, or 3 where 16 waves (128 VGPRs each) hold 3-4 accumulator
         // sets or 2 with the f32 activation's two fragments (an in-flight register must not be
         // spilled)
@@ -215,6 +239,9 @@ struct SwigluParams {
     const void* nw;   // NORM: the RMSNorm weight [K] (x is the f32 residual stream)
     int nw_bf16;
     float eps;
+    const float* acc_part;   // XN: x = res (P.x) + these S partial planes, as in gemv_kernel
+    int acc_S;
+    float* x_out;
 };
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -224,11 +251,14 @@ __device__ __forceinline__ void store_h(void* h, bool bf16, int64_t i, float v) 
     else ((float*)h)[i] = v;
 }
 
-template <int NTL, bool XF32, bool NORM = false, int WAVES = kWaves, bool STREAM = false>
+template <int NTL, bool XF32, bool NORM = false, int WAVES = kWaves, bool STREAM = false, bool XN = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_swiglu_kernel(SwigluParams P) {
+    static_assert(!XN || (NORM && STREAM && NTL == 1), "XN: one row, norm, rolling loop");
     __shared__ float red[WAVES][4][NTL][64];
     __shared__ float rrow[NORM ? 4 * NTL : 1];
-    if constexpr (NORM) rms_inv_rows<4 * NTL>((const float*)P.x, P.M, P.K, P.eps, rrow);
+    __shared__ __attribute__((aligned(16))) __bf16 xs[XN ? kXnElems : 8];
+    __shared__ float xf[XN ? kXnElems : 1];
+    if constexpr (NORM && !XN) rms_inv_rows<4 * NTL>((const float*)P.x, P.M, P.K, P.eps, rrow);
     const int64_t item = blockIdx.x;
     const int S = P.S;
     const int64_t g = item / S;
@@ -245,7 +275,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_swiglu_kernel(SwigluParams P)
             for (int j = 0; j < NTL; ++j) acc[i][r][j] = 0.f;
     const NormIn nrm{P.nw, P.nw_bf16, rrow};
     constexpr int kUnr = NTL >= 3 ? 3 : 4;   // K positions in flight (two tiles each)
-    if constexpr (STREAM) {
+    if constexpr (XN) {
+        const int kr = (kb1 - kb0) * 32;
+        float* xo = blockIdx.x == 0 ? P.x_out : nullptr;
+        if (P.nw_bf16)
+            stage_norm_acc_row<1, 64 * WAVES>((const float*)P.x, P.acc_part, P.acc_S, P.K, P.K, P.eps, P.nw, (int64_t)kb0 * 32, kr,
+                                  xs, xo, xf);
+        else
+            stage_norm_acc_row<2, 64 * WAVES>((const float*)P.x, P.acc_part, P.acc_S, P.K, P.K, P.eps, P.nw, (int64_t)kb0 * 32, kr,
+                                  xs, xo, xf);
+        gemv_rows_stream<1, false, 2, kUnr, WAVES, false, 0, DenseRows, true>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1,
+                                                                             acc, NormIn{}, xs, kr);
+    } else if constexpr (STREAM) {
         if constexpr (NORM) {
             if (P.nw_bf16)
                 gemv_rows_stream<NTL, false, 2, kUnr, WAVES, false, 1>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc,
@@ -427,6 +468,12 @@ bool gemv_stream() {
 template <int NTL, int WAVES, bool STREAM>
 void launch_swiglu_ws(bool xf32, dim3 grid, hipStream_t st, const SwigluParams& P) {
     const dim3 block(64 * WAVES);
+    if constexpr (STREAM && NTL == 1) {
+        if (P.x_out) {   // the fused deferred reduction (swiglu_impl checked that it applies)
+            hipLaunchKernelGGL((gemv_swiglu_kernel<1, false, true, WAVES, true, true>), grid, block, 0, st, P);
+            return;
+        }
+    }
     if (P.nw) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false, true, WAVES, STREAM>), grid, block, 0, st, P);
     else if (xf32) hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, true, false, WAVES, STREAM>), grid, block, 0, st, P);
     else hipLaunchKernelGGL((gemv_swiglu_kernel<NTL, false, false, WAVES, STREAM>), grid, block, 0, st, P);
@@ -447,6 +494,13 @@ void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, cons
 
 template <int NTL, int WAVES, bool Q40, bool STREAM>
 void launch_gemv_ws(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
+    if constexpr (!Q40 && STREAM && NTL == 1) {
+        if (P.x_out) {   // the fused deferred reduction (gemv_impl checked that it applies)
+            hipLaunchKernelGGL((gemv_kernel<1, false, WAVES, false, true, true, true>), grid, dim3(64 * WAVES), 0, st,
+                               P);
+            return;
+        }
+    }
     if constexpr (!Q40) {
         if (P.nw) {
             hipLaunchKernelGGL((gemv_kernel<NTL, false, WAVES, false, true, STREAM>), grid, dim3(64 * WAVES), 0, st,
@@ -513,7 +567,32 @@ struct NormSpec {
     const void* w = nullptr;   // RMSNorm weight [K]; null: x is the GEMV's input as given
     int w_bf16 = 0;
     float eps = 0.f;
+    const float* acc_part = nullptr;   // the deferred reduction (gemv_kernel's XN): x = res + part
+    int acc_S = 0;
+    float* x_out = nullptr;            // non-null: a deferred-reduction call
 };
+
+// x_out = res + the S partial planes [S][MK], in stage_norm_acc_row's order (S = 1: res +
+// part; S > 1: split_reduce's; S = 0: res): the unfused form of the deferred reduction.
+__global__ __launch_bounds__(256) void acc_reduce_kernel(const float* __restrict__ res, const float* __restrict__ part,
+                                                         int S, int64_t MK, float* __restrict__ x_out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= MK) return;
+    float x;
+    if (S == 1) {
+        x = res[i] + part[i];
+    } else {
+        float sum = 0.f;
+        for (int q = 0; q < S; ++q) sum += part[(int64_t)q * MK + i];
+        x = S == 0 ? res[i] : res[i] + sum;
+    }
+    x_out[i] = x;
+}
+
+// A deferred-reduction call's fused form applies: the rolling loop, one row, K <= 4096.
+bool acc_fused(int M, int64_t K) { return gemv_stream() && M == 1 && K <= kXnElems; }
+
+constexpr int kMaxAccSplits = 16;   // partial planes a deferred reduction takes
 
 int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* res, float* y, int M, int64_t N,
               int64_t K, void* workspace, size_t workspace_bytes, void* stream, const uint8_t* lo = nullptr,
@@ -524,6 +603,16 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
     if (!packed || !x || !y) return Q4MI_E_ARG;
     if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
+    if (nrm.x_out && !acc_fused(M, K)) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
+        const int64_t MK = (int64_t)M * K;
+        hipLaunchKernelGGL(acc_reduce_kernel, dim3((unsigned)ceil_div(MK, 256)), dim3(256), 0, (hipStream_t)stream,
+                           (const float*)x, nrm.acc_part, nrm.acc_S, MK, nrm.x_out);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        x = nrm.x_out;
+        nrm.x_out = nullptr;
+        nrm.acc_part = nullptr;
+        nrm.acc_S = 0;
+    }
     const GemvPlan plan = lo ? GemvPlan{choose_splits(N, K), 4} : plan_gemv(N, K);
     const int S = plan.S;
     GemvParams P{};
@@ -538,6 +627,9 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     P.nw = nrm.w;
     P.nw_bf16 = nrm.w_bf16;
     P.eps = nrm.eps;
+    P.acc_part = nrm.acc_part;
+    P.acc_S = nrm.acc_S;
+    P.x_out = nrm.x_out;
     if (S > 1) {   // the documented contract: at least what the query reports
         if (!workspace || workspace_bytes < q4_gemv_workspace_bytes(M, N, K)) return Q4MI_E_WORKSPACE;
         P.part = (float*)workspace;
@@ -700,6 +792,16 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     if (!gate || !up || !x || !h) return Q4MI_E_ARG;
     if (misaligned16(gate) || misaligned16(up) || misaligned16(x) || misaligned16(workspace)) return Q4MI_E_ARG;
     if (((uintptr_t)h & (h_dtype == Q4MI_BF16 ? 1 : 3)) != 0) return Q4MI_E_ARG;
+    if (nrm.x_out && !acc_fused(M, K)) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
+        const int64_t MK = (int64_t)M * K;
+        hipLaunchKernelGGL(acc_reduce_kernel, dim3((unsigned)ceil_div(MK, 256)), dim3(256), 0, (hipStream_t)stream,
+                           (const float*)x, nrm.acc_part, nrm.acc_S, MK, nrm.x_out);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        x = nrm.x_out;
+        nrm.x_out = nullptr;
+        nrm.acc_part = nullptr;
+        nrm.acc_S = 0;
+    }
     const GemvPlan plan = swiglu_plan(F, K);
     const int S = plan.S;
     SwigluParams P{};
@@ -715,6 +817,9 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     P.nw = nrm.w;
     P.nw_bf16 = nrm.w_bf16;
     P.eps = nrm.eps;
+    P.acc_part = nrm.acc_part;
+    P.acc_S = nrm.acc_S;
+    P.x_out = nrm.x_out;
     if (S > 1) {
         if (!workspace || workspace_bytes < (size_t)S * M * 2 * F * sizeof(float)) return Q4MI_E_WORKSPACE;
         P.part = (float*)workspace;
@@ -751,6 +856,99 @@ extern "C" int q4_gemv_swiglu_rmsnorm(const uint8_t* gate, const uint8_t* up, co
     const int a = norm_args(x, norm_w, norm_w_dtype, eps, M, K, &nrm);
     if (a != Q4MI_OK) return a;
     return swiglu_impl(gate, up, x, Q4MI_F32, h, h_dtype, M, F, K, workspace, workspace_bytes, stream, nrm);
+}
+
+// ---------------------------------------------------------------------------
+// The K-split reduction deferred to the consumer: q4_gemv_partials leaves a split GEMV's
+// partial sums; the norm-fused GEMVs' _acc forms add them to the residual stream in
+// split_reduce's order (so the result is the one q4_gemv_residual + the norm GEMV give),
+// write that residual to x_out, and normalise it, with no reduce launch in between.
+
+extern "C" int q4_gemv_split_count(int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0 || N % 64 || K % 32) return 0;
+    return plan_gemv(N, K).S;
+}
+
+extern "C" int q4_gemv_partials(const uint8_t* packed, const void* x, int x_dtype, float* part, int S, int M,
+                                int64_t N, int64_t K, void* stream) {
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (M < 0 || M > 16) return Q4MI_E_RANGE;
+    if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
+    if (S < 1 || S > kMaxAccSplits || S > K / 32) return Q4MI_E_RANGE;
+    if (M == 0 || N == 0) return Q4MI_OK;
+    if (!packed || !x || !part) return Q4MI_E_ARG;
+    if (misaligned16(packed) || misaligned16(x) || misaligned16(part)) return Q4MI_E_ARG;
+    GemvParams P{};
+    P.packed = packed;
+    P.x = x;
+    P.y = part;       // S = 1: the unsplit store
+    P.part = part;    // S > 1: plane s at part + s M N
+    P.M = M;
+    P.S = S;
+    P.N = N;
+    P.K = K;
+    // the plain plan's waves when S is its split count (then the planes add up, in split
+    // order, to q4_gemv's result bit for bit); other counts take 8
+    const GemvPlan plan = plan_gemv(N, K);
+    const int waves = S == plan.S ? plan.waves : 8;
+    const dim3 grid((unsigned)((N / 64) * S));
+    const hipStream_t st = (hipStream_t)stream;
+    const bool xf32 = x_dtype == Q4MI_F32;
+    switch ((M + 3) / 4) {
+        case 1: launch_gemv<1>(xf32, waves, grid, st, P); break;
+        case 2: launch_gemv<2>(xf32, waves, grid, st, P); break;
+        case 3: launch_gemv<3>(xf32, waves, grid, st, P); break;
+        default: launch_gemv<4>(xf32, waves, grid, st, P); break;
+    }
+    return launch_status();
+}
+
+// out / out_bytes: the GEMV's own output (y or h), written while other workgroups still
+// read res and the planes.
+static int acc_args(const float* res, const float* part, int S, const float* x_out, const void* out,
+                    int64_t out_bytes, int M, int64_t K, NormSpec* nrm) {
+    if (S < 0 || S > kMaxAccSplits) return Q4MI_E_RANGE;
+    if (M == 0) return Q4MI_OK;
+    if (!x_out || (S > 0 && !part)) return Q4MI_E_ARG;
+    // workgroup 0 writes x_out while the others read res and the planes
+    auto overlaps = [](const void* a, int64_t na, const void* b, int64_t nb) {
+        const char *ca = (const char*)a, *cb = (const char*)b;
+        return a && b && ca < cb + nb && cb < ca + na;
+    };
+    const int64_t row_bytes = (int64_t)M * K * 4, part_bytes = S > 0 ? S * row_bytes : 0;
+    if (overlaps(x_out, row_bytes, res, row_bytes) || overlaps(x_out, row_bytes, part, part_bytes) ||
+        overlaps(out, out_bytes, res, row_bytes) || overlaps(out, out_bytes, part, part_bytes) ||
+        overlaps(out, out_bytes, x_out, row_bytes))
+        return Q4MI_E_ARG;
+    if (misaligned16(x_out) || (S > 0 && misaligned16(part))) return Q4MI_E_ARG;
+    nrm->acc_part = part;
+    nrm->acc_S = S;
+    nrm->x_out = (float*)x_out;
+    return Q4MI_OK;
+}
+
+extern "C" int q4_gemv_rmsnorm_acc(const uint8_t* packed, const float* res, const float* part, int S,
+                                   const void* norm_w, int norm_w_dtype, float eps, float* x_out, float* y, int M,
+                                   int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+    NormSpec nrm;
+    int a = norm_args(res, norm_w, norm_w_dtype, eps, M, K, &nrm);
+    if (a != Q4MI_OK) return a;
+    if ((a = acc_args(res, part, S, x_out, y, (int64_t)M * N * 4, M, K, &nrm)) != Q4MI_OK) return a;
+    return gemv_impl(packed, res, Q4MI_F32, nullptr, y, M, N, K, workspace, workspace_bytes, stream, nullptr, false,
+                     nrm);
+}
+
+extern "C" int q4_gemv_swiglu_rmsnorm_acc(const uint8_t* gate, const uint8_t* up, const float* res, const float* part,
+                                          int S, const void* norm_w, int norm_w_dtype, float eps, float* x_out,
+                                          void* h, int h_dtype, int M, int64_t F, int64_t K, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    NormSpec nrm;
+    int a = norm_args(res, norm_w, norm_w_dtype, eps, M, K, &nrm);
+    if (a != Q4MI_OK) return a;
+    if ((a = acc_args(res, part, S, x_out, h, (int64_t)M * F * (h_dtype == Q4MI_BF16 ? 2 : 4), M, K, &nrm)) !=
+        Q4MI_OK)
+        return a;
+    return swiglu_impl(gate, up, res, Q4MI_F32, h, h_dtype, M, F, K, workspace, workspace_bytes, stream, nrm);
 }
 
 extern "C" size_t q4_gemv_q4k_workspace_bytes(int M, int64_t N, int64_t K) {

@@ -629,12 +629,17 @@ __device__ __forceinline__ void tile_math(const u32x4 (&c)[NG], const u32x4 (&s)
 // hits) and are not accumulated. Positions are visited in the same order as the batched
 // loops, with the same arithmetic, so the sums are bit-identical to theirs for the same
 // waves and K range.
-template <int NTL, bool XF32, int NG, int UNR, int WAVES, bool Q40, int NW, class Rows>
+//
+// XS: the activations were staged in LDS as bf16 fragments (xs[m][kr] over the K range
+// [kb0, kb1) of 32-wide positions, e.g. by stage_norm_acc_row), so a position is its weight
+// loads only.
+template <int NTL, bool XF32, int NG, int UNR, int WAVES, bool Q40, int NW, class Rows, bool XS = false>
 __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[NG], const void* __restrict__ x,
                                                  Rows rows, int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL],
-                                                 NormIn nrm = {}) {
+                                                 NormIn nrm = {}, const __bf16* xs = nullptr, int kr = 0) {
+    static_assert(!XS || (!XF32 && NW == 0), "staged fragments are one bf16 plane");
     constexpr int TB = Q40 ? kQ0TileBytes : kTileBytes;
-    constexpr int XL = NW == 0 ? (XF32 ? 2 : 1) : (NW == 1 ? 3 : 4);   // activation-side loads
+    constexpr int XL = XS ? 0 : NW == 0 ? (XF32 ? 2 : 1) : (NW == 1 ? 3 : 4);   // activation-side loads
     constexpr int L = 2 * NG + XL;                                     // loads per K position
     static_assert((UNR - 1) * L <= 63, "vmcnt holds 6 bits");
     static_assert(NW == 0 || !XF32, "a normalised row feeds the MFMA as one bf16 fragment");
@@ -657,7 +662,8 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[N
     constexpr int64_t ws = NW == 1 ? 2 : 4;                            // norm weight element bytes
     const uint8_t* wp = NW ? (const uint8_t*)nrm.w + kg * 8 * ws : nullptr;
     const float rr = NW ? nrm.r[xrow] : 0.f;
-    u32x4 c[UNR][NG], s[UNR][NG], xr[UNR][XL];
+    u32x4 c[UNR][NG], s[UNR][NG], xr[UNR][XL > 0 ? XL : 1];
+    const __bf16* xsl = XS ? xs + xrow * kr + kg * 8 - (int64_t)kb0 * 32 : nullptr;   // this lane's fragments
     auto issue = [&](int b, int slot) {
         const int t = first + WAVES * min(b, cnt - 1);
         const uint32_t toff = (uint32_t)t * TB;
@@ -666,6 +672,7 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[N
             pipe_load_w(c[slot][i], gbase[i], toff + coff);
             pipe_load_w(s[slot][i], gbase[i], toff + soff);
         }
+        if constexpr (XS) return;
         const uint8_t* xa = xp + (int64_t)t * 32 * es;
         pipe_load_x(xr[slot][0], xa);
         if constexpr (XF32 || NW) pipe_load_x(xr[slot][1], xa + 16);
@@ -684,9 +691,11 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[N
 #pragma unroll
         for (int h = 0; h < XL; ++h) pipe_landed(xr[slot][h]);
     };
-    auto run = [&](int u) {
+    auto run = [&](int u, int b) {
         bf16x8 xh, xl;
-        if constexpr (NW) {
+        if constexpr (XS) {
+            xh = *(const bf16x8*)(xsl + (int64_t)(first + WAVES * b) * 32);
+        } else if constexpr (NW) {
             float wv[8];
             if constexpr (NW == 1) {
                 norm_w_of_bf16(xr[u][2], wv);
@@ -725,7 +734,7 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[N
         for (int u = 0; u < UNR; ++u) {
             __builtin_amdgcn_s_waitcnt(pipe_wait_imm((UNR - 1) * L));
             land(u);
-            run(u);
+            run(u, b0 + u);
             issue(b0 + u + UNR, u);
         }
     }
@@ -733,8 +742,105 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[N
         constexpr int u = decltype(U)::value;
         __builtin_amdgcn_s_waitcnt(pipe_wait_imm((UNR - 1 - u) * L));
         land(u);
-        if (b0 + u < cnt) run(u);
+        if (b0 + u < cnt) run(u, b0 + u);
     });
+}
+
+// One activation row of K <= 256 kAccRowJ values that a split GEMV left as partial sums:
+//   x = res + (((0 + part[0]) + part[1]) + ...)     (S > 1: split_reduce's order)
+//   x = res + part[0]                               (S = 1: the unsplit store's)
+//   x = res                                         (S = 0)
+// with part planes plane_stride floats apart. From one read of res and the planes: x into
+// x_out (when given: one workgroup writes it), the row's 1/rms with rms_inv_rows'
+// arithmetic and order, and ((x * r) * w) rounded to bf16 over columns [k0, k0 + kr) into
+// xs. All NT threads of the workgroup share the loads (element i = tid + NT e), the
+// planes in batches whose loads are all issued before the first add (the planes were just
+// written by another kernel: each batch pays one trip to memory); x passes through LDS
+// (xf) to the 256 threads that form the sum of squares in rms_inv_rows' order. Every
+// thread calls it; barriers inside.
+constexpr int kAccRowJ = 16;
+template <int NW, int NT>
+__device__ __forceinline__ void stage_norm_acc_row(const float* __restrict__ res, const float* __restrict__ part,
+                                                   int S, int64_t plane_stride, int64_t K, float eps,
+                                                   const void* __restrict__ w, int64_t k0, int kr, __bf16* xs,
+                                                   float* __restrict__ x_out, float* xf) {
+    constexpr int E = 256 * kAccRowJ / NT;            // elements per thread in the sum
+    // planes per batch: 64 values in flight, 32 in a 1024-thread workgroup (128 VGPRs a lane)
+    constexpr int kFly = NT >= 1024 ? 32 : 64, PB = E >= kFly ? 1 : kFly / E;
+    __shared__ double partd[4];
+    const int tid = threadIdx.x;
+    // every load below is unconditional, at an index clamped into the row (a load under a
+    // lane condition is compiled as a branch with a wait for it inside): values past K or
+    // outside this workgroup's columns are loaded and not used
+    auto ix = [&](int64_t i) { return i < K ? i : K - 1; };
+    // this workgroup's columns of the norm weight, as raw words converted where used (a
+    // bf16 weight: the word holding element i, i's half picked by i's parity; 16-bit loads
+    // drew waits for packing ahead of the plane loads)
+    uint32_t wl[kAccRowJ];
+    if (tid < 256) {
+#pragma unroll
+        for (int j = 0; j < kAccRowJ; ++j) {
+            const int64_t i = ix(tid + 256 * j);
+            wl[j] = ((const uint32_t*)w)[NW == 1 ? i >> 1 : i];
+        }
+    }
+    float r0[E], v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) r0[e] = res[ix(tid + NT * e)];
+    if (S == 1) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = part[ix(tid + NT * e)];
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = r0[e] + v[e];
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = 0.f;
+        for (int q = 0; q < S; q += PB) {
+            float t[PB][E];
+#pragma unroll
+            for (int u = 0; u < PB; ++u)
+#pragma unroll
+                for (int e = 0; e < E; ++e) t[u][e] = part[min(q + u, S - 1) * plane_stride + ix(tid + NT * e)];
+#pragma unroll
+            for (int u = 0; u < PB; ++u)
+                if (q + u < S) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) v[e] += t[u][e];
+                }
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = S == 0 ? r0[e] : r0[e] + v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        if (tid + NT * e < K) {
+            xf[tid + NT * e] = v[e];
+            if (x_out) x_out[tid + NT * e] = v[e];
+        }
+    __syncthreads();
+    float x[kAccRowJ];
+    if (tid < 256) {
+#pragma unroll
+        for (int j = 0; j < kAccRowJ; ++j) x[j] = tid + 256 * j < K ? xf[tid + 256 * j] : 0.f;
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < kAccRowJ; ++j)
+            if (tid + 256 * j < K) ss += (double)x[j] * (double)x[j];
+        const double wsum = wave_sum_ss(ss);
+        if ((tid & 63) == 0) partd[tid >> 6] = wsum;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        const float r = inv_rms(partd, K, eps);
+#pragma unroll
+        for (int j = 0; j < kAccRowJ; ++j) {
+            const int64_t i = tid + 256 * j;
+            const float wi = NW == 1 ? bf16_hi_to_f32(i & 1 ? wl[j] & 0xffff0000u : wl[j] << 16)
+                                     : __uint_as_float(wl[j]);
+            if (i >= k0 && i < k0 + kr) ((uint16_t*)xs)[i - k0] = (uint16_t)f32_to_bf16_rne(x[j] * r * wi);
+        }
+    }
+    __syncthreads();
 }
 
 // Sum the WAVES waves' accumulators through LDS. Afterwards thread t < 256 owns

@@ -743,6 +743,103 @@ def gemm_q4_rmsnorm(w: PackedQ4, x: torch.Tensor, norm_w: torch.Tensor, eps: flo
     return y
 
 
+def gemv_split_count(w: PackedQ4) -> int:
+    """The K-split count gemm_q4 plans for ``w`` at decode sizes (1: unsplit)."""
+    return int(_lib_handle().q4_gemv_split_count(w.n, w.k))
+
+
+def gemm_q4_partials(w: PackedQ4, x, splits: int | None = None, part: torch.Tensor | None = None) -> torch.Tensor:
+    """The partial sums of a K-split gemm_q4, unreduced: part[s] = X @ W[:, K_s]^T over the
+    s-th of ``splits`` contiguous K ranges (f32 [splits, M, N]; 1 <= M <= 16). With the
+    default ``splits`` (gemv_split_count) they add up, in split order, to gemm_q4's Y bit
+    for bit. The planes go to gemm_q4_rmsnorm_acc / swiglu_q4_acc, which add them to the
+    residual stream in place of gemm_q4(residual=...)'s reduce launch."""
+    dev = w.device
+    xt = _acts(x, dev)
+    if xt.dim() == 1:
+        xt = xt.unsqueeze(0)
+    M, K = xt.shape
+    if K != w.k:
+        raise ValueError(f"x has K={K}, W is [{w.n}, {w.k}]")
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q4_partials takes 1..16 tokens, got {M}")
+    S = gemv_split_count(w) if splits is None else int(splits)
+    if not 1 <= S <= min(16, w.k // 32):
+        raise ValueError(f"splits must be 1..{min(16, w.k // 32)}, got {S}")
+    part = _buf(part, "part", torch.float32, (S, M, w.n), dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        check("q4_gemv_partials", lib.q4_gemv_partials(_ptr(w.data), _ptr(xt), _x_dtype(xt), _ptr(part), S, M, w.n,
+                                                       w.k, _stream(dev)))
+    return part
+
+
+def _acc_args(res: torch.Tensor, partials, x_out, K: int, dev):
+    xt = _norm_x(res, K, dev)
+    M = xt.shape[0]
+    if partials is None:
+        S, pp = 0, None
+    else:
+        if not isinstance(partials, torch.Tensor) or partials.dtype != torch.float32 or partials.device != dev \
+                or not partials.is_contiguous() or partials.dim() != 3 or tuple(partials.shape[1:]) != (M, K):
+            raise ValueError(f"partials must be a contiguous float32 [S, {M}, {K}] tensor on {dev}")
+        S, pp = partials.shape[0], _ptr(partials)
+        if not 1 <= S <= 16:
+            raise ValueError(f"partials hold 1..16 planes, got {S}")
+    x_out = _buf(x_out, "x_out", torch.float32, (M, K), dev)
+    lo, hi = x_out.data_ptr(), x_out.data_ptr() + x_out.numel() * 4
+    for t in (res, partials):
+        if t is not None and t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * 4:
+            raise ValueError("x_out must not overlap res or partials")
+    return xt, M, S, pp, x_out
+
+
+def gemm_q4_rmsnorm_acc(w: PackedQ4, res: torch.Tensor, partials: torch.Tensor | None, norm_w: torch.Tensor,
+                        eps: float = 1e-6, x_out: torch.Tensor | None = None, y: torch.Tensor | None = None,
+                        workspace: torch.Tensor | None = None):
+    """(y, x_out): x_out = res + the partial planes added in split order (gemm_q4(...,
+    residual=res)'s bits for the GEMV that made them), then y = gemm_q4_rmsnorm(w, x_out,
+    norm_w) -- with the reduction inside the norm GEMV's workgroups at M = 1 (K <= 4096)
+    instead of a launch of its own. ``x_out`` must not share memory with ``res``."""
+    dev = w.device
+    xt, M, S, pp, x_out = _acc_args(res, partials, x_out, w.k, dev)
+    if not 1 <= M <= 16:
+        raise ValueError(f"gemm_q4_rmsnorm_acc takes 1..16 tokens, got {M}")
+    wt, wd = _norm_w(norm_w, w.k, dev)
+    y = _buf(y, "y", torch.float32, (M, w.n), dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        check("q4_gemv_rmsnorm_acc", lib.q4_gemv_rmsnorm_acc(_ptr(w.data), _ptr(xt), pp, S, _ptr(wt), wd, float(eps),
+                                                             _ptr(x_out), _ptr(y), M, w.n, w.k, wp, wn,
+                                                             _stream(dev)))
+    return y, x_out
+
+
+def swiglu_q4_acc(gate: PackedQ4, up: PackedQ4, res: torch.Tensor, partials: torch.Tensor | None,
+                  norm_w: torch.Tensor, eps: float = 1e-6, out_dtype=torch.float32, x_out: torch.Tensor | None = None,
+                  h: torch.Tensor | None = None, workspace: torch.Tensor | None = None):
+    """(h, x_out): x_out = res + partials as in gemm_q4_rmsnorm_acc, then h =
+    swiglu_q4(gate, up, x_out, norm_w=norm_w)."""
+    if gate.n != up.n or gate.k != up.k or gate.device != up.device:
+        raise ValueError(f"gate {gate.shape} and up {up.shape} must match")
+    dev = gate.device
+    xt, M, S, pp, x_out = _acc_args(res, partials, x_out, gate.k, dev)
+    if not 1 <= M <= 16:
+        raise ValueError(f"swiglu_q4_acc takes 1..16 tokens, got {M}")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("out_dtype must be float32 or bfloat16")
+    wt, wd = _norm_w(norm_w, gate.k, dev)
+    h = _buf(h, "h", out_dtype, (M, gate.n), dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_gemv_swiglu_workspace_bytes(M, gate.n, gate.k), "swiglu", workspace)
+        check("q4_gemv_swiglu_rmsnorm_acc", lib.q4_gemv_swiglu_rmsnorm_acc(
+            _ptr(gate.data), _ptr(up.data), _ptr(xt), pp, S, _ptr(wt), wd, float(eps), _ptr(x_out), _ptr(h),
+            Q4MI_BF16 if out_dtype == torch.bfloat16 else Q4MI_F32, M, gate.n, gate.k, wp, wn, _stream(dev)))
+    return h, x_out
+
+
 def swiglu_q4(gate: PackedQ4, up: PackedQ4, x, out_dtype=torch.float32, h: torch.Tensor | None = None,
               workspace: torch.Tensor | None = None, norm_w: torch.Tensor | None = None,
               eps: float = 1e-6) -> torch.Tensor:

@@ -243,3 +243,32 @@ def test_moe_fin_argument_errors(lib):
     assert lib.q4_moe_gemv_fin(*args(odd, None, None, ws)) == -2       # misaligned residual
     assert lib.q4_moe_gemv_fin(*args(None, odd, fake, ws)) == -2       # misaligned shared
     assert lib.q4_moe_gemv_fin(*args(fake, fake, fake, ws - 1)) == -3  # short workspace
+
+
+def test_deferred_reduction_argument_errors(lib):
+    """q4_gemv_partials / the _acc norm GEMVs refuse bad split counts and outputs that
+    overlap what other workgroups still read, before any launch."""
+    fake = C.c_void_p(0x1000)
+    assert lib.q4_gemv_split_count(4096, 14336) >= 2 and lib.q4_gemv_split_count(128256, 4096) == 1
+    assert lib.q4_gemv_split_count(100, 4096) == 0
+    for S in (0, 17):
+        assert lib.q4_gemv_partials(fake, fake, 1, fake, S, 1, 4096, 4096, None) == -5
+    assert lib.q4_gemv_partials(fake, fake, 1, fake, 4, 1, 4096, 96, None) == -5     # S > K / 32
+    assert lib.q4_gemv_partials(fake, fake, 1, fake, 4, 17, 4096, 4096, None) == -5  # M
+    assert lib.q4_gemv_partials(fake, fake, 7, fake, 4, 1, 4096, 4096, None) == -2   # x dtype
+    assert lib.q4_gemv_partials(fake, fake, 1, fake, 4, 1, 4100, 4096, None) == -1   # N % 64
+    assert lib.q4_gemv_partials(fake, fake, 1, fake, 4, 0, 4096, 4096, None) == 0    # nothing to do
+    K, N = 4096, 1024
+    res, part, xo, y = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4))
+    rms = lambda *a: lib.q4_gemv_rmsnorm_acc(fake, *a, None, 0, None)
+    assert rms(res, part, 17, fake, 1, C.c_float(1e-6), xo, y, 1, N, K) == -5          # S
+    assert rms(res, None, 4, fake, 1, C.c_float(1e-6), xo, y, 1, N, K) == -2           # no planes
+    assert rms(res, part, 4, fake, 1, C.c_float(1e-6), None, y, 1, N, K) == -2         # no x_out
+    over = C.c_void_p(0x10000000 + 4 * K - 16)
+    assert rms(res, part, 4, fake, 1, C.c_float(1e-6), over, y, 1, N, K) == -2         # x_out on res
+    assert rms(res, part, 4, fake, 1, C.c_float(1e-6), xo, C.c_void_p(0x20000000 + 3 * 4 * K), 1, N, K) == -2
+    assert rms(res, part, 4, fake, 1, C.c_float(1e-6), xo, C.c_void_p(0x30000000 + 64), 1, N, K) == -2
+    h = C.c_void_p(0x40000000)
+    sw = lambda *a: lib.q4_gemv_swiglu_rmsnorm_acc(fake, fake, *a, None, 0, None)
+    assert sw(res, part, 4, fake, 1, C.c_float(1e-6), xo, C.c_void_p(0x10000000), 1, 1, 14336, K) == -2  # h on res
+    assert sw(res, part, -1, fake, 1, C.c_float(1e-6), xo, h, 1, 1, 14336, K) == -5

@@ -215,3 +215,123 @@ def test_swiglu_with_its_rmsnorm_inside(gpu, pkg, oracle, M):
         ref = pkg.swiglu_q4(g, u, xn, out_dtype=dt)
         h = pkg.swiglu_q4(g, u, x, out_dtype=dt, norm_w=nw)
         assert torch.equal(h, ref)
+
+
+def _acc_ref(res: torch.Tensor, part: torch.Tensor | None) -> torch.Tensor:
+    """res + the planes in split order, in torch's IEEE f32 adds: res + p0 for one plane,
+    res + (((0 + p0) + p1) + ...) for more (split_reduce's order)."""
+    if part is None or part.shape[0] == 0:
+        return res.clone()
+    if part.shape[0] == 1:
+        return res + part[0]
+    s = torch.zeros_like(res)
+    for q in range(part.shape[0]):
+        s = s + part[q]
+    return res + s
+
+
+@pytest.mark.parametrize("N,K,M", [(4096, 4096, 1), (4096, 14336, 1), (6144, 4096, 1), (4096, 4096, 3), (256, 96, 2)])
+def test_partials_add_up_to_the_split_gemv(gpu, pkg, oracle, N, K, M):
+    """q4_gemv_partials at the plan's split count: the planes added in split order are
+    q4_gemv's Y (and res + them q4_gemv_residual's) bit for bit; at another count they
+    hold the K ranges' products (maxrel against fp64)."""
+    say(f"partials N={N} K={K} M={M}")
+    rng = np.random.default_rng(900 + N + K + M)
+    blocks = oracle.baseline_q4_1_blocks(N, K, rng)
+    w = pkg.pack_q4_1(blocks, gpu)
+    xh = rng.standard_normal((M, K)).astype(np.float32)
+    x = torch.from_numpy(xh).to(gpu).to(torch.bfloat16)
+    res = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(gpu)
+    S = pkg.gemv_split_count(w)
+    part = pkg.gemm_q4_partials(w, x)
+    assert part.shape == (S, M, N)
+    y = pkg.gemm_q4(w, x)
+    s = part[0] if S == 1 else _acc_ref(torch.zeros_like(y), part)
+    assert torch.equal(s, y)
+    assert torch.equal(_acc_ref(res, part), pkg.gemm_q4(w, x, residual=res))
+    S2 = 3 if S != 3 else 5
+    p2 = pkg.gemm_q4_partials(w, x, splits=S2).cpu().numpy().astype(np.float64)
+    xb = x.to(torch.float32).cpu().numpy()
+    dq = oracle.dequant_q4_1(blocks, bf16_scales=True).astype(np.float64)
+    ref = oracle.gemv_reference(blocks, xb).astype(np.float64)
+    assert oracle.maxrel(p2.sum(0), ref) <= MAXREL
+    kb = K // 32                 # plane q: the 32-wide K positions [q KB / S, (q + 1) KB / S)
+    for q in range(S2):
+        k0, k1 = 32 * (q * kb // S2), 32 * ((q + 1) * kb // S2)
+        rq = xb[:, k0:k1].astype(np.float64) @ dq[:, k0:k1].T
+        assert np.abs(p2[q] - rq).max() <= MAXREL * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("wdt", ["bf16", "f32"])
+@pytest.mark.parametrize("N,K,M,S", [(6144, 4096, 1, 0), (6144, 4096, 1, 1), (6144, 4096, 1, 4), (4096, 4096, 1, 16),
+                                     (65536, 4096, 1, 16), (1024, 2048, 1, 3), (512, 8192, 1, 4), (1024, 4096, 3, 4),
+                                     (256, 96, 5, 2)])
+def test_gemv_rmsnorm_of_residual_plus_partials(gpu, pkg, oracle, N, K, M, S, wdt):
+    """q4_gemv_rmsnorm_acc: x_out = res + partials in split order, bit for bit, and y the
+    bits of q4_gemv_rmsnorm of that x -- fused inside the GEMV (one row, K <= 4096) and
+    through the reduce launch (more rows, longer rows)."""
+    say(f"gemv rmsnorm acc N={N} K={K} M={M} S={S} w={wdt}")
+    rng = np.random.default_rng(1300 + N + K + M + S)
+    w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(N, K, rng), gpu)
+    res = torch.from_numpy((rng.standard_normal((M, K)) * 3).astype(np.float32)).to(gpu)
+    part = torch.from_numpy(rng.standard_normal((S, M, K)).astype(np.float32)).to(gpu) if S else None
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(gpu)
+    if wdt == "bf16":
+        nw = nw.to(torch.bfloat16)
+    x_ref = _acc_ref(res, part)
+    y_ref = pkg.gemm_q4_rmsnorm(w, x_ref, nw, eps=1e-5)
+    res0 = res.clone()
+    for _ in range(2):      # the second call sees the first's x_out and y in place
+        y, x_out = pkg.gemm_q4_rmsnorm_acc(w, res, part, nw, eps=1e-5)
+        assert torch.equal(x_out, x_ref)
+        assert torch.equal(y, y_ref)
+    assert torch.equal(res, res0)
+    _, xn = pkg.rmsnorm_add(x_ref, nw, eps=1e-5)
+    ref = oracle.gemv_reference(oracle.baseline_q4_1_blocks(N, K, np.random.default_rng(1300 + N + K + M + S)),
+                                xn.to(torch.float32).cpu().numpy()) if N * K <= 6144 * 4096 else None
+    if ref is not None:
+        assert oracle.maxrel(y.cpu().numpy(), ref) <= MAXREL
+
+
+@pytest.mark.parametrize("M,S", [(1, 0), (1, 1), (1, 4), (1, 16), (2, 4)])
+def test_swiglu_rmsnorm_of_residual_plus_partials(gpu, pkg, oracle, M, S):
+    say(f"swiglu rmsnorm acc M={M} S={S}")
+    F, K = 14336, 4096
+    rng = np.random.default_rng(1700 + M + S)
+    g = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(F, K, rng), gpu)
+    u = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(F, K, rng), gpu)
+    res = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(gpu)
+    part = torch.from_numpy(rng.standard_normal((S, M, K)).astype(np.float32)).to(gpu) if S else None
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    x_ref = _acc_ref(res, part)
+    for dt in (torch.bfloat16, torch.float32):
+        ref = pkg.swiglu_q4(g, u, x_ref, out_dtype=dt, norm_w=nw)
+        h, x_out = pkg.swiglu_q4_acc(g, u, res, part, nw, out_dtype=dt)
+        assert torch.equal(x_out, x_ref)
+        assert torch.equal(h, ref)
+
+
+def test_deferred_reduction_chain_matches_the_residual_gemvs(gpu, pkg, oracle):
+    """A decode layer's chain with the o / down reductions deferred into the next norm GEMV
+    (partials at the plan's split counts) gives the residual stream and the outputs of the
+    chain with q4_gemv_residual, bit for bit."""
+    say("deferred reduction chain")
+    H, F = 4096, 14336
+    rng = np.random.default_rng(2024)
+    wo = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(H, H, rng), gpu)
+    wg = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(F, H, rng), gpu)
+    wu = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(F, H, rng), gpu)
+    wd = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(H, F, rng), gpu)
+    wq = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(1024, H, rng), gpu)
+    x0 = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to(gpu)
+    attn = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to(gpu).to(torch.bfloat16)
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    xa = pkg.gemm_q4(wo, attn, residual=x0)
+    h = pkg.swiglu_q4(wg, wu, xa, out_dtype=torch.bfloat16, norm_w=nw)
+    xb = pkg.gemm_q4(wd, h, residual=xa)
+    q = pkg.gemm_q4_rmsnorm(wq, xb, nw)
+    po = pkg.gemm_q4_partials(wo, attn)
+    h2, xa2 = pkg.swiglu_q4_acc(wg, wu, x0, po, nw, out_dtype=torch.bfloat16)
+    pd = pkg.gemm_q4_partials(wd, h2)
+    q2, xb2 = pkg.gemm_q4_rmsnorm_acc(wq, xa2, pd, nw)
+    assert torch.equal(xa2, xa) and torch.equal(h2, h) and torch.equal(xb2, xb) and torch.equal(q2, q)

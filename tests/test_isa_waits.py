@@ -160,11 +160,13 @@ def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
     subprocess.run(cmd, check=True, capture_output=True, timeout=900)
     text = out.read_text().splitlines()
     dense = [l.split(":")[0] for l in text
-             if re.match(r"_ZN12_GLOBAL__N_111gemv_kernelILi\dELb\dELi\d+ELb\dELb\dELb1EE\w*:", l)]
-    assert len(dense) == 4 * 3 * (2 + 2 + 1)       # NTL x waves x (f32 / bf16 x, mx0 f32 / bf16 x, norm)
+             if re.match(r"_ZN12_GLOBAL__N_111gemv_kernelILi\dELb\dELi\d+ELb\dELb\dELb1ELb\dEE\w*:", l)]
+    # NTL x waves x (f32 / bf16 x, mx0 f32 / bf16 x, norm), + waves x (norm of residual + partials)
+    assert len(dense) == 4 * 3 * (2 + 2 + 1) + 3
     swiglu = [l.split(":")[0] for l in text
-              if re.match(r"_ZN12_GLOBAL__N_118gemv_swiglu_kernelILi\dELb\dELb\dELi\d+ELb1EE\w*:", l)]
-    assert len(swiglu) == 4 * 2 * 3                # NTL x waves x (f32 x, bf16 x, norm)
+              if re.match(r"_ZN12_GLOBAL__N_118gemv_swiglu_kernelILi\dELb\dELb\dELi\d+ELb1ELb\dEE\w*:", l)]
+    # NTL x waves x (f32 x, bf16 x, norm), + waves x (norm of residual + partials)
+    assert len(swiglu) == 4 * 2 * 3 + 2
     kernels = dense + swiglu
     meta = "\n".join(text)
     for k in kernels:
@@ -180,7 +182,8 @@ def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
             n, bad = early_uses_in(body)
             assert not bad, f"{k}: registers used before their load's wait: {bad[:3]}"
             checked += n
-        assert checked >= 9, f"{k}: no pipelined K loop found"
+        # the activation-from-LDS instances issue weight loads only
+        assert checked >= (8 if "ELb1ELb1EE" in k else 9), f"{k}: no pipelined K loop found"
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
