@@ -338,8 +338,9 @@ int q4_gemv_partials(const uint8_t* packed, const void* x, int x_dtype, float* p
 /* q4_gemv_rmsnorm of x = res + ((0 + part[0]) + part[1] + ...) (S planes of [M][K], in
  * split order; S = 0: x = res; S = 1: res + part[0]), which is also stored to x_out [M][K]
  * (the residual stream's next value: q4_gemv_residual's bits for the GEMV that made the
- * planes). x_out must not overlap res or part. M = 1 with K <= 4096 reduces inside the
- * GEMV's workgroups; other shapes add one reduce launch first. Workspace as q4_gemv. */
+ * planes). x_out must not overlap res, part or y. M = 1 with K <= 4096 and a grid of at most
+ * one workgroup per CU reduces inside the GEMV's workgroups; other shapes add one reduce
+ * launch first. Workspace as q4_gemv. */
 int q4_gemv_rmsnorm_acc(const uint8_t* packed, const float* res, const float* part, int S,
                         const void* norm_w, int norm_w_dtype, float eps, float* x_out, float* y, int M,
                         int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);

@@ -34,7 +34,8 @@ struct GemvParams {
     float eps;
     const float* acc_part;   // XN kernels: x = res (P.x) + the S planes of a split GEMV's partials
     int acc_S;
-    float* x_out;            // XN kernels: that x, written by workgroup 0
+    float* x_out;            // XN kernels: that x, written by workgroup 0 (when not null)
+    bool xn;                 // launch the XN instance
 };
 
 
@@ -242,6 +243,7 @@ struct SwigluParams {
     const float* acc_part;   // XN: x = res (P.x) + these S partial planes, as in gemv_kernel
     int acc_S;
     float* x_out;
+    bool xn;
 };
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -469,7 +471,7 @@ template <int NTL, int WAVES, bool STREAM>
 void launch_swiglu_ws(bool xf32, dim3 grid, hipStream_t st, const SwigluParams& P) {
     const dim3 block(64 * WAVES);
     if constexpr (STREAM && NTL == 1) {
-        if (P.x_out) {   // the fused deferred reduction (swiglu_impl checked that it applies)
+        if (P.xn) {   // the row normalised into LDS (swiglu_impl checked that it applies)
             hipLaunchKernelGGL((gemv_swiglu_kernel<1, false, true, WAVES, true, true>), grid, block, 0, st, P);
             return;
         }
@@ -495,7 +497,7 @@ void launch_pair(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P, cons
 template <int NTL, int WAVES, bool Q40, bool STREAM>
 void launch_gemv_ws(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
     if constexpr (!Q40 && STREAM && NTL == 1) {
-        if (P.x_out) {   // the fused deferred reduction (gemv_impl checked that it applies)
+        if (P.xn) {   // the row normalised into LDS (gemv_impl checked that it applies)
             hipLaunchKernelGGL((gemv_kernel<1, false, WAVES, false, true, true, true>), grid, dim3(64 * WAVES), 0, st,
                                P);
             return;
@@ -589,8 +591,42 @@ __global__ __launch_bounds__(256) void acc_reduce_kernel(const float* __restrict
     x_out[i] = x;
 }
 
-// A deferred-reduction call's fused form applies: the rolling loop, one row, K <= 4096.
-bool acc_fused(int M, int64_t K) { return gemv_stream() && M == 1 && K <= kXnElems; }
+// CUs of the current device (256 when none is visible).
+int cus_of_device() {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            return 256;
+        }
+        return n;
+    }();
+    return cus;
+}
+
+// The row normalised once into LDS by every workgroup (the XN kernels) applies: the rolling
+// loop, one row, K <= 4096, and a grid of at most one workgroup per CU. Every workgroup
+// reads the whole row (and a deferred reduction's planes) before its first tile; past one
+// workgroup per CU those reads repeat and sit in front of each later workgroup's tiles
+// (lm_head 128256 x 4096, 2004 workgroups: 67.0 against 65.8 us for the per-position
+// normalisation with no planes, 82.8 against 65.8 + a reduce launch with 16; qkv 6144 x
+// 4096, 96 workgroups: 9.8 against 10.5 us).
+bool acc_fused(int M, int64_t K, int64_t workgroups) {
+    return gemv_stream() && M == 1 && K <= kXnElems && workgroups <= cus_of_device();
+}
+
+// The plain norm GEMVs also normalise the row once into LDS where the fused deferred form
+// applies (S = 0: x = res); Q4MI_NORM_XN=0 keeps them on the per-position normalisation.
+// A decode step measured 1.472 against 1.519 ms: the row's loads go out together with the
+// norm weight's in one trip, and the K loop then loads weights only.
+bool norm_xn() {
+    static const bool on = [] {
+        const char* e = getenv("Q4MI_NORM_XN");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
 
 constexpr int kMaxAccSplits = 16;   // partial planes a deferred reduction takes
 
@@ -603,7 +639,10 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
     if (!packed || !x || !y) return Q4MI_E_ARG;
     if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
-    if (nrm.x_out && !acc_fused(M, K)) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
+    const GemvPlan plan = lo ? GemvPlan{choose_splits(N, K), 4} : plan_gemv(N, K);
+    const int S = plan.S;
+    const bool fused = acc_fused(M, K, (N / 64) * S);
+    if (nrm.x_out && !fused) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
         const int64_t MK = (int64_t)M * K;
         hipLaunchKernelGGL(acc_reduce_kernel, dim3((unsigned)ceil_div(MK, 256)), dim3(256), 0, (hipStream_t)stream,
                            (const float*)x, nrm.acc_part, nrm.acc_S, MK, nrm.x_out);
@@ -613,8 +652,6 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
         nrm.acc_part = nullptr;
         nrm.acc_S = 0;
     }
-    const GemvPlan plan = lo ? GemvPlan{choose_splits(N, K), 4} : plan_gemv(N, K);
-    const int S = plan.S;
     GemvParams P{};
     P.packed = packed;
     P.x = x;
@@ -630,6 +667,7 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     P.acc_part = nrm.acc_part;
     P.acc_S = nrm.acc_S;
     P.x_out = nrm.x_out;
+    P.xn = nrm.x_out || (nrm.w && norm_xn() && fused);
     if (S > 1) {   // the documented contract: at least what the query reports
         if (!workspace || workspace_bytes < q4_gemv_workspace_bytes(M, N, K)) return Q4MI_E_WORKSPACE;
         P.part = (float*)workspace;
@@ -792,7 +830,10 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     if (!gate || !up || !x || !h) return Q4MI_E_ARG;
     if (misaligned16(gate) || misaligned16(up) || misaligned16(x) || misaligned16(workspace)) return Q4MI_E_ARG;
     if (((uintptr_t)h & (h_dtype == Q4MI_BF16 ? 1 : 3)) != 0) return Q4MI_E_ARG;
-    if (nrm.x_out && !acc_fused(M, K)) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
+    const GemvPlan plan = swiglu_plan(F, K);
+    const int S = plan.S;
+    const bool fused = acc_fused(M, K, (F / 64) * S);
+    if (nrm.x_out && !fused) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
         const int64_t MK = (int64_t)M * K;
         hipLaunchKernelGGL(acc_reduce_kernel, dim3((unsigned)ceil_div(MK, 256)), dim3(256), 0, (hipStream_t)stream,
                            (const float*)x, nrm.acc_part, nrm.acc_S, MK, nrm.x_out);
@@ -802,8 +843,6 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
         nrm.acc_part = nullptr;
         nrm.acc_S = 0;
     }
-    const GemvPlan plan = swiglu_plan(F, K);
-    const int S = plan.S;
     SwigluParams P{};
     P.gate = gate;
     P.up = up;
@@ -820,6 +859,7 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     P.acc_part = nrm.acc_part;
     P.acc_S = nrm.acc_S;
     P.x_out = nrm.x_out;
+    P.xn = nrm.x_out || (nrm.w && norm_xn() && fused);
     if (S > 1) {
         if (!workspace || workspace_bytes < (size_t)S * M * 2 * F * sizeof(float)) return Q4MI_E_WORKSPACE;
         P.part = (float*)workspace;
