@@ -680,7 +680,7 @@ def extra_config0(torch, q4, dev):
     rot_us = graph_time(torch, rot, ys) / 32 * 1e3
     return {"cache_resident_us": hot_us, "cache_resident_gbs": nbytes / hot_us / 1e3,
             "rotated_us": rot_us, "rotated_gbs": nbytes / rot_us / 1e3,
-            "splits": q4.gemv_workspace_bytes(1, 4096, 4096) // (4096 * 4)}
+            "splits": q4.gemv_split_count(ws_w[0])}
 
 
 def extra_config2(torch, q4, model, steps):
