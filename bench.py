@@ -761,7 +761,29 @@ def extra_config3(torch, q4, dev):
         tff = 2.0 * T * 28672 * 4096 / msf / 1e9
         out[f"T{T}_gate_up_fused_prepared"] = {"N": 28672, "K": 4096, "ms": msf, "tflops": tff,
                                                "frac_of_peak": tff / MFMA_PEAK_TFLOPS}
-        del prep, wsp, y
+        # the activation producer in front of gate/up: residual add + RMSNorm writing the
+        # prepared activations in one launch, against q4_rmsnorm_add + the pre-pass
+        xr = torch.randn(T, 4096, generator=gen, device=dev)
+        ad = torch.randn(T, 4096, generator=gen, device=dev)
+        nw = (1 + 0.1 * torch.randn(4096, generator=gen, device=dev)).to(torch.bfloat16)
+        yb = torch.empty(T, 4096, device=dev)
+        xnb = torch.empty(T, 4096, dtype=torch.bfloat16, device=dev)
+        p2 = torch.zeros_like(prep.data)
+
+        def run_two():
+            for _ in range(3):
+                q4.rmsnorm_add(xr, nw, add=ad, y=yb, xn=xnb)
+                q4.prefill_prepare(xnb, out=prep.data)
+
+        def run_one():
+            for _ in range(3):
+                q4.rmsnorm_prepare(xr, nw, add=ad, y=yb, out=p2)
+        ms_two = graph_time(torch, run_two, [yb], replays=5) / 3
+        ms_one = graph_time(torch, run_one, [yb], replays=5) / 3
+        out[f"T{T}_norm_producer_K4096"] = {"norm_then_prepare_ms": ms_two, "rmsnorm_prepare_ms": ms_one,
+                                            "same_bytes": bool(torch.equal(prep.data[:T * 4096 * 2],
+                                                                           p2[:T * 4096 * 2]))}
+        del prep, wsp, y, xr, ad, yb, xnb, p2
     return out
 
 

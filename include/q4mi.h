@@ -469,6 +469,18 @@ size_t q4_prefill_prepared_bytes(int T, int64_t K, int x_dtype, int precision);
 int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, int precision,
                        void* prepared, size_t prepared_bytes, void* stream);
 
+/* The RMSNorm producer writing prepared activations directly (one launch): per token row
+ *   y  = x + add (f32 [T][K]; add and y optional; y may be x, no other overlap),
+ *   xn = bf16((y * r) * w), r = 1 / sqrt(mean(y^2) + eps) as q4_rmsnorm_add forms it,
+ * and `prepared` = q4_prefill_prepare of xn as bf16 (q4_prefill_prepared_bytes(T, K,
+ * Q4MI_BF16, precision) bytes): the same bits as q4_rmsnorm_add (bf16 xn) followed by
+ * q4_prefill_prepare, without the bf16 row in memory or the pre-pass launch. K % 32 == 0,
+ * K <= 16384; w [K] f32 or bf16 (w_dtype). Replaces the ln design in front of a prefill
+ * projection (designs/ln/ln.py:1-6, xn = bf16(y * rsqrt(mean(y^2) + eps) * w)) together with
+ * the host's pre-tiling of the GEMM's X (block_host.cpp:228-244). */
+int q4_rmsnorm_prepare(const float* x, const float* add, const void* w, int w_dtype, float* y, int T, int64_t K,
+                       float eps, int precision, void* prepared, size_t prepared_bytes, void* stream);
+
 /* Workspace of q4_gemm_prefill_prepared: the K-split partials only (0 when unsplit). */
 size_t q4_gemm_prefill_prepared_workspace_bytes(int T, int64_t N, int64_t K);
 

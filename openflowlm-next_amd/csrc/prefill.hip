@@ -39,6 +39,7 @@
 // banks.
 #include <stdlib.h>
 
+#include "norm_core.h"
 #include "q4mi_device.h"
 #include "q4mi_internal.h"
 
@@ -592,8 +593,9 @@ __global__ __launch_bounds__(256) void prefill_scale_write_kernel(const uint8_t*
 // rounded value; the two passes' products add up to the f32 activations' to ~2^-22.
 // One token row of prefill_xprep (all 256 threads): ld8(i, v) loads the row's 8-element
 // group i as f32 (zero: a padding row, written as zeros). F32SRC: the source is f32, so the
-// lo pass of PREC 0 writes the fp16 remainder.
-template <bool F32SRC, int PREC, bool TILED, class Load>
+// lo pass of PREC 0 writes the fp16 remainder. HELD: 8-element groups per thread kept in
+// registers between the max and the conversion (0: ld8 is called twice, for a row in LDS).
+template <bool F32SRC, int PREC, bool TILED, int HELD = 8, class Load>
 __device__ __forceinline__ void xprep_row(Load ld8, bool zero, uint16_t* __restrict__ x16, int* __restrict__ texp,
                                           int t, int K, int lo_pass) {
     const int n8 = K >> 3;                       // 8-element groups of the row (K % 32 == 0)
@@ -604,10 +606,10 @@ __device__ __forceinline__ void xprep_row(Load ld8, bool zero, uint16_t* __restr
         for (int i = threadIdx.x; i < n8; i += 256) out[dst(i)] = u32x4{0u, 0u, 0u, 0u};
         return;
     }
-    // Rows of up to 2048 chunks (K <= 16384) are read once and held in registers for both
-    // the max and the conversion; longer rows are read twice.
-    constexpr int kHeld = 8;
-    const bool held = n8 <= 256 * kHeld;
+    // Rows of up to 256 HELD chunks (K <= 16384 for the default) are read once and held in
+    // registers for both the max and the conversion; longer rows are read twice.
+    constexpr int kHeld = HELD > 0 ? HELD : 1;
+    const bool held = HELD > 0 && n8 <= 256 * HELD;
     float hv[kHeld][8];
     if (held) {
 #pragma unroll
@@ -697,6 +699,64 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
     const void* xrow = (const uint8_t*)x + (int64_t)t * K * (XF32 ? 4 : 2);
     xprep_row<XF32, PREC, TILED>([&](int i, float (&v)[8]) { load_x8<XF32>(xrow, i, v); }, t >= T, x16, texp, t,
                                  K, lo_pass);
+}
+
+// The RMSNorm producer writing the prefill's prepared activations directly: per token row t
+// (one workgroup; rows past T are the tile padding, written as zeros)
+//   y  = x + add (f32, stored when y is given; y may be x: the row is read before y is written),
+//   xn = bf16((y * r) * w) with r as q4_rmsnorm_add forms it (norm_core.h),
+// then xn goes through prefill_xprep's conversion (bf16 source) from an LDS copy of the row.
+// The same bits as q4_rmsnorm_add (bf16 xn) followed by q4_prefill_prepare(xn, bf16), with
+// one launch and no bf16 row in memory. PER values per thread (K <= 256 PER); extra j terms
+// are zeros, which leave the fp64 sum of squares unchanged.
+template <int PER, int PREC, bool TILED>
+__global__ __launch_bounds__(256) void rmsnorm_prepare_kernel(const float* x, const float* __restrict__ add,
+                                                              const void* __restrict__ w, int w_bf16, float* y,
+                                                              uint16_t* __restrict__ x16, int* __restrict__ texp,
+                                                              int T, int K, float eps) {
+    __shared__ double part[4];
+    __shared__ __attribute__((aligned(16))) uint16_t xs[256 * PER];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (t < T) {
+        const float* xr = x + (int64_t)t * K;
+        const float* ar = add ? add + (int64_t)t * K : nullptr;
+        float v[PER], wv[PER];
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = tid + 256 * j;
+            v[j] = i < K ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f;
+            wv[j] = i >= K ? 0.0f
+                           : (w_bf16 ? bf16_hi_to_f32((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j) ss += (double)v[j] * (double)v[j];
+        const double ws = wave_sum_ss(ss);
+        if ((tid & 63) == 0) part[tid >> 6] = ws;
+        __syncthreads();
+        if (y) {
+            float* yr = y + (int64_t)t * K;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int i = tid + 256 * j;
+                if (i < K) yr[i] = v[j];
+            }
+        }
+        const float r = inv_rms(part, K, eps);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = tid + 256 * j;
+            if (i < K) xs[i] = (uint16_t)f32_to_bf16_rne(v[j] * r * wv[j]);
+        }
+        __syncthreads();
+    }
+    xprep_row<false, PREC, TILED, 0>(            // the row sits in LDS: read it there twice
+        [&](int i, float (&o)[8]) {
+            const u32x4 wd = *(const u32x4*)(xs + 8 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[2 * e] = bf16_lo_to_f32(wd[e]), o[2 * e + 1] = bf16_hi_to_f32(wd[e]);
+        },
+        t >= T, x16, texp, t, K, 0);
 }
 
 // Kernel variants: (BN, BT, waves along N, waves along T, 32-K blocks per stage).
@@ -1106,6 +1166,48 @@ extern "C" int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, 
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
     }
     return Q4MI_OK;
+}
+
+extern "C" int q4_rmsnorm_prepare(const float* x, const float* add, const void* w, int w_dtype, float* y, int T,
+                                  int64_t K, float eps, int precision, void* prepared, size_t prepared_bytes_,
+                                  void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (w_dtype != Q4MI_F32 && w_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (T < 0 || K <= 0 || K % 32) return Q4MI_E_SHAPE;
+    if (K > 256 * 64) return Q4MI_E_RANGE;
+    if (!(eps >= 0.0f)) return Q4MI_E_ARG;
+    if (T == 0) return Q4MI_OK;
+    if (!x || !w || !prepared || misaligned16(prepared)) return Q4MI_E_ARG;
+    const size_t need = prepared_bytes(T, K, Q4MI_BF16, precision);
+    if (prepared_bytes_ < need) return Q4MI_E_WORKSPACE;
+    // y may be x itself, but no output may overlap another argument otherwise
+    auto overlaps = [](const void* a, size_t na, const void* b, size_t nb) {
+        const char *ca = (const char*)a, *cb = (const char*)b;
+        return a && b && ca < cb + nb && cb < ca + na;
+    };
+    const size_t row_bytes = (size_t)T * K * 4;
+    if (overlaps(prepared, need, x, row_bytes) || overlaps(prepared, need, add, row_bytes) ||
+        overlaps(prepared, need, y, row_bytes) || overlaps(prepared, need, w, (size_t)K * 4) ||
+        (y != x && overlaps(y, row_bytes, x, row_bytes)) || overlaps(y, row_bytes, add, row_bytes))
+        return Q4MI_E_ARG;
+    uint16_t* x16 = (uint16_t*)prepared;
+    int* te = (int*)((char*)prepared + x16_bytes(T, K));
+    const dim3 grid((unsigned)padded_tokens(T)), block(256);
+    const hipStream_t st = (hipStream_t)stream;
+    const int wb = w_dtype == Q4MI_BF16;
+    const bool tiled = K % 64 == 0, small = K <= 256 * 16;
+#define Q4MI_RP(PER, PR, TL)                                                                                   \
+    hipLaunchKernelGGL((rmsnorm_prepare_kernel<PER, PR, TL>), grid, block, 0, st, x, add, w, wb, y, x16, te, T, \
+                       (int)K, eps)
+    if (precision == 0) {
+        if (small) { if (tiled) Q4MI_RP(16, 0, true); else Q4MI_RP(16, 0, false); }
+        else { if (tiled) Q4MI_RP(64, 0, true); else Q4MI_RP(64, 0, false); }
+    } else {
+        if (small) { if (tiled) Q4MI_RP(16, 1, true); else Q4MI_RP(16, 1, false); }
+        else { if (tiled) Q4MI_RP(64, 1, true); else Q4MI_RP(64, 1, false); }
+    }
+#undef Q4MI_RP
+    return launch_status();
 }
 
 extern "C" size_t q4_gemm_prefill_prepared_workspace_bytes(int T, int64_t N, int64_t K) {

@@ -1112,6 +1112,43 @@ def prefill_prepare(x, precision: str = "fp16", out: torch.Tensor | None = None)
     return PreparedActs(data, T, K, _x_dtype(xt), precision)
 
 
+def rmsnorm_prepare(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None = None, eps: float = 1e-6,
+                    precision: str = "fp16", y: torch.Tensor | None = None,
+                    out: torch.Tensor | None = None) -> tuple[torch.Tensor, PreparedActs]:
+    """(y, prepared): the RMSNorm producer writing the prefill GEMM's prepared activations in
+    one launch -- y = x + add (f32 [T, K]; x itself when add is None and y is not given) and
+    prefill_prepare(bf16((y * rsqrt(mean(y^2) + eps)) * w)), bit for bit what rmsnorm_add
+    (bf16 out) followed by prefill_prepare gives (designs/ln/ln.py:1-6 in front of the
+    host's X tiling, block_host.cpp:228-244). ``w`` float32 or bfloat16 [K]; ``y`` may be
+    ``x``; K % 32 == 0, K <= 16384."""
+    if precision not in _PRECISION:
+        raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
+    if not isinstance(x, torch.Tensor) or x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() \
+            or x.dim() != 2:
+        raise TypeError("x must be a contiguous float32 [T, K] GPU tensor")
+    T, K = x.shape
+    dev = x.device
+    if K % 32 or K > 16384:
+        raise ValueError(f"K must be a multiple of 32 up to 16384, got {K}")
+    if w.numel() != K or w.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"w must be float32 or bfloat16 with {K} values")
+    wt = w.to(dev).contiguous()
+    if add is not None:
+        add = _buf(add, "add", torch.float32, (T, K), dev)
+    if y is not None or add is not None:
+        y = _buf(y, "y", torch.float32, (T, K), dev)
+    lib = _lib_handle()
+    nbytes = int(lib.q4_prefill_prepared_bytes(T, K, Q4MI_BF16, _PRECISION[precision])) if T else 0
+    data = _buf(out, "out", torch.uint8, (nbytes,), dev)
+    if T:
+        with torch.cuda.device(dev):
+            check("q4_rmsnorm_prepare", lib.q4_rmsnorm_prepare(
+                _ptr(x), None if add is None else _ptr(add), _ptr(wt),
+                Q4MI_BF16 if wt.dtype == torch.bfloat16 else Q4MI_F32, None if y is None else _ptr(y), T, K,
+                float(eps), _PRECISION[precision], _ptr(data), nbytes, _stream(dev)))
+    return (x if y is None else y), PreparedActs(data, T, K, Q4MI_BF16, precision)
+
+
 def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16",
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y[T, N] = X[T, K] @ W^T for a prefill block of T tokens, fp32 out.

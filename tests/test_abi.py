@@ -272,3 +272,27 @@ def test_deferred_reduction_argument_errors(lib):
     sw = lambda *a: lib.q4_gemv_swiglu_rmsnorm_acc(fake, fake, *a, None, 0, None)
     assert sw(res, part, 4, fake, 1, C.c_float(1e-6), xo, C.c_void_p(0x10000000), 1, 1, 14336, K) == -2  # h on res
     assert sw(res, part, -1, fake, 1, C.c_float(1e-6), xo, h, 1, 1, 14336, K) == -5
+
+
+def test_rmsnorm_prepare_argument_errors(lib):
+    """q4_rmsnorm_prepare refuses bad enums, shapes, sizes and overlapping outputs before any
+    launch."""
+    T, K = 256, 4096
+    need = lib.q4_prefill_prepared_bytes(T, K, 1, 0)
+    assert need > T * K * 2
+    x, add, w, y, prep = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4, 5))
+    call = lambda *a: lib.q4_rmsnorm_prepare(*a, None)
+    eps = C.c_float(1e-6)
+    assert call(x, add, w, 1, y, T, K, eps, 2, prep, need) == -2                     # precision
+    assert call(x, add, w, 7, y, T, K, eps, 0, prep, need) == -2                     # w dtype
+    assert call(x, add, w, 1, y, T, K + 16, eps, 0, prep, need) == -1                # K % 32
+    assert call(x, add, w, 1, y, -1, K, eps, 0, prep, need) == -1                    # T
+    assert call(x, add, w, 1, y, T, 16384 + 32, eps, 0, prep, need) == -5            # K > 16384
+    assert call(x, add, w, 1, y, T, K, C.c_float(-1.0), 0, prep, need) == -2         # eps
+    assert call(x, add, w, 1, y, 0, K, eps, 0, prep, need) == 0                      # nothing to do
+    assert call(None, add, w, 1, y, T, K, eps, 0, prep, need) == -2                  # NULL x
+    assert call(x, add, w, 1, y, T, K, eps, 0, C.c_void_p(0x50000008), need) == -2   # misaligned
+    assert call(x, add, w, 1, y, T, K, eps, 0, prep, need - 1) == -3                 # too small
+    assert call(x, add, w, 1, y, T, K, eps, 0, C.c_void_p(0x10000000 + 4096), need) == -2   # on x
+    assert call(x, add, w, 1, C.c_void_p(0x10000000 + 64), T, K, eps, 0, prep, need) == -2  # y partly on x
+    assert call(x, add, w, 1, C.c_void_p(0x20000000), T, K, eps, 0, prep, need) == -2      # y on add
