@@ -784,6 +784,32 @@ def extra_config3(torch, q4, dev):
                                             "same_bytes": bool(torch.equal(prep.data[:T * 4096 * 2],
                                                                            p2[:T * 4096 * 2]))}
         del prep, wsp, y, xr, ad, yb, xnb, p2
+    # the prefill FFN block with its producers writing the prepared activations: residual add
+    # + RMSNorm -> fused gate/up GEMM -> SwiGLU (bf16 h) -> down GEMM, four launches
+    dn = q4.pack_q4_1(gen_blocks(torch, 4096, 14336, gen, dev), dev)
+    q4.prefill_scales(dn)
+    for T in (512, 2048):
+        xr = torch.randn(T, 4096, generator=gen, device=dev)
+        ad = torch.randn(T, 4096, generator=gen, device=dev)
+        nw = (1 + 0.1 * torch.randn(4096, generator=gen, device=dev)).to(torch.bfloat16)
+        yb = torch.empty(T, 4096, device=dev)
+        p1 = torch.empty(q4.load_library().q4_prefill_prepared_bytes(T, 4096, 1, 0), dtype=torch.uint8, device=dev)
+        p2 = torch.empty(q4.load_library().q4_prefill_prepared_bytes(T, 14336, 1, 0), dtype=torch.uint8, device=dev)
+        y1 = torch.empty(T, 28672, device=dev)
+        y2 = torch.empty(T, 4096, device=dev)
+        w1 = torch.empty(max(q4.prefill_workspace_bytes(T, 28672, 4096), 256), dtype=torch.uint8, device=dev)
+        w2 = torch.empty(max(q4.prefill_workspace_bytes(T, 4096, 14336), 256), dtype=torch.uint8, device=dev)
+
+        def block():
+            _, a1 = q4.rmsnorm_prepare(xr, nw, add=ad, y=yb, out=p1)
+            q4.gemm_q4_prefill(gu, a1, y1, workspace=w1)
+            a2 = q4.swiglu_prepare(y1, out=p2)
+            q4.gemm_q4_prefill(dn, a2, y2, workspace=w2)
+        ms = graph_time(torch, block, [y2, yb], replays=5)
+        fl = 2.0 * T * (28672 * 4096 + 4096 * 14336)
+        out[f"T{T}_ffn_block"] = {"ms": ms, "gemm_tflops": fl / ms / 1e9, "frac_of_peak": fl / ms / 1e9 / MFMA_PEAK_TFLOPS,
+                                  "launches": 4}
+        del xr, ad, yb, p1, p2, y1, y2, w1, w2
     return out
 
 

@@ -481,6 +481,17 @@ int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, int precisi
 int q4_rmsnorm_prepare(const float* x, const float* add, const void* w, int w_dtype, float* y, int T, int64_t K,
                        float eps, int precision, void* prepared, size_t prepared_bytes, void* stream);
 
+/* The SwiGLU producer writing the down projection's prepared activations (one launch): per
+ * token row h[f] = bf16(silu(g[t][f]) * u[t][f]), silu(g) = g / (1 + exp(-g)), from f32 rows
+ * g and u with row strides ldg / ldu in elements (a fused [T][2F] gate/up output: u = g + F,
+ * ldg = ldu = 2F), and `prepared` = q4_prefill_prepare of h as bf16
+ * (q4_prefill_prepared_bytes(T, F, Q4MI_BF16, precision) bytes). h [T][F] bf16 is also
+ * stored when not NULL. F % 32 == 0, F <= 16384, strides % 4 == 0. Replaces the reference's
+ * bf16 SwiGLU between the FFN's GEMMs (moe_batch.h:181-202, mb_silu_tile) and the host's X
+ * tiling (block_host.cpp:228-244). */
+int q4_swiglu_prepare(const float* g, const float* u, int64_t ldg, int64_t ldu, int T, int64_t F, int precision,
+                      void* h, void* prepared, size_t prepared_bytes, void* stream);
+
 /* Workspace of q4_gemm_prefill_prepared: the K-split partials only (0 when unsplit). */
 size_t q4_gemm_prefill_prepared_workspace_bytes(int T, int64_t N, int64_t K);
 

@@ -759,6 +759,45 @@ __global__ __launch_bounds__(256) void rmsnorm_prepare_kernel(const float* x, co
         t >= T, x16, texp, t, K, 0);
 }
 
+// The SwiGLU producer writing the down projection's prepared activations: per token row t
+//   h[f] = bf16(silu(g[t][f]) * u[t][f]), silu(g) = g / (1 + exp(-g))
+// (the reference's h, moe_batch.h:181-202 mb_silu_tile; the decode kernels' silu), staged
+// in LDS and converted as prefill_xprep converts a bf16 row; h is also stored [T][F] when
+// h_out is given. g and u are f32 rows with strides ldg / ldu (one fused gate/up output:
+// u = g + F, both strides 2F). Rows past T are the tile padding (zeros).
+template <int PREC, bool TILED>
+__global__ __launch_bounds__(256) void swiglu_prepare_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                             int64_t ldg, int64_t ldu, uint16_t* __restrict__ h_out,
+                                                             uint16_t* __restrict__ x16, int* __restrict__ texp,
+                                                             int T, int F) {
+    __shared__ __attribute__((aligned(16))) uint16_t hs[256 * 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (t < T) {
+        const float* gr = g + (int64_t)t * ldg;
+        const float* ur = u + (int64_t)t * ldu;
+        for (int i = 4 * tid; i < F; i += 4 * 256) {
+            const f32x4 gv = *(const f32x4*)(gr + i), uv = *(const f32x4*)(ur + i);
+            uint32_t o[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float a = gv[2 * e] / (1.0f + expf(-gv[2 * e])) * uv[2 * e];
+                const float b = gv[2 * e + 1] / (1.0f + expf(-gv[2 * e + 1])) * uv[2 * e + 1];
+                o[e] = f32_to_bf16_rne(a) | (f32_to_bf16_rne(b) << 16);
+            }
+            *(uint2*)(hs + i) = make_uint2(o[0], o[1]);
+            if (h_out) *(uint2*)(h_out + (int64_t)t * F + i) = make_uint2(o[0], o[1]);
+        }
+        __syncthreads();
+    }
+    xprep_row<false, PREC, TILED, 0>(
+        [&](int i, float (&o)[8]) {
+            const u32x4 wd = *(const u32x4*)(hs + 8 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[2 * e] = bf16_lo_to_f32(wd[e]), o[2 * e + 1] = bf16_hi_to_f32(wd[e]);
+        },
+        t >= T, x16, texp, t, F, 0);
+}
+
 // Kernel variants: (BN, BT, waves along N, waves along T, 32-K blocks per stage).
 struct TileCfg {
     int bn, bt, wgn, wgt, ks;
@@ -1207,6 +1246,38 @@ extern "C" int q4_rmsnorm_prepare(const float* x, const float* add, const void* 
         else { if (tiled) Q4MI_RP(64, 1, true); else Q4MI_RP(64, 1, false); }
     }
 #undef Q4MI_RP
+    return launch_status();
+}
+
+extern "C" int q4_swiglu_prepare(const float* g, const float* u, int64_t ldg, int64_t ldu, int T, int64_t F,
+                                 int precision, void* h, void* prepared, size_t prepared_bytes_, void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (T < 0 || F <= 0 || F % 32 || ldg < F || ldu < F || ldg % 4 || ldu % 4) return Q4MI_E_SHAPE;
+    if (F > 256 * 64) return Q4MI_E_RANGE;
+    if (T == 0) return Q4MI_OK;
+    if (!g || !u || !prepared || misaligned16(g) || misaligned16(u) || misaligned16(prepared) || misaligned16(h))
+        return Q4MI_E_ARG;
+    const size_t need = prepared_bytes(T, F, Q4MI_BF16, precision);
+    if (prepared_bytes_ < need) return Q4MI_E_WORKSPACE;
+    auto overlaps = [](const void* a, size_t na, const void* b, size_t nb) {
+        const char *ca = (const char*)a, *cb = (const char*)b;
+        return a && b && ca < cb + nb && cb < ca + na;
+    };
+    const size_t gb = ((size_t)(T - 1) * ldg + F) * 4, ub = ((size_t)(T - 1) * ldu + F) * 4, hb = (size_t)T * F * 2;
+    if (overlaps(prepared, need, g, gb) || overlaps(prepared, need, u, ub) || overlaps(h, hb, g, gb) ||
+        overlaps(h, hb, u, ub) || overlaps(h, hb, prepared, need))
+        return Q4MI_E_ARG;
+    uint16_t* x16 = (uint16_t*)prepared;
+    int* te = (int*)((char*)prepared + x16_bytes(T, F));
+    const dim3 grid((unsigned)padded_tokens(T)), block(256);
+    const hipStream_t st = (hipStream_t)stream;
+    const bool tiled = F % 64 == 0;
+#define Q4MI_SP(PR, TL)                                                                                          \
+    hipLaunchKernelGGL((swiglu_prepare_kernel<PR, TL>), grid, block, 0, st, g, u, ldg, ldu, (uint16_t*)h, x16, te, \
+                       T, (int)F)
+    if (precision == 0) { if (tiled) Q4MI_SP(0, true); else Q4MI_SP(0, false); }
+    else { if (tiled) Q4MI_SP(1, true); else Q4MI_SP(1, false); }
+#undef Q4MI_SP
     return launch_status();
 }
 

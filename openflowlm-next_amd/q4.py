@@ -1149,6 +1149,44 @@ def rmsnorm_prepare(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None =
     return (x if y is None else y), PreparedActs(data, T, K, Q4MI_BF16, precision)
 
 
+def swiglu_prepare(g: torch.Tensor, u: torch.Tensor | None = None, precision: str = "fp16",
+                   out: torch.Tensor | None = None, h: torch.Tensor | None = None) -> PreparedActs:
+    """The SwiGLU producer writing the down projection's prepared activations in one launch:
+    h = bf16(silu(g) * u) per token row (moe_batch.h:181-202's h) and prefill_prepare(h),
+    bit for bit. ``g``, ``u`` float32 [T, F] row views (any row stride, unit column stride);
+    with ``u`` None, ``g`` is the fused [T, 2F] gate/up output and its halves are taken.
+    ``h`` (bf16 [T, F]) also receives h when given."""
+    if precision not in _PRECISION:
+        raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
+    if not isinstance(g, torch.Tensor) or g.dtype != torch.float32 or not g.is_cuda or g.dim() != 2:
+        raise TypeError("g must be a float32 [T, F] GPU tensor")
+    if u is None:
+        if g.shape[1] % 2:
+            raise ValueError("a fused gate/up output has an even number of columns")
+        F = g.shape[1] // 2
+        g, u = g[:, :F], g[:, F:]
+    if u.dtype != torch.float32 or u.device != g.device or u.shape != g.shape:
+        raise ValueError(f"u must be float32 {tuple(g.shape)} on {g.device}")
+    for name, t_ in (("g", g), ("u", u)):
+        if t_.stride(1) != 1 or t_.stride(0) % 4 or t_.data_ptr() % 16:
+            raise ValueError(f"{name} needs unit column stride, a row stride of 4k and 16-byte alignment")
+    T, F = g.shape
+    dev = g.device
+    if F % 32 or F > 16384:
+        raise ValueError(f"F must be a multiple of 32 up to 16384, got {F}")
+    if h is not None:
+        h = _buf(h, "h", torch.bfloat16, (T, F), dev)
+    lib = _lib_handle()
+    nbytes = int(lib.q4_prefill_prepared_bytes(T, F, Q4MI_BF16, _PRECISION[precision])) if T else 0
+    data = _buf(out, "out", torch.uint8, (nbytes,), dev)
+    if T:
+        with torch.cuda.device(dev):
+            check("q4_swiglu_prepare", lib.q4_swiglu_prepare(
+                _ptr(g), _ptr(u), g.stride(0), u.stride(0), T, F, _PRECISION[precision],
+                None if h is None else _ptr(h), _ptr(data), nbytes, _stream(dev)))
+    return PreparedActs(data, T, F, Q4MI_BF16, precision)
+
+
 def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16",
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y[T, N] = X[T, K] @ W^T for a prefill block of T tokens, fp32 out.

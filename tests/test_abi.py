@@ -296,3 +296,24 @@ def test_rmsnorm_prepare_argument_errors(lib):
     assert call(x, add, w, 1, y, T, K, eps, 0, C.c_void_p(0x10000000 + 4096), need) == -2   # on x
     assert call(x, add, w, 1, C.c_void_p(0x10000000 + 64), T, K, eps, 0, prep, need) == -2  # y partly on x
     assert call(x, add, w, 1, C.c_void_p(0x20000000), T, K, eps, 0, prep, need) == -2      # y on add
+
+
+def test_swiglu_prepare_argument_errors(lib):
+    """q4_swiglu_prepare refuses bad enums, shapes, strides, sizes and overlapping outputs
+    before any launch."""
+    T, F = 256, 14336
+    need = lib.q4_prefill_prepared_bytes(T, F, 1, 0)
+    g, u, h, prep = (C.c_void_p(0x100000000 * i) for i in (1, 2, 3, 4))
+    call = lambda *a: lib.q4_swiglu_prepare(*a, None)
+    assert call(g, u, F, F, T, F, 2, h, prep, need) == -2                         # precision
+    assert call(g, u, F, F, T, F + 16, 0, h, prep, need) == -1                    # F % 32
+    assert call(g, u, F - 32, F, T, F, 0, h, prep, need) == -1                    # ldg < F
+    assert call(g, u, F, F + 2, T, F, 0, h, prep, need) == -1                     # ldu % 4
+    assert call(g, u, F, F, -1, F, 0, h, prep, need) == -1                        # T
+    assert call(g, u, 16416, 16416, T, 16416, 0, h, prep, need) == -5             # F > 16384
+    assert call(g, u, F, F, 0, F, 0, h, prep, need) == 0                          # nothing to do
+    assert call(None, u, F, F, T, F, 0, h, prep, need) == -2                      # NULL g
+    assert call(g, u, F, F, T, F, 0, C.c_void_p(0x300000008), prep, need) == -2   # misaligned h
+    assert call(g, u, F, F, T, F, 0, h, prep, need - 1) == -3                     # too small
+    assert call(g, u, F, F, T, F, 0, h, C.c_void_p(0x100000000 + 4096), need) == -2   # on g
+    assert call(g, u, F, F, T, F, 0, C.c_void_p(0x200000000 + 64), prep, need) == -2  # h on u

@@ -1,6 +1,8 @@
-"""The RMSNorm producer that writes the prefill GEMM's prepared activations in one launch
-(q4_rmsnorm_prepare): the same bytes as q4_rmsnorm_add (bf16 out) followed by
-q4_prefill_prepare, padding rows and token exponents included, and the same GEMM bits."""
+"""The producers that write the prefill GEMM's prepared activations in one launch: the
+RMSNorm in front of gate/up (q4_rmsnorm_prepare: the same bytes as q4_rmsnorm_add (bf16
+out) followed by q4_prefill_prepare, padding rows and token exponents included, and the
+same GEMM bits) and the SwiGLU in front of down (q4_swiglu_prepare: h = bf16(silu(g) u)
+and the bytes q4_prefill_prepare makes from it)."""
 from __future__ import annotations
 
 import numpy as np
@@ -66,3 +68,55 @@ def test_rmsnorm_prepare_y_may_be_x(gpu, pkg):
     assert y.data_ptr() == xx.data_ptr()
     assert torch.equal(xx, y_ref)
     assert torch.equal(prep.data, prep_ref.data)
+
+
+@pytest.mark.parametrize("T,F", [(1, 14336), (300, 14336), (257, 4128), (40, 96)])
+@pytest.mark.parametrize("precision", ["fp16", "bf16"])
+@pytest.mark.parametrize("fused", [False, True])
+def test_swiglu_prepare_equals_swiglu_then_prepare(gpu, pkg, T, F, precision, fused):
+    """h = bf16(silu(g) u) within one bf16 rounding of torch's, and the prepared image the
+    bytes q4_prefill_prepare makes from that h; g and u as separate rows or the two halves of
+    one fused gate/up output."""
+    say(f"swiglu_prepare T={T} F={F} {precision} fused={fused}")
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(T + F)
+    if fused:
+        gu = torch.randn(T, 2 * F, generator=gen, device=gpu) * 4.0
+        g, u = gu[:, :F], gu[:, F:]
+    else:
+        g = torch.randn(T, F, generator=gen, device=gpu) * 4.0
+        u = torch.randn(T, F, generator=gen, device=gpu)
+    lib = pkg.load_library()
+    nbytes = int(lib.q4_prefill_prepared_bytes(T, F, 1, 0 if precision == "fp16" else 1))
+    h = torch.empty(T, F, dtype=torch.bfloat16, device=gpu)
+    prep = pkg.swiglu_prepare(gu if fused else g, None if fused else u, precision=precision,
+                              out=torch.zeros(nbytes, dtype=torch.uint8, device=gpu), h=h)
+    ref = pkg.prefill_prepare(h, precision, out=torch.zeros(nbytes, dtype=torch.uint8, device=gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(prep.data, ref.data), "prepared bytes differ from prefill_prepare(h)"
+    want = (g.double() / (1 + torch.exp(-g.double())) * u.double())
+    got = h.double()
+    # one RNE to bf16 of an f32 value within a few ulp of the fp64 one: <= 2^-8 relative
+    err = ((got - want).abs() / want.abs().clamp_min(1e-30))
+    assert float(err.max()) <= 2.0 ** -8 + 1e-6
+    exact = (got == want.float().to(torch.bfloat16).double()).float().mean().item()
+    assert exact >= 0.999
+
+
+def test_swiglu_prepare_feeds_the_down_gemm(gpu, pkg, oracle):
+    """down over the SwiGLU producer's prepared activations: the GEMM bits of the same h
+    given as bf16 rows, and within 1e-3 of the fp64 reference on that h."""
+    say("swiglu_prepare -> down GEMM")
+    T, F, N = 300, 4096, 256
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(11)
+    gu = torch.randn(T, 2 * F, generator=gen, device=gpu) * 3.0
+    h = torch.empty(T, F, dtype=torch.bfloat16, device=gpu)
+    prep = pkg.swiglu_prepare(gu, h=h)
+    blocks = oracle.baseline_q4_1_blocks(N, F, np.random.default_rng(3))
+    w = pkg.pack_q4_1(blocks, gpu)
+    a = pkg.gemm_q4_prefill(w, prep).cpu().numpy()
+    b = pkg.gemm_q4_prefill(w, h).cpu().numpy()
+    assert a.tobytes() == b.tobytes()
+    ref = oracle.gemv_reference(blocks, h.float().cpu().numpy())
+    assert oracle.maxrel(a, ref) <= 1e-3
