@@ -492,6 +492,17 @@ int q4_rmsnorm_prepare(const float* x, const float* add, const void* w, int w_dt
 int q4_swiglu_prepare(const float* g, const float* u, int64_t ldg, int64_t ldu, int T, int64_t F, int precision,
                       void* h, void* prepared, size_t prepared_bytes, void* stream);
 
+/* The FFN's gate/up prefill GEMM with SwiGLU in its epilogue: h[T][F] bf16 =
+ * bf16(silu(X . G^T) * (X . U^T)) from prepared activations (one activation pass: bf16 x, or
+ * precision 1), over gate_up, an mx matrix [2F, K] whose 64-row groups alternate gate / up
+ * (the q4_moe_gemv expert layout), with its prefill scales for precision 0 (q4_prefill_scales
+ * of that matrix). Each h is what q4_swiglu_prepare forms from the plain GEMM's f32 gate and
+ * up outputs (the same GEMM bits where that GEMM's plan is unsplit), without the f32 output
+ * in memory. 256-row tiles, no K split. F % 128 == 0, K % 64 == 0. Replaces the reference's
+ * gate/up prefill dispatches and the bf16 SwiGLU after them (moe_batch.h:181-202). */
+int q4_gemm_prefill_swiglu(const uint8_t* gate_up, const void* scales, const void* prepared, int x_dtype, void* h,
+                           int T, int64_t F, int64_t K, int precision, void* stream);
+
 /* Workspace of q4_gemm_prefill_prepared: the K-split partials only (0 when unsplit). */
 size_t q4_gemm_prefill_prepared_workspace_bytes(int T, int64_t N, int64_t K);
 

@@ -122,6 +122,45 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[FN][FT], float* __
     }
 }
 
+// The SwiGLU epilogue of the gate/up GEMM over an interleaved matrix (per 128-row pair p,
+// 64 gate rows of F, then the same 64 rows of up: N = 2F). A 256-row tile's wave holds one
+// pair, fragments 0..3 gate and 4..7 up at the same lane positions, so
+// h = bf16(silu(g) * u) (q4_swiglu_prepare's arithmetic) is formed from the accumulators and
+// only h [T][F] bf16 is stored: the f32 gate/up output never reaches memory.
+template <int FT, bool SCALED>
+__device__ __forceinline__ void store_swiglu(const f32x4 (&acc)[8][FT], uint16_t* __restrict__ h,
+                                             const int* __restrict__ texp, const int* __restrict__ wexp, int T, int N,
+                                             int wt0, int wn0) {
+    const int lane = threadIdx.x & 63, i16 = lane & 15, kg = lane >> 4;
+    const int F = N >> 1, f0 = wn0 >> 1;          // wn0 = 128 p: gate rows from 64 p
+#pragma unroll
+    for (int j = 0; j < FT; ++j) {
+        const int t = wt0 + j * 16 + i16;
+        if (t >= T) continue;
+        const int st = SCALED ? texp[t] : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ng = wn0 + i * 16 + kg * 4;
+            f32x4 g = acc[i][j], u = acc[i + 4][j];
+            if constexpr (SCALED) {
+                const int4 eg = *(const int4*)(wexp + ng), eu = *(const int4*)(wexp + ng + 64);
+                g[0] = ldexpf(g[0], st + eg.x), g[1] = ldexpf(g[1], st + eg.y);
+                g[2] = ldexpf(g[2], st + eg.z), g[3] = ldexpf(g[3], st + eg.w);
+                u[0] = ldexpf(u[0], st + eu.x), u[1] = ldexpf(u[1], st + eu.y);
+                u[2] = ldexpf(u[2], st + eu.z), u[3] = ldexpf(u[3], st + eu.w);
+            }
+            uint32_t o[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float a = g[2 * e] / (1.0f + expf(-g[2 * e])) * u[2 * e];
+                const float b = g[2 * e + 1] / (1.0f + expf(-g[2 * e + 1])) * u[2 * e + 1];
+                o[e] = f32_to_bf16_rne(a) | (f32_to_bf16_rne(b) << 16);
+            }
+            *(uint2*)(h + (int64_t)t * F + f0 + i * 16 + kg * 4) = make_uint2(o[0], o[1]);
+        }
+    }
+}
+
 // BN x BT workgroup tile, WGN x WGT waves (wave tile BN/WGN x BT/WGT), KS
 // 32-K blocks per LDS stage.
 template <int BN, int BT, int WGN, int WGT, int KS, int PREC>
@@ -311,13 +350,14 @@ __device__ __forceinline__ void vgpr_landed(u32x4& v) { asm volatile("" : "+v"(v
 // tile's loads, DMA and dequant unchanged: the waves of row group 3 load row group 2's mx
 // tile again and store it to LDS rows 192..255, which no fragment reads, so every wave
 // issues the same loads and the wait counts below hold for both.
-template <int PREC, int FN>
+template <int PREC, int FN, bool SWI = false>
 __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict__ packed,
                                          const uint16_t* __restrict__ x16, const int* __restrict__ texp,
                                          const int* __restrict__ wexp, const uint32_t* __restrict__ s16,
                                          float* __restrict__ y, int T, int N, int K, int n0, int bt, int split,
                                          int splits, int accum) {
     static_assert(FN == 8 || FN == 6, "256- or 192-row tiles");
+    static_assert(!SWI || FN == 8, "the SwiGLU epilogue pairs a 256-row tile's gate and up halves");
     constexpr int WN = 16 * FN, WT = 64, FT = WT / 16, RG = FN / 2;
     typedef typename std::conditional<PREC == 0, f16x8, bf16x8>::type frag_t;
 
@@ -476,7 +516,10 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
     if (st + 3 < NST) stage(I3{}, st + 3);
     if (st + 4 < NST) stage(I4{}, st + 4);
 
-    store_tile<FN, FT, PREC == 0>(acc, y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN, accum);
+    if constexpr (SWI)
+        store_swiglu<FT, PREC == 0>(acc, (uint16_t*)y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN);
+    else
+        store_tile<FN, FT, PREC == 0>(acc, y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN, accum);
 }
 
 // Workgroups [0, wide_wgs) take the 256-row tiles of rows [0, narrow_row0), the rest the
@@ -502,6 +545,22 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const uint8_t* __restr
         dma_tile<PREC, 6>(lds, packed, x16, texp, wexp, s16, y, T, N, K, narrow_row0 + (tile / tiles_t) * 192,
                           tile % tiles_t, i % splits, splits, accum);
     }
+}
+
+// The gate/up GEMM with the SwiGLU epilogue: workgroup b takes the 256-row tile of pair rows
+// (b / tiles_t) * 256 and token tile b % tiles_t over all of K (no split), writing h.
+template <int PREC>
+__global__ __launch_bounds__(512) void prefill_swiglu_kernel(const uint8_t* __restrict__ packed,
+                                                             const uint16_t* __restrict__ x16,
+                                                             const int* __restrict__ texp,
+                                                             const int* __restrict__ wexp,
+                                                             const uint32_t* __restrict__ s16,
+                                                             uint16_t* __restrict__ h, int T, int N, int K,
+                                                             int tiles_t) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
+    const int b = blockIdx.x;
+    dma_tile<PREC, 8, true>(lds, packed, x16, texp, wexp, s16, (float*)h, T, N, K, (b / tiles_t) * 256, b % tiles_t,
+                            0, 1, 0);
 }
 
 // The exponent that puts a positive finite magnitude v in [2^14, 2^15) after scaling by
@@ -1278,6 +1337,33 @@ extern "C" int q4_swiglu_prepare(const float* g, const float* u, int64_t ldg, in
     if (precision == 0) { if (tiled) Q4MI_SP(0, true); else Q4MI_SP(0, false); }
     else { if (tiled) Q4MI_SP(1, true); else Q4MI_SP(1, false); }
 #undef Q4MI_SP
+    return launch_status();
+}
+
+extern "C" int q4_gemm_prefill_swiglu(const uint8_t* gate_up, const void* scales, const void* prepared, int x_dtype,
+                                      void* h, int T, int64_t F, int64_t K, int precision, void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
+    if (activation_passes(x_dtype, precision) != 1) return Q4MI_E_ARG;   // f32 x in precision 0: two passes
+    if (T < 0 || F <= 0 || K <= 0 || F % 128 || K % 64) return Q4MI_E_SHAPE;
+    if (2 * F > 0x7FFFFFFF || K > 0x7FFFFFFF) return Q4MI_E_RANGE;
+    if (T == 0) return Q4MI_OK;
+    if (!gate_up || !prepared || !h || misaligned16(gate_up) || misaligned16(prepared) || misaligned16(h))
+        return Q4MI_E_ARG;
+    if (precision == 0 && (!scales || misaligned16(scales))) return Q4MI_E_ARG;
+    const int64_t N = 2 * F;
+    const int* we = precision == 0 ? (const int*)scales : nullptr;
+    const uint32_t* s16 = precision == 0 ? (const uint32_t*)((const char*)scales + scales_wexp_bytes(N)) : nullptr;
+    const int* te = (const int*)((const char*)prepared + x16_bytes(T, K));
+    const int tiles_t = (int)ceil_div(T, 256);
+    const dim3 grid((unsigned)((N / 256) * tiles_t)), block(512);
+    const hipStream_t st = (hipStream_t)stream;
+    if (precision == 0)
+        hipLaunchKernelGGL(prefill_swiglu_kernel<0>, grid, block, 0, st, gate_up, (const uint16_t*)prepared, te, we,
+                           s16, (uint16_t*)h, T, (int)N, (int)K, tiles_t);
+    else
+        hipLaunchKernelGGL(prefill_swiglu_kernel<1>, grid, block, 0, st, gate_up, (const uint16_t*)prepared, nullptr,
+                           nullptr, nullptr, (uint16_t*)h, T, (int)N, (int)K, tiles_t);
     return launch_status();
 }
 

@@ -1187,6 +1187,49 @@ def swiglu_prepare(g: torch.Tensor, u: torch.Tensor | None = None, precision: st
     return PreparedActs(data, T, F, Q4MI_BF16, precision)
 
 
+def interleave_gate_up(gate: PackedQ4, up: PackedQ4) -> PackedQ4:
+    """One mx matrix [2F, K] whose 64-row groups alternate gate / up (a device copy of the two
+    matrices' row groups): the layout gemm_q4_prefill_swiglu and the MoE experts take."""
+    if gate.n != up.n or gate.k != up.k or gate.device != up.device:
+        raise ValueError("gate and up must have the same shape and device")
+    rg = gate.nbytes // (gate.n // 64)
+    g = gate.data[:gate.nbytes].view(gate.n // 64, rg)
+    u = up.data[:up.nbytes].view(up.n // 64, rg)
+    return PackedQ4(torch.stack((g, u), 1).reshape(-1), 2 * gate.n, gate.k)
+
+
+def gemm_q4_prefill_swiglu(gate_up: PackedQ4, x, h: torch.Tensor | None = None,
+                           precision: str = "fp16") -> torch.Tensor:
+    """h [T, F] bf16 = bf16(silu(X G^T) * (X U^T)): the FFN's gate/up prefill GEMM with the
+    SwiGLU in its epilogue (moe_batch.h:181-202's bf16 h), over an interleaved gate/up matrix
+    (interleave_gate_up) and bf16 or prepared activations; the same h swiglu_prepare forms
+    from the plain GEMM's f32 outputs, with no f32 output in memory. F % 128 == 0, K % 64 == 0."""
+    dev = gate_up.device
+    if isinstance(x, PreparedActs):
+        precision = x.precision
+        prep = x
+    else:
+        xt = _acts(x, dev)
+        if xt.dtype != torch.bfloat16 and precision == "fp16":
+            raise ValueError("the SwiGLU epilogue takes one activation pass: bf16 x, or precision 'bf16'")
+        prep = prefill_prepare(xt, precision)
+    if precision not in _PRECISION:
+        raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
+    if prep.k != gate_up.k:
+        raise ValueError(f"x has K={prep.k}, W is [{gate_up.n}, {gate_up.k}]")
+    T, F = prep.t, gate_up.n // 2
+    if F % 128 or gate_up.k % 64:
+        raise ValueError(f"the SwiGLU epilogue needs F % 128 == 0 and K % 64 == 0, got F={F}, K={gate_up.k}")
+    h = _buf(h, "h", torch.bfloat16, (T, F), dev)
+    sc = prefill_scales(gate_up) if precision == "fp16" else None
+    if T:
+        with torch.cuda.device(dev):
+            check("q4_gemm_prefill_swiglu", _lib_handle().q4_gemm_prefill_swiglu(
+                _ptr(gate_up.data), None if sc is None else _ptr(sc), _ptr(prep.data), prep.x_dtype, _ptr(h), T, F,
+                gate_up.k, _PRECISION[precision], _stream(dev)))
+    return h
+
+
 def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16",
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y[T, N] = X[T, K] @ W^T for a prefill block of T tokens, fp32 out.

@@ -317,3 +317,17 @@ def test_swiglu_prepare_argument_errors(lib):
     assert call(g, u, F, F, T, F, 0, h, prep, need - 1) == -3                     # too small
     assert call(g, u, F, F, T, F, 0, h, C.c_void_p(0x100000000 + 4096), need) == -2   # on g
     assert call(g, u, F, F, T, F, 0, C.c_void_p(0x200000000 + 64), prep, need) == -2  # h on u
+
+
+def test_gemm_prefill_swiglu_argument_errors(lib):
+    """q4_gemm_prefill_swiglu refuses two-pass activations and shapes the epilogue cannot pair
+    before any launch."""
+    gu, sc, prep, h = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4))
+    call = lambda *a: lib.q4_gemm_prefill_swiglu(*a, None)
+    assert call(gu, sc, prep, 1, h, 256, 14336, 4096, 2) == -2        # precision
+    assert call(gu, sc, prep, 0, h, 256, 14336, 4096, 0) == -2        # f32 x, precision 0: two passes
+    assert call(gu, sc, prep, 1, h, 256, 14336 + 64, 4096, 0) == -1   # F % 128
+    assert call(gu, sc, prep, 1, h, 256, 14336, 4096 + 32, 0) == -1   # K % 64
+    assert call(gu, sc, prep, 1, h, 0, 14336, 4096, 0) == 0           # nothing to do
+    assert call(gu, None, prep, 1, h, 256, 14336, 4096, 0) == -2      # precision 0 needs scales
+    assert call(gu, sc, prep, 1, C.c_void_p(0x40000008), 256, 14336, 4096, 0) == -2   # misaligned h

@@ -110,14 +110,16 @@ def test_prefill_loop_waits_cover_every_asm_load(tmp_path):
                 n, bad = early_uses_in(body)
                 assert n >= 6, f"{what}: expected the weight loads of the unrolled loop, found {n}"
                 assert not bad, f"{what}: registers used before their load's wait: {bad[:3]}"
-        # the grouped expert GEMM's tile loop
-        start = next(i for i, l in enumerate(text) if re.match(rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}EE\w*:", l))
-        stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
-        loops = inner_loops(text[start:stop])
-        assert len(loops) == 1, f"moe precision {prec}: expected 1 tile loop, found {len(loops)}"
-        for body in loops:
-            n, bad = early_uses_in(body)
-            assert n >= 6 and not bad, f"moe precision {prec}: {n} loads, early uses {bad[:3]}"
+        # the grouped expert GEMM's tile loop and the gate/up GEMM with the SwiGLU epilogue
+        for kname, what in ((rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}EE", "moe"),
+                            (rf"_ZN12_GLOBAL__N_121prefill_swiglu_kernelILi{prec}EE", "swiglu")):
+            start = next(i for i, l in enumerate(text) if re.match(kname + r"\w*:", l))
+            stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
+            loops = inner_loops(text[start:stop])
+            assert len(loops) == 1, f"{what} precision {prec}: expected 1 tile loop, found {len(loops)}"
+            for body in loops:
+                n, bad = early_uses_in(body)
+                assert n >= 6 and not bad, f"{what} precision {prec}: {n} loads, early uses {bad[:3]}"
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
