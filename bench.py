@@ -898,15 +898,18 @@ def extra_moe_prefill(torch, q4, dev):
         flops = 2.0 * T * K8 * 3 * H * F
         wbytes = len(np.unique(ids)) * (gb + db)
         rec = {"pairs": T * K8, "distinct_experts": int(len(np.unique(ids)))}
-        paths = [("prefill_fp16", "prefill", "fp16"), ("prefill_bf16", "prefill", "bf16")]
+        # prefill_fp16_bf16h: the fp16 tile with h rounded to bf16 (the reference kernel's h): one
+        # down pass instead of the f32 h's value and remainder passes
+        paths = [("prefill_fp16", "prefill", "fp16", False), ("prefill_fp16_bf16h", "prefill", "fp16", True),
+                 ("prefill_bf16", "prefill", "bf16", False)]
         if T * K8 <= q4.MOE_DECODE_MAX_PAIRS:
-            paths.append(("decode", "decode", "fp16"))
-        for name, path, prec in paths:
+            paths.append(("decode", "decode", "fp16", False))
+        for name, path, prec, hb in paths:
             ws = torch.empty(max(q4.moe_prefill_workspace_bytes(T, E, K8, H, F) if path == "prefill"
                                  else q4.moe_workspace_bytes(T, E, K8, H, F), 256), dtype=torch.uint8, device=dev)
-            q4.moe_batch(gup, dnp, x, ids_t, w_t, y, workspace=ws, path=path, precision=prec)   # scales, once
+            q4.moe_batch(gup, dnp, x, ids_t, w_t, y, workspace=ws, path=path, precision=prec, h_bf16=hb)  # scales
             ms = graph_time(torch, lambda: q4.moe_batch(gup, dnp, x, ids_t, w_t, y, workspace=ws, path=path,
-                                                        precision=prec), [y], replays=10)
+                                                        precision=prec, h_bf16=hb), [y], replays=10)
             rec[name] = {"us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1),
                          "weight_gbs": round(wbytes / ms / 1e6, 1)}
             del ws

@@ -543,7 +543,9 @@ size_t q4_moe_prefill_workspace_bytes(int T, int E, int topk, int H, int F);
  * precision 0: fp16 tiles with power-of-two scaling as q4_gemm_prefill precision 0, with
  * gate_up_scales / down_scales = q4_prefill_scales of the stacked matrices ([E 2F, H] and
  * [E H, F]); f32 x and h go in two passes (value and remainder). precision 1: the reference's
- * bf16 tile RNE(q d + m), x and h rounded to bf16 (scales may be NULL).
+ * bf16 tile RNE(q d + m), x and h rounded to bf16 (scales may be NULL). precision 2: the fp16
+ * tile of precision 0 with h rounded to bf16 as the reference's kernel rounds it, so down
+ * takes one pass (scales as precision 0).
  * H % 256 == 0, F % 128 == 0, 1 <= topk <= 16, T * topk <= 2^22, E <= 8192.
  * Replaces the host loop over expert dispatches of 256 slots (Core::moe_block,
  * core.cpp:5163-5178; moe_batch.h:98-172 mb_step_parity / mb_step_tile, h in bf16 as

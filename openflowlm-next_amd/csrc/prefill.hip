@@ -1614,8 +1614,9 @@ __global__ __launch_bounds__(256) void moe_xprep_kernel(const void* __restrict__
 }
 
 // h[f] = silu(g[f]) u[f] of slot t from G[t][2F], where the 64 gate rows of row group j are
-// columns 128 j .. 128 j + 63 and its up rows the next 64.
-template <int PREC>
+// columns 128 j .. 128 j + 63 and its up rows the next 64. HB16 (PREC 0): h rounded to bf16
+// first (the reference's h, moe_batch.h:181-202), so the fp16 tile takes it in one pass.
+template <int PREC, bool HB16 = false>
 __global__ __launch_bounds__(256) void moe_hprep_kernel(const float* __restrict__ G, const int* __restrict__ rowmap,
                                                         const int* __restrict__ meta, uint16_t* __restrict__ x16,
                                                         int* __restrict__ texp, int F, int lo_pass) {
@@ -1631,13 +1632,30 @@ __global__ __launch_bounds__(256) void moe_hprep_kernel(const float* __restrict_
             v[e] = g0[e] / (1.0f + expf(-g0[e])) * u0[e];
             v[e + 4] = g1[e] / (1.0f + expf(-g1[e])) * u1[e];
         }
+        if constexpr (HB16) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = bf16_hi_to_f32(f32_to_bf16_rne(v[e]) << 16);
+        }
     };
-    xprep_row_wave<true, PREC>(ld8, rowmap[t] < 0, x16, texp, t, F, lo_pass);
+    xprep_row_wave<!HB16, PREC>(ld8, rowmap[t] < 0, x16, texp, t, F, lo_pass);
+}
+
+// Slot t's bf16 h row (from the gate/up GEMM's SwiGLU epilogue, h[S][F]) into down's 16-bit
+// layout; pad slots (rowmap < 0) as zeros.
+template <int PREC>
+__global__ __launch_bounds__(256) void moe_h16prep_kernel(const uint16_t* __restrict__ h,
+                                                          const int* __restrict__ rowmap, const int* __restrict__ meta,
+                                                          uint16_t* __restrict__ x16, int* __restrict__ texp, int F) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= meta[0] * 256) return;
+    const uint16_t* hrow = h + (int64_t)t * F;
+    xprep_row_wave<false, PREC>([&](int i, float (&v)[8]) { load_x8<false>(hrow, i, v); }, rowmap[t] < 0, x16, texp,
+                                t, F, 0);
 }
 
 // Workgroup (token tile tt, 256-row tile rt) of a grouped expert GEMM: dma_tile on tile tt's
 // expert's matrix (N rows, ebytes each expert), slots [256 tt, tile_end) valid.
-template <int PREC>
+template <int PREC, bool SWI = false>
 __global__ __launch_bounds__(512) void moe_dma_kernel(const uint8_t* __restrict__ packed, int64_t ebytes,
                                                       const uint16_t* __restrict__ x16,
                                                       const int* __restrict__ texp, const int* __restrict__ wexp,
@@ -1649,8 +1667,9 @@ __global__ __launch_bounds__(512) void moe_dma_kernel(const uint8_t* __restrict_
     const int b = blockIdx.x, tt = b / tiles_n, rt = b % tiles_n;
     if (tt >= meta[0]) return;
     const int e = tile_e[tt];
-    dma_tile<PREC, 8>(lds, packed + e * ebytes, x16, texp, PREC == 0 ? wexp + (int64_t)e * N : nullptr,
-                      PREC == 0 ? s16 + e * s16_words : nullptr, y, tile_end[tt], N, K, rt * 256, tt, 0, 1, accum);
+    dma_tile<PREC, 8, SWI>(lds, packed + e * ebytes, x16, texp, PREC == 0 ? wexp + (int64_t)e * N : nullptr,
+                           PREC == 0 ? s16 + e * s16_words : nullptr, y, tile_end[tt], N, K, rt * 256, tt, 0, 1,
+                           accum);
 }
 
 // out[t][n..n+3] = sum_j w[t][j] Y[slot(t, j)][n..n+3], slot order j.
@@ -1718,7 +1737,10 @@ extern "C" int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const
                               const void* down_scales, const void* x, int x_dtype, const int32_t* topk_ids,
                               const float* topk_w, float* out, int T, int E, int topk, int64_t H, int64_t F,
                               int precision, void* workspace, size_t workspace_bytes, void* stream) {
-    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (precision < 0 || precision > 2) return Q4MI_E_ARG;
+    // precision 2: the fp16 tile of precision 0 with h rounded to bf16 (one down pass)
+    const bool hb16 = precision != 0;
+    precision = precision == 2 ? 0 : precision;
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
     if (H <= 0 || F <= 0 || H % 256 || F % 128) return Q4MI_E_SHAPE;
     if (H > (1 << 20) || F > (1 << 20)) return Q4MI_E_RANGE;
@@ -1769,6 +1791,7 @@ extern "C" int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const
 
     // gate/up: G = X . [gate; up]^T per expert
     const int xpasses = precision == 0 && xf32 ? 2 : 1;
+    const bool swi = hb16 && xpasses == 1;
     for (int pass = 0; pass < xpasses; ++pass) {
         if (xf32) {
             if (precision == 0)
@@ -1786,7 +1809,15 @@ extern "C" int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const
                                    texp, (int)H, pass);
         }
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
-        if (precision == 0)
+        // bf16 h from one activation pass: SwiGLU in the gate/up epilogue, h [S][F] bf16 in
+        // the G/Y buffer (G itself is never written)
+        if (swi && precision == 0)
+            hipLaunchKernelGGL((moe_dma_kernel<0, true>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1,
+                               sw1, gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), 0);
+        else if (swi)
+            hipLaunchKernelGGL((moe_dma_kernel<1, true>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1,
+                               sw1, gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), 0);
+        else if (precision == 0)
             hipLaunchKernelGGL((moe_dma_kernel<0>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1, sw1,
                                gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), pass);
         else
@@ -1796,10 +1827,19 @@ extern "C" int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const
     }
     // h = silu(g) u into the 16-bit layout (precision 0: value and remainder planes, both
     // made before the down GEMM overwrites G with Y)
-    const int hpasses = precision == 0 ? 2 : 1;
+    const int hpasses = precision == 0 && !hb16 ? 2 : 1;
     uint16_t* h16[2] = {x16, x16 + (size_t)S * F};
     for (int pass = 0; pass < hpasses; ++pass) {
-        if (precision == 0)
+        if (swi && precision == 0)
+            hipLaunchKernelGGL((moe_h16prep_kernel<0>), dim3(SP), dim3(256), 0, st, (const uint16_t*)gy, rowmap, meta,
+                               h16[0], texp, (int)F);
+        else if (swi)
+            hipLaunchKernelGGL((moe_h16prep_kernel<1>), dim3(SP), dim3(256), 0, st, (const uint16_t*)gy, rowmap, meta,
+                               h16[0], texp, (int)F);
+        else if (precision == 0 && hb16)
+            hipLaunchKernelGGL((moe_hprep_kernel<0, true>), dim3(SP), dim3(256), 0, st, gy, rowmap, meta, h16[pass],
+                               texp, (int)F, 0);
+        else if (precision == 0)
             hipLaunchKernelGGL((moe_hprep_kernel<0>), dim3(SP), dim3(256), 0, st, gy, rowmap, meta, h16[pass], texp,
                                (int)F, pass);
         else

@@ -1316,7 +1316,8 @@ MOE_DECODE_MAX_PAIRS = 4096        # T * topk the decode kernels take (q4_moe_ge
 def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
               out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
               residual: torch.Tensor | None = None, shared: torch.Tensor | None = None,
-              shared_gate_w=None, path: str = "auto", precision: str = "fp16") -> torch.Tensor:
+              shared_gate_w=None, path: str = "auto", precision: str = "fp16",
+              h_bf16: bool = False) -> torch.Tensor:
     """out[t] = sum_j w[t,j] * down_e(silu(gate_e x_t) * (up_e x_t)), e = ids[t,j]; fp32 h,
     fp32 out [T, H] (moe_batch.py's per-slot product plus core.cpp:5150-5245's
     gather/scatter, done on the device).
@@ -1329,7 +1330,8 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
     ``path``: "decode" (q4_moe_gemv: routed-expert GEMVs, T * topk <= 4096), "prefill"
     (q4_moe_prefill: the experts' tokens batched into 256-token tiles of the prefill GEMM,
     any T; ``precision`` "fp16" or "bf16" as gemm_q4_prefill, h rounded to bf16 in "bf16" as
-    the reference's moe_batch does), or "auto" (decode up to 4096 pairs, then prefill). The
+    the reference's moe_batch does, and in "fp16" too with ``h_bf16``: down then takes one
+    pass over h instead of two), or "auto" (decode up to 4096 pairs, then prefill). The
     prefill path takes no residual / shared expert."""
     dev = gate_up.data.device
     xt = _acts(x, dev)
@@ -1380,7 +1382,8 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
             check("q4_moe_prefill", lib.q4_moe_prefill(
                 _ptr(gate_up.data), _ptr(down.data), None if sc[0] is None else _ptr(sc[0]),
                 None if sc[1] is None else _ptr(sc[1]), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts), _ptr(out),
-                T, E, topk, H, F, _PRECISION[precision], wp, wn, _stream(dev)))
+                T, E, topk, H, F, 2 if (precision == "fp16" and h_bf16) else _PRECISION[precision], wp, wn,
+                _stream(dev)))
         return out
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_moe_workspace_bytes(T, E, topk, H, F), "moe", workspace)

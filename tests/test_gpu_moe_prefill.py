@@ -39,6 +39,8 @@ def _make(oracle, pkg, gpu, E, H, F, seed, bf16_weights=False):
     (16, 512, 256, 97, 4, "bf16", "fp16"),        # ragged tiles, some experts empty
     (8, 256, 128, 300, 2, "bf16", "bf16"),
     (16, 512, 256, 97, 4, "f32", "bf16"),
+    (8, 256, 128, 300, 2, "bf16", "fp16h"),       # fp16 tile, h rounded to bf16: one down pass
+    (16, 512, 256, 97, 4, "f32", "fp16h"),
 ])
 def test_moe_prefill_matches_oracle(gpu, pkg, oracle, E, H, F, T, K, xdt, prec):
     say(f"moe prefill E={E} H={H} F={F} T={T} top{K} {xdt} {prec}")
@@ -46,11 +48,12 @@ def test_moe_prefill_matches_oracle(gpu, pkg, oracle, E, H, F, T, K, xdt, prec):
     x = rng.standard_normal((T, H)).astype(np.float32)
     xt = torch.from_numpy(x).to(torch.bfloat16) if xdt == "bf16" else torch.from_numpy(x)
     ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
-    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill", precision=prec).cpu().numpy()
+    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill", precision="bf16" if prec == "bf16" else "fp16",
+                        h_bf16=prec == "fp16h").cpu().numpy()
     xr = xt.to(torch.float32).numpy()
     if prec == "bf16":
         xr = oracle.bf16_round(xr)
-    ref = oracle.moe_reference(g_of, u_of, d_of, xr, ids, w, h_bf16=prec == "bf16")
+    ref = oracle.moe_reference(g_of, u_of, d_of, xr, ids, w, h_bf16=prec != "fp16")
     assert out.shape == (T, H) and np.isfinite(out).all()
     assert oracle.maxrel(out, ref) <= 1e-3, oracle.maxrel(out, ref)
     assert oracle.rel_fro(out, ref) <= 5e-3

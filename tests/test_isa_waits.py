@@ -111,7 +111,8 @@ def test_prefill_loop_waits_cover_every_asm_load(tmp_path):
                 assert n >= 6, f"{what}: expected the weight loads of the unrolled loop, found {n}"
                 assert not bad, f"{what}: registers used before their load's wait: {bad[:3]}"
         # the grouped expert GEMM's tile loop and the gate/up GEMM with the SwiGLU epilogue
-        for kname, what in ((rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}EE", "moe"),
+        for kname, what in ((rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb0EE", "moe"),
+                            (rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb1EE", "moe swiglu"),
                             (rf"_ZN12_GLOBAL__N_121prefill_swiglu_kernelILi{prec}EE", "swiglu")):
             start = next(i for i, l in enumerate(text) if re.match(kname + r"\w*:", l))
             stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
