@@ -824,7 +824,38 @@ def extra_config3(torch, q4, dev):
                                   "launches": 4,
                                   "swiglu_epilogue_ms": ms_epi, "swiglu_epilogue_gemm_tflops": fl / ms_epi / 1e9,
                                   "swiglu_epilogue_frac_of_peak": fl / ms_epi / 1e9 / MFMA_PEAK_TFLOPS}
-        del xr, ad, yb, p1, p2, y1, y2, w1, w2, hh
+        # two layers back to back, down's K-split sum either reduced by its own launch or left
+        # as planes for the next layer's norm producer (no reduce launch): per layer
+        yc = torch.empty_like(yb)
+        parts = [torch.empty(q4.load_library().q4_prefill_split_count(T, 4096, 14336), T, 4096, device=dev)
+                 for _ in range(2)]
+
+        def two_layers(deferred):
+            def fn():
+                _, a1 = q4.rmsnorm_prepare(xr, nw, add=ad, y=yb, out=p1)
+                q4.gemm_q4_prefill_swiglu(gu_il, a1, h=hh)
+                a2 = q4.prefill_prepare(hh, out=p2)
+                if deferred:
+                    q4.gemm_q4_prefill_partials(dn, a2, part=parts[0])
+                else:
+                    q4.gemm_q4_prefill(dn, a2, y2, workspace=w2)
+                _, a1 = q4.rmsnorm_prepare(yb, nw, add=parts[0] if deferred else y2, y=yc, out=p1)
+                q4.gemm_q4_prefill_swiglu(gu_il, a1, h=hh)
+                a2 = q4.prefill_prepare(hh, out=p2)
+                if deferred:
+                    q4.gemm_q4_prefill_partials(dn, a2, part=parts[1])
+                else:
+                    q4.gemm_q4_prefill(dn, a2, y2, workspace=w2)
+            return fn
+        ms2r = graph_time(torch, two_layers(False), [yc], replays=5)
+        yc_r = yc.clone()
+        ms2d = graph_time(torch, two_layers(True), [yc], replays=5)
+        rec = out[f"T{T}_ffn_block"]
+        rec["two_layers_reduce_ms_per_layer"] = ms2r / 2
+        rec["two_layers_deferred_sums_ms_per_layer"] = ms2d / 2
+        rec["deferred_same_residual"] = bool(torch.equal(yc, yc_r))
+        rec["down_splits"] = parts[0].shape[0]
+        del xr, ad, yb, yc, yc_r, p1, p2, y1, y2, w1, w2, hh, parts
     return out
 
 

@@ -470,7 +470,11 @@ int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, int precisi
                        void* prepared, size_t prepared_bytes, void* stream);
 
 /* The RMSNorm producer writing prepared activations directly (one launch): per token row
- *   y  = x + add (f32 [T][K]; add and y optional; y may be x, no other overlap),
+ *   y  = x + add (f32 [T][K]; add and y optional; y may be x, no other overlap), where add
+ *        is add_planes planes [add_planes][T][K] summed in q4_gemm_prefill's split-reduce
+ *        order (((p0 + p1) + p2) ...): a K-split projection's unreduced partials
+ *        (q4_gemm_prefill_prepared_partials) land here with no reduce launch; add_planes 0
+ *        with add NULL, 1 for a plain addend, at most 64,
  *   xn = bf16((y * r) * w), r = 1 / sqrt(mean(y^2) + eps) as q4_rmsnorm_add forms it,
  * and `prepared` = q4_prefill_prepare of xn as bf16 (q4_prefill_prepared_bytes(T, K,
  * Q4MI_BF16, precision) bytes): the same bits as q4_rmsnorm_add (bf16 xn) followed by
@@ -478,8 +482,20 @@ int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, int precisi
  * K <= 16384; w [K] f32 or bf16 (w_dtype). Replaces the ln design in front of a prefill
  * projection (designs/ln/ln.py:1-6, xn = bf16(y * rsqrt(mean(y^2) + eps) * w)) together with
  * the host's pre-tiling of the GEMM's X (block_host.cpp:228-244). */
-int q4_rmsnorm_prepare(const float* x, const float* add, const void* w, int w_dtype, float* y, int T, int64_t K,
-                       float eps, int precision, void* prepared, size_t prepared_bytes, void* stream);
+int q4_rmsnorm_prepare(const float* x, const float* add, int add_planes, const void* w, int w_dtype, float* y, int T,
+                       int64_t K, float eps, int precision, void* prepared, size_t prepared_bytes, void* stream);
+
+/* The K splits the prefill GEMM's plan takes for (T, N, K) (1: unsplit), 0 for bad shapes. */
+int q4_prefill_split_count(int T, int64_t N, int64_t K);
+
+/* q4_gemm_prefill_prepared without the split reduce: plane s of the plan's S K-splits at
+ * part + s T N (f32 [S][T][N]; S = q4_prefill_split_count; the whole product when S = 1). The
+ * planes summed in order are the prepared GEMM's Y bit for bit; q4_rmsnorm_prepare takes them
+ * as its addend. One activation pass only (bf16 x, or precision 1). Replaces the reference's
+ * down K-pieces summed on the host (ironutil.py:98-115) with the sum folded into the next
+ * layer's norm. */
+int q4_gemm_prefill_prepared_partials(const uint8_t* packed, const void* scales, const void* prepared, int x_dtype,
+                                      float* part, int T, int64_t N, int64_t K, int precision, void* stream);
 
 /* The SwiGLU producer writing the down projection's prepared activations (one launch): per
  * token row h[f] = bf16(silu(g[t][f]) * u[t][f]), silu(g) = g / (1 + exp(-g)), from f32 rows

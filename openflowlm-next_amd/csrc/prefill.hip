@@ -770,21 +770,27 @@ __global__ __launch_bounds__(256) void prefill_xprep(const void* __restrict__ x,
 // are zeros, which leave the fp64 sum of squares unchanged.
 template <int PER, int PREC, bool TILED>
 __global__ __launch_bounds__(256) void rmsnorm_prepare_kernel(const float* x, const float* __restrict__ add,
-                                                              const void* __restrict__ w, int w_bf16, float* y,
-                                                              uint16_t* __restrict__ x16, int* __restrict__ texp,
-                                                              int T, int K, float eps) {
+                                                              int add_planes, const void* __restrict__ w, int w_bf16,
+                                                              float* y, uint16_t* __restrict__ x16,
+                                                              int* __restrict__ texp, int T, int K, float eps) {
     __shared__ double part[4];
     __shared__ __attribute__((aligned(16))) uint16_t xs[256 * PER];
     const int t = blockIdx.x, tid = threadIdx.x;
     if (t < T) {
         const float* xr = x + (int64_t)t * K;
         const float* ar = add ? add + (int64_t)t * K : nullptr;
+        const int64_t pstride = (int64_t)T * K;      // plane q of add at add + q T K
         float v[PER], wv[PER];
         double ss = 0.0;
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int i = tid + 256 * j;
-            v[j] = i < K ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f;
+            float a = 0.0f;
+            if (ar && i < K) {          // the planes in prefill_reduce_kernel's order
+                a = ar[i];
+                for (int q = 1; q < add_planes; ++q) a += ar[q * pstride + i];
+            }
+            v[j] = i < K ? (ar ? xr[i] + a : xr[i]) : 0.0f;
             wv[j] = i >= K ? 0.0f
                            : (w_bf16 ? bf16_hi_to_f32((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i]);
         }
@@ -1266,10 +1272,11 @@ extern "C" int q4_prefill_prepare(const void* x, int x_dtype, int T, int64_t K, 
     return Q4MI_OK;
 }
 
-extern "C" int q4_rmsnorm_prepare(const float* x, const float* add, const void* w, int w_dtype, float* y, int T,
-                                  int64_t K, float eps, int precision, void* prepared, size_t prepared_bytes_,
-                                  void* stream) {
+extern "C" int q4_rmsnorm_prepare(const float* x, const float* add, int add_planes, const void* w, int w_dtype,
+                                  float* y, int T, int64_t K, float eps, int precision, void* prepared,
+                                  size_t prepared_bytes_, void* stream) {
     if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (add_planes < 0 || add_planes > 64 || (add_planes > 0) != (add != nullptr)) return Q4MI_E_ARG;
     if (w_dtype != Q4MI_F32 && w_dtype != Q4MI_BF16) return Q4MI_E_ARG;
     if (T < 0 || K <= 0 || K % 32) return Q4MI_E_SHAPE;
     if (K > 256 * 64) return Q4MI_E_RANGE;
@@ -1283,10 +1290,11 @@ extern "C" int q4_rmsnorm_prepare(const float* x, const float* add, const void* 
         const char *ca = (const char*)a, *cb = (const char*)b;
         return a && b && ca < cb + nb && cb < ca + na;
     };
-    const size_t row_bytes = (size_t)T * K * 4;
-    if (overlaps(prepared, need, x, row_bytes) || overlaps(prepared, need, add, row_bytes) ||
-        overlaps(prepared, need, y, row_bytes) || overlaps(prepared, need, w, (size_t)K * 4) ||
-        (y != x && overlaps(y, row_bytes, x, row_bytes)) || overlaps(y, row_bytes, add, row_bytes))
+    const size_t row_bytes = (size_t)T * K * 4, add_bytes = row_bytes * (size_t)add_planes;
+    if (overlaps(prepared, need, x, row_bytes) || overlaps(prepared, need, add, add_bytes) ||
+        overlaps(prepared, need, y, row_bytes) ||
+        overlaps(prepared, need, w, (size_t)K * (w_dtype == Q4MI_BF16 ? 2 : 4)) ||
+        (y != x && overlaps(y, row_bytes, x, row_bytes)) || overlaps(y, row_bytes, add, add_bytes))
         return Q4MI_E_ARG;
     uint16_t* x16 = (uint16_t*)prepared;
     int* te = (int*)((char*)prepared + x16_bytes(T, K));
@@ -1295,8 +1303,8 @@ extern "C" int q4_rmsnorm_prepare(const float* x, const float* add, const void* 
     const int wb = w_dtype == Q4MI_BF16;
     const bool tiled = K % 64 == 0, small = K <= 256 * 16;
 #define Q4MI_RP(PER, PR, TL)                                                                                   \
-    hipLaunchKernelGGL((rmsnorm_prepare_kernel<PER, PR, TL>), grid, block, 0, st, x, add, w, wb, y, x16, te, T, \
-                       (int)K, eps)
+    hipLaunchKernelGGL((rmsnorm_prepare_kernel<PER, PR, TL>), grid, block, 0, st, x, add, add_planes, w, wb, y, x16, \
+                       te, T, (int)K, eps)
     if (precision == 0) {
         if (small) { if (tiled) Q4MI_RP(16, 0, true); else Q4MI_RP(16, 0, false); }
         else { if (tiled) Q4MI_RP(64, 0, true); else Q4MI_RP(64, 0, false); }
@@ -1393,6 +1401,35 @@ extern "C" int q4_gemm_prefill_prepared(const uint8_t* packed, const void* scale
         if (rc != Q4MI_OK) return rc;
     }
     return Q4MI_OK;
+}
+
+extern "C" int q4_prefill_split_count(int T, int64_t N, int64_t K) {
+    if (T <= 0 || N <= 0 || K <= 0 || N % 64 || K % 32) return 0;
+    return make_plan(T, N, K).splits;
+}
+
+extern "C" int q4_gemm_prefill_prepared_partials(const uint8_t* packed, const void* scales, const void* prepared,
+                                                 int x_dtype, float* part, int T, int64_t N, int64_t K, int precision,
+                                                 void* stream) {
+    if (precision != 0 && precision != 1) return Q4MI_E_ARG;
+    if (activation_passes(x_dtype, precision) != 1) return Q4MI_E_ARG;   // f32 x in precision 0: two passes
+    const int a = prefill_args(packed, prepared, x_dtype, part, T, N, K, nullptr);
+    if (a != Q4MI_OK) return a > 0 ? Q4MI_OK : a;
+    if (precision == 0 && (!scales || misaligned16(scales))) return Q4MI_E_ARG;
+    const PrefillPlan plan = make_plan(T, N, K);
+    if ((plan.cfg == kDmaCfg) != (K % 64 == 0)) return Q4MI_E_ARG;
+    const int* te = (const int*)((const char*)prepared + x16_bytes(T, K));
+    const int* we = precision == 0 ? (const int*)scales : nullptr;
+    const uint32_t* s16 = precision == 0 ? (const uint32_t*)((const char*)scales + scales_wexp_bytes(N)) : nullptr;
+    const hipStream_t st = (hipStream_t)stream;
+    // plane s of the K split at part + s T N (one plane, the whole product, when unsplit)
+    if (precision == 0)
+        launch_prefill<0>(plan.cfg, plan.grid, st, packed, (const uint16_t*)prepared, te, we, s16, part, T, (int)N,
+                          (int)K, plan.tiles_t, plan.splits, plan.wide_wgs, plan.narrow_row0, 0);
+    else
+        launch_prefill<1>(plan.cfg, plan.grid, st, packed, (const uint16_t*)prepared, nullptr, nullptr, nullptr, part, T,
+                          (int)N, (int)K, plan.tiles_t, plan.splits, plan.wide_wgs, plan.narrow_row0, 0);
+    return launch_status();
 }
 
 // ---------------------------------------------------------------------------

@@ -1119,8 +1119,9 @@ def rmsnorm_prepare(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None =
     one launch -- y = x + add (f32 [T, K]; x itself when add is None and y is not given) and
     prefill_prepare(bf16((y * rsqrt(mean(y^2) + eps)) * w)), bit for bit what rmsnorm_add
     (bf16 out) followed by prefill_prepare gives (designs/ln/ln.py:1-6 in front of the
-    host's X tiling, block_host.cpp:228-244). ``w`` float32 or bfloat16 [K]; ``y`` may be
-    ``x``; K % 32 == 0, K <= 16384."""
+    host's X tiling, block_host.cpp:228-244). ``add`` [T, K], or [S, T, K] partial planes
+    (gemm_q4_prefill_partials) summed in the split reduce's order, so no reduce launch runs.
+    ``w`` float32 or bfloat16 [K]; ``y`` may be ``x``; K % 32 == 0, K <= 16384."""
     if precision not in _PRECISION:
         raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
     if not isinstance(x, torch.Tensor) or x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() \
@@ -1133,8 +1134,12 @@ def rmsnorm_prepare(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None =
     if w.numel() != K or w.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError(f"w must be float32 or bfloat16 with {K} values")
     wt = w.to(dev).contiguous()
+    planes = 0
     if add is not None:
-        add = _buf(add, "add", torch.float32, (T, K), dev)
+        planes = add.shape[0] if isinstance(add, torch.Tensor) and add.dim() == 3 else 1
+        if not 1 <= planes <= 64:
+            raise ValueError(f"add holds 1..64 planes, got {planes}")
+        add = _buf(add, "add", torch.float32, (planes, T, K) if add.dim() == 3 else (T, K), dev)
     if y is not None or add is not None:
         y = _buf(y, "y", torch.float32, (T, K), dev)
     lib = _lib_handle()
@@ -1143,7 +1148,7 @@ def rmsnorm_prepare(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None =
     if T:
         with torch.cuda.device(dev):
             check("q4_rmsnorm_prepare", lib.q4_rmsnorm_prepare(
-                _ptr(x), None if add is None else _ptr(add), _ptr(wt),
+                _ptr(x), None if add is None else _ptr(add), planes, _ptr(wt),
                 Q4MI_BF16 if wt.dtype == torch.bfloat16 else Q4MI_F32, None if y is None else _ptr(y), T, K,
                 float(eps), _PRECISION[precision], _ptr(data), nbytes, _stream(dev)))
     return (x if y is None else y), PreparedActs(data, T, K, Q4MI_BF16, precision)
@@ -1228,6 +1233,28 @@ def gemm_q4_prefill_swiglu(gate_up: PackedQ4, x, h: torch.Tensor | None = None,
                 _ptr(gate_up.data), None if sc is None else _ptr(sc), _ptr(prep.data), prep.x_dtype, _ptr(h), T, F,
                 gate_up.k, _PRECISION[precision], _stream(dev)))
     return h
+
+
+def gemm_q4_prefill_partials(w: PackedQ4, x: PreparedActs, part: torch.Tensor | None = None) -> torch.Tensor:
+    """The prepared prefill GEMM without its K-split reduce: f32 [S, T, N] planes whose ordered
+    sum is gemm_q4_prefill's Y bit for bit (S = the plan's split count, 1 when unsplit). They go
+    to rmsnorm_prepare(add=...), which sums them in the residual add of the next norm
+    (the reference sums its down K-pieces on the host, ironutil.py:98-115)."""
+    if not isinstance(x, PreparedActs):
+        raise TypeError("gemm_q4_prefill_partials takes prepared activations (prefill_prepare / rmsnorm_prepare)")
+    if x.k != w.k:
+        raise ValueError(f"x has K={x.k}, W is [{w.n}, {w.k}]")
+    dev = w.device
+    lib = _lib_handle()
+    S = max(1, int(lib.q4_prefill_split_count(max(x.t, 1), w.n, w.k)))
+    part = _buf(part, "part", torch.float32, (S, x.t, w.n), dev)
+    sc = prefill_scales(w) if x.precision == "fp16" else None
+    if x.t:
+        with torch.cuda.device(dev):
+            check("q4_gemm_prefill_prepared_partials", lib.q4_gemm_prefill_prepared_partials(
+                _ptr(w.data), None if sc is None else _ptr(sc), _ptr(x.data), x.x_dtype, _ptr(part), x.t, w.n, w.k,
+                _PRECISION[x.precision], _stream(dev)))
+    return part
 
 
 def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: str = "fp16",

@@ -281,8 +281,14 @@ def test_rmsnorm_prepare_argument_errors(lib):
     need = lib.q4_prefill_prepared_bytes(T, K, 1, 0)
     assert need > T * K * 2
     x, add, w, y, prep = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4, 5))
-    call = lambda *a: lib.q4_rmsnorm_prepare(*a, None)
+    call = lambda x_, add_, *a: lib.q4_rmsnorm_prepare(x_, add_, 0 if add_ is None else 1, *a, None)
     eps = C.c_float(1e-6)
+    assert lib.q4_rmsnorm_prepare(x, add, 0, w, 1, y, T, K, eps, 0, prep, need, None) == -2    # planes vs add
+    assert lib.q4_rmsnorm_prepare(x, None, 2, w, 1, y, T, K, eps, 0, prep, need, None) == -2
+    assert lib.q4_rmsnorm_prepare(x, add, 65, w, 1, y, T, K, eps, 0, prep, need, None) == -2
+    # y on the second of two planes
+    assert lib.q4_rmsnorm_prepare(x, add, 2, w, 1, C.c_void_p(0x20000000 + T * K * 4), T, K, eps, 0, prep, need,
+                                  None) == -2
     assert call(x, add, w, 1, y, T, K, eps, 2, prep, need) == -2                     # precision
     assert call(x, add, w, 7, y, T, K, eps, 0, prep, need) == -2                     # w dtype
     assert call(x, add, w, 1, y, T, K + 16, eps, 0, prep, need) == -1                # K % 32
@@ -331,3 +337,32 @@ def test_gemm_prefill_swiglu_argument_errors(lib):
     assert call(gu, sc, prep, 1, h, 0, 14336, 4096, 0) == 0           # nothing to do
     assert call(gu, None, prep, 1, h, 256, 14336, 4096, 0) == -2      # precision 0 needs scales
     assert call(gu, sc, prep, 1, C.c_void_p(0x40000008), 256, 14336, 4096, 0) == -2   # misaligned h
+
+
+def test_prefill_partials_argument_errors(lib):
+    """q4_gemm_prefill_prepared_partials refuses two-pass activations and bad shapes before any
+    launch; the split count query follows the plan."""
+    assert lib.q4_prefill_split_count(2048, 4096, 14336) >= 1
+    assert lib.q4_prefill_split_count(2048, 4100, 14336) == 0
+    w, sc, prep, part = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4))
+    call = lambda *a: lib.q4_gemm_prefill_prepared_partials(*a, None)
+    assert call(w, sc, prep, 0, part, 256, 4096, 14336, 0) == -2      # f32 x, precision 0: two passes
+    assert call(w, sc, prep, 1, part, 256, 4096, 14336, 3) == -2      # precision
+    assert call(w, sc, prep, 1, part, 256, 4100, 14336, 0) == -1      # N % 64
+    assert call(w, None, prep, 1, part, 256, 4096, 14336, 0) == -2    # precision 0 needs scales
+    assert call(w, sc, prep, 1, part, 0, 4096, 14336, 0) == 0         # nothing to do
+
+
+def test_rmsnorm_prepare_weight_extent_follows_its_dtype(lib):
+    """The norm weight's extent in the overlap check follows its dtype: K * 2 bytes for bf16,
+    K * 4 for f32 (every call here is refused before any launch)."""
+    T, K = 256, 4096
+    need = lib.q4_prefill_prepared_bytes(T, K, 1, 0)
+    x, y = C.c_void_p(0x10000000), C.c_void_p(0x30000000)
+    w = 0x50000000
+    eps = C.c_float(1e-6)
+    call = lambda wdt, at: lib.q4_rmsnorm_prepare(x, None, 0, C.c_void_p(w), wdt, y, T, K, eps, 0, C.c_void_p(at),
+                                                  need, None)
+    assert call(1, w + K * 2 - 16) == -2       # bf16: the buffer's first 16 bytes on the weight's last 8 values
+    assert call(0, w + K * 2) == -2            # f32: the same address is inside its K * 4 bytes
+    assert call(0, w + K * 4 - 16) == -2

@@ -120,3 +120,38 @@ def test_swiglu_prepare_feeds_the_down_gemm(gpu, pkg, oracle):
     assert a.tobytes() == b.tobytes()
     ref = oracle.gemv_reference(blocks, h.float().cpu().numpy())
     assert oracle.maxrel(a, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("precision", ["fp16", "bf16"])
+def test_rmsnorm_prepare_sums_split_gemm_planes(gpu, pkg, oracle, precision):
+    """A K-split prefill GEMM's unreduced planes (gemm_q4_prefill_partials), summed in order, are
+    its reduced Y bit for bit, and the norm producer taking the planes as its addend gives the
+    bytes it gives for that Y: the next layer's norm does the split reduce, no launch of its own."""
+    T, N, K = 300, 512, 4096
+    say(f"rmsnorm_prepare over split planes T={T} N={N} K={K} {precision}")
+    lib = pkg.load_library()
+    S = lib.q4_prefill_split_count(T, N, K)
+    assert S > 1, "the shape should split"
+    rng = np.random.default_rng(17)
+    w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(N, K, rng), gpu)
+    x = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    prep = pkg.prefill_prepare(x, precision)
+    part = pkg.gemm_q4_prefill_partials(w, prep)
+    y = pkg.gemm_q4_prefill(w, prep)
+    assert part.shape == (S, T, N)
+    s = part[0].clone()
+    for q in range(1, S):
+        s += part[q]
+    assert torch.equal(s, y)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(3)
+    res = torch.randn(T, N, generator=g, device=gpu)
+    nw = (1 + 0.1 * torch.randn(N, generator=g, device=gpu)).to(torch.bfloat16)
+    nbytes = int(lib.q4_prefill_prepared_bytes(T, N, 1, 0))
+    ya, pa = pkg.rmsnorm_prepare(res, nw, add=part, y=torch.empty_like(res),
+                                 out=torch.zeros(nbytes, dtype=torch.uint8, device=gpu))
+    yb, pb = pkg.rmsnorm_prepare(res, nw, add=y, y=torch.empty_like(res),
+                                 out=torch.zeros(nbytes, dtype=torch.uint8, device=gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb)
+    assert torch.equal(pa.data, pb.data)
