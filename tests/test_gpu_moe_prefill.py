@@ -74,10 +74,13 @@ def test_moe_prefill_deterministic_and_equal_to_decode_path(gpu, pkg, oracle):
     assert oracle.maxrel(a, d) <= 1e-3
 
 
-def test_moe_prefill_one_expert_takes_every_token(gpu, pkg, oracle):
-    """All pairs on one expert (many full tiles), the rest empty; ids outside [0, E) add nothing."""
-    say("moe prefill, one popular expert")
-    E, H, F, T = 6, 256, 128, 700
+@pytest.mark.parametrize("E", [6, 16])
+def test_moe_prefill_one_expert_takes_every_token(gpu, pkg, oracle, E):
+    """All pairs on one expert (many full tiles), the rest empty; ids outside [0, E) add nothing.
+    E = 6: 256-token tiles (1400 pairs > 192 per expert); E = 16: the same expert's three tiles
+    as 128-token halves, the last one's upper half partly empty."""
+    say(f"moe prefill, one popular expert, E={E}")
+    H, F, T = 256, 128, 700
     rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 77)
     x = rng.standard_normal((T, H)).astype(np.float32)
     xt = torch.from_numpy(x).to(torch.bfloat16)
