@@ -155,3 +155,43 @@ def test_rmsnorm_prepare_sums_split_gemm_planes(gpu, pkg, oracle, precision):
     torch.cuda.synchronize()
     assert torch.equal(ya, yb)
     assert torch.equal(pa.data, pb.data)
+
+
+@pytest.mark.parametrize("precision", ["fp16", "bf16"])
+def test_producers_hold_small_rows_to_the_oracle(gpu, pkg, oracle, precision):
+    """Rows far below fp16's normal range (h ~ 1e-15 to 1e-5, normed rows ~ 1e-6): the producers write
+    the bytes the pre-pass writes (each token row scaled by a power of two into fp16's top
+    binade) and every row of the GEMM over them stays within 1e-3 of the fp64 reference."""
+    say(f"producers at small magnitude {precision}")
+    T, F, K, N = 64, 1024, 1024, 256
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(23)
+    row_scale = (10.0 ** -torch.linspace(3, 7, T, device=gpu)).unsqueeze(1)
+    gu = torch.randn(T, 2 * F, generator=gen, device=gpu) * row_scale
+    lib = pkg.load_library()
+    zeros = lambda K_: torch.zeros(int(lib.q4_prefill_prepared_bytes(T, K_, 1, 0 if precision == "fp16" else 1)),
+                                   dtype=torch.uint8, device=gpu)
+    h = torch.empty(T, F, dtype=torch.bfloat16, device=gpu)
+    prep = pkg.swiglu_prepare(gu, precision=precision, h=h, out=zeros(F))
+    ref_prep = pkg.prefill_prepare(h, precision, out=zeros(F))
+    x = torch.randn(T, K, generator=gen, device=gpu)
+    w = (5e-7 * (1 + 0.1 * torch.randn(K, generator=gen, device=gpu)) * (1 + torch.arange(K, device=gpu) % 7)
+         ).to(torch.bfloat16)
+    _, nprep = pkg.rmsnorm_prepare(x, w, eps=1e-6, precision=precision, out=zeros(K))
+    _, xn = pkg.rmsnorm_add(x.clone(), w, eps=1e-6, out_dtype=torch.bfloat16)
+    ref_nprep = pkg.prefill_prepare(xn, precision, out=zeros(K))
+    torch.cuda.synchronize()
+    assert float(h.float().abs().max()) < 2.0 ** -14, "h should lie below fp16's normal range"
+    assert float(xn.float().abs().max()) < 2.0 ** -14
+    assert torch.equal(prep.data, ref_prep.data)
+    assert torch.equal(nprep.data, ref_nprep.data)
+    blocks = oracle.baseline_q4_1_blocks(N, F, np.random.default_rng(5))
+    wq = pkg.pack_q4_1(blocks, gpu)
+    # the bf16 tile is RNE_bf16(q d + m), the reference's: its bar is over those weights
+    wd = oracle.dequant_q4_1(blocks)
+    wd = (oracle.bf16_round(wd) if precision == "bf16" else wd).astype(np.float64)
+    for p, xin in ((prep, h), (nprep, xn)):
+        got = pkg.gemm_q4_prefill(wq, p).cpu().numpy()
+        ref = xin.double().cpu().numpy() @ wd.T
+        worst = max(oracle.maxrel(got[t], ref[t]) for t in range(T))
+        assert worst <= 1e-3, worst
