@@ -31,17 +31,22 @@ def test_interleave_gate_up_alternates_row_groups(gpu, pkg, oracle):
         assert torch.equal(a[2 * j], g.data.view(4, rg)[j]) and torch.equal(a[2 * j + 1], u.data.view(4, rg)[j])
 
 
+@pytest.mark.parametrize("small", [False, True])
 @pytest.mark.parametrize("precision", ["fp16", "bf16"])
-def test_swiglu_epilogue_equals_plain_gemm_then_swiglu(gpu, pkg, oracle, precision):
+def test_swiglu_epilogue_equals_plain_gemm_then_swiglu(gpu, pkg, oracle, precision, small):
     """At T = 2048, 2F = 8192 the plain GEMM's plan has no K split (256 tiles), so its f32
-    outputs are the epilogue's accumulators: the h of both paths must be the same bits."""
+    outputs are the epilogue's accumulators: the h of both paths must be the same bits. small:
+    token rows scaled by 1 .. 1e-7, so the fp16 path's per-token exponents span 24 binades."""
     T, F, K = 2048, 4096, 1024
-    say(f"swiglu epilogue vs plain GEMM + swiglu_prepare T={T} F={F} K={K} {precision}")
+    say(f"swiglu epilogue vs plain GEMM + swiglu_prepare T={T} F={F} K={K} {precision} small={small}")
     lib = pkg.load_library()
     assert lib.q4_gemm_prefill_prepared_workspace_bytes(T, 2 * F, K) == 0, "plain plan is split"
     rng = np.random.default_rng(7)
     _, _, _, _, gu = _gate_up(pkg, oracle, F, K, rng, gpu)
-    x = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    xf = rng.standard_normal((T, K)).astype(np.float32)
+    if small:
+        xf *= (10.0 ** -np.linspace(0, 7, T)).astype(np.float32)[:, None]
+    x = torch.from_numpy(xf).to(torch.bfloat16).to(gpu)
     prep = pkg.prefill_prepare(x, precision)
     h = pkg.gemm_q4_prefill_swiglu(gu, prep)
     y = pkg.gemm_q4_prefill(gu, prep).view(T, F // 64, 2, 64)
@@ -50,6 +55,8 @@ def test_swiglu_epilogue_equals_plain_gemm_then_swiglu(gpu, pkg, oracle, precisi
     pkg.swiglu_prepare(g, u, h=h_ref)
     torch.cuda.synchronize()
     assert torch.equal(h, h_ref)
+    if small:
+        assert float(h[-1].float().abs().max()) < 2.0 ** -24 and bool((h[-1] != 0).any())
 
 
 @pytest.mark.parametrize("T", [1, 300])
