@@ -107,3 +107,22 @@ def test_moe_prefill_config4_matrices_sampled_tokens(gpu, pkg, oracle, T):
     pick = np.sort(rng.choice(T, 12, replace=False))
     ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy()[pick], ids[pick], w[pick])
     assert oracle.maxrel(out[pick], ref) <= 1e-3, oracle.maxrel(out[pick], ref)
+
+
+@pytest.mark.parametrize("prec", ["fp16", "fp16h", "bf16"])
+def test_moe_prefill_small_rows(gpu, pkg, oracle, prec):
+    """Token rows scaled by 1 .. 1e-6 (h down to ~1e-13, far below fp16's normal range): the fp16
+    paths' per-token power-of-two exponents for x and h keep every output row within 1e-3 of the
+    fp64 oracle, measured row by row."""
+    E, H, F, T, K = 8, 256, 128, 300, 2
+    say(f"moe prefill small rows {prec}")
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 91, bf16_weights=prec == "bf16")
+    x = rng.standard_normal((T, H)).astype(np.float32) * (10.0 ** -np.linspace(0, 6, T)).astype(np.float32)[:, None]
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill", precision="bf16" if prec == "bf16" else "fp16",
+                        h_bf16=prec == "fp16h").cpu().numpy()
+    ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy(), ids, w, h_bf16=prec != "fp16")
+    assert np.abs(ref[-1]).max() < 1e-9
+    worst = max(oracle.maxrel(out[t], ref[t]) for t in range(T))
+    assert worst <= 1e-3, worst
