@@ -190,7 +190,10 @@ int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stre
  * 64-row groups to fill the GPU). A short matrix is split along K: the
  * workspace holds the per-split partial sums, which a second launch adds in
  * split order. No initial contents are needed; calls sharing one workspace
- * must be ordered on one stream. */
+ * must be ordered on one stream. The bytes a split call writes (the query's
+ * count from the workspace pointer on) must not overlap x, y or, for the _acc
+ * forms, res, the partial planes or x_out: workgroups store their partials
+ * while others still read those (Q4MI_E_ARG, before any launch). */
 size_t q4_gemv_workspace_bytes(int M, int64_t N, int64_t K);
 
 /* Decode GEMV / skinny GEMM: Y[M][N] = X[M][K] . W[N][K]^T, fp32 accumulate,
@@ -340,7 +343,9 @@ int q4_gemv_partials(const uint8_t* packed, const void* x, int x_dtype, float* p
  * (the residual stream's next value: q4_gemv_residual's bits for the GEMV that made the
  * planes). x_out must not overlap res, part or y. M = 1 with K <= 4096 and a grid of at most
  * one workgroup per CU reduces inside the GEMV's workgroups; other shapes add one reduce
- * launch first. Workspace as q4_gemv. */
+ * launch first. Workspace as q4_gemv; where the GEMV itself is split (e.g. 4096 x 4096 at
+ * M = 1), its partials must not overlap res, part, x_out or y (Q4MI_E_ARG): a workspace
+ * shared with the planes of q4_gemv_partials is carved apart from them. */
 int q4_gemv_rmsnorm_acc(const uint8_t* packed, const float* res, const float* part, int S,
                         const void* norm_w, int norm_w_dtype, float eps, float* x_out, float* y, int M,
                         int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
@@ -491,11 +496,14 @@ int q4_prefill_split_count(int T, int64_t N, int64_t K);
 /* q4_gemm_prefill_prepared without the split reduce: plane s of the plan's S K-splits at
  * part + s T N (f32 [S][T][N]; S = q4_prefill_split_count; the whole product when S = 1). The
  * planes summed in order are the prepared GEMM's Y bit for bit; q4_rmsnorm_prepare takes them
- * as its addend. One activation pass only (bf16 x, or precision 1). Replaces the reference's
- * down K-pieces summed on the host (ironutil.py:98-115) with the sum folded into the next
- * layer's norm. */
+ * as its addend. One activation pass only (bf16 x, or precision 1). part_bytes is part's size:
+ * below S T N 4 for this process's plan the call returns Q4MI_E_WORKSPACE before any launch
+ * (the plan follows the device's CU count, so query q4_prefill_split_count on the device that
+ * runs the call). Replaces the reference's down K-pieces summed on the host
+ * (ironutil.py:98-115) with the sum folded into the next layer's norm. */
 int q4_gemm_prefill_prepared_partials(const uint8_t* packed, const void* scales, const void* prepared, int x_dtype,
-                                      float* part, int T, int64_t N, int64_t K, int precision, void* stream);
+                                      float* part, size_t part_bytes, int T, int64_t N, int64_t K, int precision,
+                                      void* stream);
 
 /* The SwiGLU producer writing the down projection's prepared activations (one launch): per
  * token row h[f] = bf16(silu(g[t][f]) * u[t][f]), silu(g) = g / (1 + exp(-g)), from f32 rows

@@ -89,7 +89,7 @@ SIGNATURES = {
     "q4_swiglu_prepare": (_i32, [_vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _sz, _vp]),
     "q4_rmsnorm_prepare": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, C.c_float, _i32, _vp, _sz, _vp]),
     "q4_prefill_split_count": (_i32, [_i32, _i64, _i64]),
-    "q4_gemm_prefill_prepared_partials": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _vp]),
+    "q4_gemm_prefill_prepared_partials": (_i32, [_vp, _vp, _vp, _i32, _vp, _sz, _i32, _i64, _i64, _i32, _vp]),
     "q4_gemm_prefill_prepared_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemm_prefill_prepared": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _vp, _sz, _vp]),
     "q4_moe_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),

@@ -574,6 +574,17 @@ struct NormSpec {
     float* x_out = nullptr;            // non-null: a deferred-reduction call
 };
 
+// A split GEMV's workgroups store their partial sums to [ws, ws + ws_used) while other
+// workgroups still read x and the deferred planes, workgroup 0 writes x_out, and the reduce
+// launch then writes out (out_bytes) from the partials: none of those may share a byte with
+// the partials, or the result depends on timing.
+bool split_ws_conflict(const void* ws, int64_t ws_used, const void* x, int64_t x_bytes, const NormSpec& nrm,
+                       const void* out, int64_t out_bytes, int M, int64_t K) {
+    const int64_t row_bytes = (int64_t)M * K * 4;
+    return overlaps(ws, ws_used, x, x_bytes) || overlaps(ws, ws_used, nrm.acc_part, nrm.acc_S * row_bytes) ||
+           overlaps(ws, ws_used, nrm.x_out, row_bytes) || overlaps(ws, ws_used, out, out_bytes);
+}
+
 // x_out = res + the S partial planes [S][MK], in stage_norm_acc_row's order (S = 1: res +
 // part; S > 1: split_reduce's; S = 0: res): the unfused form of the deferred reduction.
 __global__ __launch_bounds__(256) void acc_reduce_kernel(const float* __restrict__ res, const float* __restrict__ part,
@@ -641,6 +652,12 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     if (misaligned16(packed) || misaligned16(x) || misaligned16(y) || misaligned16(workspace)) return Q4MI_E_ARG;
     const GemvPlan plan = lo ? GemvPlan{choose_splits(N, K), 4} : plan_gemv(N, K);
     const int S = plan.S;
+    if (S > 1) {   // the documented contract: at least what the query reports (checked before any launch)
+        if (!workspace || workspace_bytes < q4_gemv_workspace_bytes(M, N, K)) return Q4MI_E_WORKSPACE;
+        if (split_ws_conflict(workspace, (int64_t)workspace_for(M, N, K, S), x,
+                              (int64_t)M * K * (x_dtype == Q4MI_F32 ? 4 : 2), nrm, y, (int64_t)M * N * 4, M, K))
+            return Q4MI_E_ARG;
+    }
     const bool fused = acc_fused(M, K, (N / 64) * S);
     if (nrm.x_out && !fused) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
         const int64_t MK = (int64_t)M * K;
@@ -668,10 +685,7 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     P.acc_S = nrm.acc_S;
     P.x_out = nrm.x_out;
     P.xn = nrm.x_out || (nrm.w && norm_xn() && fused);
-    if (S > 1) {   // the documented contract: at least what the query reports
-        if (!workspace || workspace_bytes < q4_gemv_workspace_bytes(M, N, K)) return Q4MI_E_WORKSPACE;
-        P.part = (float*)workspace;
-    }
+    if (S > 1) P.part = (float*)workspace;
     const dim3 grid((unsigned)((N / 64) * S));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
@@ -832,6 +846,12 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     if (((uintptr_t)h & (h_dtype == Q4MI_BF16 ? 1 : 3)) != 0) return Q4MI_E_ARG;
     const GemvPlan plan = swiglu_plan(F, K);
     const int S = plan.S;
+    if (S > 1) {   // checked before any launch
+        if (!workspace || workspace_bytes < (size_t)S * M * 2 * F * sizeof(float)) return Q4MI_E_WORKSPACE;
+        if (split_ws_conflict(workspace, (int64_t)S * M * 2 * F * 4, x, (int64_t)M * K * (x_dtype == Q4MI_F32 ? 4 : 2),
+                              nrm, h, (int64_t)M * F * (h_dtype == Q4MI_BF16 ? 2 : 4), M, K))
+            return Q4MI_E_ARG;
+    }
     const bool fused = acc_fused(M, K, (F / 64) * S);
     if (nrm.x_out && !fused) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
         const int64_t MK = (int64_t)M * K;
@@ -860,10 +880,7 @@ static int swiglu_impl(const uint8_t* gate, const uint8_t* up, const void* x, in
     P.acc_S = nrm.acc_S;
     P.x_out = nrm.x_out;
     P.xn = nrm.x_out || (nrm.w && norm_xn() && fused);
-    if (S > 1) {
-        if (!workspace || workspace_bytes < (size_t)S * M * 2 * F * sizeof(float)) return Q4MI_E_WORKSPACE;
-        P.part = (float*)workspace;
-    }
+    if (S > 1) P.part = (float*)workspace;
     const dim3 grid((unsigned)((F / 64) * S));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
@@ -951,10 +968,6 @@ static int acc_args(const float* res, const float* part, int S, const float* x_o
     if (M == 0) return Q4MI_OK;
     if (!x_out || (S > 0 && !part)) return Q4MI_E_ARG;
     // workgroup 0 writes x_out while the others read res and the planes
-    auto overlaps = [](const void* a, int64_t na, const void* b, int64_t nb) {
-        const char *ca = (const char*)a, *cb = (const char*)b;
-        return a && b && ca < cb + nb && cb < ca + na;
-    };
     const int64_t row_bytes = (int64_t)M * K * 4, part_bytes = S > 0 ? S * row_bytes : 0;
     if (overlaps(x_out, row_bytes, res, row_bytes) || overlaps(x_out, row_bytes, part, part_bytes) ||
         overlaps(out, out_bytes, res, row_bytes) || overlaps(out, out_bytes, part, part_bytes) ||

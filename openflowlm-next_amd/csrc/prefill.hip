@@ -1409,8 +1409,8 @@ extern "C" int q4_prefill_split_count(int T, int64_t N, int64_t K) {
 }
 
 extern "C" int q4_gemm_prefill_prepared_partials(const uint8_t* packed, const void* scales, const void* prepared,
-                                                 int x_dtype, float* part, int T, int64_t N, int64_t K, int precision,
-                                                 void* stream) {
+                                                 int x_dtype, float* part, size_t part_bytes, int T, int64_t N,
+                                                 int64_t K, int precision, void* stream) {
     if (precision != 0 && precision != 1) return Q4MI_E_ARG;
     if (activation_passes(x_dtype, precision) != 1) return Q4MI_E_ARG;   // f32 x in precision 0: two passes
     const int a = prefill_args(packed, prepared, x_dtype, part, T, N, K, nullptr);
@@ -1418,6 +1418,8 @@ extern "C" int q4_gemm_prefill_prepared_partials(const uint8_t* packed, const vo
     if (precision == 0 && (!scales || misaligned16(scales))) return Q4MI_E_ARG;
     const PrefillPlan plan = make_plan(T, N, K);
     if ((plan.cfg == kDmaCfg) != (K % 64 == 0)) return Q4MI_E_ARG;
+    // the planes this call writes follow this process's plan, not a count queried elsewhere
+    if (part_bytes < (size_t)plan.splits * T * N * sizeof(float)) return Q4MI_E_WORKSPACE;
     const int* te = (const int*)((const char*)prepared + x16_bytes(T, K));
     const int* we = precision == 0 ? (const int*)scales : nullptr;
     const uint32_t* s16 = precision == 0 ? (const uint32_t*)((const char*)scales + scales_wexp_bytes(N)) : nullptr;

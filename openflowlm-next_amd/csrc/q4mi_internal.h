@@ -18,4 +18,11 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // The kernels move packed weights, activations, outputs and workspaces in 16-byte vectors.
 inline bool misaligned16(const void* p) { return ((uintptr_t)p & 15u) != 0; }
 
+// Whether the byte ranges [a, a + na) and [b, b + nb) intersect (a NULL pointer or an
+// empty range intersects nothing).
+inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+    const char *ca = (const char*)a, *cb = (const char*)b;
+    return a && b && na > 0 && nb > 0 && ca < cb + nb && cb < ca + na;
+}
+
 }  // namespace q4mi

@@ -1211,6 +1211,8 @@ def gemm_q4_prefill_swiglu(gate_up: PackedQ4, x, h: torch.Tensor | None = None,
     from the plain GEMM's f32 outputs, with no f32 output in memory. F % 128 == 0, K % 64 == 0."""
     dev = gate_up.device
     if isinstance(x, PreparedActs):
+        if x.data.device != dev:
+            raise ValueError(f"prepared activations are on {x.data.device}, W on {dev}")
         precision = x.precision
         prep = x
     else:
@@ -1245,6 +1247,8 @@ def gemm_q4_prefill_partials(w: PackedQ4, x: PreparedActs, part: torch.Tensor | 
     if x.k != w.k:
         raise ValueError(f"x has K={x.k}, W is [{w.n}, {w.k}]")
     dev = w.device
+    if x.data.device != dev:
+        raise ValueError(f"prepared activations are on {x.data.device}, W on {dev}")
     lib = _lib_handle()
     S = max(1, int(lib.q4_prefill_split_count(max(x.t, 1), w.n, w.k)))
     part = _buf(part, "part", torch.float32, (S, x.t, w.n), dev)
@@ -1252,8 +1256,8 @@ def gemm_q4_prefill_partials(w: PackedQ4, x: PreparedActs, part: torch.Tensor | 
     if x.t:
         with torch.cuda.device(dev):
             check("q4_gemm_prefill_prepared_partials", lib.q4_gemm_prefill_prepared_partials(
-                _ptr(w.data), None if sc is None else _ptr(sc), _ptr(x.data), x.x_dtype, _ptr(part), x.t, w.n, w.k,
-                _PRECISION[x.precision], _stream(dev)))
+                _ptr(w.data), None if sc is None else _ptr(sc), _ptr(x.data), x.x_dtype, _ptr(part),
+                part.numel() * 4, x.t, w.n, w.k, _PRECISION[x.precision], _stream(dev)))
     return part
 
 

@@ -274,6 +274,33 @@ def test_deferred_reduction_argument_errors(lib):
     assert sw(res, part, -1, fake, 1, C.c_float(1e-6), xo, h, 1, 1, 14336, K) == -5
 
 
+def test_split_workspace_must_not_overlap_what_the_gemv_reads(lib):
+    """A split norm GEMV (4096 x 4096 at M = 1 plans 4 K splits and reduces the deferred
+    planes inside its workgroups) stores its partials to the workspace while other
+    workgroups still read res and the planes: a workspace carved over the planes, res,
+    x_out or y is refused before any launch."""
+    K = N = 4096
+    assert lib.q4_gemv_split_count(N, K) > 1
+    need = lib.q4_gemv_workspace_bytes(1, N, K)
+    assert need > 0
+    fake = C.c_void_p(0x1000)
+    res, part, xo, y = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4))
+    eps = C.c_float(1e-6)
+    rms = lambda ws: lib.q4_gemv_rmsnorm_acc(fake, res, part, 2, fake, 1, eps, xo, y, 1, N, K,
+                                              ws, need, None)
+    for base in (0x20000000 + 4 * K, 0x10000000, 0x30000000 - 16, 0x40000000 + 4 * N - 16):
+        assert rms(C.c_void_p(base)) == -2, hex(base)
+    assert lib.q4_gemv_rmsnorm_acc(fake, res, part, 2, fake, 1, eps, xo, y, 1, N, K, C.c_void_p(0x50000000),
+                                   need - 16, None) == -3                           # short, checked first
+    F, h = 1024, C.c_void_p(0x40000000)
+    need_sw = lib.q4_gemv_swiglu_workspace_bytes(1, F, K)
+    if need_sw:   # the SwiGLU form splits too at this shape: same rule over its planes
+        sw = lambda ws: lib.q4_gemv_swiglu_rmsnorm_acc(fake, fake, res, part, 2, fake, 1, eps, xo, h, 1, 1, F,
+                                                       K, ws, need_sw, None)
+        assert sw(C.c_void_p(0x20000000)) == -2
+        assert sw(C.c_void_p(0x30000000 + 4 * K - 16)) == -2
+
+
 def test_rmsnorm_prepare_argument_errors(lib):
     """q4_rmsnorm_prepare refuses bad enums, shapes, sizes and overlapping outputs before any
     launch."""
@@ -345,12 +372,18 @@ def test_prefill_partials_argument_errors(lib):
     assert lib.q4_prefill_split_count(2048, 4096, 14336) >= 1
     assert lib.q4_prefill_split_count(2048, 4100, 14336) == 0
     w, sc, prep, part = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4))
-    call = lambda *a: lib.q4_gemm_prefill_prepared_partials(*a, None)
+    big = 1 << 40
+    call = lambda w_, sc_, prep_, dt, part_, *a: lib.q4_gemm_prefill_prepared_partials(w_, sc_, prep_, dt, part_, big,
+                                                                                       *a, None)
     assert call(w, sc, prep, 0, part, 256, 4096, 14336, 0) == -2      # f32 x, precision 0: two passes
     assert call(w, sc, prep, 1, part, 256, 4096, 14336, 3) == -2      # precision
     assert call(w, sc, prep, 1, part, 256, 4100, 14336, 0) == -1      # N % 64
     assert call(w, None, prep, 1, part, 256, 4096, 14336, 0) == -2    # precision 0 needs scales
     assert call(w, sc, prep, 1, part, 0, 4096, 14336, 0) == 0         # nothing to do
+    # part smaller than the plan's S planes: refused before any launch
+    S = lib.q4_prefill_split_count(256, 4096, 14336)
+    need = S * 256 * 4096 * 4
+    assert lib.q4_gemm_prefill_prepared_partials(w, sc, prep, 1, part, need - 4, 256, 4096, 14336, 0, None) == -3
 
 
 def test_rmsnorm_prepare_weight_extent_follows_its_dtype(lib):
