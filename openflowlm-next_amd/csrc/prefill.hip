@@ -350,6 +350,11 @@ __device__ __forceinline__ void vgpr_landed(u32x4& v) { asm volatile("" : "+v"(v
 // tile's loads, DMA and dequant unchanged: the waves of row group 3 load row group 2's mx
 // tile again and store it to LDS rows 192..255, which no fragment reads, so every wave
 // issues the same loads and the wait counts below hold for both.
+// Invariant: every wave issues the same loads, DMA, dequant, waits and barriers in every
+// stage. Wave w's loads and dequant fill row group w & 3, K block w >> 2 of the shared weight
+// buffer for all waves; its DMA copies token rows [32 w, 32 w + 32) of the stage; its wait
+// counts cover only its own loads. Only a wave's fragment reads and MFMAs are private (its
+// accumulators reach memory only for its tokens [64 (w >> 1), +64) below T).
 template <int PREC, int FN, bool SWI = false>
 __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict__ packed,
                                          const uint16_t* __restrict__ x16, const int* __restrict__ texp,

@@ -3,8 +3,9 @@ compiler does not wait for them: every wait is explicit. This checks the gfx950
 ISA of that kernel's main loop: each register-destination load's registers are
 touched only after an s_waitcnt vmcnt(N) with N no larger than the number of
 vector-memory loads issued after it (vector-memory loads retire in issue order).
-A compiler change that schedules a use ahead of its wait would fail here.
-Needs hipcc (present on the build host); no GPU."""
+A compiler change that schedules a use ahead of its wait would fail here. The
+same checker gates the build (openflowlm-next_amd/build.py): a planted violation
+below makes build() fail. Needs hipcc (present on the build host); no GPU."""
 from __future__ import annotations
 
 import re
@@ -18,76 +19,18 @@ ROOT = Path(__file__).resolve().parents[1]
 SRC = ROOT / "openflowlm-next_amd" / "csrc" / "prefill.hip"
 
 
-def _regs(tok: str) -> set[int]:
-    m = re.match(r"v\[(\d+):(\d+)\]", tok)
-    if m:
-        return set(range(int(m.group(1)), int(m.group(2)) + 1))
-    m = re.match(r"v(\d+)$", tok)
-    return {int(m.group(1))} if m else set()
+def _load(name: str, path: Path):
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
 
 
-def _operands(line: str) -> list[str]:
-    parts = line.split(None, 1)
-    return [t.strip().split()[0] for t in parts[1].split(",") if t.strip()] if len(parts) > 1 else []
-
-
-def inner_loops(asm: list[str]) -> list[list[str]]:
-    """The instructions of each innermost loop, in layout order: the header's block, the
-    blocks marked as inside it (a latch may sit above the header and fall into it), up to
-    the last branch back to any of them."""
-    loops = []
-    inner = any("Inner Loop Header" in l for l in asm)     # else: a lone loop's "Loop Header"
-    for h, line in enumerate(asm):
-        if "Loop Header" not in line or (inner and "Inner" not in line):
-            continue
-        # the header comment may sit on its own line under the block's label
-        label = (asm[h - 1] if line.lstrip().startswith(";") and h else line).split(":")[0].strip()
-        name = label[2:] if label.startswith(".L") else label.lstrip(".")   # ".LBB0_1" -> "BB0_1"
-        members = {label} | {l.split(":")[0].strip() for l in asm if f"in Loop: Header={name} " in l + " "}
-        first = min(i for i, l in enumerate(asm) if l.split(":")[0].strip() in members and ":" in l)
-        back = [i for i, l in enumerate(asm)
-                if re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l)
-                and re.search(r"s_(?:cbranch_\w+|branch)\s+(\S+)", l).group(1) in members]
-        if not back:                            # no branch back to the loop's blocks: not a loop body
-            continue
-        last = max(back)
-        loops.append([l for l in asm[first:last + 1] if l.strip() and not l.strip().startswith((";", "."))])
-    return loops
-
-
-def early_uses_in(body: list[str]) -> tuple[int, list[str]]:
-    """(loads checked, descriptions of uses before the load's wait) for one loop body."""
-    bad, n = [], 0
-    for i, l in enumerate(body):
-        if not re.match(r"\s*global_load_dword", l) or "lds" in l:
-            continue
-        n += 1
-        dst, younger, done = _regs(_operands(l)[0]), 0, False
-        for k in range(1, 2 * len(body)):
-            m = body[(i + k) % len(body)]
-            if re.match(r"\s*global_load", m):
-                younger += 1
-            w = re.search(r"vmcnt\((\d+)\)", m)
-            # vmcnt(0) waits sit on the last stages' branches; only count steady-state waits
-            if w and 0 < int(w.group(1)) <= younger:
-                done = True
-            if re.match(r"\s*s_waitcnt", m):
-                continue
-            touched = set().union(*[_regs(t) for t in _operands(m)]) if _operands(m) else set()
-            if dst & touched:
-                if not done:
-                    bad.append(f"{l.strip()} -> {m.strip()}")
-                break
-    return n, bad
-
-
-def early_uses(asm: list[str]) -> tuple[int, list[str]]:
-    """(loads checked, early uses) summed over every innermost loop of asm."""
-    n, bad = 0, []
-    for body in inner_loops(asm):
-        k, b = early_uses_in(body)
-        n, bad = n + k, bad + b
-    return n, bad
+# the checker is the build's own gate (openflowlm-next_amd/isa_gate.py); these tests hold it
+# to the kernels' known structure and plant mistakes for it to find
+G = _load("q4mi_isa_gate", ROOT / "openflowlm-next_amd" / "isa_gate.py")
+inner_loops, early_uses_in, early_uses = G.inner_loops, G.early_uses_in, G.early_uses
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
@@ -264,3 +207,75 @@ def test_gemv_kernels_load_global_and_keep_accumulators_in_vgprs(tmp_path, src):
     for m in re.finditer(r"\.agpr_count:\s+(\d+).*?\.name:\s+(\S+)", text, re.S):
         if m.group(2) in kernels:
             assert int(m.group(1)) == 0, f"{m.group(2)} holds {m.group(1)} AGPRs"
+
+
+PLANTED = r"""
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+// A two-deep pipeline of inline-asm loads over p[0 .. n + 1] (compiled only, never run).
+__global__ void planted(const uint32_t* __restrict__ p, uint32_t* __restrict__ out, int n) {
+    uint32_t a0, a1, acc = 0;
+    const uint32_t off = threadIdx.x * 4u;
+    asm volatile("global_load_dword %0, %1, %2" : "=v"(a0) : "v"(off), "s"(p) : "memory");
+    asm volatile("global_load_dword %0, %1, %2 offset:4" : "=v"(a1) : "v"(off), "s"(p) : "memory");
+    for (int i = 0; i < n; i += 2) {
+        const uint32_t nx = off + (uint32_t)(i + 2) * 4u;
+#ifndef EARLY
+        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+#endif
+        asm volatile("" : "+v"(a0));
+        acc += a0 * 3u;
+        asm volatile("global_load_dword %0, %1, %2" : "=v"(a0) : "v"(nx), "s"(p) : "memory");
+        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+        asm volatile("" : "+v"(a1));
+        acc ^= a1;
+        asm volatile("global_load_dword %0, %1, %2 offset:4" : "=v"(a1) : "v"(nx), "s"(p) : "memory");
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("" : "+v"(a0), "+v"(a1));
+    out[threadIdx.x] = acc + a0 + a1;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+@pytest.mark.parametrize("early", [False, True])
+def test_build_fails_on_a_planted_early_use(tmp_path, early):
+    """build() over a source whose loop reads an asm load's register before the wait that
+    covers it raises IsaGateError and leaves no library; the same source with the wait in
+    place builds."""
+    b = _load("q4mi_build_gate", ROOT / "openflowlm-next_amd" / "build.py")
+    csrc = tmp_path / "csrc"
+    csrc.mkdir()
+    (csrc / "planted.hip").write_text(("#define EARLY 1\n" if early else "") + PLANTED)
+    lib = tmp_path / "libplanted.so"
+    if early:
+        with pytest.raises(b.IsaGateError, match="touched before their wait"):
+            b.build(jobs=2, csrc=csrc, lib=lib, build_dir=tmp_path / "_build")
+        assert not lib.exists()
+    else:
+        assert b.build(jobs=2, csrc=csrc, lib=lib, build_dir=tmp_path / "_build") == lib and lib.exists()
+        assert b.check_isa([csrc / "planted.hip"], tmp_path / "_build2", 1) >= 2   # both loads checked
+
+
+def test_gate_flags_agpr_parking_and_spills():
+    """The two forms the GPU faults took: an in-flight load's register parked in an AGPR
+    before its wait, and a kernel with asm loads that spills VGPRs."""
+    def kernel(body, spill):
+        return "\n".join([
+            "k:", "\ts_load_dwordx2 s[2:3], s[0:1], 0x0",
+            ".LBB0_1: ; %loop", "\t; Loop Header: Depth=1",
+            *body,
+            "\ts_cbranch_scc1 .LBB0_1", "\ts_endpgm", ".Lfunc_end0:",
+            "amdhsa.kernels:", "  - .agpr_count: 4", "    .name:           k",
+            f"    .vgpr_spill_count: {spill}", "    .wavefront_size: 64"])
+    load = lambda regs: ["\t;;#ASMSTART", f"\tglobal_load_dwordx4 {regs}, v1, s[2:3] nt", "\t;;#ASMEND"]
+    # two loads in flight: each register set is read after a wait that leaves only the other
+    good = ["\ts_waitcnt vmcnt(1)", "\tv_add_u32_e32 v12, v5, v6", *load("v[4:7]"),
+            "\ts_waitcnt vmcnt(1)", "\tv_add_u32_e32 v13, v9, v10", *load("v[8:11]")]
+    assert G.check_assembly(kernel(good, 0)) == (2, [])
+    parked = good[:2] + load("v[4:7]") + ["\tv_accvgpr_write_b32 a0, v5"] + good[5:]
+    n, problems = G.check_assembly(kernel(parked, 0))
+    assert n == 2 and len(problems) == 1 and "v_accvgpr_write_b32 a0, v5" in problems[0]
+    n, problems = G.check_assembly(kernel(good, 3))
+    assert problems == ["k: 3 VGPRs spilled in a kernel with in-flight asm loads"]
