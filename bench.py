@@ -643,19 +643,57 @@ def extra_q4k(torch, q4, dev):
     return out
 
 
-def extra_peaks(torch, dev):
-    """On-box reference points: HBM read bandwidth of a plain reduction over
-    4 GiB (torch.sum, reads only) and dense bf16 GEMM throughput of the vendor
-    library (torch.matmul, 8192^3, hipBLASLt) -- measured, beside the vendor peaks."""
-    x = torch.ones(1 << 30, dtype=torch.float32, device=dev)
-    _, ms = time_launches(torch, lambda: x.sum(), 10, 3)
-    read_gbs = x.numel() * 4 / ms / 1e6
-    del x
+def extra_peaks(torch, q4, dev):
+    """On-box reference points beside the vendor peaks, from the library's own probes
+    (q4_probe_stream_read, q4_probe_mfma): the HBM read rate of a plain streaming kernel
+    over 4 GiB (16-byte non-temporal loads, past the 256 MB MALL; the best of three grid
+    sizes), and the dense fp16 MFMA rate of a loop of independent 16x16x32 MFMAs on register
+    operands at 1, 2 and 4 waves per SIMD. The vendor library's dense bf16 GEMM (torch.matmul,
+    8192^3, hipBLASLt) is reported as the GEMM a library reaches on this box."""
+    lib = q4._lib.load()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    st = lambda: torch.cuda.current_stream(dev).cuda_stream
+    nbytes = 1 << 32
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    read = {}
+    for per_cu in (2, 4, 8):
+        wgs = cus * per_cu
+        out = torch.empty(lib.q4_probe_stream_read_out_bytes(wgs) // 4, dtype=torch.int32, device=dev)
+        call = lambda: lib.q4_probe_stream_read(buf.data_ptr(), nbytes, wgs, out.data_ptr(), st())
+        if call() != 0:
+            raise RuntimeError("q4_probe_stream_read failed")
+        _, ms = time_launches(torch, call, 10, 3)
+        read[f"wg_per_cu_{per_cu}"] = nbytes / ms / 1e6
+    del buf
+    # random fp16 operand sets (N(0,1), as the prefill's scaled operands toggle their bits)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+    ops = torch.randn(64, 16, 8, generator=gen, device=dev).to(torch.float16)
+    mfma, mfma_data = {}, {}
+    for waves in (1, 2, 4):
+        wgs = cus * waves
+        out = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+        for table, operands, iters, per_round in ((mfma, None, 20000, 8), (mfma_data, ops.data_ptr(), 2500, 64)):
+            call = lambda: lib.q4_probe_mfma(wgs, iters, operands, out.data_ptr(), st())
+            if call() != 0:
+                raise RuntimeError("q4_probe_mfma failed")
+            _, ms = time_launches(torch, call, 5, 2)
+            flops = wgs * 4 * iters * per_round * 16 * 16 * 32 * 2
+            table[f"waves_per_simd_{waves}"] = flops / ms / 1e9
     a = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     b = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     _, ms2 = time_launches(torch, lambda: a @ b, 10, 3)
-    return {"hbm_read_gbs_torch_sum": read_gbs, "bf16_gemm_tflops_torch_matmul": 2 * 8192 ** 3 / ms2 / 1e9,
-            "vendor_hbm_gbs": HBM_PEAK_GBS, "vendor_bf16_tflops": MFMA_PEAK_TFLOPS}
+    return {"hbm_read_gbs": max(read.values()), "hbm_read_gbs_by_grid": read,
+            "mfma_f16_tflops": max(mfma.values()), "mfma_f16_tflops_by_waves": mfma,
+            "mfma_f16_tflops_random_operands": max(mfma_data.values()),
+            "mfma_f16_tflops_random_operands_by_waves": mfma_data,
+            "bf16_gemm_tflops_torch_matmul": 2 * 8192 ** 3 / ms2 / 1e9,
+            "vendor_hbm_gbs": HBM_PEAK_GBS, "vendor_bf16_tflops": MFMA_PEAK_TFLOPS,
+            "how": "hbm_read_gbs: q4_probe_stream_read over 4 GiB, best of 2/4/8 workgroups per CU; "
+                   "mfma_f16_tflops: q4_probe_mfma, 8 independent 16x16x32 fp16 MFMA chains per wave on constant "
+                   "operands, best of 1/2/4 waves per SIMD; _random_operands: the same with 8 A x 8 B sets of "
+                   "N(0,1) fp16 operands paired differently by consecutive MFMAs (the multipliers toggle as on real "
+                   "data, and the clock falls under the power limit)"}
 
 
 def extra_config0(torch, q4, dev):
@@ -1070,7 +1108,7 @@ def main() -> int:
             elif cfg == "4":
                 out["config4_moe"] = extra_config4(torch, q4, dev)
             elif cfg == "peaks":
-                out["measured_peaks"] = extra_peaks(torch, dev)
+                out["measured_peaks"] = extra_peaks(torch, q4, dev)
             elif cfg == "lm_head":
                 out["lm_head_topk"] = extra_lm_head(torch, q4, dev)
             elif cfg == "q8":
@@ -1101,7 +1139,7 @@ def main() -> int:
         t = time.perf_counter()
         try:
             if cfg == "peaks":
-                extras["measured_peaks"] = extra_peaks(torch, dev)
+                extras["measured_peaks"] = extra_peaks(torch, q4, dev)
             elif cfg == "staged":
                 extras["config1_staged_decode_order"] = extra_staged(torch, q4, model, acts, xhead)
             elif cfg == "step":

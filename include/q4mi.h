@@ -591,6 +591,23 @@ int q4_moe_gemv_fin(const uint8_t* gate_up, const uint8_t* down, const void* x, 
                     int T, int E, int topk, int64_t H, int64_t F,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Measurement probes (no counterpart in the reference: on-box reference points for the
+ * roofline fractions the benchmark reports).
+ * q4_probe_stream_read: `workgroups` workgroups of 256 threads read `bytes` (a multiple of
+ * 16) of buf once, in contiguous shares, with 16-byte non-temporal loads; the xor of the
+ * words lands in out (q4_probe_stream_read_out_bytes(workgroups) bytes). Bytes / time is
+ * the HBM read rate a plain stream sustains (buf beyond the 256 MB MALL).
+ * q4_probe_mfma: `workgroups` workgroups of 4 waves each run iters rounds of independent
+ * v_mfma_f32_16x16x32_f16 (16 * 16 * 32 * 2 flops each) on register operands, 8 per round
+ * with operands NULL (the same constant A and B every time), 64 per round otherwise: each lane
+ * then loads 8 A and 8 B fragments (operands = fp16 [64 lanes][16][8], 16 KB, 16-byte
+ * aligned) and consecutive MFMAs pair different sets, so the multipliers toggle as on real
+ * data. One float per thread goes to out (workgroups * 256 floats). Flops / time is the dense
+ * fp16 MFMA rate with no operand traffic; workgroups = k x CUs runs k waves per SIMD. */
+size_t q4_probe_stream_read_out_bytes(int workgroups);
+int q4_probe_stream_read(const void* buf, size_t bytes, int workgroups, uint32_t* out, void* stream);
+int q4_probe_mfma(int workgroups, int iters, const void* operands, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

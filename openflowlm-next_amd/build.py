@@ -48,6 +48,8 @@ COMMON = [
 # set per source file.
 EXTRA = {
     "gemv_grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # the MFMA probe's accumulators in AGPRs get shuffled through VGPRs every iteration
+    "peaks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

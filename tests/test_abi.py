@@ -399,3 +399,15 @@ def test_rmsnorm_prepare_weight_extent_follows_its_dtype(lib):
     assert call(1, w + K * 2 - 16) == -2       # bf16: the buffer's first 16 bytes on the weight's last 8 values
     assert call(0, w + K * 2) == -2            # f32: the same address is inside its K * 4 bytes
     assert call(0, w + K * 4 - 16) == -2
+
+
+def test_probes_refuse_bad_arguments(lib):
+    """The measurement probes validate before any launch."""
+    assert lib.q4_probe_stream_read(None, 16, 0, None, None) == -5     # workgroups
+    assert lib.q4_probe_stream_read(None, 17, 4, None, None) == -1     # bytes % 16
+    assert lib.q4_probe_stream_read(None, 16, 4, None, None) == -2     # NULL
+    assert lib.q4_probe_stream_read(None, 0, 4, None, None) == 0       # nothing to read
+    assert lib.q4_probe_stream_read_out_bytes(8) == 128 and lib.q4_probe_stream_read_out_bytes(0) == 0
+    assert lib.q4_probe_mfma(0, 1, None, None, None) == -5
+    assert lib.q4_probe_mfma(1, 1, None, None, None) == -2
+    assert lib.q4_probe_mfma(1, 1, C.c_void_p(0x1004), C.c_void_p(0x1000), None) == -2   # misaligned operands
