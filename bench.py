@@ -341,7 +341,7 @@ def extra_staged(torch, q4, model, acts, xhead):
     return {"ms": ms, "gbs": nbytes / ms / 1e6, "calls": len(calls), "bytes": nbytes}
 
 
-def extra_decode_step(torch, q4, model, acts, xhead):
+def extra_decode_step(torch, q4, model, acts, xhead, only=None):
     """A decode step's weight traffic in order with its own epilogues (attention itself
     left out: its output is a fixed bf16 vector): per layer RMSNorm -> fused qkv -> o with
     the residual -> RMSNorm -> SwiGLU gate/up (bf16 h) -> down with the residual; then the
@@ -415,8 +415,12 @@ def extra_decode_step(torch, q4, model, acts, xhead):
     variants = (("separate_norms", step), ("norms_in_gemv", step_fused),
                 (f"deferred_sums_o{so}_d{sd}", deferred(so, sd)), ("deferred_sums_o4_d4", deferred(4, 4)))
     for name, fn in variants:
+        if only and name not in only:
+            continue
         ms = graph_time(torch, fn, [logits, xres, xalt], replays=10, reset=reset)
         out[name] = {"ms": ms, "gbs": nbytes / ms / 1e6}
+    if only:            # a profiling run of some variants: no cross-variant checks
+        return out
     reset()
     step()
     a = logits.clone()
@@ -898,6 +902,12 @@ def extra_config3(torch, q4, dev):
 
 
 def extra_config4(torch, q4, dev):
+    """Config 4: the routed block (128 experts, top-8 of 16 tokens, H 2048, F 768) over 4
+    rotating expert pools, graph replays; and the block with its residual and a shared expert
+    of an expert's size (F 768) as the reference's one-dispatch block runs it
+    (moe_experts.py:1-13): the shared expert inside the expert launches
+    (q4_moe_gemv_shared) against the two-step form (its own one-expert block, then the
+    finish)."""
     import numpy as np
     E, K8, H, F, T, pools = 128, 8, 2048, 768, 16, 4
     gen = torch.Generator(device=dev)
@@ -905,11 +915,10 @@ def extra_config4(torch, q4, dev):
     experts = []
     gb, db = q4.packed_bytes(2 * F, H), q4.packed_bytes(H, F)
     for _ in range(pools):             # 4 independent expert pools (4 x 377 MB) defeat the 256 MB MALL
-        gu = torch.empty(E * gb, dtype=torch.uint8, device=dev)
-        dn = torch.empty(E * db, dtype=torch.uint8, device=dev)
-        for e in range(E):
-            q4.pack_q4_1(gen_blocks(torch, 2 * F, H, gen, dev), dev, out=gu[e * gb:(e + 1) * gb])
-            q4.pack_q4_1(gen_blocks(torch, H, F, gen, dev), dev, out=dn[e * db:(e + 1) * db])
+        # an expert's matrix is whole 64-row groups, so the E experts stacked are one mx matrix:
+        # one pack per pool and matrix kind, byte-identical to packing expert by expert
+        gu = q4.pack_q4_1(gen_blocks(torch, E * 2 * F, H, gen, dev), dev).data
+        dn = q4.pack_q4_1(gen_blocks(torch, E * H, F, gen, dev), dev).data
         experts.append((q4.PackedExperts(gu, E, 2 * F, H), q4.PackedExperts(dn, E, H, F)))
     rng = np.random.default_rng(SEED)
     logits = rng.standard_normal((T, E))
@@ -930,8 +939,37 @@ def extra_config4(torch, q4, dev):
         for i, (gu, dn) in enumerate(experts):
             q4.moe_batch(gu, dn, x, ids_t, w_t, outs[i], workspace=ws)
     ms = graph_time(torch, run, outs, replays=10) / pools
-    return {"ms": ms, "gbs": nbytes / ms / 1e6, "distinct_experts": distinct, "bytes": nbytes,
-            "tflops": 2.0 * T * K8 * 3 * H * F / ms / 1e9}
+    rec = {"ms": ms, "gbs": nbytes / ms / 1e6, "distinct_experts": distinct, "bytes": nbytes,
+           "tflops": 2.0 * T * K8 * 3 * H * F / ms / 1e9}
+    # the block with the residual and a shared expert (Fs = F), one per pool
+    Fs = F
+    shared = [(q4.pack_q4_1(gen_blocks(torch, 2 * Fs, H, gen, dev), dev),
+               q4.pack_q4_1(gen_blocks(torch, H, Fs, gen, dev), dev)) for _ in range(pools)]
+    sgw = (0.05 * torch.randn(H, generator=gen, device=dev)).to(torch.bfloat16)
+    res = torch.randn(T, H, generator=gen, device=dev)
+    one_id = torch.zeros(T, 1, dtype=torch.int32, device=dev)
+    one_w = torch.ones(T, 1, device=dev)
+    ys = torch.empty(T, H, device=dev)
+    ws_s = torch.empty(q4.moe_shared_workspace_bytes(T, E, K8, H, F, Fs), dtype=torch.uint8, device=dev)
+    ws_1 = torch.empty(q4.moe_workspace_bytes(T, 1, 1, H, Fs), dtype=torch.uint8, device=dev)
+
+    def fused():
+        for i, (gu, dn) in enumerate(experts):
+            q4.moe_batch(gu, dn, x, ids_t, w_t, outs[i], workspace=ws_s, residual=res, shared_gate_w=sgw,
+                         shared_expert=shared[i])
+
+    def two_step():
+        for i, (gu, dn) in enumerate(experts):
+            sgu, sdn = shared[i]
+            q4.moe_batch(q4.PackedExperts(sgu.data, 1, 2 * Fs, H), q4.PackedExperts(sdn.data, 1, H, Fs), x, one_id,
+                         one_w, ys, workspace=ws_1)
+            q4.moe_batch(gu, dn, x, ids_t, w_t, outs[i], workspace=ws, residual=res, shared=ys, shared_gate_w=sgw)
+    sbytes = nbytes + shared[0][0].nbytes + shared[0][1].nbytes + T * H * 4
+    ms_f = graph_time(torch, fused, outs, replays=10) / pools
+    ms_2 = graph_time(torch, two_step, outs, replays=10) / pools
+    rec["with_shared_expert"] = {"Fs": Fs, "bytes": sbytes, "fused_ms": ms_f, "fused_gbs": sbytes / ms_f / 1e6,
+                                 "two_step_ms": ms_2, "two_step_gbs": sbytes / ms_2 / 1e6}
+    return rec
 
 
 def extra_moe_prefill(torch, q4, dev):
@@ -1067,6 +1105,8 @@ def main() -> int:
     ap.add_argument("--tensor", default="model.layers.0.mlp.up_proj.weight", help="the tensor --model-dir decodes")
     ap.add_argument("--shape", type=int, nargs=2, default=None, metavar=("OUT", "IN"),
                     help="the tensor's logical [out, in] for --model-dir (default [32 * chunks, 256])")
+    ap.add_argument("--step-variants", default=None,
+                    help="decode-step extra: only these variants (comma-separated names), for profiling runs")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only copy this many bytes device-to-device 5 times (calibrates HBM traffic counters)")
     a = ap.parse_args()
@@ -1143,7 +1183,8 @@ def main() -> int:
             elif cfg == "staged":
                 extras["config1_staged_decode_order"] = extra_staged(torch, q4, model, acts, xhead)
             elif cfg == "step":
-                extras["config1_decode_step"] = extra_decode_step(torch, q4, model, acts, xhead)
+                extras["config1_decode_step"] = extra_decode_step(torch, q4, model, acts, xhead,
+                                                                  a.step_variants.split(",") if a.step_variants else None)
             elif cfg == "0":
                 extras["config0_gemv_4096_f32x"] = extra_config0(torch, q4, dev)
             elif cfg == "2":

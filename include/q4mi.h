@@ -591,6 +591,26 @@ int q4_moe_gemv_fin(const uint8_t* gate_up, const uint8_t* down, const void* x, 
                     int T, int E, int topk, int64_t H, int64_t F,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* The whole decode MoE block with its shared expert inside the same launches (one
+ * dispatch chain: the expert kernels, then the finish):
+ *   out[t] = (residual[t] + sum_j topk_w[t][j] y[t][j]) + sigmoid(x[t] . sgw) * y_s[t],
+ *   y_s[t] = down_s(silu(gate_s x[t]) * (up_s x[t])), h_s in fp32,
+ * the routed y as q4_moe_gemv. The shared expert's gate/up is shared_gate_up [2 Fs, H]
+ * (gate and up 64-row groups interleaved, as an expert of gate_up) and its down shared_down
+ * [H, Fs], Fs % 64 == 0; its workgroups lead the expert kernels' grids, every token taking
+ * it with weight sigmoid(x . sgw) (shared_gate_w bf16 [H], the dot product in fp32).
+ * residual may be NULL or alias out; out must not overlap the workspace
+ * (q4_moe_shared_workspace_bytes: q4_moe_gemv's, then h_s [T][Fs] and y_s [T][H] f32).
+ * Replaces the reference's one-dispatch block, 8 routed experts plus the shared expert as a
+ * 9th streamed the same way and the combine (designs/moe_experts/moe_experts.py:1-13,
+ * moe_fin.cc), and the replica's moe_decode (model/replica.py:131-144). */
+size_t q4_moe_shared_workspace_bytes(int T, int E, int topk, int H, int F, int Fs);
+int q4_moe_gemv_shared(const uint8_t* gate_up, const uint8_t* down, const uint8_t* shared_gate_up,
+                       const uint8_t* shared_down, int64_t Fs, const uint16_t* shared_gate_w,
+                       const void* x, int x_dtype, const int32_t* topk_ids, const float* topk_w,
+                       const float* residual, float* out, int T, int E, int topk, int64_t H, int64_t F,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Measurement probes (no counterpart in the reference: on-box reference points for the
  * roofline fractions the benchmark reports).
  * q4_probe_stream_read: `workgroups` workgroups of 256 threads read `bytes` (a multiple of

@@ -137,23 +137,54 @@ __device__ __forceinline__ void up_chunk(const uint8_t* wexp, const void* x, int
     }
 }
 
+// The shared expert of a block (q4_moe_gemv_shared): a dense expert every token goes
+// through, its gate/up [2 Fs, H] interleaved as the routed experts' and its down [H, Fs].
+// Its workgroups lead the expert kernels' grids: workgroup (chunk c, row group) covers the
+// tokens [4 MAXNTL c, 4 MAXNTL (c + 1)), its h goes to hs [T][Fs] and its y to ys [T][H].
+struct SharedExpert {
+    const uint8_t* w = nullptr;   // gate/up (up kernel) or down (down kernel); null: none
+    float* out = nullptr;         // hs (up kernel) or ys (down kernel)
+    const float* h = nullptr;     // hs (down kernel)
+    int Fs = 0, T = 0, wgs = 0;   // wgs: the leading workgroups that take it
+};
+
 // Workgroup (a, rgp): the a-th routed expert's gate/up row-group pair rgp, for all the
 // pairs routed to it. MAXNTL: accumulators per row (chunks of 4 * MAXNTL routed tokens);
 // the register allocation follows the largest instance a kernel holds, so batches of at
 // most 2 pairs per expert on average take the one-accumulator instance. An expert with
-// more than 4 * MAXNTL pairs streams its rows once per chunk.
+// more than 4 * MAXNTL pairs streams its rows once per chunk. The shared expert's
+// workgroups (sh.wgs of them) come first.
 template <bool XF32, int MAXNTL>
 __global__ __launch_bounds__(64 * kUpWaves) void moe_up_kernel(const uint8_t* __restrict__ gate_up,
                                                                const void* __restrict__ x,
                                                                const int32_t* __restrict__ ids, int P, int E,
-                                                               int topk, int H, int F, float* __restrict__ hbuf) {
+                                                               int topk, int H, int F, float* __restrict__ hbuf,
+                                                               SharedExpert sh) {
     __shared__ int list[kMaxPairs];
     __shared__ int rows[16];
     __shared__ float red[kUpWaves * 4 * MAXNTL * 64];
-    const int fg = F >> 6;
-    const int e = active_expert<kUpWaves>(ids, P, E, blockIdx.x / fg);
+    if ((int)blockIdx.x < sh.wgs) {   // the shared expert: every token, chunk by chunk
+        const int fgs = sh.Fs >> 6, rgp = blockIdx.x % fgs, c0 = (blockIdx.x / fgs) * 4 * MAXNTL;
+        const int M = min(4 * MAXNTL, sh.T - c0);
+        if (threadIdx.x < 16) {
+            rows[threadIdx.x] = c0 + min((int)threadIdx.x, M - 1);
+            list[threadIdx.x] = c0 + threadIdx.x;
+        }
+        __syncthreads();
+        switch ((M + 3) / 4) {
+            case 1: up_chunk<1, XF32, kUpWaves, kUpUnr>(sh.w, x, H, sh.Fs, rgp, rows, list, M, red, sh.out); break;
+            case 2: up_chunk<MAXNTL < 2 ? 1 : 2, XF32, kUpWaves, kUpUnr>(sh.w, x, H, sh.Fs, rgp, rows, list, M, red,
+                                                                         sh.out); break;
+            case 3: up_chunk<MAXNTL < 3 ? 1 : 3, XF32, kUpWaves, kUpUnr>(sh.w, x, H, sh.Fs, rgp, rows, list, M, red,
+                                                                         sh.out); break;
+            default: up_chunk<MAXNTL, XF32, kUpWaves, kUpUnr>(sh.w, x, H, sh.Fs, rgp, rows, list, M, red, sh.out);
+        }
+        return;
+    }
+    const int fg = F >> 6, b = (int)blockIdx.x - sh.wgs;
+    const int e = active_expert<kUpWaves>(ids, P, E, b / fg);
     if (e < 0) return;
-    const int rgp = blockIdx.x % fg;
+    const int rgp = b % fg;
     const int cnt = collect_pairs<kUpWaves>(ids, P, e, list);
     const uint8_t* wexp = gate_up + (int64_t)e * (2 * F / 64) * (H / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 4 * MAXNTL) {
@@ -210,17 +241,34 @@ __device__ __forceinline__ void down_chunk(const uint8_t* wexp, const float* hbu
 }
 
 // Workgroup (a, g): NG row groups of H from g * NG of the a-th routed expert's down matrix.
+// The shared expert's workgroups (sh.wgs, token chunk by row-group span) come first.
 template <int NG, int MAXNTL>
 __global__ __launch_bounds__(64 * kDnWaves) void moe_down_kernel(const uint8_t* __restrict__ down,
                                                                  const float* __restrict__ hbuf,
                                                                  const int32_t* __restrict__ ids, int P, int E, int H,
-                                                                 int F, float* __restrict__ ypair) {
+                                                                 int F, float* __restrict__ ypair, SharedExpert sh) {
     __shared__ int list[kMaxPairs];
     __shared__ float red[kDnWaves * 4 * MAXNTL * 64];
     const int wg_per_e = (H >> 6) / NG;
-    const int e = active_expert<kDnWaves>(ids, P, E, blockIdx.x / wg_per_e);
+    if ((int)blockIdx.x < sh.wgs) {   // the shared expert: y_s = down_s h_s for a chunk of tokens
+        const int rg0 = (blockIdx.x % wg_per_e) * NG, c0 = (blockIdx.x / wg_per_e) * 4 * MAXNTL;
+        const int M = min(4 * MAXNTL, sh.T - c0);
+        if (threadIdx.x < 16) list[threadIdx.x] = c0 + threadIdx.x;
+        __syncthreads();
+        switch ((M + 3) / 4) {
+            case 1: down_chunk<1, NG, kDnWaves, kDnUnr>(sh.w, sh.h, H, sh.Fs, rg0, list, M, red, sh.out); break;
+            case 2: down_chunk<MAXNTL < 2 ? 1 : 2, NG, kDnWaves, kDnUnr>(sh.w, sh.h, H, sh.Fs, rg0, list, M, red,
+                                                                         sh.out); break;
+            case 3: down_chunk<MAXNTL < 3 ? 1 : 3, NG, kDnWaves, kDnUnr>(sh.w, sh.h, H, sh.Fs, rg0, list, M, red,
+                                                                         sh.out); break;
+            default: down_chunk<MAXNTL, NG, kDnWaves, kDnUnr>(sh.w, sh.h, H, sh.Fs, rg0, list, M, red, sh.out);
+        }
+        return;
+    }
+    const int b = (int)blockIdx.x - sh.wgs;
+    const int e = active_expert<kDnWaves>(ids, P, E, b / wg_per_e);
     if (e < 0) return;
-    const int rg0 = (blockIdx.x % wg_per_e) * NG;
+    const int rg0 = (b % wg_per_e) * NG;
     const int cnt = collect_pairs<kDnWaves>(ids, P, e, list);
     const uint8_t* wexp = down + (int64_t)e * (H / 64) * (F / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 4 * MAXNTL) {
@@ -267,19 +315,22 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     *(f32x4*)(out + t * H + n) = s;
 }
 
-// The block output with the residual and the gated shared expert folded into the combine,
-// one workgroup per token (moe_fin, designs/moe_combine/moe_fin.py:1-4 and
-// designs/moe_experts/moe_fin.cc: out = xres + sum_j w y + sigmoid(xm . sgw) * shared):
-//   g = sigmoid(x[t] . sgw) (sgw bf16 [H], the dot product in fp32, fixed reduction order),
-//   out[t][n] = (res[t][n] + sum_j w[t][j] y_pair[t][j][n]) + g shared[t][n].
-// res may be null (no residual) and may alias out; shared null leaves the gate out.
+// The block output with the residual and the gated shared expert folded into the combine
+// (moe_fin, designs/moe_combine/moe_fin.py:1-4 and designs/moe_experts/moe_fin.cc:
+// out = xres + sum_j w y + sigmoid(xm . sgw) * shared). Workgroup (chunk of 1024 n, token t),
+// as moe_combine_kernel:
+//   g = sigmoid(x[t] . sgw) (sgw bf16 [H], the dot product in fp32 in a fixed order, so every
+//       workgroup of a token forms the same g),
+//   out[t][n] = (res[t][n] + sum_j w[t][j] y_pair[t][j][n]) + g shared[t][n],
+// the routed sum formed exactly as moe_combine_kernel forms it. res may be null (no
+// residual) and may alias out; shared null leaves the gate out.
 template <bool XF32>
 __global__ __launch_bounds__(256) void moe_fin_kernel(const float* __restrict__ ypair, const int32_t* __restrict__ ids,
                                                       const float* __restrict__ w, int topk, int E, int H,
                                                       const void* __restrict__ x, const uint16_t* __restrict__ sgw,
                                                       const float* __restrict__ shared, const float* res, float* out) {
     __shared__ float red[4];
-    const int64_t t = blockIdx.x;
+    const int64_t t = blockIdx.y, n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     float g = 0.f;
     if (shared) {
         float dot = 0.f;
@@ -295,17 +346,31 @@ __global__ __launch_bounds__(256) void moe_fin_kernel(const float* __restrict__ 
         dot = (red[0] + red[1]) + (red[2] + red[3]);
         g = 1.0f / (1.0f + expf(-dot));
     }
-    for (int n = threadIdx.x; n < H; n += 256) {
-        float s = 0.f;
-        for (int j = 0; j < topk; ++j) {
-            const int64_t p = t * topk + j;
-            const int e = ids[p];
-            if (e >= 0 && e < E) s += w[p] * ypair[p * H + n];
+    if (n >= H) return;
+    f32x4 y[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < topk) y[j] = load_global<f32x4>(ypair + (t * topk + j) * H + n);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < topk) {
+            const int e = ids[t * topk + j];
+            if (e >= 0 && e < E) {
+                const float wp = w[t * topk + j];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) s[c] += wp * y[j][c];
+            }
         }
-        float v = res ? res[t * H + n] + s : s;
-        if (shared) v = __builtin_fmaf(g, shared[t * H + n], v);
-        out[t * H + n] = v;
     }
+    f32x4 v = s;
+    if (res) v = *(const f32x4*)(res + t * H + n) + s;
+    if (shared) {
+        const f32x4 sv = *(const f32x4*)(shared + t * H + n);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = __builtin_fmaf(g, sv[c], v[c]);
+    }
+    *(f32x4*)(out + t * H + n) = v;
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -319,23 +384,37 @@ extern "C" size_t q4_moe_workspace_bytes(int T, int E, int topk, int H, int F) {
     return align256(P * F * 4) + align256(P * H * 4);
 }
 
+extern "C" size_t q4_moe_shared_workspace_bytes(int T, int E, int topk, int H, int F, int Fs) {
+    if (Fs <= 0) return 0;
+    const size_t base = q4_moe_workspace_bytes(T, E, topk, H, F);
+    return base ? base + align256((size_t)T * Fs * 4) + align256((size_t)T * H * 4) : 0;
+}
+
 // The expert kernels, then the plain combine (fin == false) or the finish with residual and
-// gated shared expert (fin == true).
+// gated shared expert (fin == true). With shared_gu / shared_dn the shared expert (inner size
+// Fs) runs inside the expert kernels and its output, in the workspace, is the finish's
+// `shared`.
 static int moe_impl(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype, const int32_t* topk_ids,
                     const float* topk_w, float* out, int T, int E, int topk, int64_t H, int64_t F, void* workspace,
                     size_t workspace_bytes, void* stream, bool fin, const float* residual, const float* shared,
-                    const uint16_t* shared_gate_w) {
+                    const uint16_t* shared_gate_w, const uint8_t* shared_gu = nullptr,
+                    const uint8_t* shared_dn = nullptr, int64_t Fs = 0) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
-    if (fin && (!shared) != (!shared_gate_w)) return Q4MI_E_ARG;
+    if (fin && !shared_gu && (!shared) != (!shared_gate_w)) return Q4MI_E_ARG;
     if (H <= 0 || F <= 0 || H % 64 || F % 64) return Q4MI_E_SHAPE;
     if (H > (1 << 24) || F > (1 << 24)) return Q4MI_E_RANGE;
     if (T < 0 || E <= 0 || E > kMaxExperts || topk <= 0 || topk > 16 || (int64_t)T * topk > kMaxPairs)
         return Q4MI_E_RANGE;
+    const bool with_shared = shared_gu != nullptr;
+    if (with_shared && (Fs <= 0 || Fs % 64)) return Q4MI_E_SHAPE;
+    if (with_shared && Fs > (1 << 24)) return Q4MI_E_RANGE;
     if (T == 0) return Q4MI_OK;
     if (!gate_up || !down || !x || !topk_ids || !topk_w || !out) return Q4MI_E_ARG;
     if (misaligned16(gate_up) || misaligned16(down) || misaligned16(x) || misaligned16(out) || misaligned16(workspace))
         return Q4MI_E_ARG;
-    const size_t need = q4_moe_workspace_bytes(T, E, topk, (int)H, (int)F);
+    if (with_shared && (!shared_dn || misaligned16(shared_gu) || misaligned16(shared_dn))) return Q4MI_E_ARG;
+    const size_t need = with_shared ? q4_moe_shared_workspace_bytes(T, E, topk, (int)H, (int)F, (int)Fs)
+                                    : q4_moe_workspace_bytes(T, E, topk, (int)H, (int)F);
     if (!workspace || workspace_bytes < need) return Q4MI_E_WORKSPACE;
     const int P = T * topk;
     float* hbuf = (float*)workspace;
@@ -345,51 +424,61 @@ static int moe_impl(const uint8_t* gate_up, const uint8_t* down, const void* x, 
     // routed count leave at once.
     const int64_t routed_max = E < P ? E : P;
     const int ng = H % (64 * kDnGroups) == 0 ? kDnGroups : 1;
-    const dim3 gu((unsigned)(routed_max * (F / 64))), dn((unsigned)(routed_max * (H / (64 * ng))));
-    const dim3 bu(64 * kUpWaves), bd(64 * kDnWaves);
     // At most 2 routed pairs per expert on average (decode batches): the one-accumulator
     // instances, whose lower register use keeps more waves per SIMD. Larger batches stream
     // each expert's rows once per 16 tokens instead of once per 4.
     const bool few = P <= 2 * E;
+    SharedExpert su{}, sd{};
+    if (with_shared) {   // its buffers follow the routed ones; T / (4 MAXNTL) token chunks
+        const int chunks = (int)ceil_div(T, few ? 4 : 16);
+        float* hs = (float*)((char*)ypair + align256((size_t)P * H * 4));
+        float* ys = (float*)((char*)hs + align256((size_t)T * Fs * 4));
+        su = SharedExpert{shared_gu, hs, nullptr, (int)Fs, T, chunks * (int)(Fs / 64)};
+        sd = SharedExpert{shared_dn, ys, hs, (int)Fs, T, chunks * (int)(H / (64 * ng))};
+        shared = ys;
+    }
+    const dim3 gu((unsigned)(su.wgs + routed_max * (F / 64))), dn((unsigned)(sd.wgs + routed_max * (H / (64 * ng))));
+    const dim3 bu(64 * kUpWaves), bd(64 * kDnWaves);
     if (x_dtype == Q4MI_F32) {
         if (few)
             hipLaunchKernelGGL((moe_up_kernel<true, 1>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
-                               (int)F, hbuf);
+                               (int)F, hbuf, su);
         else
             hipLaunchKernelGGL((moe_up_kernel<true, 4>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
-                               (int)F, hbuf);
+                               (int)F, hbuf, su);
     } else {
         if (few)
             hipLaunchKernelGGL((moe_up_kernel<false, 1>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
-                               (int)F, hbuf);
+                               (int)F, hbuf, su);
         else
             hipLaunchKernelGGL((moe_up_kernel<false, 4>), gu, bu, 0, st, gate_up, x, topk_ids, P, E, topk, (int)H,
-                               (int)F, hbuf);
+                               (int)F, hbuf, su);
     }
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
     if (ng == kDnGroups) {
         if (few)
             hipLaunchKernelGGL((moe_down_kernel<kDnGroups, 1>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H,
-                               (int)F, ypair);
+                               (int)F, ypair, sd);
         else
             hipLaunchKernelGGL((moe_down_kernel<kDnGroups, 4>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H,
-                               (int)F, ypair);
+                               (int)F, ypair, sd);
     } else {
         if (few)
             hipLaunchKernelGGL((moe_down_kernel<1, 1>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H, (int)F,
-                               ypair);
+                               ypair, sd);
         else
             hipLaunchKernelGGL((moe_down_kernel<1, 4>), dn, bd, 0, st, down, hbuf, topk_ids, P, E, (int)H, (int)F,
-                               ypair);
+                               ypair, sd);
     }
     if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
     if (fin) {
+        const dim3 grid((unsigned)ceil_div(H / 4, 256), (unsigned)T);
         if (x_dtype == Q4MI_F32)
-            hipLaunchKernelGGL(moe_fin_kernel<true>, dim3((unsigned)T), dim3(256), 0, st, ypair, topk_ids, topk_w, topk,
-                               E, (int)H, x, shared_gate_w, shared, residual, out);
+            hipLaunchKernelGGL(moe_fin_kernel<true>, grid, dim3(256), 0, st, ypair, topk_ids, topk_w, topk, E, (int)H,
+                               x, shared_gate_w, shared, residual, out);
         else
-            hipLaunchKernelGGL(moe_fin_kernel<false>, dim3((unsigned)T), dim3(256), 0, st, ypair, topk_ids, topk_w,
-                               topk, E, (int)H, x, shared_gate_w, shared, residual, out);
+            hipLaunchKernelGGL(moe_fin_kernel<false>, grid, dim3(256), 0, st, ypair, topk_ids, topk_w, topk, E,
+                               (int)H, x, shared_gate_w, shared, residual, out);
         return launch_status();
     }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)ceil_div(H / 4, 256), (unsigned)T), dim3(256), 0, st, ypair,
@@ -402,6 +491,20 @@ extern "C" int q4_moe_gemv(const uint8_t* gate_up, const uint8_t* down, const vo
                            int64_t H, int64_t F, void* workspace, size_t workspace_bytes, void* stream) {
     return moe_impl(gate_up, down, x, x_dtype, topk_ids, topk_w, out, T, E, topk, H, F, workspace, workspace_bytes,
                     stream, false, nullptr, nullptr, nullptr);
+}
+
+extern "C" int q4_moe_gemv_shared(const uint8_t* gate_up, const uint8_t* down, const uint8_t* shared_gate_up,
+                                  const uint8_t* shared_down, int64_t Fs, const uint16_t* shared_gate_w,
+                                  const void* x, int x_dtype, const int32_t* topk_ids, const float* topk_w,
+                                  const float* residual, float* out, int T, int E, int topk, int64_t H, int64_t F,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    if (!shared_gate_up || !shared_down || !shared_gate_w) return Q4MI_E_ARG;
+    if (residual && misaligned16(residual)) return Q4MI_E_ARG;
+    // out [T][H] may alias the residual, nothing else the kernels read or the workspace
+    const int64_t row_bytes = (int64_t)T * H * 4;
+    if (out && workspace && overlaps(out, row_bytes, workspace, (int64_t)workspace_bytes)) return Q4MI_E_ARG;
+    return moe_impl(gate_up, down, x, x_dtype, topk_ids, topk_w, out, T, E, topk, H, F, workspace, workspace_bytes,
+                    stream, true, residual, nullptr, shared_gate_w, shared_gate_up, shared_down, Fs);
 }
 
 extern "C" int q4_moe_gemv_fin(const uint8_t* gate_up, const uint8_t* down, const void* x, int x_dtype,

@@ -623,6 +623,11 @@ def moe_prefill_workspace_bytes(t: int, e: int, topk: int, h: int, f: int) -> in
     return int(_lib_handle().q4_moe_prefill_workspace_bytes(t, e, topk, h, f))
 
 
+def moe_shared_workspace_bytes(t: int, e: int, topk: int, h: int, f: int, fs: int) -> int:
+    """Bytes q4_moe_gemv_shared needs: q4_moe_gemv's, then the shared expert's h and y."""
+    return int(_lib_handle().q4_moe_shared_workspace_bytes(t, e, topk, h, f, fs))
+
+
 def moe_workspace_bytes(t: int, e: int, topk: int, h: int, f: int) -> int:
     return int(_lib_handle().q4_moe_workspace_bytes(t, e, topk, h, f))
 
@@ -1348,7 +1353,7 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
               out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
               residual: torch.Tensor | None = None, shared: torch.Tensor | None = None,
               shared_gate_w=None, path: str = "auto", precision: str = "fp16",
-              h_bf16: bool = False) -> torch.Tensor:
+              h_bf16: bool | None = None, shared_expert: tuple | None = None) -> torch.Tensor:
     """out[t] = sum_j w[t,j] * down_e(silu(gate_e x_t) * (up_e x_t)), e = ids[t,j]; fp32 h,
     fp32 out [T, H] (moe_batch.py's per-slot product plus core.cpp:5150-5245's
     gather/scatter, done on the device).
@@ -1361,9 +1366,23 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
     ``path``: "decode" (q4_moe_gemv: routed-expert GEMVs, T * topk <= 4096), "prefill"
     (q4_moe_prefill: the experts' tokens batched into 256-token tiles of the prefill GEMM,
     any T; ``precision`` "fp16" or "bf16" as gemm_q4_prefill, h rounded to bf16 in "bf16" as
-    the reference's moe_batch does, and in "fp16" too with ``h_bf16``: down then takes one
-    pass over h instead of two), or "auto" (decode up to 4096 pairs, then prefill). The
-    prefill path takes no residual / shared expert."""
+    the reference's moe_batch does, and in "fp16" too unless ``h_bf16=False``), or "auto"
+    (decode up to 4096 pairs, then prefill). The prefill path takes no residual / shared
+    expert.
+
+    ``shared_expert`` = (gate_up_s, down_s): the block's shared expert as weights, run inside
+    the same expert launches (decode path, q4_moe_gemv_shared): gate_up_s the interleaved
+    [2 Fs, H] matrix (interleave_gate_up of its gate and up), down_s [H, Fs]; with
+    ``shared_gate_w`` it adds sigmoid(x . sgw) * down_s(silu(gate_s x) * (up_s x)) (fp32 h),
+    the replica's moe_decode (replica.py:131-144) and the reference's one-dispatch block
+    (designs/moe_experts/moe_experts.py:1-13). Takes the place of ``shared``.
+
+    ``h_bf16`` (prefill path): None, the default, rounds h to bf16, the reference kernel's
+    own h (moe_batch.h:181-202): down then takes one pass over h, and the gate/up GEMM forms h
+    in its epilogue (T = 2048 at config 4's experts: 422 us against 690 us for f32 h). False
+    keeps h in fp32 (value and fp16 remainder, two down passes), the decode kernels' h and
+    the model replica's (replica.py:139-144), for a caller that wants the same h on both sides
+    of the 4096-pair switch."""
     dev = gate_up.data.device
     xt = _acts(x, dev)
     if xt.dim() == 1:
@@ -1381,7 +1400,19 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
         raise ValueError("topk_ids / topk_w must be [T, topk]")
     topk = ids.shape[1]
     out = _buf(out, "out", torch.float32, (T, H), dev)
-    if (shared is None) != (shared_gate_w is None):
+    if shared_expert is not None:
+        if shared is not None:
+            raise ValueError("give the shared expert as its output (shared) or as weights (shared_expert), not both")
+        if shared_gate_w is None:
+            raise ValueError("shared_expert needs shared_gate_w")
+        sgu, sdn = shared_expert
+        if not isinstance(sgu, PackedQ4) or not isinstance(sdn, PackedQ4):
+            raise TypeError("shared_expert must be (PackedQ4 gate_up [2 Fs, H], PackedQ4 down [H, Fs])")
+        if sgu.k != H or sgu.n % 128 or sdn.n != H or sdn.k != sgu.n // 2:
+            raise ValueError(f"shared expert shapes {sgu.shape}, {sdn.shape} do not fit H={H}")
+        if sgu.device != dev or sdn.device != dev:
+            raise ValueError(f"the shared expert's weights must be on {dev}")
+    elif (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w go together")
     for name, t_ in (("residual", residual), ("shared", shared)):
         if t_ is not None and (t_.dtype != torch.float32 or not t_.is_contiguous() or t_.numel() != T * H
@@ -1401,7 +1432,7 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
         path = "decode" if T * topk <= MOE_DECODE_MAX_PAIRS else "prefill"
     lib = _lib_handle()
     if path == "prefill":
-        if residual is not None or shared is not None:
+        if residual is not None or shared is not None or shared_expert is not None:
             raise ValueError("the prefill MoE path takes no residual or shared expert")
         if precision not in _PRECISION:
             raise ValueError(f"precision must be one of {sorted(_PRECISION)}, got {precision!r}")
@@ -1413,8 +1444,18 @@ def moe_batch(gate_up: PackedExperts, down: PackedExperts, x, topk_ids, topk_w,
             check("q4_moe_prefill", lib.q4_moe_prefill(
                 _ptr(gate_up.data), _ptr(down.data), None if sc[0] is None else _ptr(sc[0]),
                 None if sc[1] is None else _ptr(sc[1]), _ptr(xt), _x_dtype(xt), _ptr(ids), _ptr(wts), _ptr(out),
-                T, E, topk, H, F, 2 if (precision == "fp16" and h_bf16) else _PRECISION[precision], wp, wn,
+                T, E, topk, H, F, 2 if (precision == "fp16" and h_bf16 is not False) else _PRECISION[precision], wp, wn,
                 _stream(dev)))
+        return out
+    if shared_expert is not None:
+        sgu, sdn = shared_expert
+        Fs = sgu.n // 2
+        with torch.cuda.device(dev):
+            wp, wn = _ws_arg(dev, lib.q4_moe_shared_workspace_bytes(T, E, topk, H, F, Fs), "moe", workspace)
+            check("q4_moe_gemv_shared", lib.q4_moe_gemv_shared(
+                _ptr(gate_up.data), _ptr(down.data), _ptr(sgu.data), _ptr(sdn.data), Fs, _ptr(sgw), _ptr(xt),
+                _x_dtype(xt), _ptr(ids), _ptr(wts), None if residual is None else _ptr(residual), _ptr(out),
+                T, E, topk, H, F, wp, wn, _stream(dev)))
         return out
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_moe_workspace_bytes(T, E, topk, H, F), "moe", workspace)

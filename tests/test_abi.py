@@ -411,3 +411,19 @@ def test_probes_refuse_bad_arguments(lib):
     assert lib.q4_probe_mfma(0, 1, None, None, None) == -5
     assert lib.q4_probe_mfma(1, 1, None, None, None) == -2
     assert lib.q4_probe_mfma(1, 1, C.c_void_p(0x1004), C.c_void_p(0x1000), None) == -2   # misaligned operands
+
+
+def test_moe_shared_argument_errors(lib):
+    """q4_moe_gemv_shared validates the shared expert before any launch."""
+    f = C.c_void_p(0x1000)
+    ws = lib.q4_moe_shared_workspace_bytes(16, 128, 8, 2048, 768, 768)
+    assert ws > lib.q4_moe_workspace_bytes(16, 128, 8, 2048, 768)
+    assert lib.q4_moe_shared_workspace_bytes(16, 128, 8, 2048, 768, 0) == 0
+    call = lambda sgu, sdn, Fs, sgw, out=C.c_void_p(0x9000000), wsp=C.c_void_p(0x10000000), wsb=ws: \
+        lib.q4_moe_gemv_shared(f, f, sgu, sdn, Fs, sgw, f, 1, f, f, None, out, 16, 128, 8, 2048, 768, wsp, wsb, None)
+    assert call(None, f, 768, f) == -2                 # no shared gate/up
+    assert call(f, None, 768, f) == -2                 # no shared down
+    assert call(f, f, 768, None) == -2                 # no gate vector
+    assert call(f, f, 96, f) == -1                     # Fs % 64
+    assert call(f, f, 768, f, wsb=ws - 1) == -3        # short workspace
+    assert call(f, f, 768, f, out=C.c_void_p(0x10000000 + 256)) == -2   # out inside the workspace

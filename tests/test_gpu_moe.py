@@ -170,3 +170,48 @@ def test_moe_fin_residual_and_shared_expert(gpu, pkg, oracle, E, H, F, T, K, xdt
     acc_buf = res.clone()
     pkg.moe_batch(gu, dn, xt, ids, w, out=acc_buf, residual=acc_buf, shared=sh, shared_gate_w=sgw)
     assert np.array_equal(acc_buf.cpu().numpy(), out)
+
+
+@pytest.mark.parametrize("E,H,F,Fs,T,K,xdt", [
+    (128, 2048, 768, 768, 16, 8, "bf16"),   # config 4 with a shared expert of an expert's size
+    (8, 256, 128, 192, 5, 2, "bf16"),        # Fs != F; 4-token chunks, the last one partial
+    (4, 256, 192, 128, 40, 2, "f32"),        # 16-token chunks (more than 2 pairs per expert)
+    (8, 192, 128, 256, 7, 3, "bf16"),        # H % 256 != 0: one row group per down workgroup
+])
+def test_moe_block_with_shared_expert(gpu, pkg, oracle, E, H, F, Fs, T, K, xdt):
+    """The shared expert inside the block's launches (q4_moe_gemv_shared):
+    out = (residual + routed sum) + sigmoid(x . sgw) * down_s(silu(gate_s x) (up_s x)), the
+    replica's moe_decode (replica.py:131-144), against fp64 with fp32 h; the same within fp32
+    noise as the two-step form (the shared expert run as a one-expert block, its output given
+    as `shared`); the residual may be the output buffer."""
+    say(f"moe block + shared expert E={E} H={H} F={F} Fs={Fs} T={T} top{K} {xdt}")
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 700 + Fs)
+    bgs, bus = oracle.baseline_q4_1_blocks(Fs, H, rng), oracle.baseline_q4_1_blocks(Fs, H, rng)
+    bds = oracle.baseline_q4_1_blocks(H, Fs, rng)
+    sgu = pkg.interleave_gate_up(pkg.pack_q4_1(bgs, gpu), pkg.pack_q4_1(bus, gpu))
+    sdn = pkg.pack_q4_1(bds, gpu)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xt = (torch.from_numpy(x).to(torch.bfloat16) if xdt == "bf16" else torch.from_numpy(x)).to(gpu)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    res = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(gpu)
+    sgw = torch.from_numpy(rng.standard_normal(H).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu)
+    out = pkg.moe_batch(gu, dn, xt, ids, w, residual=res, shared_gate_w=sgw, shared_expert=(sgu, sdn))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    xr = xt.to(torch.float32).cpu().numpy()
+    acc = oracle.moe_reference(g_of, u_of, d_of, xr, ids, w)
+    one = np.zeros((T, 1), np.int32)
+    sh = oracle.moe_reference(lambda e: oracle.dequant_q4_1(bgs), lambda e: oracle.dequant_q4_1(bus),
+                              lambda e: oracle.dequant_q4_1(bds), xr, one, np.ones((T, 1), np.float32))
+    ref = oracle.moe_fin_reference(acc, res.cpu().numpy(), sh, xr, sgw.cpu().view(torch.int16).numpy().view(np.uint16))
+    assert np.isfinite(got).all()
+    assert oracle.maxrel(got, ref) <= 1e-3, oracle.maxrel(got, ref)
+    # two-step form: the shared expert as a one-expert block, then the finish with its output
+    sgu_e = pkg.PackedExperts(sgu.data, 1, 2 * Fs, H)
+    sdn_e = pkg.PackedExperts(sdn.data, 1, H, Fs)
+    ys = pkg.moe_batch(sgu_e, sdn_e, xt, one, np.ones((T, 1), np.float32))
+    two = pkg.moe_batch(gu, dn, xt, ids, w, residual=res, shared=ys, shared_gate_w=sgw)
+    assert oracle.maxrel(got, two.cpu().numpy()) <= 1e-6
+    acc_buf = res.clone()
+    pkg.moe_batch(gu, dn, xt, ids, w, out=acc_buf, residual=acc_buf, shared_gate_w=sgw, shared_expert=(sgu, sdn))
+    assert np.array_equal(acc_buf.cpu().numpy(), got)

@@ -67,9 +67,9 @@ def test_moe_prefill_deterministic_and_equal_to_decode_path(gpu, pkg, oracle):
     rng, gu, dn, *_ = _make(oracle, pkg, gpu, E, H, F, 31)
     x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).to(gpu)
     ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
-    a = pkg.moe_batch(gu, dn, x, ids, w, path="prefill").cpu().numpy()
+    a = pkg.moe_batch(gu, dn, x, ids, w, path="prefill", h_bf16=False).cpu().numpy()
     for _ in range(2):
-        assert pkg.moe_batch(gu, dn, x, ids, w, path="prefill").cpu().numpy().tobytes() == a.tobytes()
+        assert pkg.moe_batch(gu, dn, x, ids, w, path="prefill", h_bf16=False).cpu().numpy().tobytes() == a.tobytes()
     d = pkg.moe_batch(gu, dn, x, ids, w, path="decode").cpu().numpy()
     assert oracle.maxrel(a, d) <= 1e-3
 
@@ -86,27 +86,39 @@ def test_moe_prefill_one_expert_takes_every_token(gpu, pkg, oracle, E):
     xt = torch.from_numpy(x).to(torch.bfloat16)
     ids = np.stack([np.full(T, 4), np.full(T, -1)], axis=1).astype(np.int32)
     w = np.stack([np.ones(T), np.full(T, 3.0)], axis=1).astype(np.float32)
-    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill").cpu().numpy()
+    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill", h_bf16=False).cpu().numpy()
     ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy(), ids[:, :1], w[:, :1])
     assert oracle.maxrel(out, ref) <= 1e-3
 
 
-@pytest.mark.parametrize("T", [512, 2048])
-def test_moe_prefill_config4_matrices_sampled_tokens(gpu, pkg, oracle, T):
+@pytest.mark.parametrize("T,prec", [(512, "fp16"), (2048, "fp16"), (2048, "fp16h"), (2048, "bf16"), (512, "auto")])
+def test_moe_prefill_config4_matrices_sampled_tokens(gpu, pkg, oracle, T, prec):
     """Config 4's experts (128 x [1536, 2048] gate/up, [2048, 768] down, top-8 routing) at
-    prefill scale: T * 8 = 4096 and 16384 pairs through the prefill path; sampled tokens held
-    to the fp64 oracle."""
+    prefill scale: T * 8 = 4096 and 16384 pairs through the prefill path, in each form the
+    bench times (fp16 tile with f32 h; fp16 tile with bf16 h and the SwiGLU epilogue, the
+    default; the reference's bf16 tile), so moe_dma_kernel runs at K = 2048 over 1536-row
+    expert matrices and at down's K = 768. "auto" at T = 512 is the decode path (4096 pairs).
+    Sampled tokens are held to the fp64 oracle (bf16 h where the form rounds h, over
+    bf16-rounded weights for the bf16 tile)."""
     E, H, F, K = 128, 2048, 768, 8
-    say(f"moe prefill config-4 matrices T={T}")
-    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 4000 + T)
+    say(f"moe prefill config-4 matrices T={T} {prec}")
+    rng, gu, dn, g_of, u_of, d_of = _make(oracle, pkg, gpu, E, H, F, 4000 + T, bf16_weights=prec == "bf16")
     x = rng.standard_normal((T, H)).astype(np.float32)
     xt = torch.from_numpy(x).to(torch.bfloat16)
     ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
-    out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill").cpu().numpy()
+    if prec == "auto":
+        out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w).cpu().numpy()
+    else:
+        out = pkg.moe_batch(gu, dn, xt.to(gpu), ids, w, path="prefill", precision="bf16" if prec == "bf16" else "fp16",
+                            h_bf16=prec != "fp16").cpu().numpy()
     assert np.isfinite(out).all()
     pick = np.sort(rng.choice(T, 12, replace=False))
-    ref = oracle.moe_reference(g_of, u_of, d_of, xt.to(torch.float32).numpy()[pick], ids[pick], w[pick])
+    xr = xt.to(torch.float32).numpy()[pick]
+    if prec == "bf16":
+        xr = oracle.bf16_round(xr)
+    ref = oracle.moe_reference(g_of, u_of, d_of, xr, ids[pick], w[pick], h_bf16=prec in ("fp16h", "bf16"))
     assert oracle.maxrel(out[pick], ref) <= 1e-3, oracle.maxrel(out[pick], ref)
+    assert oracle.rel_fro(out[pick], ref) <= 5e-3
 
 
 @pytest.mark.parametrize("prec", ["fp16", "fp16h", "bf16"])

@@ -90,3 +90,33 @@ def test_swiglu_epilogue_refuses_two_pass_activations(gpu, pkg, oracle):
     prep = pkg.prefill_prepare(x, "fp16")
     with pytest.raises(RuntimeError):
         pkg.gemm_q4_prefill_swiglu(gu, prep)
+
+
+def test_swiglu_epilogue_at_the_bench_geometry(gpu, pkg, oracle):
+    """The bench's FFN block shape: Llama-3-8B gate/up interleaved (2F = 28672, K = 4096) at
+    T = 2048. The plain GEMM's plan is unsplit there, so h equals GEMM + swiglu_prepare bit for
+    bit; sampled tokens are also held to silu(g) u of the fp64 reference GEMMs (the GEMM's
+    1e-3 bar, amplified by at most 3 through silu(g) u, plus one bf16 rounding of h)."""
+    T, F, K = 2048, 14336, 4096
+    say(f"swiglu epilogue at the bench geometry T={T} F={F} K={K}")
+    lib = pkg.load_library()
+    assert lib.q4_gemm_prefill_prepared_workspace_bytes(T, 2 * F, K) == 0, "plain plan is split"
+    rng = np.random.default_rng(2024)
+    bg, bu, _, _, gu = _gate_up(pkg, oracle, F, K, rng, gpu)
+    x = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(torch.bfloat16)
+    prep = pkg.prefill_prepare(x.to(gpu))
+    h = pkg.gemm_q4_prefill_swiglu(gu, prep)
+    y = pkg.gemm_q4_prefill(gu, prep).view(T, F // 64, 2, 64)
+    g, u = y[:, :, 0, :].reshape(T, F).contiguous(), y[:, :, 1, :].reshape(T, F).contiguous()
+    del y
+    h_ref = torch.empty(T, F, dtype=torch.bfloat16, device=gpu)
+    pkg.swiglu_prepare(g, u, h=h_ref)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_ref)
+    pick = np.array([0, 1, 255, 256, 1023, 1500, 2046, 2047])
+    xb = x.float().numpy()[pick].astype(np.float64)
+    gr = xb @ oracle.dequant_q4_1(bg).astype(np.float64).T
+    ur = xb @ oracle.dequant_q4_1(bu).astype(np.float64).T
+    ref = gr / (1.0 + np.exp(-gr)) * ur
+    got = h.float().cpu().numpy()[pick]
+    assert oracle.maxrel(got, ref) <= 3e-3 + 2.0 ** -8, oracle.maxrel(got, ref)
