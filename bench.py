@@ -91,7 +91,7 @@ class Llama:
     gate/up in one [28672, 4096] buffer: mx row groups are contiguous, so the
     fused matrix and its row slices are the same bytes."""
 
-    def __init__(self, torch, q4, dev, layers: int = 32):
+    def __init__(self, torch, q4, dev, layers: int = 32, scales: str = "bf16"):
         gen = torch.Generator(device=dev)
         gen.manual_seed(SEED)
         self.layers = []
@@ -109,11 +109,11 @@ class Llama:
                     off[key] += nb
                 else:
                     dst = torch.empty(nb, dtype=torch.uint8, device=dev)
-                parts[name] = q4.pack_q4_1(gen_blocks(torch, n, k, gen, dev), dev, out=dst)
-            parts["qkv"] = q4.PackedQ4(qkv, 6144, 4096)
-            parts["gate_up"] = q4.PackedQ4(gu, 28672, 4096)
+                parts[name] = q4.pack_q4_1(gen_blocks(torch, n, k, gen, dev), dev, out=dst, scales=scales)
+            parts["qkv"] = q4.PackedQ4(qkv, 6144, 4096, scales=scales)
+            parts["gate_up"] = q4.PackedQ4(gu, 28672, 4096, scales=scales)
             self.layers.append(parts)
-        self.head = q4.pack_q4_1(gen_blocks(torch, LM_HEAD[1], LM_HEAD[2], gen, dev), dev)
+        self.head = q4.pack_q4_1(gen_blocks(torch, LM_HEAD[1], LM_HEAD[2], gen, dev), dev, scales=scales)
         torch.cuda.synchronize()
         self.weight_bytes = sum(p[n].nbytes for p in self.layers for n, _, _ in LLAMA_LAYER) + self.head.nbytes
         self.matrices = len(self.layers) * len(LLAMA_LAYER) + 1
@@ -725,6 +725,23 @@ def extra_config0(torch, q4, dev):
             "splits": q4.gemv_split_count(ws_w[0])}
 
 
+def extra_fp16_scales(torch, q4, model, acts, xhead, steps, warmup):
+    """The headline sweep (M = 1, one grouped launch) over the same synthetic weights packed
+    with GGUF's fp16 d and m kept exactly (pack_q4_1(..., scales="fp16"), the opt-in
+    exact-scale mode), timed back to back with the bf16-scale model as an A/B on one box."""
+    dev = model.head.device
+    m16 = Llama(torch, q4, dev, scales="fp16")
+    g16, nbytes = grouped_sweep(torch, q4, m16, acts, xhead, 1)
+    gb, _ = grouped_sweep(torch, q4, model, acts, xhead, 1)
+    out = {}
+    for name, grp in (("bf16_scales", gb), ("fp16_scales", g16), ("bf16_scales_again", gb)):
+        _, per = time_launches(torch, grp.run, steps, warmup)
+        out[name] = {"ms": per, "gbs": nbytes / per / 1e6}
+    out["fp16_vs_bf16"] = out["fp16_scales"]["ms"] / (0.5 * (out["bf16_scales"]["ms"] + out["bf16_scales_again"]["ms"]))
+    del g16, m16
+    return out
+
+
 def extra_config2(torch, q4, model, steps):
     out = {}
     for M in (4, 8, 16):
@@ -1091,7 +1108,7 @@ def main() -> int:
     # HBM-bound launches reach their steady clocks after ~20 ms of load: the headline launch
     # measured 0.740 ms/step at 5 warmup steps, 0.745 at 5 of 20, 0.697 at 30 (one box)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--extras", default="staged,step,0,2,3,4,moe_prefill,lm_head,ffn,q8,q4k,q40,peaks",
+    ap.add_argument("--extras", default="staged,step,0,2,3,4,moe_prefill,lm_head,ffn,q8,q4k,q40,fp16s,peaks",
                     help="comma list (staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks) or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=3, help="passes over one layer per timed CPU run")
@@ -1180,6 +1197,8 @@ def main() -> int:
         try:
             if cfg == "peaks":
                 extras["measured_peaks"] = extra_peaks(torch, q4, dev)
+            elif cfg == "fp16s":
+                extras["fp16_scales_sweep"] = extra_fp16_scales(torch, q4, model, acts, xhead, a.steps, 10)
             elif cfg == "staged":
                 extras["config1_staged_decode_order"] = extra_staged(torch, q4, model, acts, xhead)
             elif cfg == "step":

@@ -78,7 +78,12 @@ int64_t q4_packed_bytes(int64_t N, int64_t K);
  * `gguf_blocks`: uint8[N][K/32][block_bytes], block_bytes 20 (Q4_1: fp16 d,
  * fp16 m, 16 code bytes) or 18 (Q4_0: fp16 d, codes; its min is -8 d).
  * scale_mode 0: d and m narrowed fp16 -> bf16 round-to-nearest-even, the
- * reference's pool semantics (q4_1_pack.py:104-109, :129-130). No other mode.
+ * reference's pool semantics (q4_1_pack.py:104-109, :129-130).
+ * scale_mode 1 (opt in, Q4_1 blocks only): GGUF's fp16 d and m kept exactly, the scale
+ * word fp16 d << 16 | fp16 m, as the reference's GGUF-direct pool keeps them
+ * (open_kernels/gguf_pool/gguf_pool.py:1-17, designs/gemv_q4/gemv_q4.h:54-65). Same tile
+ * size; such a matrix is read by the _fp16s entry points (q4_dequant_fp16s, q4_gemv_fp16s,
+ * q4_gemv_grouped_fp16s) and by no other.
  * Replaces pack_q4_1_pool (q4_1_pack.py:124-142) as the packer. */
 int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* packed,
               int64_t N, int64_t K, int scale_mode, void* stream);
@@ -185,6 +190,11 @@ int q4_repack_q8_split(const uint8_t* src, int src_format, int rs, int part, uin
 /* mx layout -> f32 W[N][K] row-major, w = fl32(q * d + m), bit-exact with
  * dequant_pool / dq_chunks_q4_1 (q4_1_pack.py:155-180, q4nx.py:105-126). */
 int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
+
+/* q4_dequant of a matrix packed with scale_mode 1: w = fl32(q * d + m) with GGUF's fp16 d
+ * and m, bit-exact with the reference's f32-scale unpack (q4_1_pack.py:104-109 with
+ * scale_dtype float32; q*d has 4 + 11 significant bits, exact in f32). */
+int q4_dequant_fp16s(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream);
 
 /* Workspace bytes q4_gemv needs for (M, N, K); 0 when it needs none (enough
  * 64-row groups to fill the GPU). A short matrix is split along K: the
@@ -384,6 +394,15 @@ typedef struct q4_gemv_desc {
  * gemv_q4.py:46-53 YOFF/YTOT; designs/dense, designs/moe_experts). */
 int q4_gemv_grouped(const q4_gemv_desc* descs, int count, int64_t total_items,
                     int M, int x_dtype, void* stream);
+
+/* q4_gemv_residual and q4_gemv_grouped over matrices packed with scale_mode 1 (fp16 d and m
+ * in the scale words): the same work items, plans, workspaces and arithmetic, d and m
+ * converted from fp16 (1 <= M <= 16). The GGUF-direct pool's exact-scale GEMV
+ * (designs/gemv_q4/gemv_q4.h:54-65). */
+int q4_gemv_fp16s(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
+                  int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+int q4_gemv_grouped_fp16s(const q4_gemv_desc* descs, int count, int64_t total_items,
+                          int M, int x_dtype, void* stream);
 
 /* Workspace bytes q4_logits_topk needs for M rows of n logits and k (0 if none). */
 size_t q4_topk_workspace_bytes(int M, int64_t n, int k);

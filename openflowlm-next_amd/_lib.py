@@ -28,6 +28,9 @@ class Q4GemvDesc(C.Structure):
 # name -> (restype, argtypes); every function declared in include/q4mi.h
 SIGNATURES = {
     "q4mi_version": (_i32, []),
+    "q4_dequant_fp16s": (_i32, [_vp, _vp, _i64, _i64, _vp]),
+    "q4_gemv_fp16s": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
+    "q4_gemv_grouped_fp16s": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp]),
     "q4_moe_shared_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "q4_moe_gemv_shared": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
                                   _i64, _i64, _vp, _sz, _vp]),

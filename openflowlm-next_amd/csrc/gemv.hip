@@ -69,9 +69,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // P.x_out, so the producer needs no reduce launch.
 constexpr int kXnElems = 256 * kAccRowJ;
 
-template <int NTL, bool XF32, int WAVES, bool Q40 = false, bool NORM = false, bool STREAM = false, bool XN = false>
+// F16S: the scale words hold fp16 d and m (q4_repack scale_mode 1; rolling loop, plain x).
+template <int NTL, bool XF32, int WAVES, bool Q40 = false, bool NORM = false, bool STREAM = false, bool XN = false,
+          bool F16S = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
     static_assert(!XN || (NORM && STREAM && NTL == 1 && !Q40), "XN: one row, norm, rolling loop");
+    static_assert(!F16S || (STREAM && !NORM && !Q40), "fp16 scales: the rolling loop over plain activations");
     __shared__ float red[WAVES][4][NTL][64];
     __shared__ float rrow[NORM ? 4 * NTL : 1];
     __shared__ __attribute__((aligned(16))) __bf16 xs[XN ? kXnElems : 8];
@@ -114,7 +117,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams P) {
             else
                 gemv_rows_stream<NTL, false, 1, 3, WAVES, Q40, 2>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc, nrm);
         } else {
-            gemv_rows_stream<NTL, XF32, 1, kUnr, WAVES, Q40, 0>(gb, P.x, DenseRows{P.M}, P.K, kb0, kb1, acc);
+            gemv_rows_stream<NTL, XF32, 1, kUnr, WAVES, Q40, 0, DenseRows, false, F16S>(gb, P.x, DenseRows{P.M}, P.K,
+                                                                                     kb0, kb1, acc);
         }
     } else {
         gemv_rows<NTL, XF32, DenseRows, WAVES, Q40, NORM>(P.packed, P.x, DenseRows{P.M}, P.K, g, kb0, kb1, acc[0],
@@ -527,6 +531,22 @@ void launch_gemv(bool xf32, int waves, dim3 grid, hipStream_t st, const GemvPara
     else launch_gemv_w<NTL, 4, Q40>(xf32, grid, st, P);
 }
 
+// fp16 scale words: the rolling loop only (plain activations, M <= 16).
+template <int NTL>
+void launch_gemv_f16s(bool xf32, int waves, dim3 grid, hipStream_t st, const GemvParams& P) {
+    const dim3 b(64 * waves);
+    if (waves == 16) {
+        if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, 16, false, false, true, false, true>), grid, b, 0, st, P);
+        else hipLaunchKernelGGL((gemv_kernel<NTL, false, 16, false, false, true, false, true>), grid, b, 0, st, P);
+    } else if (waves == 8) {
+        if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, 8, false, false, true, false, true>), grid, b, 0, st, P);
+        else hipLaunchKernelGGL((gemv_kernel<NTL, false, 8, false, false, true, false, true>), grid, b, 0, st, P);
+    } else {
+        if (xf32) hipLaunchKernelGGL((gemv_kernel<NTL, true, 4, false, false, true, false, true>), grid, b, 0, st, P);
+        else hipLaunchKernelGGL((gemv_kernel<NTL, false, 4, false, false, true, false, true>), grid, b, 0, st, P);
+    }
+}
+
 template <int NTL2, int WAVES>
 void launch_tb2_w(bool xf32, dim3 grid, hipStream_t st, const GemvParams& P) {
     if (xf32) hipLaunchKernelGGL((gemv_tb2_kernel<NTL2, true, WAVES>), grid, dim3(64 * WAVES), 0, st, P);
@@ -643,9 +663,9 @@ constexpr int kMaxAccSplits = 16;   // partial planes a deferred reduction takes
 
 int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* res, float* y, int M, int64_t N,
               int64_t K, void* workspace, size_t workspace_bytes, void* stream, const uint8_t* lo = nullptr,
-              bool q40 = false, NormSpec nrm = {}) {
+              bool q40 = false, NormSpec nrm = {}, bool f16s = false) {
     if (x_dtype != Q4MI_F32 && x_dtype != Q4MI_BF16) return Q4MI_E_ARG;
-    if (M < 0 || M > (lo || q40 ? 16 : kMaxGemvTokens)) return Q4MI_E_RANGE;
+    if (M < 0 || M > (lo || q40 || f16s ? 16 : kMaxGemvTokens)) return Q4MI_E_RANGE;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     if (M == 0 || N == 0) return Q4MI_OK;   // nothing to compute
     if (!packed || !x || !y) return Q4MI_E_ARG;
@@ -689,7 +709,14 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
     const dim3 grid((unsigned)((N / 64) * S));
     const hipStream_t st = (hipStream_t)stream;
     const bool xf32 = x_dtype == Q4MI_F32;
-    if (lo) {
+    if (f16s) {
+        switch ((M + 3) / 4) {
+            case 1: launch_gemv_f16s<1>(xf32, plan.waves, grid, st, P); break;
+            case 2: launch_gemv_f16s<2>(xf32, plan.waves, grid, st, P); break;
+            case 3: launch_gemv_f16s<3>(xf32, plan.waves, grid, st, P); break;
+            default: launch_gemv_f16s<4>(xf32, plan.waves, grid, st, P); break;
+        }
+    } else if (lo) {
         switch ((M + 3) / 4) {
             case 1: launch_pair<1>(xf32, grid, st, P, lo); break;
             case 2: launch_pair<2>(xf32, grid, st, P, lo); break;
@@ -794,6 +821,14 @@ extern "C" int q4_gemv_q8(const uint8_t* hi, const uint8_t* lo, const void* x, i
                           void* stream) {
     if (M > 0 && N > 0 && (!lo || misaligned16(lo))) return Q4MI_E_ARG;
     return gemv_impl(hi, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream, lo);
+}
+
+// The GEMV over fp16 scale words (q4_repack scale_mode 1): q4_gemv's work items, plan,
+// workspace and arithmetic, d and m converted from fp16 instead of bf16.
+extern "C" int q4_gemv_fp16s(const uint8_t* packed, const void* x, int x_dtype, const float* residual, float* y,
+                             int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+    return gemv_impl(packed, x, x_dtype, residual, y, M, N, K, workspace, workspace_bytes, stream, nullptr, false,
+                     NormSpec{}, true);
 }
 
 // The mx0 (Q4_0-native) GEMV: q4_gemv's work items, plan and workspace over 1152 B tiles.

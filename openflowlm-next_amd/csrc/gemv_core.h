@@ -579,7 +579,8 @@ __device__ __forceinline__ void gemv_rows_pipe(const uint8_t* const (&gbase)[NG]
 // One K position's arithmetic over NG row groups (gemv_rows' per-tile body; multi_tile's
 // for NG > 1): codes c[i], scale words s[i] (mx: d<<16 | m per row sub-tile; mx0: four
 // bf16 d in s[i][0..1]), activation fragment xh (+ xl for f32 x) shared by the groups.
-template <int NTL, bool XF32, bool Q40, int NG>
+// F16S: the scale words hold fp16 d and m (q4_repack scale_mode 1).
+template <int NTL, bool XF32, bool Q40, int NG, bool F16S = false>
 __device__ __forceinline__ void tile_math(const u32x4 (&c)[NG], const u32x4 (&s)[NG], bf16x8 xh, bf16x8 xl,
                                           CodeConsts kc, float (&acc)[NG][4][NTL]) {
     const bf16x8 neg128 = __builtin_bit_cast(bf16x8, u32x4{0xC300C300u, 0xC300C300u, 0xC300C300u, 0xC300C300u});
@@ -605,8 +606,8 @@ __device__ __forceinline__ void tile_math(const u32x4 (&c)[NG], const u32x4 (&s)
                 d = bf16_hi_to_f32(r & 1 ? s[i][r >> 1] : s[i][r >> 1] << 16);
                 m = -8.0f * d;
             } else {
-                d = bf16_hi_to_f32(s[i][r]);
-                m = bf16_lo_to_f32(s[i][r]);
+                d = scale_d<F16S>(s[i][r]);
+                m = scale_m<F16S>(s[i][r]);
             }
 #pragma unroll
             for (int j = 0; j < NTL; ++j) {
@@ -633,11 +634,13 @@ __device__ __forceinline__ void tile_math(const u32x4 (&c)[NG], const u32x4 (&s)
 // XS: the activations were staged in LDS as bf16 fragments (xs[m][kr] over the K range
 // [kb0, kb1) of 32-wide positions, e.g. by stage_norm_acc_row), so a position is its weight
 // loads only.
-template <int NTL, bool XF32, int NG, int UNR, int WAVES, bool Q40, int NW, class Rows, bool XS = false>
+template <int NTL, bool XF32, int NG, int UNR, int WAVES, bool Q40, int NW, class Rows, bool XS = false,
+          bool F16S = false>
 __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[NG], const void* __restrict__ x,
                                                  Rows rows, int64_t K, int kb0, int kb1, float (&acc)[NG][4][NTL],
                                                  NormIn nrm = {}, const __bf16* xs = nullptr, int kr = 0) {
     static_assert(!XS || (!XF32 && NW == 0), "staged fragments are one bf16 plane");
+    static_assert(!F16S || !Q40, "fp16 scale words are an mx-layout mode");
     constexpr int TB = Q40 ? kQ0TileBytes : kTileBytes;
     constexpr int XL = XS ? 0 : NW == 0 ? (XF32 ? 2 : 1) : (NW == 1 ? 3 : 4);   // activation-side loads
     constexpr int L = 2 * NG + XL;                                     // loads per K position
@@ -724,7 +727,7 @@ __device__ __forceinline__ void gemv_rows_stream(const uint8_t* const (&gbase)[N
             sw[i] = s[u][i];
             if constexpr (Q40) sw[i] = odd ? u32x4{sw[i][2], sw[i][3], 0u, 0u} : u32x4{sw[i][0], sw[i][1], 0u, 0u};
         }
-        tile_math<NTL, XF32, Q40, NG>(c[u], sw, xh, xl, kc, acc);
+        tile_math<NTL, XF32, Q40, NG, F16S>(c[u], sw, xh, xl, kc, acc);
     };
 #pragma unroll
     for (int u = 0; u < UNR; ++u) issue(u, u);

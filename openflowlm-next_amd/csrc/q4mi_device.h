@@ -111,6 +111,20 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+// The scale word's d and m as f32: bf16 halves (the mx layout's default, the reference
+// pool's narrowing) or, with F16S, GGUF's own fp16 d and m kept exactly (q4_repack
+// scale_mode 1). Either converts exactly.
+template <bool F16S>
+__device__ __forceinline__ float scale_d(uint32_t s) {
+    if constexpr (F16S) return f16_bits_to_f32(s >> 16);
+    else return bf16_hi_to_f32(s);
+}
+template <bool F16S>
+__device__ __forceinline__ float scale_m(uint32_t s) {
+    if constexpr (F16S) return f16_bits_to_f32(s & 0xFFFFu);
+    else return bf16_lo_to_f32(s);
+}
+
 // Device buffers are global memory. Loads through these address-space-1 pointers are
 // global_load instructions whatever the pointer's origin: a pointer read from memory (a
 // descriptor table) is otherwise a flat pointer, and flat loads count on lgkmcnt too, so

@@ -13,6 +13,9 @@
 //   dequant: w = fl32(q * d + m) (q4_1_pack.py:155-170, q4nx.py:105-126);
 //     q*d is exact in f32 (4-bit x 8-bit significands), so one fma equals the
 //     reference's multiply-then-add bit for bit.
+//   scale_mode 1 (opt in): GGUF's fp16 d and m kept exactly in the scale word
+//     (fp16 d << 16 | fp16 m), as the GGUF-direct pool keeps them (gguf_pool.py:1-17,
+//     gemv_q4.h:54-65); then q*d has 4 + 11 significant bits, still exact in f32.
 #include "q4mi_device.h"
 #include "q4mi_internal.h"
 
@@ -38,7 +41,8 @@ __device__ __forceinline__ void mx_write_block(uint8_t* packed, int64_t KB, int6
 }
 
 __global__ __launch_bounds__(256) void repack_gguf_kernel(const uint8_t* __restrict__ src, int bw,
-                                                          uint8_t* __restrict__ packed, int64_t N, int64_t KB) {
+                                                          uint8_t* __restrict__ packed, int64_t N, int64_t KB,
+                                                          int f16s) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= N * KB) return;
     // idx -> (tile, row): 64 consecutive threads fill one tile
@@ -46,14 +50,16 @@ __global__ __launch_bounds__(256) void repack_gguf_kernel(const uint8_t* __restr
     const int64_t n = (tile / KB) * 64 + (idx & 63);
     const int64_t kb = tile % KB;
     const uint8_t* b = src + (n * KB + kb) * bw;
-    uint32_t dbits = (uint32_t)b[0] | ((uint32_t)b[1] << 8);
+    uint32_t dbits = (uint32_t)b[0] | ((uint32_t)b[1] << 8), mbits;
     float d = f16_bits_to_f32(dbits), m;
     const uint8_t* qs;
     if (bw == 20) {
-        m = f16_bits_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+        mbits = (uint32_t)b[2] | ((uint32_t)b[3] << 8);
+        m = f16_bits_to_f32(mbits);
         qs = b + 4;
     } else {
         m = -8.0f * d;   // Q4_0 written the Q4_1 way; exact
+        mbits = 0;       // (scale_mode 1 takes Q4_1 blocks only)
         qs = b + 2;
     }
     uint8_t code[32];
@@ -63,7 +69,8 @@ __global__ __launch_bounds__(256) void repack_gguf_kernel(const uint8_t* __restr
         code[j] = v & 0xF;
         code[j + 16] = v >> 4;
     }
-    mx_write_block(packed, KB, n, kb, code, (f32_to_bf16_rne(d) << 16) | f32_to_bf16_rne(m));
+    const uint32_t word = f16s ? (dbits << 16) | mbits : (f32_to_bf16_rne(d) << 16) | f32_to_bf16_rne(m);
+    mx_write_block(packed, KB, n, kb, code, word);
 }
 
 // f32_scales: the GGUF-direct pool's 6144 B chunks (open_kernels/gguf_pool/gguf_pool.py:
@@ -545,7 +552,9 @@ __global__ __launch_bounds__(256) void dequant_mx0_kernel(const uint8_t* __restr
     out[1] = hi;
 }
 
-// Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats.
+// Thread per (row n, 8-wide k group): one codes dword + one scale word -> 8 floats. F16S: the
+// scale word holds fp16 d and m (scale_mode 1).
+template <bool F16S>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ packed, float* __restrict__ w,
                                                       int64_t N, int64_t K) {
     const int64_t K8 = K >> 3;
@@ -558,7 +567,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
     const uint8_t* tile = packed + (g * KB + kb) * kTileBytes;
     const uint32_t c = *(const uint32_t*)(tile + (kg * 16 + i16) * 16 + r * 4);
     const uint32_t s = *(const uint32_t*)(tile + kCodeBytes + i16 * 16 + r * 4);
-    const float d = bf16_hi_to_f32(s), m = bf16_lo_to_f32(s);
+    const float d = scale_d<F16S>(s), m = scale_m<F16S>(s);
     f32x4 lo, hi;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -581,7 +590,8 @@ extern "C" int64_t q4_packed_bytes(int64_t N, int64_t K) {
 extern "C" int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* packed, int64_t N, int64_t K,
                          int scale_mode, void* stream) {
     if (block_bytes != 20 && block_bytes != 18) return Q4MI_E_ARG;
-    if (scale_mode != 0) return Q4MI_E_ARG;
+    if (scale_mode != 0 && scale_mode != 1) return Q4MI_E_ARG;
+    if (scale_mode == 1 && block_bytes != 20) return Q4MI_E_ARG;   // Q4_0 has its exact mx0 layout
     if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;   // empty: nothing to touch
     if (!gguf_blocks || !packed) return Q4MI_E_ARG;
     if (misaligned16(packed)) return Q4MI_E_ARG;
@@ -589,7 +599,7 @@ extern "C" int q4_repack(const uint8_t* gguf_blocks, int block_bytes, uint8_t* p
     const int64_t KB = K / 32, total = N * KB;
     const unsigned grid = (unsigned)((total + 255) / 256);
     hipLaunchKernelGGL(repack_gguf_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, gguf_blocks,
-                       block_bytes, packed, N, KB);
+                       block_bytes, packed, N, KB, scale_mode);
     return launch_status();
 }
 
@@ -617,15 +627,26 @@ extern "C" int q4_repack_pool_f32(const uint8_t* pool, int rs, uint8_t* packed, 
     return launch_status();
 }
 
-extern "C" int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
+static int dequant_impl(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream, bool f16s) {
     if (N == 0 && K > 0 && K % 32 == 0) return Q4MI_OK;
     if (!packed || !w) return Q4MI_E_ARG;
     if (misaligned16(packed) || misaligned16(w)) return Q4MI_E_ARG;
     if (N < 0 || K <= 0 || N % 64 || K % 32) return Q4MI_E_SHAPE;
     const int64_t total = N * (K / 8);
     const unsigned grid = (unsigned)((total + 255) / 256);
-    hipLaunchKernelGGL(dequant_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, packed, w, N, K);
+    if (f16s)
+        hipLaunchKernelGGL(dequant_kernel<true>, dim3(grid), dim3(256), 0, (hipStream_t)stream, packed, w, N, K);
+    else
+        hipLaunchKernelGGL(dequant_kernel<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream, packed, w, N, K);
     return launch_status();
+}
+
+extern "C" int q4_dequant(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
+    return dequant_impl(packed, w, N, K, stream, false);
+}
+
+extern "C" int q4_dequant_fp16s(const uint8_t* packed, float* w, int64_t N, int64_t K, void* stream) {
+    return dequant_impl(packed, w, N, K, stream, true);
 }
 
 extern "C" int q4_repack_q4k(const uint8_t* q4k_blocks, uint8_t* packed, int64_t N, int64_t K, void* stream) {

@@ -115,6 +115,10 @@ class PackedQ4:
     n: int
     k: int
     prefill_scales: torch.Tensor | None = field(default=None, repr=False, compare=False)
+    # "bf16": d and m narrowed to bf16 (the reference pool's scales); "fp16": GGUF's fp16 d
+    # and m kept exactly (pack_q4_1(..., scales="fp16")), read by dequant, gemm_q4 (M <= 16),
+    # gemv_q4 and GemvGroup only
+    scales: str = "bf16"
 
     @property
     def shape(self):
@@ -149,12 +153,16 @@ class PackedExperts:
 # packing and dequant
 # --------------------------------------------------------------------------
 
-def pack_q4_1(blocks, device=None, out: torch.Tensor | None = None) -> PackedQ4:
+def pack_q4_1(blocks, device=None, out: torch.Tensor | None = None, scales: str = "bf16") -> PackedQ4:
     """GGUF Q4_1 (20 B) or Q4_0 (18 B) blocks uint8[N, K/32, w] -> mx layout on the GPU.
 
-    d and m are narrowed fp16 -> bf16 (RNE), exactly the reference pool's
-    semantics (q4_1_pack.py:104-109, :129-130); the block width says which
-    format it is, as in q4_1_pack.py:8-9."""
+    ``scales="bf16"``: d and m are narrowed fp16 -> bf16 (RNE), exactly the reference
+    pool's semantics (q4_1_pack.py:104-109, :129-130); the block width says which format
+    it is, as in q4_1_pack.py:8-9. ``scales="fp16"`` (Q4_1 only): GGUF's fp16 d and m kept
+    exactly, as the reference's GGUF-direct pool keeps them (gguf_pool.py:1-17); such a
+    matrix goes to dequant, gemm_q4 / gemv_q4 (M <= 16) and GemvGroup."""
+    if scales not in ("bf16", "fp16"):
+        raise ValueError(f"scales must be 'bf16' or 'fp16', got {scales!r}")
     dev = _device(device if device is not None else (blocks.device if isinstance(blocks, torch.Tensor)
                                                      and blocks.is_cuda else None))
     src = _to_dev(blocks, dev, torch.uint8)
@@ -164,9 +172,12 @@ def pack_q4_1(blocks, device=None, out: torch.Tensor | None = None) -> PackedQ4:
     k = nb * BLK
     nbytes = packed_bytes(n, k)
     out = _buf(out, "out", torch.uint8, (nbytes,), dev)
+    if scales == "fp16" and w != 20:
+        raise ValueError("fp16 scales are a Q4_1 mode (Q4_0 has the exact mx0 layout: pack_q4_0_native)")
     with torch.cuda.device(dev):
-        check("q4_repack", _lib_handle().q4_repack(_ptr(src), w, _ptr(out), n, k, 0, _stream(dev)))
-    return PackedQ4(out[:nbytes], n, k)
+        check("q4_repack", _lib_handle().q4_repack(_ptr(src), w, _ptr(out), n, k, int(scales == "fp16"),
+                                                   _stream(dev)))
+    return PackedQ4(out[:nbytes], n, k, scales=scales)
 
 
 def pack_q4_1_pool(pool, n: int, k: int, rs: int, device=None) -> PackedQ4:
@@ -571,9 +582,17 @@ def dequant(w: PackedQ4, out: torch.Tensor | None = None) -> torch.Tensor:
     """mx layout -> f32[n, k], w = fl32(q*d + m), bit-exact with dequant_pool."""
     dev = w.device
     out = _buf(out, "out", torch.float32, (w.n, w.k), dev)
+    fn = "q4_dequant_fp16s" if w.scales == "fp16" else "q4_dequant"
     with torch.cuda.device(dev):
-        check("q4_dequant", _lib_handle().q4_dequant(_ptr(w.data), _ptr(out), w.n, w.k, _stream(dev)))
+        check(fn, getattr(_lib_handle(), fn)(_ptr(w.data), _ptr(out), w.n, w.k, _stream(dev)))
     return out
+
+
+def _bf16_scales(op: str, *ws) -> None:
+    """Refuse matrices packed with fp16 scale words where only the bf16 form is built."""
+    for w in ws:
+        if getattr(w, "scales", "bf16") != "bf16":
+            raise ValueError(f"{op} takes matrices with bf16 scales (pack_q4_1(..., scales='bf16'))")
 
 
 # --------------------------------------------------------------------------
@@ -671,6 +690,18 @@ def gemm_q4(w: PackedQ4, x, y: torch.Tensor | None = None, workspace: torch.Tens
         raise ValueError(f"gemm_q4 takes 1..24 tokens, got {M} (use gemm_q4_prefill)")
     y = _buf(y, "y", torch.float32, (M, w.n), dev)
     lib = _lib_handle()
+    if w.scales == "fp16":
+        if M > 16:
+            raise ValueError(f"a matrix with fp16 scales takes 1..16 tokens, got {M}")
+        if residual is not None and (residual.dtype != torch.float32 or not residual.is_contiguous()
+                                     or residual.numel() != M * w.n or residual.device != dev):
+            raise ValueError(f"residual must be a contiguous float32 [{M}, {w.n}] tensor on {dev}")
+        with torch.cuda.device(dev):
+            wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+            check("q4_gemv_fp16s", lib.q4_gemv_fp16s(_ptr(w.data), _ptr(xt), _x_dtype(xt),
+                                                     None if residual is None else _ptr(residual), _ptr(y), M, w.n,
+                                                     w.k, wp, wn, _stream(dev)))
+        return y
     with torch.cuda.device(dev):
         wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
         if residual is None:
@@ -733,6 +764,7 @@ def gemm_q4_rmsnorm(w: PackedQ4, x: torch.Tensor, norm_w: torch.Tensor, eps: flo
     """Y = bf16(RMSNorm(x) * norm_w) @ W^T with the norm formed inside the GEMV from the f32
     residual stream x [M, K] (1 <= M <= 16, K <= 16384): the bits of rmsnorm_add (bf16 out)
     followed by gemm_q4, with no launch and no copy for the norm."""
+    _bf16_scales("gemm_q4_rmsnorm", w)
     dev = w.device
     xt = _norm_x(x, w.k, dev)
     M = xt.shape[0]
@@ -750,6 +782,7 @@ def gemm_q4_rmsnorm(w: PackedQ4, x: torch.Tensor, norm_w: torch.Tensor, eps: flo
 
 def gemv_split_count(w: PackedQ4) -> int:
     """The K-split count gemm_q4 plans for ``w`` at decode sizes (1: unsplit)."""
+    _bf16_scales("gemv_split_count", w)
     return int(_lib_handle().q4_gemv_split_count(w.n, w.k))
 
 
@@ -759,6 +792,7 @@ def gemm_q4_partials(w: PackedQ4, x, splits: int | None = None, part: torch.Tens
     default ``splits`` (gemv_split_count) they add up, in split order, to gemm_q4's Y bit
     for bit. The planes go to gemm_q4_rmsnorm_acc / swiglu_q4_acc, which add them to the
     residual stream in place of gemm_q4(residual=...)'s reduce launch."""
+    _bf16_scales("gemm_q4_partials", w)
     dev = w.device
     xt = _acts(x, dev)
     if xt.dim() == 1:
@@ -806,6 +840,7 @@ def gemm_q4_rmsnorm_acc(w: PackedQ4, res: torch.Tensor, partials: torch.Tensor |
     residual=res)'s bits for the GEMV that made them), then y = gemm_q4_rmsnorm(w, x_out,
     norm_w) -- with the reduction inside the norm GEMV's workgroups at M = 1 (K <= 4096)
     instead of a launch of its own. ``x_out`` must not share memory with ``res``."""
+    _bf16_scales("gemm_q4_rmsnorm_acc", w)
     dev = w.device
     xt, M, S, pp, x_out = _acc_args(res, partials, x_out, w.k, dev)
     if not 1 <= M <= 16:
@@ -826,6 +861,7 @@ def swiglu_q4_acc(gate: PackedQ4, up: PackedQ4, res: torch.Tensor, partials: tor
                   h: torch.Tensor | None = None, workspace: torch.Tensor | None = None):
     """(h, x_out): x_out = res + partials as in gemm_q4_rmsnorm_acc, then h =
     swiglu_q4(gate, up, x_out, norm_w=norm_w)."""
+    _bf16_scales("swiglu_q4_acc", gate, up)
     if gate.n != up.n or gate.k != up.k or gate.device != up.device:
         raise ValueError(f"gate {gate.shape} and up {up.shape} must match")
     dev = gate.device
@@ -853,6 +889,7 @@ def swiglu_q4(gate: PackedQ4, up: PackedQ4, x, out_dtype=torch.float32, h: torch
     epilogue (designs/silu_mul/silu_mul.cc). ``out_dtype`` float32 or bfloat16 (RNE),
     the down projection's input. With ``norm_w``, x is the f32 residual stream and
     X = bf16(RMSNorm(x) * norm_w) is formed inside the kernel (rmsnorm_add's bits)."""
+    _bf16_scales("swiglu_q4", gate, up)
     if gate.n != up.n or gate.k != up.k or gate.device != up.device:
         raise ValueError(f"gate {gate.shape} and up {up.shape} must match")
     dev = gate.device
@@ -987,6 +1024,7 @@ def lm_head_topk(w: PackedQ4, x, k: int = 1, mode: str = "sampler", n_valid: int
     """lm_head over 1..16 tokens and its sampling epilogue in one call:
     (ids int32[M, k], vals f32[M, k], logits f32[M, N]) (designs/lm_head_q4 plus the
     host's greedy / top-k pass; see logits_topk for ``mode`` and ``n_valid``)."""
+    _bf16_scales("lm_head_topk", w)
     dev = w.device
     xt = _acts(x, dev)
     if xt.dim() == 1:
@@ -1024,7 +1062,10 @@ class GemvGroup:
         begin = 0
         m0 = dt = None
         self._keep = []
+        self.scales = items[0][0].scales
         for i, (w, x, y) in enumerate(items):
+            if w.scales != self.scales:
+                raise ValueError("all group members need the same scale form (bf16 or fp16)")
             if x.device != dev or y.device != dev or w.device != dev:
                 raise ValueError("all group members must be on one device")
             xx = x if x.dim() == 2 else x.view(1, -1)
@@ -1054,8 +1095,9 @@ class GemvGroup:
         self.weight_bytes = sum(w.nbytes for w, _, _ in self._keep)
 
     def run(self) -> None:
+        fn = "q4_gemv_grouped_fp16s" if self.scales == "fp16" else "q4_gemv_grouped"
         with torch.cuda.device(self.device):
-            check("q4_gemv_grouped", _lib_handle().q4_gemv_grouped(
+            check(fn, getattr(_lib_handle(), fn)(
                 _ptr(self.table), self.count, self.total_items, self.M, self.x_dtype, _stream(self.device)))
 
     __call__ = run
@@ -1072,6 +1114,7 @@ def prefill_scales(w) -> torch.Tensor:
     """The matrix's fp16 prefill scales (per-row power-of-two exponents and the scale words
     in fp16, q4_prefill_scales), computed on first use and kept on ``w`` (a PackedQ4, or a
     PackedExperts as its stacked [E n, k] matrix)."""
+    _bf16_scales("prefill_scales", w)
     if w.prefill_scales is None:
         dev = w.data.device
         n = w.n * w.experts if isinstance(w, PackedExperts) else w.n
@@ -1200,6 +1243,7 @@ def swiglu_prepare(g: torch.Tensor, u: torch.Tensor | None = None, precision: st
 def interleave_gate_up(gate: PackedQ4, up: PackedQ4) -> PackedQ4:
     """One mx matrix [2F, K] whose 64-row groups alternate gate / up (a device copy of the two
     matrices' row groups): the layout gemm_q4_prefill_swiglu and the MoE experts take."""
+    _bf16_scales("interleave_gate_up", gate, up)
     if gate.n != up.n or gate.k != up.k or gate.device != up.device:
         raise ValueError("gate and up must have the same shape and device")
     rg = gate.nbytes // (gate.n // 64)
@@ -1214,6 +1258,7 @@ def gemm_q4_prefill_swiglu(gate_up: PackedQ4, x, h: torch.Tensor | None = None,
     SwiGLU in its epilogue (moe_batch.h:181-202's bf16 h), over an interleaved gate/up matrix
     (interleave_gate_up) and bf16 or prepared activations; the same h swiglu_prepare forms
     from the plain GEMM's f32 outputs, with no f32 output in memory. F % 128 == 0, K % 64 == 0."""
+    _bf16_scales("gemm_q4_prefill_swiglu", gate_up)
     dev = gate_up.device
     if isinstance(x, PreparedActs):
         if x.data.device != dev:
@@ -1247,6 +1292,7 @@ def gemm_q4_prefill_partials(w: PackedQ4, x: PreparedActs, part: torch.Tensor | 
     sum is gemm_q4_prefill's Y bit for bit (S = the plan's split count, 1 when unsplit). They go
     to rmsnorm_prepare(add=...), which sums them in the residual add of the next norm
     (the reference sums its down K-pieces on the host, ironutil.py:98-115)."""
+    _bf16_scales("gemm_q4_prefill_partials", w)
     if not isinstance(x, PreparedActs):
         raise TypeError("gemm_q4_prefill_partials takes prepared activations (prefill_prepare / rmsnorm_prepare)")
     if x.k != w.k:
@@ -1274,6 +1320,7 @@ def gemm_q4_prefill(w: PackedQ4, x, y: torch.Tensor | None = None, precision: st
     rows scaled into fp16's range by powers of two (the matrix's prefill scales, computed
     once and kept on ``w``); "bf16": the reference tile RNE_bf16(fl32(q*d+m))
     (gemm_q4_dequant.h:283-286). ``x`` may be a PreparedActs (its own precision is used)."""
+    _bf16_scales("gemm_q4_prefill", w)
     dev = w.device
     if isinstance(x, PreparedActs):
         if x.k != w.k:

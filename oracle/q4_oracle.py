@@ -427,10 +427,19 @@ _E = np.arange(8)
 _NIB_SHIFT = 16 * (_E % 2) + 4 * (_E // 2)        # bit position of element e
 
 
-def pack_mx(blocks: np.ndarray) -> np.ndarray:
+def pack_mx(blocks: np.ndarray, fp16_scales: bool = False) -> np.ndarray:
     """GGUF Q4_1/Q4_0 blocks [N, K/32, 20|18] -> the MI355X layout bytes
-    (d and m narrowed to bf16 by RNE, as q4_1_pack.py:129-130 does)."""
+    (d and m narrowed to bf16 by RNE, as q4_1_pack.py:129-130 does). ``fp16_scales``
+    (Q4_1 blocks): the scale word carries GGUF's own fp16 d and m bits unchanged, the
+    exact-scale mode (the GGUF-direct pool keeps them, gguf_pool/gguf_pool.py:1-17)."""
     d, m, q = unpack_q4_1_blocks(blocks)
+    if fp16_scales:
+        if blocks.shape[2] != Q4_1_BYTES:
+            raise ValueError("fp16 scale words are a Q4_1 mode")
+        n, nb = d.shape
+        d16 = np.ascontiguousarray(blocks[..., 0:2]).view(np.uint16).reshape(n, nb)
+        m16 = np.ascontiguousarray(blocks[..., 2:4]).view(np.uint16).reshape(n, nb)
+        return pack_mx_from_parts(d16, m16, q)
     return pack_mx_from_parts(f32_to_bf16(d), f32_to_bf16(m), q)
 
 
@@ -449,11 +458,13 @@ def unpack_mx(packed: np.ndarray, n: int, k: int):
     return (s >> np.uint32(16)).astype(np.uint16), (s & np.uint32(0xFFFF)).astype(np.uint16), q.reshape(n, k)
 
 
-def dequant_mx(packed: np.ndarray, n: int, k: int) -> np.ndarray:
-    """MI355X layout -> f32[n, k] = fl32(q*d + m) with the stored bf16 d, m."""
+def dequant_mx(packed: np.ndarray, n: int, k: int, fp16_scales: bool = False) -> np.ndarray:
+    """MI355X layout -> f32[n, k] = fl32(q*d + m) with the stored bf16 d, m (or, with
+    ``fp16_scales``, the stored fp16 d, m of the exact-scale mode)."""
     d16, m16, q = unpack_mx(packed, n, k)
-    d = np.repeat(bf16_to_f32(d16), BLK, axis=1)
-    m = np.repeat(bf16_to_f32(m16), BLK, axis=1)
+    conv = (lambda b: b.view(np.float16).astype(np.float32)) if fp16_scales else bf16_to_f32
+    d = np.repeat(conv(d16), BLK, axis=1)
+    m = np.repeat(conv(m16), BLK, axis=1)
     return q.astype(np.float32) * d + m
 
 

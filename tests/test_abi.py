@@ -56,7 +56,12 @@ def test_argument_errors_before_any_launch(lib):
     """Every one of these returns before a HIP call (no GPU needed)."""
     fake = C.c_void_p(0x1000)   # never dereferenced: each call fails validation first
     assert lib.q4_repack(fake, 19, fake, 64, 32, 0, None) == -2          # block width
-    assert lib.q4_repack(fake, 20, fake, 64, 32, 1, None) == -2          # scale mode
+    assert lib.q4_repack(fake, 20, fake, 64, 32, 2, None) == -2          # scale mode
+    assert lib.q4_repack(fake, 18, fake, 64, 32, 1, None) == -2          # fp16 scales: Q4_1 only
+    assert lib.q4_dequant_fp16s(fake, None, 64, 32, None) == -2
+    assert lib.q4_gemv_fp16s(fake, fake, 1, None, fake, 17, 64, 32, None, 0, None) == -5   # M > 16
+    assert lib.q4_gemv_fp16s(fake, fake, 1, None, fake, 1, 4096, 4096, None, 0, None) == -3   # split: workspace
+    assert lib.q4_gemv_grouped_fp16s(None, 1, 1, 1, 1, None) == -2
     assert lib.q4_repack(None, 20, fake, 64, 32, 0, None) == -2          # NULL
     assert lib.q4_repack(fake, 20, fake, 96, 32, 0, None) == -1          # N % 64
     assert lib.q4_repack(fake, 20, fake, 64, 40, 0, None) == -1          # K % 32

@@ -106,9 +106,10 @@ def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
     subprocess.run(cmd, check=True, capture_output=True, timeout=900)
     text = out.read_text().splitlines()
     dense = [l.split(":")[0] for l in text
-             if re.match(r"_ZN12_GLOBAL__N_111gemv_kernelILi\dELb\dELi\d+ELb\dELb\dELb1ELb\dEE\w*:", l)]
-    # NTL x waves x (f32 / bf16 x, mx0 f32 / bf16 x, norm), + waves x (norm of residual + partials)
-    assert len(dense) == 4 * 3 * (2 + 2 + 1) + 3
+             if re.match(r"_ZN12_GLOBAL__N_111gemv_kernelILi\dELb\dELi\d+ELb\dELb\dELb1ELb\dELb\dEE\w*:", l)]
+    # NTL x waves x (f32 / bf16 x, mx0 f32 / bf16 x, norm, fp16-scale f32 / bf16 x),
+    # + waves x (norm of residual + partials)
+    assert len(dense) == 4 * 3 * (2 + 2 + 1 + 2) + 3
     swiglu = [l.split(":")[0] for l in text
               if re.match(r"_ZN12_GLOBAL__N_118gemv_swiglu_kernelILi\dELb\dELb\dELi\d+ELb1ELb\dEE\w*:", l)]
     # NTL x waves x (f32 x, bf16 x, norm), + waves x (norm of residual + partials)
@@ -129,7 +130,10 @@ def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
             assert not bad, f"{k}: registers used before their load's wait: {bad[:3]}"
             checked += n
         # the activation-from-LDS instances issue weight loads only
-        assert checked >= (8 if "ELb1ELb1EE" in k else 9), f"{k}: no pipelined K loop found"
+        # the activation-from-LDS (XN) instances: second-to-last template argument of gemv_kernel
+        # (gemv_swiglu_kernel: the last), set
+        xn = re.search(r"ELb1ELb\dEEEvNS_10GemvParamsE", k) if "gemv_kernel" in k else "ELb1ELb1EE" in k
+        assert checked >= (8 if xn else 9), f"{k}: no pipelined K loop found"
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
@@ -145,8 +149,9 @@ def test_grouped_stream_loops_wait_for_every_asm_load(tmp_path):
     subprocess.run(["hipcc", *b.flags(path), "--cuda-device-only", "-S", str(path), "-o", str(out)], check=True,
                    capture_output=True, timeout=600)
     text = out.read_text().splitlines()
-    kernels = [l.split(":")[0] for l in text if re.match(r"_ZN12_GLOBAL__N_119gemv_grouped_kernelILi\dELb\dELb1EE\w*:", l)]
-    assert len(kernels) == 8                       # NTL x (f32 / bf16 x)
+    kernels = [l.split(":")[0] for l in text
+               if re.match(r"_ZN12_GLOBAL__N_119gemv_grouped_kernelILi\dELb\dELb1ELb\dEE\w*:", l)]
+    assert len(kernels) == 16                      # NTL x (f32 / bf16 x) x (bf16 / fp16 scale words)
     for k in kernels:
         start = next(i for i, l in enumerate(text) if l.startswith(k + ":"))
         stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))

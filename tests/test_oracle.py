@@ -317,6 +317,32 @@ def test_mx_round_trip(oracle, kind):
     assert np.array_equal(oracle.dequant_mx(packed, 192, 320), oracle.dequant_q4_1(blocks))
 
 
+def test_mx_fp16_scales_keep_ggufs_scales(oracle):
+    """The exact-scale mode: the scale word carries GGUF's fp16 d and m bits unchanged, and
+    its dequant equals the f32-scale unpack (q4_1_pack.py:104-109 with f32 scales) -- pinned
+    by a scalar loop in Python floats, each product rounded once to f32 (q d is exact) -- and
+    differs from the bf16 mode on scales bf16 cannot hold."""
+    rng = np.random.default_rng(17)
+    n, k = 128, 96
+    blocks = oracle.baseline_q4_1_blocks(n, k, rng)
+    p = oracle.pack_mx(blocks, fp16_scales=True)
+    d16, m16, q = oracle.unpack_mx(p, n, k)
+    assert np.array_equal(d16, np.ascontiguousarray(blocks[..., 0:2]).view(np.uint16).reshape(n, k // 32))
+    assert np.array_equal(m16, np.ascontiguousarray(blocks[..., 2:4]).view(np.uint16).reshape(n, k // 32))
+    w = oracle.dequant_mx(p, n, k, fp16_scales=True)
+    assert np.array_equal(w, oracle.dequant_q4_1(blocks, bf16_scales=False))
+    for (row, kk) in [(0, 0), (5, 31), (64, 40), (127, 95), (77, 63)]:
+        b = blocks[row, kk // 32]
+        d = float(np.frombuffer(bytes(b[0:2]), np.float16)[0])
+        m = float(np.frombuffer(bytes(b[2:4]), np.float16)[0])
+        j = kk % 32
+        code = (b[4 + j] & 0xF) if j < 16 else (b[4 + j - 16] >> 4)
+        assert w[row, kk] == np.float32(code * d + m)
+    assert not np.array_equal(w, oracle.dequant_q4_1(blocks))       # the bf16 mode's values differ
+    with pytest.raises(ValueError):
+        oracle.pack_mx(oracle.random_q4_0_blocks_ref(64, 32, rng), fp16_scales=True)
+
+
 def test_mx_byte_positions_scalar(oracle):
     """Spot-check the layout formula: tile (g, kb), codes dword (lane, r), scales."""
     rng = np.random.default_rng(15)
