@@ -14,12 +14,13 @@ code:
   brackets with ``;;#ASMSTART`` / ``;;#ASMEND``) is scanned, in layout order and
   wrapping around the back edge, and any instruction touching an asm load's destination
   registers before a covering wait is reported (a copy, a spill store and an AGPR write
-  of the register all touch it);
+  of the register all touch it); asm loads outside those loops (prologues, loads issued
+  ahead of a prelude) are scanned forward to their first covering wait the same way;
 * a kernel with asm loads must spill no VGPRs.
 
-``check_assembly(text)`` returns the problems found in one ``--cuda-device-only -S``
-output; ``build.py`` runs it on the sources listed in ``GATED`` and fails the build on
-any problem.
+``check_assembly(text, straight)`` returns the problems found in one
+``--cuda-device-only -S`` output; ``build.py`` runs it on the sources listed in ``GATED``
+(with the path check on those in ``STRAIGHT``) and fails the build on any problem.
 """
 from __future__ import annotations
 
@@ -27,6 +28,9 @@ import re
 
 # the sources whose kernels issue loads from inline asm
 GATED = ("gemv.hip", "gemv_grouped.hip", "moe.hip", "prefill.hip")
+# of those, the ones whose loads outside the steady-state loops are issued unconditionally,
+# so that every control-flow path from such a load to its uses is checked too
+STRAIGHT = ("gemv.hip", "gemv_grouped.hip", "moe.hip")
 
 ASM_MARK = "; asm-load"
 
@@ -65,6 +69,12 @@ def inner_loops(asm: list[str]) -> list[list[str]]:
     """The instructions of each innermost loop, in layout order: the header's block, the
     blocks marked as inside it (a latch may sit above the header and fall into it), up to
     the last branch back to any of them."""
+    return [[l for l in asm[a:b + 1] if l.strip() and not l.strip().startswith((";", "."))]
+            for a, b in inner_loop_ranges(asm)]
+
+
+def inner_loop_ranges(asm: list[str]) -> list[tuple[int, int]]:
+    """(first, last) line indices of each innermost loop (see inner_loops)."""
     loops = []
     inner = any("Inner Loop Header" in l for l in asm)     # else: a lone loop's "Loop Header"
     for h, line in enumerate(asm):
@@ -81,8 +91,102 @@ def inner_loops(asm: list[str]) -> list[list[str]]:
         if not back:                            # no branch back to the loop's blocks: not a loop body
             continue
         last = max(back)
-        loops.append([l for l in asm[first:last + 1] if l.strip() and not l.strip().startswith((";", "."))])
+        loops.append((first, last))
     return loops
+
+
+_LABEL = re.compile(r"^(\.L\w+|\w+):")
+_BRANCH = re.compile(r"\s*(s_branch|s_cbranch_\w+)\s+(\S+)")
+_END = re.compile(r"\s*(s_endpgm|s_setpc_b64|s_trap)\b")
+
+
+def basic_blocks(asm: list[str]):
+    """(blocks, successors, block of line): blocks as lists of (line index, instruction) in
+    layout order, split at labels and after branches; successors by branch target and
+    fall-through."""
+    blocks, labels, cur = [], {}, []
+    def close():
+        nonlocal cur
+        if cur:
+            blocks.append(cur)
+            cur = []
+    for i, l in enumerate(asm):
+        st = l.strip()
+        m = _LABEL.match(l)
+        if m:
+            close()
+            labels[m.group(1)] = len(blocks)
+            cur = [(i, None)]               # a block may start with its label only
+            continue
+        if not st or st.startswith((";", ".")):
+            continue
+        cur.append((i, l))
+        if _BRANCH.match(l) or _END.match(l):
+            close()
+    close()
+    succ = []
+    for k, blk in enumerate(blocks):
+        last = next((l for _, l in reversed(blk) if l is not None), "")
+        m = _BRANCH.match(last)
+        out = []
+        if m:
+            if m.group(2) in labels:
+                out.append(labels[m.group(2)])
+            if m.group(1) != "s_branch" and k + 1 < len(blocks):
+                out.append(k + 1)
+        elif not _END.match(last) and k + 1 < len(blocks):
+            out.append(k + 1)
+        succ.append(out)
+    where = {i: (k, p) for k, blk in enumerate(blocks) for p, (i, _) in enumerate(blk)}
+    return blocks, succ, where
+
+
+def early_uses_straight(asm: list[str], in_loop) -> tuple[int, list[str]]:
+    """Marked loads outside every innermost loop (a pipeline's prologue, loads issued ahead of
+    a prelude), followed along every control-flow path from the load to the first wait that
+    covers it on that path (vmcnt(N), N no larger than the vector-memory loads issued since
+    on that path, vmcnt(0) included); any instruction touching the load's registers on a
+    path before such a wait is reported. The paths are those of the control-flow graph, a
+    superset of the feasible ones, so a clean result is a proof; it suits code whose loads
+    are issued unconditionally (the rolling pipelines' prologues). Code that issues loads
+    under conditions correlated with later branches (the prefill tile's prologue) reads as
+    uncovered on infeasible paths: STRAIGHT names the sources this check applies to."""
+    blocks, succ, where = basic_blocks(asm)
+    bad, n = [], 0
+    for i, l in enumerate(asm):
+        if ASM_MARK not in l or in_loop(i) or not _REG_LOAD.match(l):
+            continue
+        n += 1
+        dst = _regs(_operands(l)[0])
+        k0, p0 = where[i]
+        work, seen, found = [(k0, p0 + 1, 0)], set(), None
+        while work and found is None:
+            k, p, younger = work.pop()
+            key = (k, p, min(younger, 64))
+            if key in seen:
+                continue
+            seen.add(key)
+            covered = False
+            for _, m in blocks[k][p:]:
+                if m is None:
+                    continue
+                if _LOAD.match(m):
+                    younger += 1
+                w = _VMCNT.search(m)
+                if w and int(w.group(1)) <= younger:
+                    covered = True
+                    break
+                if _WAIT.match(m):
+                    continue
+                ops = _operands(m)
+                if ops and dst & set().union(*[_regs(t) for t in ops]):
+                    found = f"{l.strip()} -> {m.strip()}"
+                    break
+            if not covered and found is None:
+                work += [(s, 0, younger) for s in succ[k]]
+        if found:
+            bad.append(found)
+    return n, bad
 
 
 _LOAD = re.compile(r"\s*global_load")
@@ -158,10 +262,10 @@ def spill_counts(text: str) -> dict[str, int]:
     return out
 
 
-def check_assembly(text: str) -> tuple[int, list[str]]:
-    """(asm loads checked inside loops, problems) for one device assembly file: early uses
-    of asm-load registers in any kernel's innermost loops, and VGPR spills in any kernel
-    that issues asm loads."""
+def check_assembly(text: str, straight: bool = True) -> tuple[int, list[str]]:
+    """(asm loads checked, problems) for one device assembly file: early uses of asm-load
+    registers in any kernel's innermost loops and, with ``straight``, on every path from the
+    loads outside them; and VGPR spills in any kernel that issues asm loads."""
     lines = mark_asm_loads(text.splitlines())
     spills = spill_counts(text)
     checked, problems = 0, []
@@ -170,8 +274,12 @@ def check_assembly(text: str) -> tuple[int, list[str]]:
         if not any(ASM_MARK in l for l in body):
             continue
         n, bad = early_uses(body, only_marked=True)
-        checked += n
-        problems += [f"{name}: asm-load registers touched before their wait: {x}" for x in bad]
+        n2, bad2 = 0, []
+        if straight:
+            ranges = inner_loop_ranges(body)
+            n2, bad2 = early_uses_straight(body, lambda i: any(a <= i <= b for a, b in ranges))
+        checked += n + n2
+        problems += [f"{name}: asm-load registers touched before their wait: {x}" for x in bad + bad2]
         if spills.get(name, 0):
             problems.append(f"{name}: {spills[name]} VGPRs spilled in a kernel with in-flight asm loads")
     return checked, problems

@@ -284,3 +284,25 @@ def test_gate_flags_agpr_parking_and_spills():
     assert n == 2 and len(problems) == 1 and "v_accvgpr_write_b32 a0, v5" in problems[0]
     n, problems = G.check_assembly(kernel(good, 3))
     assert problems == ["k: 3 VGPRs spilled in a kernel with in-flight asm loads"]
+
+
+def test_gate_follows_prologue_loads_on_every_path():
+    """A load issued ahead of straight-line work (a prologue, or a prelude the pipeline's
+    first loads overlap) is followed along both sides of a branch: a use on either side
+    before a covering wait is reported; waits on both sides pass."""
+    def kernel(left, right):
+        return "\n".join([
+            "k:", "\ts_load_dwordx2 s[2:3], s[0:1], 0x0",
+            "\t;;#ASMSTART", "\tglobal_load_dwordx4 v[4:7], v1, s[2:3]", "\t;;#ASMEND",
+            "\ts_cbranch_scc1 .LBB0_2",
+            *left, "\ts_branch .LBB0_3",
+            ".LBB0_2:", *right,
+            ".LBB0_3:", "\tv_add_u32_e32 v13, v5, v6", "\ts_endpgm", ".Lfunc_end0:",
+            "amdhsa.kernels:", "  - .name:           k", "    .vgpr_spill_count: 0"])
+    ok = ["\ts_waitcnt vmcnt(0)", "\tv_mov_b32_e32 v20, v0"]
+    assert G.check_assembly(kernel(ok, ok)) == (1, [])
+    n, problems = G.check_assembly(kernel(ok, ["\tv_accvgpr_write_b32 a0, v5", *ok]))
+    assert n == 1 and len(problems) == 1 and "v_accvgpr_write_b32 a0, v5" in problems[0]
+    n, problems = G.check_assembly(kernel(["\tv_mov_b32_e32 v20, v0"], ok))   # one side never waits
+    assert len(problems) == 1 and "v_add_u32_e32 v13, v5, v6" in problems[0]
+    assert G.check_assembly(kernel(["\tv_mov_b32_e32 v20, v0"], ok), straight=False) == (0, [])
