@@ -64,6 +64,23 @@ def measured_traffic():
     return None
 
 
+def measured_traffic_ratios():
+    """HBM traffic over algorithmic bytes for the decode-step, skinny and MoE workloads,
+    from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summaries under profiles/ (lines
+    'traffic_over_algorithmic <key>: <ratio>'), with the file each came from."""
+    out = {}
+    for p in sorted((ROOT / "profiles").glob("*.md")):
+        try:
+            lines = p.read_text().splitlines()
+        except OSError:
+            continue
+        for line in lines:
+            if line.startswith("traffic_over_algorithmic "):
+                key, val = line[len("traffic_over_algorithmic "):].split(":", 1)
+                out[key.strip()] = {"ratio": float(val), "source": f"profiles/{p.name}"}
+    return out
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -918,6 +935,38 @@ def extra_config3(torch, q4, dev):
     return out
 
 
+def extra_prefill_power(torch, q4, dev):
+    """The prepared prefill GEMM at T=2048 on the gate_up shape, same kernel and launch, on
+    three operand sets: config 3's (seeded Q4_1 weights, N(0,1) tokens), all-zero weights
+    (d = m = 0 and zero codes: every dequantized tile is 0) and all-zero tokens. Only the
+    data differ, so a rate gap between them is the MFMA datapath's switching energy under
+    the board's power limit, not the instruction stream (run it under rocprofv3 with
+    GRBM_GUI_ACTIVE to read each one's clock)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+    n, k, T = 14336, 4096, 2048
+    blk = gen_blocks(torch, n, k, gen, dev)
+    weights = {"config": q4.pack_q4_1(blk, dev), "zero": q4.pack_q4_1(torch.zeros_like(blk), dev)}
+    del blk
+    for w in weights.values():
+        q4.prefill_scales(w)
+    x = torch.randn(T, k, generator=gen, device=dev).to(torch.bfloat16)
+    preps = {"config": q4.prefill_prepare(x), "zero": q4.prefill_prepare(torch.zeros_like(x))}
+    y = torch.empty(T, n, device=dev)
+    wsp = torch.empty(max(q4.prefill_workspace_bytes(T, n, k), 256), dtype=torch.uint8, device=dev)
+    out = {}
+    for label, (wk, xk) in {"config_data": ("config", "config"), "zero_weights": ("zero", "config"),
+                            "zero_tokens": ("config", "zero")}.items():
+        def run():
+            for _ in range(3):
+                q4.gemm_q4_prefill(weights[wk], preps[xk], y, workspace=wsp)
+        ms = graph_time(torch, run, [y], replays=5) / 3
+        tf = 2.0 * T * n * k / ms / 1e9
+        out[label] = {"ms": ms, "tflops": tf, "frac_of_peak": tf / MFMA_PEAK_TFLOPS}
+    out["shape"] = {"T": T, "N": n, "K": k}
+    return out
+
+
 def extra_config4(torch, q4, dev):
     """Config 4: the routed block (128 experts, top-8 of 16 tokens, H 2048, F 768) over 4
     rotating expert pools, graph replays; and the block with its residual and a shared expert
@@ -1108,8 +1157,9 @@ def main() -> int:
     # HBM-bound launches reach their steady clocks after ~20 ms of load: the headline launch
     # measured 0.740 ms/step at 5 warmup steps, 0.745 at 5 of 20, 0.697 at 30 (one box)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--extras", default="staged,step,0,2,3,4,moe_prefill,lm_head,ffn,q8,q4k,q40,fp16s,peaks",
-                    help="comma list (staged,0,2,3,4,lm_head,ffn,q8,q4k,peaks) or 'none'")
+    ap.add_argument("--extras", default="staged,step,0,2,3,pfpower,4,moe_prefill,lm_head,ffn,q8,q4k,q40,fp16s,peaks",
+                    help="comma list (staged,step,0,2,3,pfpower,4,moe_prefill,lm_head,ffn,q8,q4k,q40,fp16s,peaks) "
+                         "or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-passes", type=int, default=3, help="passes over one layer per timed CPU run")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed runs per CPU worker (the median is reported)")
@@ -1176,6 +1226,8 @@ def main() -> int:
                 out["q4_0_native_gemv"] = extra_q40(torch, q4, dev)
             elif cfg == "moe_prefill":
                 out["moe_prefill"] = extra_moe_prefill(torch, q4, dev)
+            elif cfg == "pfpower":
+                out["prefill_power"] = extra_prefill_power(torch, q4, dev)
         print(json.dumps(out), flush=True)
         return 0
 
@@ -1224,6 +1276,8 @@ def main() -> int:
                 extras["q4_0_native_gemv"] = extra_q40(torch, q4, dev)
             elif cfg == "moe_prefill":
                 extras["moe_prefill"] = extra_moe_prefill(torch, q4, dev)
+            elif cfg == "pfpower":
+                extras["prefill_power"] = extra_prefill_power(torch, q4, dev)
         except Exception as e:                      # keep the headline line whatever an extra does
             extras[f"config{cfg}_error"] = repr(e)[:300]
         log(f"extra {cfg}: {time.perf_counter() - t:.1f}s")
@@ -1278,6 +1332,9 @@ def main() -> int:
         "cpu_baseline": cpu,
         "extras": extras,
     }
+    ratios = measured_traffic_ratios()
+    if ratios:
+        extras["measured_traffic_ratios"] = ratios
     print(json.dumps(line), flush=True)
     return 0
 
