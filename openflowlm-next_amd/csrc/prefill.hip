@@ -92,17 +92,18 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, uint32_t s, uint32_t nib2,
 // Store a wave's FN x FT fragments of 16 x 16 (rows from wn0, tokens from wt0): the lane
 // holds D[n = 4 kg + r][t = i16] of each, 4 consecutive rows of one token, scaled back by
 // 2^(s_t + e_n) when the operands were scaled (texp / wexp not null), exactly; accum adds
-// the result to what y holds (the second pass of f32 activations).
+// the result to what y holds (the second pass of f32 activations). tmap: token t's exponent
+// is texp[tmap[t]] (activations gathered from another row order), else texp[t].
 template <int FN, int FT, bool SCALED>
 __device__ __forceinline__ void store_tile(const f32x4 (&acc)[FN][FT], float* __restrict__ y,
                                            const int* __restrict__ texp, const int* __restrict__ wexp, int T, int N,
-                                           int wt0, int wn0, int accum) {
+                                           int wt0, int wn0, int accum, const int* __restrict__ tmap = nullptr) {
     const int lane = threadIdx.x & 63, i16 = lane & 15, kg = lane >> 4;
 #pragma unroll
     for (int j = 0; j < FT; ++j) {
         const int t = wt0 + j * 16 + i16;
         if (t >= T) continue;
-        const int st = SCALED ? texp[t] : 0;
+        const int st = SCALED ? texp[tmap ? max(tmap[t], 0) : t] : 0;
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
             const int n = wn0 + i * 16 + kg * 4;
@@ -130,14 +131,14 @@ __device__ __forceinline__ void store_tile(const f32x4 (&acc)[FN][FT], float* __
 template <int FT, bool SCALED>
 __device__ __forceinline__ void store_swiglu(const f32x4 (&acc)[8][FT], uint16_t* __restrict__ h,
                                              const int* __restrict__ texp, const int* __restrict__ wexp, int T, int N,
-                                             int wt0, int wn0) {
+                                             int wt0, int wn0, const int* __restrict__ tmap = nullptr) {
     const int lane = threadIdx.x & 63, i16 = lane & 15, kg = lane >> 4;
     const int F = N >> 1, f0 = wn0 >> 1;          // wn0 = 128 p: gate rows from 64 p
 #pragma unroll
     for (int j = 0; j < FT; ++j) {
         const int t = wt0 + j * 16 + i16;
         if (t >= T) continue;
-        const int st = SCALED ? texp[t] : 0;
+        const int st = SCALED ? texp[tmap ? max(tmap[t], 0) : t] : 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int ng = wn0 + i * 16 + kg * 4;
@@ -367,12 +368,18 @@ __device__ __forceinline__ void vgpr_landed(u32x4& v) { asm volatile("" : "+v"(v
 // buffer for all waves; its DMA copies token rows [32 w, 32 w + 32) of the stage; its wait
 // counts cover only its own loads. Only a wave's fragment reads and MFMAs are private (its
 // accumulators reach memory only for its tokens [64 (w >> 1), +64) below T).
-template <int PREC, int FN, bool SWI = false>
+// GATHER: x16 is a row-major 16-bit matrix of K columns instead of the pre-tiled image, and
+// tile row s (token slot 256 bt + s) is DMA'd from its row gmap[256 bt + s] (gmap null: row
+// 256 bt + s itself; a negative entry, a padding slot: row 0, whose products feed only that
+// slot's accumulators, which are never stored). Each lane fetches the 16-byte chunk that
+// its LDS slot holds under the swizzle, so the LDS image is the pre-tiled one's. The
+// token exponents (PREC 0) are then indexed by source row too: texp[gmap[s]].
+template <int PREC, int FN, bool SWI = false, bool GATHER = false>
 __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict__ packed,
                                          const uint16_t* __restrict__ x16, const int* __restrict__ texp,
                                          const int* __restrict__ wexp, const uint32_t* __restrict__ s16,
                                          float* __restrict__ y, int T, int N, int K, int n0, int bt, int split,
-                                         int splits, int accum) {
+                                         int splits, int accum, const int* __restrict__ gmap = nullptr) {
     static_assert(FN == 8 || FN == 6, "256- or 192-row tiles");
     static_assert(!SWI || FN == 8, "the SwiGLU epilogue pairs a 256-row tile's gate and up halves");
     constexpr int WN = 16 * FN, WT = 64, FT = WT / 16, RG = FN / 2;
@@ -405,6 +412,18 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
     const uint8_t* const xsrc = (const uint8_t*)x16 + (((int64_t)bt * NSTK + st0) * kTileB + wave * 32 * 64);
     const uint32_t xoff = lane * 16;
     const uint32_t xdst = (uint32_t)(uintptr_t)lds + kXRing + wave * 32 * 64;   // LDS byte address
+    // GATHER: the byte offset of this lane's chunk in its two token rows (rows 32 w + 16 h +
+    // lane / 4 of the tile; LDS slot lane & 3 holds chunk (lane & 3) ^ ((lane >> 3) & 3))
+    uint32_t goff[2] = {0u, 0u};
+    if constexpr (GATHER) {
+        const uint32_t chunk = (uint32_t)((lane & 3) ^ ((lane >> 3) & 3)) * 16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int slot = t0 + wave * 32 + h * 16 + (lane >> 2);
+            const int r = gmap ? gmap[slot] : slot;
+            goff[h] = (uint32_t)(r < 0 ? 0 : r) * (uint32_t)(2 * K) + chunk;
+        }
+    }
 
     // fragment bases: A = weight rows wn*128 + 16i + i16, B = token rows wt*64 + 16j + i16
     const uint32_t abase = (wn * WN) * 64 + lane_row;
@@ -421,13 +440,22 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
 
     u32x4 wc[3], ws[3];                          // three register sets of weight codes + scales
     auto issue_x = [&](int st, int slot) {
-        const uint8_t* src = xsrc + (int64_t)st * kTileB;               // uniform
         const uint32_t dst = xdst + slot * kTileB;
+        if constexpr (GATHER) {
+            const uint8_t* src = (const uint8_t*)x16 + (int64_t)(st0 + st) * 128;   // uniform: columns 64 (st0 + st)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-                lds_dma16(src + kk * kPlaneB + h * 1024, xoff, dst + kk * kPlaneB + h * 1024);
+                for (int kk = 0; kk < 2; ++kk)
+                    lds_dma16(src + kk * 64, goff[h], dst + kk * kPlaneB + h * 1024);
+        } else {
+            const uint8_t* src = xsrc + (int64_t)st * kTileB;           // uniform
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+                    lds_dma16(src + kk * kPlaneB + h * 1024, xoff, dst + kk * kPlaneB + h * 1024);
+        }
     };
     auto issue_w = [&](int st, u32x4& c, u32x4& sc) {
         load16_async(c, wsrc + st * (2 * kTileBytes), coff);           // uniform bases
@@ -533,10 +561,12 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
     if (st + 3 < NST) stage(I3{}, st + 3);
     if (st + 4 < NST) stage(I4{}, st + 4);
 
+    // gathered activations carry their exponents by source row
+    const int* tmap = GATHER ? gmap : nullptr;
     if constexpr (SWI)
-        store_swiglu<FT, PREC == 0>(acc, (uint16_t*)y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN);
+        store_swiglu<FT, PREC == 0>(acc, (uint16_t*)y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN, tmap);
     else
-        store_tile<FN, FT, PREC == 0>(acc, y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN, accum);
+        store_tile<FN, FT, PREC == 0>(acc, y, texp, wexp, T, N, t0 + wt * WT, n0 + wn * WN, accum, tmap);
 }
 
 // Workgroups [0, wide_wgs) take the 256-row tiles of rows [0, narrow_row0), the rest the
@@ -1712,22 +1742,24 @@ __global__ __launch_bounds__(256) void moe_h16prep_kernel(const uint16_t* __rest
 }
 
 // Workgroup (token tile tt, 256-row tile rt) of a grouped expert GEMM: dma_tile on tile tt's
-// expert's matrix (N rows, ebytes each expert), slots [256 tt, tile_end) valid.
-template <int PREC, bool SWI = false>
+// expert's matrix (N rows, ebytes each expert), slots [256 tt, tile_end) valid. GATHER: x16
+// is row-major ([rows][K]), slot s's row gmap[s] (gmap null: row s).
+template <int PREC, bool SWI = false, bool GATHER = false>
 __global__ __launch_bounds__(512) void moe_dma_kernel(const uint8_t* __restrict__ packed, int64_t ebytes,
                                                       const uint16_t* __restrict__ x16,
                                                       const int* __restrict__ texp, const int* __restrict__ wexp,
                                                       const uint32_t* __restrict__ s16, int64_t s16_words,
                                                       float* __restrict__ y, const int* __restrict__ tile_e,
                                                       const int* __restrict__ tile_end, const int* __restrict__ meta,
-                                                      int N, int K, int tiles_n, int accum) {
+                                                      int N, int K, int tiles_n, int accum,
+                                                      const int* __restrict__ gmap = nullptr) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * kTileB];
     const int b = blockIdx.x, tt = b / tiles_n, rt = b % tiles_n;
     if (tt >= meta[0]) return;
     const int e = tile_e[tt];
-    dma_tile<PREC, 8, SWI>(lds, packed + e * ebytes, x16, texp, PREC == 0 ? wexp + (int64_t)e * N : nullptr,
-                           PREC == 0 ? s16 + e * s16_words : nullptr, y, tile_end[tt], N, K, rt * 256, tt, 0, 1,
-                           accum);
+    dma_tile<PREC, 8, SWI, GATHER>(lds, packed + e * ebytes, x16, texp, PREC == 0 ? wexp + (int64_t)e * N : nullptr,
+                                   PREC == 0 ? s16 + e * s16_words : nullptr, y, tile_end[tt], N, K, rt * 256, tt, 0,
+                                   1, accum, gmap);
 }
 
 // out[t][n..n+3] = sum_j w[t][j] Y[slot(t, j)][n..n+3], slot order j.
@@ -1847,11 +1879,35 @@ extern "C" int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const
     const uint32_t* s2 = precision == 0 ? plane(down_scales, (int64_t)E * N2) : nullptr;
     const unsigned g1 = (unsigned)(w.tiles_max * (N1 / 256)), g2 = (unsigned)(w.tiles_max * (N2 / 256));
 
-    // gate/up: G = X . [gate; up]^T per expert
+    // precision 1 on bf16 x: the expert GEMMs DMA their token rows straight from x (gate/up,
+    // slot s <- token rowmap[s]) and from h (down, slot s <- h row s): no per-slot activation
+    // images. h [S][F] bf16 from the gate/up epilogue goes to the x16 region, Y to gy. The DMA
+    // offsets are 32-bit.
+    const bool gather = precision == 1 && !xf32 && (uint64_t)T * H * 2 <= 0xffffffffull &&
+                        (uint64_t)S * F * 2 <= 0xffffffffull;
+    if (gather) {
+        hipLaunchKernelGGL((moe_dma_kernel<1, true, true>), dim3(g1), dim3(512), 0, st, gate_up, eb1,
+                           (const uint16_t*)x, texp, we1, s1, sw1, (float*)x16, tile_e, tile_end, meta, (int)N1,
+                           (int)H, (int)(N1 / 256), 0, (const int*)rowmap);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        hipLaunchKernelGGL((moe_dma_kernel<1, false, true>), dim3(g2), dim3(512), 0, st, down, eb2, x16, texp, we2, s2,
+                           sw2, gy, tile_e, tile_end, meta, (int)N2, (int)F, (int)(N2 / 256), 0, (const int*)nullptr);
+        if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
+        hipLaunchKernelGGL(moe_prefill_combine_kernel, dim3((unsigned)ceil_div(H / 4, 256), (unsigned)T), dim3(256), 0,
+                           st, gy, sop, topk_ids, topk_w, topk, E, (int)H, out);
+        return launch_status();
+    }
+
+    // gate/up: G = X . [gate; up]^T per expert. Precision 0: the token rows go through the
+    // pre-pass once per token ([T][H] fp16 and the token exponents, in the x16 and texp
+    // regions) and the GEMM gathers them per slot; the h preps overwrite both afterwards.
     const int xpasses = precision == 0 && xf32 ? 2 : 1;
     const bool swi = hb16 && xpasses == 1;
+    const bool gx = precision == 0 && (uint64_t)T * H * 2 <= 0xffffffffull;
     for (int pass = 0; pass < xpasses; ++pass) {
-        if (xf32) {
+        if (gx) {
+            launch_xprep(xf32, 0, false, dim3((unsigned)T), st, x, x16, texp, T, (int)H, pass);
+        } else if (xf32) {
             if (precision == 0)
                 hipLaunchKernelGGL((moe_xprep_kernel<true, 0>), dim3(SP), dim3(256), 0, st, x, rowmap, meta, x16, texp,
                                    (int)H, pass);
@@ -1869,12 +1925,20 @@ extern "C" int q4_moe_prefill(const uint8_t* gate_up, const uint8_t* down, const
         if (launch_status() != Q4MI_OK) return Q4MI_E_LAUNCH;
         // bf16 h from one activation pass: SwiGLU in the gate/up epilogue, h [S][F] bf16 in
         // the G/Y buffer (G itself is never written)
-        if (swi && precision == 0)
+        if (swi && gx)
+            hipLaunchKernelGGL((moe_dma_kernel<0, true, true>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp,
+                               we1, s1, sw1, gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), 0,
+                               (const int*)rowmap);
+        else if (swi && precision == 0)
             hipLaunchKernelGGL((moe_dma_kernel<0, true>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1,
                                sw1, gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), 0);
         else if (swi)
             hipLaunchKernelGGL((moe_dma_kernel<1, true>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1,
                                sw1, gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), 0);
+        else if (gx)
+            hipLaunchKernelGGL((moe_dma_kernel<0, false, true>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp,
+                               we1, s1, sw1, gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), pass,
+                               (const int*)rowmap);
         else if (precision == 0)
             hipLaunchKernelGGL((moe_dma_kernel<0>), dim3(g1), dim3(512), 0, st, gate_up, eb1, x16, texp, we1, s1, sw1,
                                gy, tile_e, tile_end, meta, (int)N1, (int)H, (int)(N1 / 256), pass);

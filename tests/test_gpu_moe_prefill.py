@@ -74,6 +74,27 @@ def test_moe_prefill_deterministic_and_equal_to_decode_path(gpu, pkg, oracle):
     assert oracle.maxrel(a, d) <= 1e-3
 
 
+@pytest.mark.parametrize("E,H,F,T,K", [(8, 256, 128, 300, 2), (16, 512, 256, 97, 4), (6, 256, 128, 700, 2),
+                                       (128, 2048, 768, 512, 8)])
+def test_moe_prefill_bf16_gather_equals_tiled_image(gpu, pkg, oracle, E, H, F, T, K):
+    """The bf16 tile on bf16 x DMAs its token rows straight from x and h (gather form); on
+    f32 x it runs the per-slot activation images (x prep, h prep). x's values are bf16 in
+    both calls, so both forms feed the MFMAs the same operands: the outputs are equal bit
+    for bit (ragged tiles, empty experts, several tiles per expert, ids outside [0, E),
+    config 4's shapes)."""
+    say(f"moe prefill bf16 gather vs image E={E} H={H} F={F} T={T} top{K}")
+    rng, gu, dn, *_ = _make(oracle, pkg, gpu, E, H, F, 5 * E + T, bf16_weights=True)
+    xb = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    if E == 6:                                    # one expert takes every token; -1 ids add nothing
+        ids = np.stack([np.full(T, 4), np.full(T, -1)], axis=1).astype(np.int32)
+        w = np.stack([np.ones(T), np.full(T, 3.0)], axis=1).astype(np.float32)
+    a = pkg.moe_batch(gu, dn, xb.to(gpu), ids, w, path="prefill", precision="bf16").cpu().numpy()
+    b = pkg.moe_batch(gu, dn, xb.to(torch.float32).to(gpu), ids, w, path="prefill", precision="bf16").cpu().numpy()
+    assert np.isfinite(a).all()
+    assert a.tobytes() == b.tobytes()
+
+
 @pytest.mark.parametrize("E", [6, 16])
 def test_moe_prefill_one_expert_takes_every_token(gpu, pkg, oracle, E):
     """All pairs on one expert (many full tiles), the rest empty; ids outside [0, E) add nothing.
