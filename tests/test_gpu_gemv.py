@@ -274,6 +274,34 @@ def test_grouped_gemv(gpu, pkg, oracle, M, xdt):
         assert lone.cpu().numpy().tobytes() == y[M - 1:M].cpu().numpy().tobytes()
 
 
+@pytest.mark.parametrize("M", [2, 4, 8, 12, 16])
+def test_grouped_shared_fragment_rows_equal_lone_tokens(gpu, pkg, oracle, M):
+    """From M = 2 the grouped sweep shares each token fragment among 2 (M <= 8) or 4 row
+    groups of a matrix. Matrices of 3, 5, 1 and 7 row groups put workgroups across matrix
+    boundaries and past the end (those take their row groups one at a time). Every token
+    row must equal that token run alone (M = 1, the one-group kernel) bit for bit, and the
+    fp64 reference to the north-star bar."""
+    say(f"grouped gemv, shared fragments, ragged row groups, M={M}")
+    rng = np.random.default_rng(700 + M)
+    items, refs = [], []
+    for n, k in ((192, 256), (320, 512), (64, 128), (448, 256)):
+        blocks = oracle.baseline_q4_1_blocks(n, k, rng)
+        X = _bf16(rng.standard_normal((M, k)))
+        y = torch.full((M, n), float("nan"), device=gpu)
+        items.append((pkg.pack_q4_1(blocks, gpu), X.to(gpu), y))
+        refs.append(X.to(torch.float64).numpy() @ oracle.dequant_q4_1(blocks).astype(np.float64).T)
+    pkg.GemvGroup(items).run()
+    torch.cuda.synchronize()
+    for (w, X, y), ref in zip(items, refs):
+        assert oracle.maxrel(y.cpu().numpy(), ref) <= MAXREL
+    for m in range(M):
+        lone = [(w, X[m:m + 1].contiguous(), torch.full((1, w.n), float("nan"), device=gpu)) for w, X, _ in items]
+        pkg.GemvGroup(lone).run()
+        torch.cuda.synchronize()
+        for (_, _, y), (_, _, y1) in zip(items, lone):
+            assert y1.cpu().numpy().tobytes() == y[m:m + 1].cpu().numpy().tobytes()
+
+
 def test_rejects_bad_shapes(gpu, pkg, oracle):
     say("gemv bad shapes")
     rng = np.random.default_rng(40)
