@@ -53,9 +53,12 @@ def test_prefill_loop_waits_cover_every_asm_load(tmp_path):
                 n, bad = early_uses_in(body)
                 assert n >= 6, f"{what}: expected the weight loads of the unrolled loop, found {n}"
                 assert not bad, f"{what}: registers used before their load's wait: {bad[:3]}"
-        # the grouped expert GEMM's tile loop and the gate/up GEMM with the SwiGLU epilogue
-        for kname, what in ((rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb0EE", "moe"),
-                            (rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb1EE", "moe swiglu"),
+        # the grouped expert GEMM's tile loop (pre-tiled activations, and the rows gathered
+        # through the slot map) and the gate/up GEMMs with the SwiGLU epilogue
+        for kname, what in ((rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb0ELb0EE", "moe"),
+                            (rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb1ELb0EE", "moe swiglu"),
+                            (rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb0ELb1EE", "moe gathered"),
+                            (rf"_ZN12_GLOBAL__N_114moe_dma_kernelILi{prec}ELb1ELb1EE", "moe swiglu gathered"),
                             (rf"_ZN12_GLOBAL__N_121prefill_swiglu_kernelILi{prec}EE", "swiglu")):
             start = next(i for i, l in enumerate(text) if re.match(kname + r"\w*:", l))
             stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
@@ -152,7 +155,11 @@ def test_grouped_stream_loops_wait_for_every_asm_load(tmp_path):
     kernels = [l.split(":")[0] for l in text
                if re.match(r"_ZN12_GLOBAL__N_119gemv_grouped_kernelILi\dELb\dELb1ELb\dEE\w*:", l)]
     assert len(kernels) == 16                      # NTL x (f32 / bf16 x) x (bf16 / fp16 scale words)
-    for k in kernels:
+    # the shared-fragment form (M >= 2, bf16 x): NTL 1, 2 over 2 row groups, 3, 4 over 4
+    shared = [l.split(":")[0] for l in text
+              if re.match(r"_ZN12_GLOBAL__N_122gemv_grouped_ng_kernelILi\dELb0ELi[24]ELi[24]EE\w*:", l)]
+    assert len(shared) == 4
+    for k in kernels + shared:
         start = next(i for i, l in enumerate(text) if l.startswith(k + ":"))
         stop = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
         checked = 0
