@@ -764,7 +764,7 @@ def extra_config2(torch, q4, model, steps):
     for M in (4, 8, 16):
         acts, xhead = sweep_inputs(torch, model, model.head.device, M)
         grp, nbytes = grouped_sweep(torch, q4, model, acts, xhead, M)
-        _, per = time_launches(torch, grp.run, steps, 2)
+        _, per = time_launches(torch, grp.run, steps, 5)
         out[f"M{M}"] = {"ms": per, "gbs": nbytes / per / 1e6, "tflops": 2 * M * model.weight_bytes * 1.6 / per / 1e9}
         del grp, acts
     return out
@@ -1259,7 +1259,7 @@ def main() -> int:
             elif cfg == "0":
                 extras["config0_gemv_4096_f32x"] = extra_config0(torch, q4, dev)
             elif cfg == "2":
-                extras["config2_skinny"] = extra_config2(torch, q4, model, max(3, a.steps // 4))
+                extras["config2_skinny"] = extra_config2(torch, q4, model, max(5, a.steps // 2))
             elif cfg == "3":
                 extras["config3_prefill"] = extra_config3(torch, q4, dev)
             elif cfg == "4":
