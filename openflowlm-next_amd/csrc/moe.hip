@@ -42,9 +42,10 @@ constexpr int kDnWaves = 4, kDnUnr = 2, kDnGroups = 4;
 // same answer: the routed experts are marked in an LDS bitmap, each thread counts one
 // 32-expert word, and a block-wide prefix sum of the counts finds the word and bit. The
 // expert kernels map their workgroups onto this list, so the workgroups of routed experts
-// come first in the grid and the rest leave at once.
+// come first in the grid and the rest leave at once. The ids are also left in sids (LDS, P
+// entries) for collect_pairs, so the routing reads them from memory once.
 template <int WAVES>
-__device__ int active_expert(const int32_t* __restrict__ ids, int P, int E, int a) {
+__device__ int active_expert(const int32_t* __restrict__ ids, int P, int E, int a, int* sids) {
     __shared__ uint32_t bits[kMaxExperts / 32];
     __shared__ int wsum[WAVES];
     __shared__ int found;
@@ -54,6 +55,7 @@ __device__ int active_expert(const int32_t* __restrict__ ids, int P, int E, int 
     __syncthreads();
     for (int p = tid; p < P; p += 64 * WAVES) {
         const int e = ids[p];
+        sids[p] = e;
         if (e >= 0 && e < E) atomicOr(&bits[e >> 5], 1u << (e & 31));
     }
     __syncthreads();
@@ -79,9 +81,9 @@ __device__ int active_expert(const int32_t* __restrict__ ids, int P, int E, int 
 }
 
 // The pairs p = t * topk + j with ids[p] == e, ascending, into `list`; returns their count
-// (every thread calls it; barriers inside).
+// (every thread calls it; barriers inside). sids: the ids as active_expert left them in LDS.
 template <int WAVES>
-__device__ int collect_pairs(const int32_t* __restrict__ ids, int P, int e, int* list) {
+__device__ int collect_pairs(const int* sids, int P, int e, int* list) {
     __shared__ int wave_cnt[WAVES];
     __shared__ int base;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -89,7 +91,7 @@ __device__ int collect_pairs(const int32_t* __restrict__ ids, int P, int e, int*
     __syncthreads();
     for (int p0 = 0; p0 < P; p0 += 64 * WAVES) {
         const int p = p0 + tid;
-        const bool hit = p < P && ids[p] == e;
+        const bool hit = p < P && sids[p] == e;
         const uint64_t mask = __ballot(hit);
         const int within = __popcll(mask & ((1ull << lane) - 1ull));
         if (lane == 0) wave_cnt[wave] = __popcll(mask);
@@ -182,10 +184,11 @@ __global__ __launch_bounds__(64 * kUpWaves) void moe_up_kernel(const uint8_t* __
         return;
     }
     const int fg = F >> 6, b = (int)blockIdx.x - sh.wgs;
-    const int e = active_expert<kUpWaves>(ids, P, E, b / fg);
+    __shared__ int sids[kMaxPairs];
+    const int e = active_expert<kUpWaves>(ids, P, E, b / fg, sids);
     if (e < 0) return;
     const int rgp = b % fg;
-    const int cnt = collect_pairs<kUpWaves>(ids, P, e, list);
+    const int cnt = collect_pairs<kUpWaves>(sids, P, e, list);
     const uint8_t* wexp = gate_up + (int64_t)e * (2 * F / 64) * (H / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 4 * MAXNTL) {
         const int M = min(4 * MAXNTL, cnt - c0);
@@ -266,10 +269,11 @@ __global__ __launch_bounds__(64 * kDnWaves) void moe_down_kernel(const uint8_t* 
         return;
     }
     const int b = (int)blockIdx.x - sh.wgs;
-    const int e = active_expert<kDnWaves>(ids, P, E, b / wg_per_e);
+    __shared__ int sids[kMaxPairs];
+    const int e = active_expert<kDnWaves>(ids, P, E, b / wg_per_e, sids);
     if (e < 0) return;
     const int rg0 = (b % wg_per_e) * NG;
-    const int cnt = collect_pairs<kDnWaves>(ids, P, e, list);
+    const int cnt = collect_pairs<kDnWaves>(sids, P, e, list);
     const uint8_t* wexp = down + (int64_t)e * (H / 64) * (F / 32) * kTileBytes;
     for (int c0 = 0; c0 < cnt; c0 += 4 * MAXNTL) {
         const int M = min(4 * MAXNTL, cnt - c0);
