@@ -423,6 +423,27 @@ def extra_decode_step(torch, q4, model, acts, xhead, only=None):
             q4.gemm_q4_rmsnorm_acc(model.head, cur, pd, nw, x_out=nxt, y=logits, workspace=ws)
         return fn
 
+    NQ = model.layers[0]["qkv"].n
+    sg_o, sg_d, sg_q = q4.decode_segment_splits(H, F, NQ)
+    xmid = torch.empty(1, H, device=dev)
+    pdg = torch.empty(sg_d, 1, H, device=dev)
+    pqg = torch.empty(sg_q, 1, NQ, device=dev)
+    wseg = q4.decode_segment_workspace(H, F, NQ, dev)
+
+    def segments():
+        """Between two attentions, one launch (decode_segment): o -> norm -> SwiGLU -> down ->
+        norm -> the next layer's qkv (its K-split planes, what attention would take). Layer 0's
+        norm + qkv and the final norm + lm_head (over the last segment's down planes) are the
+        norm GEMVs of the other forms. The residual stream advances in place."""
+        q4.gemm_q4_rmsnorm(model.layers[0]["qkv"], xres, nw, y=qkv, workspace=ws)
+        last = len(model.layers) - 1
+        for i, p in enumerate(model.layers):
+            nxt = model.layers[i + 1]["qkv"] if i < last else None
+            q4.decode_segment(p["o"], p["gate"], p["up"], p["down"], nxt, attn[i], xres, nw,
+                              nw if nxt is not None else None, x_mid=xmid, x_next=xres if nxt is not None else None,
+                              down_planes=pdg, qkv_planes=pqg if nxt is not None else None, workspace=wseg)
+        q4.gemm_q4_rmsnorm_acc(model.head, xmid, pdg, nw, x_out=xalt, y=logits, workspace=ws)
+
     l0 = model.layers[0]
     so, sd = q4.gemv_split_count(l0["o"]), q4.gemv_split_count(l0["down"])
 
@@ -430,7 +451,8 @@ def extra_decode_step(torch, q4, model, acts, xhead, only=None):
         xres.copy_(xres0)
     out = {"bytes": nbytes}
     variants = (("separate_norms", step), ("norms_in_gemv", step_fused),
-                (f"deferred_sums_o{so}_d{sd}", deferred(so, sd)), ("deferred_sums_o4_d4", deferred(4, 4)))
+                (f"deferred_sums_o{so}_d{sd}", deferred(so, sd)), ("deferred_sums_o4_d4", deferred(4, 4)),
+                ("segments", segments))
     for name, fn in variants:
         if only and name not in only:
             continue
@@ -450,6 +472,13 @@ def extra_decode_step(torch, q4, model, acts, xhead, only=None):
     reset()
     variants[3][1]()
     out["deferred_o4_d4_maxrel"] = float(((logits - a).abs().max() / a.abs().max()).item())
+    b = logits.clone()
+    reset()
+    segments()
+    # the segments' residual stream is the o4 / d4 chain's: same splits, tiles, sums and order
+    out["segments_same_logits_as_o4_d4"] = bool(torch.equal(b, logits))
+    out["segments_timed_out"] = bool(wseg[12544:12548].view(torch.int32).item() != 0)
+    out["segment_splits"] = {"o": sg_o, "down": sg_d, "qkv": sg_q}
     return out
 
 

@@ -367,6 +367,36 @@ int q4_gemv_swiglu_rmsnorm_acc(const uint8_t* gate, const uint8_t* up, const flo
                                int h_dtype, int M, int64_t F, int64_t K, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* The decoder layer's GEMV chain between two attentions at M = 1, as one persistent launch
+ * (one workgroup per CU, phases handed over by device-scope counters in the workspace; the
+ * reference's whole-layer dispatch, open_kernels/designs/dense/dx.py:1-5, with attention
+ * left out):
+ *   x_mid  = x + o . attn                                   (attn bf16 [H])
+ *   h      = bf16(silu(gate . n1) * (up . n1)),  n1 = bf16(RMSNorm(x_mid) * nw_post)
+ *   down_planes[s] = the s-th K split of down . h, s < Sd  (f32 [Sd][H])
+ *   x_next = x_mid + ((0 + down_planes[0]) + down_planes[1] + ...)
+ *   qkv_planes[s]  = the s-th K split of qkv . n2, s < Sq  (f32 [Sq][NQ]),
+ *                    n2 = bf16(RMSNorm(x_next) * nw_next)
+ * o [H, H], gate and up [F, H], down [H, F], qkv [NQ, H] in the mx layout (bf16 scale words);
+ * norm weights f32 or bf16 (nw_dtype); RMSNorm as q4_rmsnorm_add. qkv NULL (the last layer):
+ * the chain ends with down_planes (nw_next, x_next, qkv_planes unused), which the next norm
+ * GEMV adds (q4_gemv_rmsnorm_acc). Split counts: q4_decode_segment_splits. The sums of
+ * the planes in split order are the projections' outputs.
+ * Shapes: H, F, NQ multiples of 64, H <= 4096, H and F >= 256. x_next may be x; x_mid,
+ * the planes and the workspace must not overlap each other or x, attn and x_next
+ * (Q4MI_E_ARG). The workspace (q4_decode_segment_workspace_bytes) starts with the
+ * hand-over counters: its first 12800 bytes must be zero before the first call on it, and
+ * each call leaves them zero, except the 32-bit word at byte 12544, which becomes nonzero
+ * if a hand-over timed out (about a second: the grid could not be resident), in which case
+ * the outputs are not valid. Calls sharing one workspace must not overlap in time. */
+size_t q4_decode_segment_workspace_bytes(int64_t H, int64_t F, int64_t NQ);
+int q4_decode_segment_splits(int64_t H, int64_t F, int64_t NQ, int* splits /* [3]: So, Sd, Sq */);
+int q4_decode_segment(const uint8_t* o, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                      const uint8_t* qkv, const void* attn, const float* x, const void* nw_post,
+                      const void* nw_next, int nw_dtype, float eps, float* x_mid, float* x_next,
+                      float* down_planes, float* qkv_planes, int64_t H, int64_t F, int64_t NQ,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* The activation producer: per row m < M of N values,
  *   y = x + add (add may be NULL; y may be NULL, or x itself when N <= 16384),
  *   xn = (y * r) * w, r = 1 / sqrt(mean(y^2) + eps) with the sum in fp64,

@@ -28,6 +28,10 @@ class Q4GemvDesc(C.Structure):
 # name -> (restype, argtypes); every function declared in include/q4mi.h
 SIGNATURES = {
     "q4mi_version": (_i32, []),
+    "q4_decode_segment_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "q4_decode_segment_splits": (_i32, [_i64, _i64, _i64, _vp]),
+    "q4_decode_segment": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, C.c_float, _vp, _vp, _vp, _vp,
+                                 _i64, _i64, _i64, _vp, _sz, _vp]),
     "q4_dequant_fp16s": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "q4_gemv_fp16s": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_gemv_grouped_fp16s": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp]),

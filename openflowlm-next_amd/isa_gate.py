@@ -27,10 +27,10 @@ from __future__ import annotations
 import re
 
 # the sources whose kernels issue loads from inline asm
-GATED = ("gemv.hip", "gemv_grouped.hip", "moe.hip", "prefill.hip")
+GATED = ("decode.hip", "gemv.hip", "gemv_grouped.hip", "moe.hip", "prefill.hip")
 # of those, the ones whose loads outside the steady-state loops are issued unconditionally,
 # so that every control-flow path from such a load to its uses is checked too
-STRAIGHT = ("gemv.hip", "gemv_grouped.hip", "moe.hip")
+STRAIGHT = ("decode.hip", "gemv.hip", "gemv_grouped.hip", "moe.hip")
 
 ASM_MARK = "; asm-load"
 

@@ -33,6 +33,7 @@ __all__ = [
     "gemv_q4", "gemm_q4", "gemm_q4_prefill", "moe_batch", "pack_moe_experts", "GemvGroup",
     "gemv_workspace_bytes", "prefill_workspace_bytes", "moe_workspace_bytes", "logits_topk", "lm_head_topk",
     "swiglu_q4", "rmsnorm_add", "pack_chunks", "PackedQ8", "pack_q8", "gemm_q8", "prefill_scales",
+    "decode_segment", "decode_segment_splits", "decode_segment_workspace",
 ]
 
 ROWS = 64          # rows per mx tile / row group
@@ -925,6 +926,86 @@ def swiglu_q4(gate: PackedQ4, up: PackedQ4, x, out_dtype=torch.float32, h: torch
                                                    Q4MI_BF16 if out_dtype == torch.bfloat16 else Q4MI_F32, M,
                                                    gate.n, gate.k, wp, wn, _stream(dev)))
     return h
+
+
+def decode_segment_splits(h: int, f: int, nq: int) -> tuple[int, int, int]:
+    """(So, Sd, Sq): the K splits of o, down and qkv in decode_segment for hidden size h,
+    FFN size f and nq qkv rows (nq = 0: no qkv; Sq 0)."""
+    out = (C.c_int * 3)()
+    check("q4_decode_segment_splits", _lib_handle().q4_decode_segment_splits(h, f, nq, out))
+    return int(out[0]), int(out[1]), int(out[2])
+
+
+def decode_segment_workspace(h: int, f: int, nq: int, device=None) -> torch.Tensor:
+    """A zero-filled workspace for decode_segment at these sizes (its counters must start at
+    zero; every call leaves them at zero, so one workspace serves all calls of a stream)."""
+    n = int(_lib_handle().q4_decode_segment_workspace_bytes(h, f, nq))
+    if n == 0:
+        raise ValueError(f"decode_segment does not take h={h}, f={f}, nq={nq}")
+    return torch.zeros(n, dtype=torch.uint8, device=_device(device))
+
+
+def decode_segment(o: PackedQ4, gate: PackedQ4, up: PackedQ4, down: PackedQ4, qkv: PackedQ4 | None,
+                   attn: torch.Tensor, x: torch.Tensor, nw_post: torch.Tensor, nw_next: torch.Tensor | None = None,
+                   eps: float = 1e-6, x_mid: torch.Tensor | None = None, x_next: torch.Tensor | None = None,
+                   down_planes: torch.Tensor | None = None, qkv_planes: torch.Tensor | None = None,
+                   workspace: torch.Tensor | None = None):
+    """The decoder layer's GEMVs between two attentions at M = 1, in one launch (the
+    reference's whole-layer dispatch, designs/dense/dx.py:1-5, attention left out):
+
+        x_mid  = x + o @ attn
+        h      = bf16(silu(gate @ n1) * (up @ n1)),   n1 = bf16(RMSNorm(x_mid) * nw_post)
+        x_next = x_mid + down @ h                     (down_planes: its K splits, f32 [Sd, H])
+        qkv    = sum over s of qkv_planes[s]          (f32 [Sq, NQ]; qkv @ n2,
+                                                       n2 = bf16(RMSNorm(x_next) * nw_next))
+
+    attn bf16 [H]; x the f32 residual stream [H] (``x_next`` may be ``x``); norm weights f32
+    or bf16 [H]. ``qkv`` None (the last layer) stops after down: x_next and qkv_planes are
+    not formed, and gemm_q4_rmsnorm_acc(lm_head, x_mid, down_planes, ...) goes on from
+    there. Returns (x_mid, x_next, down_planes, qkv_planes). ``workspace`` from
+    decode_segment_workspace (else a zero-filled one per call)."""
+    mats = [o, gate, up, down] + ([qkv] if qkv is not None else [])
+    _bf16_scales("decode_segment", *mats)
+    dev = o.device
+    H, F = o.k, gate.n
+    NQ = qkv.n if qkv is not None else 0
+    if o.n != H or gate.shape != (F, H) or up.shape != (F, H) or down.shape != (H, F) \
+            or (qkv is not None and qkv.k != H) or any(m.device != dev for m in mats):
+        raise ValueError(f"decode_segment needs o [H, H], gate/up [F, H], down [H, F], qkv [NQ, H] on one device; "
+                         f"got {[m.shape for m in mats]}")
+    So, Sd, Sq = decode_segment_splits(H, F, NQ)
+    if not isinstance(attn, torch.Tensor) or attn.dtype != torch.bfloat16 or attn.numel() != H \
+            or attn.device != dev or not attn.is_contiguous():
+        raise ValueError(f"attn must be a contiguous bfloat16 tensor of {H} values on {dev}")
+    xt = _norm_x(x, H, dev)
+    if xt.shape[0] != 1:
+        raise ValueError("decode_segment takes one token")
+    wpost, wd = _norm_w(nw_post, H, dev)
+    wnext = None
+    if qkv is not None:
+        if nw_next is None:
+            raise ValueError("nw_next is needed with qkv")
+        wnext, wd2 = _norm_w(nw_next, H, dev)
+        if wd2 != wd:
+            raise TypeError("nw_post and nw_next must share a dtype")
+    x_mid = _buf(x_mid, "x_mid", torch.float32, (1, H), dev)
+    down_planes = _buf(down_planes, "down_planes", torch.float32, (Sd, 1, H), dev)
+    if qkv is not None:
+        x_next = _buf(x_next, "x_next", torch.float32, (1, H), dev)
+        qkv_planes = _buf(qkv_planes, "qkv_planes", torch.float32, (Sq, 1, NQ), dev)
+    else:
+        x_next = qkv_planes = None
+    if workspace is None:
+        workspace = decode_segment_workspace(H, F, NQ, dev)
+    lib = _lib_handle()
+    with torch.cuda.device(dev):
+        wp, wn = _ws_arg(dev, lib.q4_decode_segment_workspace_bytes(H, F, NQ), "decode_segment", workspace)
+        opt = lambda t: None if t is None else _ptr(t)
+        check("q4_decode_segment", lib.q4_decode_segment(
+            _ptr(o.data), _ptr(gate.data), _ptr(up.data), _ptr(down.data), opt(qkv.data if qkv is not None else None),
+            _ptr(attn), _ptr(xt), _ptr(wpost), opt(wnext), wd, float(eps), _ptr(x_mid), opt(x_next),
+            _ptr(down_planes), opt(qkv_planes), H, F, NQ, wp, wn, _stream(dev)))
+    return x_mid, x_next, down_planes, qkv_planes
 
 
 def rmsnorm_add(x: torch.Tensor, w: torch.Tensor, add: torch.Tensor | None = None, eps: float = 1e-6,

@@ -432,3 +432,39 @@ def test_moe_shared_argument_errors(lib):
     assert call(f, f, 96, f) == -1                     # Fs % 64
     assert call(f, f, 768, f, wsb=ws - 1) == -3        # short workspace
     assert call(f, f, 768, f, out=C.c_void_p(0x10000000 + 256)) == -2   # out inside the workspace
+
+
+def test_decode_segment_plan_and_argument_errors(lib):
+    """q4_decode_segment: the split plan and the workspace size need no GPU (256 CUs, as on
+    MI355X, when none is visible); shapes, the norm dtype, pointers, overlaps and the
+    workspace are checked before any launch."""
+    sp = (C.c_int * 3)()
+    assert lib.q4_decode_segment_splits(4096, 14336, 6144, sp) == 0 and list(sp) == [4, 4, 8]
+    assert lib.q4_decode_segment_splits(4096, 14336, 0, sp) == 0 and list(sp) == [4, 4, 0]
+    assert lib.q4_decode_segment_splits(4096, 14336, 100, sp) == -1
+    assert lib.q4_decode_segment_splits(8192, 14336, 6144, sp) == -1          # H > 4096
+    ws = lib.q4_decode_segment_workspace_bytes(4096, 14336, 6144)
+    assert ws == 12800 + 4 * 4096 * 4 + 14336 * 2
+    assert lib.q4_decode_segment_workspace_bytes(4096, 14336, 96) == 0
+    f = lambda a: C.c_void_p(a)
+    base = dict(o=0x1000, g=0x2000, u=0x3000, d=0x4000, q=0x5000, attn=0x6000, x=0x100000, n1=0x7000, n2=0x8000,
+                nwd=1, xm=0x200000, xn=0x300000, pd=0x400000, pq=0x500000, H=4096, F=14336, NQ=6144,
+                ws=0x600000, wsb=ws)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return lib.q4_decode_segment(f(a["o"]), f(a["g"]), f(a["u"]), f(a["d"]), None if a["q"] is None else f(a["q"]),
+                                     f(a["attn"]), f(a["x"]), f(a["n1"]), f(a["n2"]), a["nwd"], 1e-6, f(a["xm"]),
+                                     f(a["xn"]), f(a["pd"]), f(a["pq"]), a["H"], a["F"], a["NQ"], f(a["ws"]),
+                                     a["wsb"], None)
+    assert call(H=4000) == -1                       # H % 64
+    assert call(F=100) == -1                        # F % 64
+    assert call(nwd=7) == -2                        # norm weight dtype
+    assert call(o=0) == -2                          # NULL weights
+    assert call(n2=0) == -2                         # qkv without its norm weight
+    assert call(attn=0x6008) == -2                  # misaligned
+    assert call(wsb=ws - 1) == -3                   # short workspace
+    assert call(xm=0x100000) == -2                  # x_mid over x
+    assert call(xn=0x200000 + 64) == -2             # x_next over x_mid
+    assert call(pd=0x600000 + 12800) == -2          # planes inside the workspace
+    assert call(pq=0x400000 + 4 * 4096 * 4 - 16) == -2   # qkv planes over the down planes

@@ -97,6 +97,34 @@ def test_moe_pipelined_loops_wait_for_every_asm_load(tmp_path):
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
+def test_decode_segment_waits_spills_and_hand_over(tmp_path):
+    """The decode segment's weight loads are primed before a grid hand-over and consumed after
+    it: along every control-flow path from each asm load (the prime, the polls, the norm
+    prelude, the rolling K loops) its registers are touched only after a covering wait, no
+    instance spills, and the hand-over uses no cache-wide fence (buffer_wbl2 / buffer_inv):
+    the values crossing workgroups are device-scope stores and the arrivals device-scope
+    atomics."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("q4mi_isa_gate", ROOT / "openflowlm-next_amd" / "isa_gate.py")
+    gate = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gate)
+    src = SRC.parent / "decode.hip"
+    out = tmp_path / "decode.s"
+    cmd = ["hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{ROOT / 'include'}", f"-I{SRC.parent}", "--cuda-device-only", "-S",
+           str(src), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    text = out.read_text()
+    n, problems = gate.check_assembly(text, straight=True)
+    assert n > 0 and not problems, problems[:3]
+    kernels = re.findall(r"\.name:\s+(_ZN12_GLOBAL__N_121decode_segment_kernel\w+)", text)
+    assert len(kernels) == 8
+    assert set(re.findall(r"\.vgpr_spill_count:\s+(\d+)", text)) == {"0"}
+    assert "buffer_wbl2" not in text and "buffer_inv" not in text
+    assert re.search(r"global_atomic_add\b", text) and re.search(r"global_store_dword\w* .* sc1", text)
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
 def test_dense_gemv_stream_loops_wait_for_every_asm_load(tmp_path):
     """The dense GEMV and the SwiGLU pair stream through gemv_rows_stream (inline-asm loads,
     an explicit wait per K position): in every instance's K loop each load's registers are
