@@ -336,6 +336,18 @@ __device__ __forceinline__ void lds_dma16(const void* gbase, uint32_t goff, uint
                  : "memory", "m0");
 }
 
+// The same through a buffer resource: 16 bytes per lane from rsrc's base + soff + voff into
+// LDS at m0 + 16 * lane. A lane whose voff is past the resource's num_records reads zeros
+// (the buffer range check), with no memory access.
+__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff,
+                                              uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+                 "s"(lds_base)
+                 : "memory", "m0");
+}
+constexpr uint32_t kPadOffset = 0x80000000u;   // past the gather resource's range: a zero row
+constexpr int kBufferWord3 = 0x00020000;       // raw buffer resource, 32-bit data format
+
 // 16 bytes per lane into registers (uniform base + 32-bit lane offset). The compiler does not
 // track this load: the caller waits for it (s_waitcnt vmcnt) and then passes the registers
 // through vgpr_landed before any other use. No non-temporal hint: every weight tile is read
@@ -370,10 +382,13 @@ __device__ __forceinline__ void vgpr_landed(u32x4& v) { asm volatile("" : "+v"(v
 // accumulators reach memory only for its tokens [64 (w >> 1), +64) below T).
 // GATHER: x16 is a row-major 16-bit matrix of K columns instead of the pre-tiled image, and
 // tile row s (token slot 256 bt + s) is DMA'd from its row gmap[256 bt + s] (gmap null: row
-// 256 bt + s itself; a negative entry, a padding slot: row 0, whose products feed only that
-// slot's accumulators, which are never stored). Each lane fetches the 16-byte chunk that
-// its LDS slot holds under the swizzle, so the LDS image is the pre-tiled one's. The
-// token exponents (PREC 0) are then indexed by source row too: texp[gmap[s]].
+// 256 bt + s itself) through a buffer resource over x16. A padding slot (a negative entry, or
+// a slot at or past T, the tile's valid end) gets a lane offset past the resource's range, so
+// its LDS row is zeros and no memory is read: its products feed only that slot's
+// accumulators, which are never stored, and zero operands spare the MFMAs' power. Each lane
+// fetches the 16-byte chunk that its LDS slot holds under the swizzle, so the LDS image is
+// the pre-tiled one's. The token exponents (PREC 0) are then indexed by source row too:
+// texp[gmap[s]].
 template <int PREC, int FN, bool SWI = false, bool GATHER = false>
 __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict__ packed,
                                          const uint16_t* __restrict__ x16, const int* __restrict__ texp,
@@ -415,13 +430,15 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
     // GATHER: the byte offset of this lane's chunk in its two token rows (rows 32 w + 16 h +
     // lane / 4 of the tile; LDS slot lane & 3 holds chunk (lane & 3) ^ ((lane >> 3) & 3))
     uint32_t goff[2] = {0u, 0u};
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)x16, 0, (int)(kPadOffset - 1),
+                                                                         kBufferWord3);   // GATHER only
     if constexpr (GATHER) {
         const uint32_t chunk = (uint32_t)((lane & 3) ^ ((lane >> 3) & 3)) * 16;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int slot = t0 + wave * 32 + h * 16 + (lane >> 2);
-            const int r = gmap ? gmap[slot] : slot;
-            goff[h] = (uint32_t)(r < 0 ? 0 : r) * (uint32_t)(2 * K) + chunk;
+            const int r = slot >= T ? -1 : gmap ? gmap[slot] : slot;
+            goff[h] = r < 0 ? kPadOffset : (uint32_t)r * (uint32_t)(2 * K) + chunk;
         }
     }
 
@@ -442,12 +459,12 @@ __device__ __forceinline__ void dma_tile(uint8_t* lds, const uint8_t* __restrict
     auto issue_x = [&](int st, int slot) {
         const uint32_t dst = xdst + slot * kTileB;
         if constexpr (GATHER) {
-            const uint8_t* src = (const uint8_t*)x16 + (int64_t)(st0 + st) * 128;   // uniform: columns 64 (st0 + st)
+            const uint32_t col = (uint32_t)(st0 + st) * 128;   // uniform: columns 64 (st0 + st)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk)
-                    lds_dma16(src + kk * 64, goff[h], dst + kk * kPlaneB + h * 1024);
+                    lds_dma16_buf(xrs, goff[h], col + kk * 64, dst + kk * kPlaneB + h * 1024);
         } else {
             const uint8_t* src = xsrc + (int64_t)st * kTileB;           // uniform
 #pragma unroll

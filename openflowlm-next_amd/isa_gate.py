@@ -189,7 +189,7 @@ def early_uses_straight(asm: list[str], in_loop) -> tuple[int, list[str]]:
     return n, bad
 
 
-_LOAD = re.compile(r"\s*global_load")
+_LOAD = re.compile(r"\s*(global_load|buffer_load)")   # every vector-memory load counts in vmcnt
 _REG_LOAD = re.compile(r"\s*global_load_dword")
 _WAIT = re.compile(r"\s*s_waitcnt")
 _VMCNT = re.compile(r"vmcnt\((\d+)\)")

@@ -214,6 +214,10 @@ def test_checker_flags_an_early_use():
                     "\tglobal_load_dwordx4 v[30:33], v1, s[2:3] nt", "\ts_waitcnt vmcnt(1)",
                     "\tv_add_u32_e32 v13, v9, v10", asm[-1]]
     assert early_uses(ok) == (3, [])
+    # an LDS-DMA buffer load counts as a younger load in vmcnt like a global one
+    dma = asm[:2] + ["\tbuffer_load_dwordx4 v2, s[8:11], s4 offen lds", "\ts_waitcnt vmcnt(1)",
+                     "\tv_add_u32_e32 v12, v5, v6", asm[-1]]
+    assert early_uses(dma) == (1, [])
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not available")
