@@ -188,7 +188,7 @@ def graph_time(torch, fn, outputs, replays: int = 20, reset=None) -> float:
     """Capture fn() in a HIP graph, check one replay against the eager run
     (bit for bit: every kernel here is deterministic), replay it untimed for
     about 25 ms (clocks settle under load), then time `replays` replays with
-    events. Returns mean ms per replay. `reset` restores the state
+    events (at least ~1 ms of them). Returns mean ms per replay. `reset` restores the state
     of an fn that updates its inputs in place (a residual stream) before the
     eager run and before the checked replay."""
     if reset:
@@ -227,6 +227,9 @@ def graph_time(torch, fn, outputs, replays: int = 20, reset=None) -> float:
     for _ in range(max(2, min(2000, int(25.0 / one)))):
         g.replay()
     torch.cuda.synchronize()
+    # at least ~1 ms of timed replays: a short graph's mean then does not hang on one late
+    # submission (a 5-replay timing of the 8 us activation pre-pass once read 0.24 ms)
+    replays = max(replays, min(2000, int(1.0 / one) + 1))
     a.record(st)
     for _ in range(replays):
         g.replay()
