@@ -385,10 +385,11 @@ int q4_gemv_swiglu_rmsnorm_acc(const uint8_t* gate, const uint8_t* up, const flo
  * Shapes: H, F, NQ multiples of 64, H <= 4096, H and F >= 256. x_next may be x; x_mid,
  * the planes and the workspace must not overlap each other or x, attn and x_next
  * (Q4MI_E_ARG). The workspace (q4_decode_segment_workspace_bytes) starts with the
- * hand-over counters: its first 12800 bytes must be zero before the first call on it, and
- * each call leaves them zero, except the 32-bit word at byte 12544, which becomes nonzero
- * if a hand-over timed out (about a second: the grid could not be resident), in which case
- * the outputs are not valid. Calls sharing one workspace must not overlap in time. */
+ * hand-over counters: its first 12800 bytes must be zero before the first call on it; each
+ * call leaves them ready for the next (not all zero). The 32-bit word at byte 12544 becomes
+ * nonzero if a hand-over timed out (about a second: the grid could not be resident); the
+ * outputs are then not valid and the counters must be zeroed again. Calls sharing one
+ * workspace must not overlap in time. */
 size_t q4_decode_segment_workspace_bytes(int64_t H, int64_t F, int64_t NQ);
 int q4_decode_segment_splits(int64_t H, int64_t F, int64_t NQ, int* splits /* [3]: So, Sd, Sq */);
 int q4_decode_segment(const uint8_t* o, const uint8_t* gate, const uint8_t* up, const uint8_t* down,

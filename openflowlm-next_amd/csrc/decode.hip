@@ -37,8 +37,14 @@
 //   reached the device's coherence point before the arrival was issued.
 // - Every wait is bounded (kSpinLimit polls, about a second): a wait that runs out raises
 //   the flag word and goes on, so the grid always drains (the results are then not to be
-//   used). The last workgroup to leave returns the counters to zero, so a graph replays
-//   with no memset.
+//   used).
+// - The counters return to zero off the critical path, so a graph replays with no memset
+//   and no workgroup waits for a last atomic before it exits: workgroup 0 zeroes hand-overs
+//   1 and 2 (which the previous call left counted) when it starts, and hand-over 0 once it
+//   has passed hand-over 1 (every wait on hand-over 0 is over by then). A workgroup arrives
+//   at hand-over h + 1 only after hand-over h is complete (a workgroup with no item in a
+//   phase still waits for that phase's hand-over), so no arrival at hand-over 1 or 2 can
+//   come before workgroup 0's zeroing, which it completes before its own first arrival.
 // The grid is at most one workgroup per CU (checked against the occupancy the runtime
 // reports), so every workgroup is resident while others wait for it.
 //
@@ -61,9 +67,9 @@ constexpr int kSegXs = 16384;               // bf16 activations staged per workg
 constexpr int kSegRow = 256 * kAccRowJ;     // the longest row stage_norm_acc_row normalises
 constexpr uint32_t kSpinLimit = 1u << 20;   // polls before a grid wait gives up
 // The workspace's first kSyncBytes: hand-over h (0..2), counter j (0..15) at word
-// (16 h + j) * 64; departures at word 48 * 64; the time-out flag at word 49 * 64.
+// (16 h + j) * 64; the time-out flag at word 49 * 64.
 constexpr int kSlots = 16, kSlotWords = 64;
-constexpr int kDepartWord = 48 * kSlotWords, kFlagWord = 49 * kSlotWords;
+constexpr int kFlagWord = 49 * kSlotWords;
 constexpr size_t kSyncBytes = 50 * kSlotWords * 4;
 
 struct SegParams {
@@ -95,13 +101,16 @@ struct SegParams {
 // kb0 + w + 8, ...; every wave of an item has at least one (the host's splits leave >= 8
 // positions per item). Positions of the last chunk past the wave's count re-load its last
 // tile and are not accumulated. Same arithmetic and order as gemv_rows_stream.
-template <int NG, int UNR>
+// XG: the activations come from a bf16 row in global memory instead (xg, position t at
+// t * 32), one more load per position, so no staging pass sits in front of the stream.
+template <int NG, int UNR, bool XG = false>
 struct SegStream {
-    static constexpr int L = 2 * NG;                    // loads per position
+    static constexpr int L = 2 * NG + (XG ? 1 : 0);     // loads per position
     static_assert((UNR - 1) * L <= 63, "vmcnt holds 6 bits");
     const uint8_t* gb[NG];
+    const uint16_t* xg = nullptr;
     int first, cnt;
-    u32x4 c[UNR][NG], s[UNR][NG];
+    u32x4 c[UNR][NG], s[UNR][NG], xr[UNR];
 
     __device__ __forceinline__ void setup(const uint8_t* const (&gbase)[NG], int kb0, int kb1) {
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -119,12 +128,15 @@ struct SegStream {
             pipe_load_w(c[slot][i], gb[i], toff + coff);
             pipe_load_w(s[slot][i], gb[i], toff + soff);
         }
+        if constexpr (XG)
+            pipe_load_x(xr[slot], xg + (int64_t)(first + kSegWaves * min(b, cnt - 1)) * 32 + (lane >> 4) * 8);
     }
     __device__ __forceinline__ void prime() {
 #pragma unroll
         for (int u = 0; u < UNR; ++u) issue(u, u);
     }
-    // xs: the activations of positions [xkb, ...) as bf16 in LDS (position t at (t - xkb) * 32)
+    // xs: the activations of positions [xkb, ...) as bf16 in LDS (position t at (t - xkb) * 32),
+    // unless XG
     __device__ __forceinline__ void run(const __bf16* xs, int xkb, float (&acc)[NG][4][1]) {
         const int lane = threadIdx.x & 63;
         const CodeConsts kc = code_consts();
@@ -135,9 +147,12 @@ struct SegStream {
                 pipe_landed(c[slot][i]);
                 pipe_landed(s[slot][i]);
             }
+            if constexpr (XG) pipe_landed(xr[slot]);
         };
         auto pos = [&](int u, int b) {
-            const bf16x8 xh = *(const bf16x8*)(xsl + (int64_t)(first + kSegWaves * b) * 32);
+            bf16x8 xh;
+            if constexpr (XG) xh = __builtin_bit_cast(bf16x8, xr[u]);
+            else xh = *(const bf16x8*)(xsl + (int64_t)(first + kSegWaves * b) * 32);
             tile_math<1, false, false, NG>(c[u], s[u], xh, xh, kc, acc);
         };
         int b0 = 0;
@@ -203,6 +218,11 @@ __device__ __forceinline__ void grid_wait(uint32_t* sync, int hop) {
         }
     }
     __syncthreads();
+}
+
+// Zero hand-over hop's counters (lanes of the first wave, one counter each).
+__device__ __forceinline__ void zero_hop(uint32_t* sync, int hop) {
+    if (threadIdx.x < kSlots) store_dev(sync + (hop * kSlots + (int)threadIdx.x) * kSlotWords, 0u);
 }
 
 // Store the NG row groups' sums (rows n0[i] .. + 64) into y (thread t < 256 of lane group
@@ -322,15 +342,19 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
     const int G = (int)gridDim.x, w = (int)blockIdx.x;
     const int KBh = P.H >> 5, KBf = P.F >> 5;
     const int64_t th = (int64_t)KBh * kTileBytes, tf = (int64_t)KBf * kTileBytes;   // bytes per row group
+    if (w == 0) {              // the previous call's hand-overs 1 and 2 (see the hand-over notes)
+        zero_hop(P.sync, 1);
+        zero_hop(P.sync, 2);
+    }
 
     // ---- 1. o: items (row group, split); the attention row is an input, no wait ----
     {
         const int items = (P.H >> 6) * P.So;
-        if (w < items) stage_bf16(P.attn, P.H, xs);
         for (int it = w; it < items; it += G) {
             const int g = it / P.So, sp = it % P.So;
             const uint8_t* const gb[1] = {P.o + g * th};
-            SegStream<1, 4> st;
+            SegStream<1, 4, true> st;
+            st.xg = P.attn;
             st.setup(gb, sp * KBh / P.So, (sp + 1) * KBh / P.So);
             st.prime();
             float acc[1][4][1];
@@ -380,6 +404,8 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
                 s2.run(xs, 0, acc);
                 finish(acc, it);
             }
+        } else {
+            grid_wait(P.sync, 0);     // no arrival at hand-over 1 before hand-over 0 completes
         }
     }
     grid_arrive(P.sync, 1);
@@ -400,6 +426,7 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
             st.setup(gb, k0, k1);
             st.prime();                           // in flight across the hand-over
             grid_wait(P.sync, 1);
+            if (w == 0) zero_hop(P.sync, 0);      // every wait on hand-over 0 is over
             stage_bf16(P.h + (int64_t)k0 * 32, (k1 - k0) * 32, xs);
             float acc[1][4][1];
             zero_acc(acc);
@@ -418,6 +445,8 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
                 const int64_t n2[1] = {(int64_t)(it % P.Sd) * P.H + (it / P.Sd) * 64};
                 store_rows<true>(acc, red, P.pd, n2);
             }
+        } else if (P.qkv) {
+            grid_wait(P.sync, 1);     // no arrival at hand-over 2 before hand-over 1 completes
         }
     }
 
@@ -460,18 +489,6 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
                 s2.run(xs, 0, acc);
                 store_rows<false>(acc, red, P.pq, n0);
             }
-        }
-    }
-
-    // the last workgroup out returns the counters to zero (every wait of the grid is over)
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        uint32_t d = 0;
-        if (threadIdx.x == 0)
-            d = __hip_atomic_fetch_add(P.sync + kDepartWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__builtin_amdgcn_readfirstlane(d) == (uint32_t)G - 1) {
-            if (threadIdx.x < 3 * kSlots) store_dev(P.sync + threadIdx.x * kSlotWords, 0u);
-            if (threadIdx.x == 0) store_dev(P.sync + kDepartWord, 0u);
         }
     }
 }

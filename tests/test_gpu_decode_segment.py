@@ -46,11 +46,13 @@ def _acc(res: torch.Tensor, planes: torch.Tensor) -> torch.Tensor:
     return res + s
 
 
-def _sync_words(ws: torch.Tensor) -> list[int]:
-    """The hand-over counters' words (3 x 16 counters, 256 bytes apart), the departures and
-    the time-out flag: all zero after a call that completed."""
+def _check_sync(ws: torch.Tensor, qkv: bool = True) -> None:
+    """After a completed call: hand-over 0's 16 counters (256 bytes apart) back at zero,
+    hand-overs 1 and 2 holding one arrival per workgroup (2: none without qkv; the next
+    call zeroes them as it starts), the time-out flag clear."""
     w = ws[:12800].view(torch.int32).view(50, 64)[:, 0].cpu().tolist()
-    return [sum(w[:48]), w[48], w[49], 0, 0]
+    h0, h1, h2, flag = sum(w[0:16]), sum(w[16:32]), sum(w[32:48]), w[49]
+    assert flag == 0 and h0 == 0 and h1 > 0 and h2 == (h1 if qkv else 0), (h0, h1, h2, flag)
 
 
 def test_segment_equals_the_separate_launches_at_llama3_8b(gpu, pkg, oracle):
@@ -62,7 +64,7 @@ def test_segment_equals_the_separate_launches_at_llama3_8b(gpu, pkg, oracle):
     xm, xn, pd, pq = pkg.decode_segment(w["o"], w["gate"], w["up"], w["down"], w["qkv"], attn, x, nw1, nw2,
                                         workspace=ws)
     torch.cuda.synchronize()
-    assert _sync_words(ws) == [0, 0, 0, 0, 0]
+    _check_sync(ws)
     po = pkg.gemm_q4_partials(w["o"], attn, splits=So)
     h, xm_ref = pkg.swiglu_q4_acc(w["gate"], w["up"], x, po, nw1, out_dtype=torch.bfloat16)
     pd_ref = pkg.gemm_q4_partials(w["down"], h, splits=Sd)
@@ -109,7 +111,7 @@ def test_segment_against_fp64(gpu, pkg, oracle, monkeypatch, H, F, NQ, nwd, wgs)
     xm, xn, pd, pq = pkg.decode_segment(w["o"], w["gate"], w["up"], w["down"], w["qkv"], attn, x, nw1, nw2,
                                         eps=1e-5, workspace=ws)
     torch.cuda.synchronize()
-    assert _sync_words(ws) == [0, 0, 0, 0, 0]
+    _check_sync(ws)
     _check_against_fp64(pkg, oracle, blk, x, attn, nw1, nw2, xm, xn, pd, pq, 1e-5)
 
 
@@ -125,6 +127,8 @@ def test_last_layer_form_and_in_place_residual(gpu, pkg, oracle):
     xm2, xn2, pd2, pq2 = pkg.decode_segment(w["o"], w["gate"], w["up"], w["down"], None, attn, x, nw1,
                                             workspace=ws)
     assert xn2 is None and pq2 is None
+    torch.cuda.synchronize()
+    _check_sync(ws, qkv=False)
     assert torch.equal(xm2, xm) and torch.equal(pd2, pd)
     _check_against_fp64(pkg, oracle, blk, x, attn, nw1, nw2, xm2, None, pd2, None, 1e-6)
     y, xo = pkg.gemm_q4_rmsnorm_acc(w["qkv"], xm2, pd2, nw2)
@@ -135,7 +139,7 @@ def test_last_layer_form_and_in_place_residual(gpu, pkg, oracle):
     assert xn3.data_ptr() == xi.data_ptr()
     assert torch.equal(xi, xn) and torch.equal(xm3, xm) and torch.equal(pq3, pq)
     torch.cuda.synchronize()
-    assert _sync_words(ws) == [0, 0, 0, 0, 0]
+    _check_sync(ws)
 
 
 def test_segment_repeats_and_replays_bit_for_bit(gpu, pkg, oracle):
@@ -173,7 +177,7 @@ def test_segment_repeats_and_replays_bit_for_bit(gpu, pkg, oracle):
         g.replay()
         torch.cuda.synchronize()
         assert all(torch.equal(a, b) for a, b in zip((xm, xn, pd, pq), ref))
-        assert _sync_words(ws) == [0, 0, 0, 0, 0]
+        _check_sync(ws)
 
 
 def test_segment_refuses_bad_arguments(gpu, pkg, oracle):
