@@ -261,27 +261,49 @@ __device__ __forceinline__ void stage_bf16(const uint16_t* __restrict__ src, int
     __syncthreads();
 }
 
-// The row x = res + S partial planes (stride floats apart), its 1/rms and
-// xs = bf16((x * r) * w) over [0, K), K <= kSegRow: stage_norm_acc_row's arithmetic and
-// order (gemv_core.h: planes added to 0 in split order and the sum to res; S = 1: res +
-// part[0]; the fp64 sum of squares over i = tid + 256 j by the first 256 threads, the waves'
-// sums as (w0 + w1) + (w2 + w3)). A thread's elements are tid + 512 e, e < 8; its loads go
-// out together, the planes four at a time (one trip to memory per four planes), so the
-// registers of a primed weight pipeline stay live across it. x is left in xf.
+// What a norm prelude can load before its hand-over wait: res (thread t's elements t + 512 e,
+// e < 8) and the norm weight (threads t < 256: elements t + 256 j, the ones it scales).
+struct SegRowPre {
+    static constexpr int E = kSegRow / kSegThreads;
+    float r0[E];
+    float wv[kAccRowJ];
+};
+
 template <int NW>
-__device__ __forceinline__ void seg_norm_row(const float* __restrict__ res, const float* __restrict__ part, int S,
-                                             int64_t stride, int K, float eps, const void* __restrict__ w,
-                                             __bf16* xs, float* xf) {
-    constexpr int E = kSegRow / kSegThreads, PB = 4;
+__device__ __forceinline__ void seg_row_pre(const float* __restrict__ res, const void* __restrict__ w, int K,
+                                            SegRowPre& pre) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < SegRowPre::E; ++e) pre.r0[e] = res[min(tid + kSegThreads * e, K - 1)];
+    if (tid < 256) {                                  // waves 0-3: the scaling threads
+#pragma unroll
+        for (int j = 0; j < kAccRowJ; ++j) {
+            const int i = min(tid + 256 * j, K - 1);
+            pre.wv[j] = NW == 1 ? __uint_as_float((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i];
+        }
+    }
+}
+
+// The row x = res + S partial planes (stride floats apart), its 1/rms and
+// xs = bf16((x * r) * w) over [0, K), K <= kSegRow, with res and w from seg_row_pre:
+// stage_norm_acc_row's arithmetic and order (gemv_core.h: planes added to 0 in split order and
+// the sum to res; S = 1: res + part[0]; the fp64 sum of squares over i = tid + 256 j by the
+// first 256 threads, the waves' sums as (w0 + w1) + (w2 + w3)). A thread's elements are
+// tid + 512 e, e < 8; its plane loads go out together, four planes at a time (one trip to
+// memory per four planes), so the registers of a primed weight pipeline stay live across it.
+// x is left in xf.
+__device__ __forceinline__ void seg_norm_row(const SegRowPre& pre, const float* __restrict__ part, int S,
+                                             int64_t stride, int K, float eps, __bf16* xs, float* xf) {
+    constexpr int E = SegRowPre::E, PB = 4;
     __shared__ double partd[4];
     const int tid = threadIdx.x;
     auto ix = [&](int e) { return min(tid + kSegThreads * e, K - 1); };   // loads stay in the row
-    float r0[E], v[E];
+    float v[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) r0[e] = res[ix(e)], v[e] = 0.f;
+    for (int e = 0; e < E; ++e) v[e] = 0.f;
     if (S == 1) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = r0[e] + part[ix(e)];
+        for (int e = 0; e < E; ++e) v[e] = pre.r0[e] + part[ix(e)];
     } else {
         for (int q = 0; q < S; q += PB) {
             float t[PB][E];
@@ -297,7 +319,7 @@ __device__ __forceinline__ void seg_norm_row(const float* __restrict__ res, cons
                 }
         }
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = S == 0 ? r0[e] : r0[e] + v[e];
+        for (int e = 0; e < E; ++e) v[e] = S == 0 ? pre.r0[e] : pre.r0[e] + v[e];
     }
 #pragma unroll
     for (int e = 0; e < E; ++e)
@@ -320,11 +342,7 @@ __device__ __forceinline__ void seg_norm_row(const float* __restrict__ res, cons
 #pragma unroll
         for (int j = 0; j < kAccRowJ; ++j) {
             const int i = tid + 256 * j;
-            if (i < K) {
-                const float wi = NW == 1 ? __uint_as_float((uint32_t)((const uint16_t*)w)[i] << 16)
-                                         : ((const float*)w)[i];
-                ((uint16_t*)xs)[i] = (uint16_t)f32_to_bf16_rne(x[j] * r * wi);
-            }
+            if (i < K) ((uint16_t*)xs)[i] = (uint16_t)f32_to_bf16_rne(x[j] * r * pre.wv[j]);
         }
     }
     __syncthreads();
@@ -388,8 +406,10 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
             const uint8_t* const gb[2] = {P.gate + w * th, P.up + w * th};
             st.setup(gb, 0, KBh);
             st.prime();                           // in flight across the hand-over
+            SegRowPre pre;
+            seg_row_pre<NW>(P.x, P.nw_post, P.H, pre);     // inputs of the call: no wait needed
             grid_wait(P.sync, 0);
-            seg_norm_row<NW>(P.x, P.po, P.So, P.H, P.H, P.eps, P.nw_post, xs, xf);
+            seg_norm_row(pre, P.po, P.So, P.H, P.H, P.eps, xs, xf);
             if (w == 0) store_row<true>(xf, P.xmid, P.H);
             float acc[2][4][1];
             zero_acc(acc);
@@ -473,8 +493,10 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
             SegStream<QNG, QU> st;
             st.setup(gb, k0, k1);
             st.prime();                           // in flight across the hand-over
+            SegRowPre pre;
+            seg_row_pre<NW>(P.xmid, P.nw_next, P.H, pre);  // x' is complete since hand-over 1
             grid_wait(P.sync, 2);
-            seg_norm_row<NW>(P.xmid, P.pd, P.Sd, P.H, P.H, P.eps, P.nw_next, xs, xf);
+            seg_norm_row(pre, P.pd, P.Sd, P.H, P.H, P.eps, xs, xf);
             if (w == 0) store_row<false>(xf, P.xnext, P.H);
             float acc[QNG][4][1];
             zero_acc(acc);
