@@ -40,11 +40,17 @@
 //   used).
 // - The counters return to zero off the critical path, so a graph replays with no memset
 //   and no workgroup waits for a last atomic before it exits: workgroup 0 zeroes hand-overs
-//   1 and 2 (which the previous call left counted) when it starts, and hand-over 0 once it
-//   has passed hand-over 1 (every wait on hand-over 0 is over by then). A workgroup arrives
-//   at hand-over h + 1 only after hand-over h is complete (a workgroup with no item in a
-//   phase still waits for that phase's hand-over), so no arrival at hand-over 1 or 2 can
-//   come before workgroup 0's zeroing, which it completes before its own first arrival.
+//   1 and 2 (which the previous call left counted) before its arrival at hand-over 0, and
+//   hand-over 0 after its first down item (every wait on hand-over 0 is over once it has
+//   passed hand-over 1). A workgroup arrives at hand-over h + 1 only after hand-over h is
+//   complete (a workgroup with no item in a phase still waits for that phase's hand-over),
+//   so no arrival at hand-over 1 or 2 can come before workgroup 0's zeroing, which its own
+//   first arrival waits for.
+// - A wave's stores count in its vmcnt, so a store issued ahead of a weight stream holds the
+//   stream's first wait until the store is acknowledged. Workgroup 0's extra stores (the
+//   zeroing, x', x") therefore come after its streams, and the loads a norm prelude can
+//   issue early (the residual row, the norm weight; x' is complete from hand-over 1 on) go
+//   out with the primed weights, before the wait.
 // The grid is at most one workgroup per CU (checked against the occupancy the runtime
 // reports), so every workgroup is resident while others wait for it.
 //
@@ -360,11 +366,6 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
     const int G = (int)gridDim.x, w = (int)blockIdx.x;
     const int KBh = P.H >> 5, KBf = P.F >> 5;
     const int64_t th = (int64_t)KBh * kTileBytes, tf = (int64_t)KBf * kTileBytes;   // bytes per row group
-    if (w == 0) {              // the previous call's hand-overs 1 and 2 (see the hand-over notes)
-        zero_hop(P.sync, 1);
-        zero_hop(P.sync, 2);
-    }
-
     // ---- 1. o: items (row group, split); the attention row is an input, no wait ----
     {
         const int items = (P.H >> 6) * P.So;
@@ -381,6 +382,13 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
             const int64_t n0[1] = {(int64_t)sp * P.H + g * 64};
             store_rows<true>(acc, red, P.po, n0);
         }
+    }
+    // The previous call's hand-overs 1 and 2 (see the hand-over notes), zeroed after workgroup
+    // 0's stream: a wave's stores count in its vmcnt, so stores ahead of a stream's first wait
+    // would hold that wait for their acknowledgements. The arrival waits for them.
+    if (w == 0) {
+        zero_hop(P.sync, 1);
+        zero_hop(P.sync, 2);
     }
     grid_arrive(P.sync, 0);
 
@@ -410,11 +418,11 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
             seg_row_pre<NW>(P.x, P.nw_post, P.H, pre);     // inputs of the call: no wait needed
             grid_wait(P.sync, 0);
             seg_norm_row(pre, P.po, P.So, P.H, P.H, P.eps, xs, xf);
-            if (w == 0) store_row<true>(xf, P.xmid, P.H);
             float acc[2][4][1];
             zero_acc(acc);
             st.run(xs, 0, acc);
             finish(acc, w);
+            if (w == 0) store_row<true>(xf, P.xmid, P.H);   // after the stream (vmcnt), before arrival 1
             for (int it = w + G; it < items; it += G) {
                 const uint8_t* const gb2[2] = {P.gate + it * th, P.up + it * th};
                 SegStream<2, 4> s2;
@@ -446,13 +454,13 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
             st.setup(gb, k0, k1);
             st.prime();                           // in flight across the hand-over
             grid_wait(P.sync, 1);
-            if (w == 0) zero_hop(P.sync, 0);      // every wait on hand-over 0 is over
             stage_bf16(P.h + (int64_t)k0 * 32, (k1 - k0) * 32, xs);
             float acc[1][4][1];
             zero_acc(acc);
             st.run(xs, k0, acc);
             const int64_t n0[1] = {(int64_t)(w % P.Sd) * P.H + (w / P.Sd) * 64};
             store_rows<true>(acc, red, P.pd, n0);
+            if (w == 0) zero_hop(P.sync, 0);      // every wait on hand-over 0 is over
             for (int it = w + G; it < items; it += G) {
                 range(it, k0, k1);
                 const uint8_t* const gb2[1] = {P.down + (it / P.Sd) * tf};
@@ -497,11 +505,11 @@ __global__ __launch_bounds__(kSegThreads) void decode_segment_kernel(SegParams P
             seg_row_pre<NW>(P.xmid, P.nw_next, P.H, pre);  // x' is complete since hand-over 1
             grid_wait(P.sync, 2);
             seg_norm_row(pre, P.pd, P.Sd, P.H, P.H, P.eps, xs, xf);
-            if (w == 0) store_row<false>(xf, P.xnext, P.H);
             float acc[QNG][4][1];
             zero_acc(acc);
             st.run(xs, 0, acc);
             store_rows<false>(acc, red, P.pq, n0);
+            if (w == 0) store_row<false>(xf, P.xnext, P.H);   // after the stream (vmcnt)
             for (int it = w + G; it < items; it += G) {
                 item(it, gb, n0, k0, k1);
                 SegStream<QNG, QU> s2;
