@@ -233,12 +233,20 @@ int q4_gemv(const uint8_t* packed, const void* x, int x_dtype, float* y,
 int q4_gemv_noalloc(const uint8_t* packed, const void* x, int x_dtype, float* y,
                     int M, int64_t N, int64_t K, void* stream);
 
+/* Workspace bytes for q4_gemv_rmsnorm / q4_gemv_rmsnorm_acc: q4_gemv_workspace_bytes, and for
+ * vocabulary-sized matrices (N / 64 row groups x the split count >= 1024, e.g. an lm_head) room
+ * after the split partials for the normalised rows (bf16 [M][K], at the partials' size rounded
+ * up to 256 bytes). With that room the rows are normalised once by q4_rmsnorm_add's kernel and
+ * the plain GEMV reads them (one more launch, same bits); with less, every workgroup
+ * normalises per position as before. The rows' room must not overlap x, x_out or y. */
+size_t q4_gemv_rmsnorm_workspace_bytes(int M, int64_t N, int64_t K);
+
 /* The GEMV with its RMSNorm inside: Y = X . W^T with X = bf16(RMSNorm(x) * norm_w), formed per
  * tile from the f32 residual stream x [M][K] (1 <= M <= 16, K <= 16384, norm_w [K] bf16 or
  * f32). Same bits as q4_rmsnorm_add (bf16 out, no add) then q4_gemv: every workgroup first
  * computes the rows' 1/rms with q4_rmsnorm_add's arithmetic. Saves the norm's launch and its
  * bf16 copy in a decode step (the reference's ln design ahead of a projection,
- * designs/ln/ln.py:1-6). Workspace as q4_gemv. */
+ * designs/ln/ln.py:1-6). Workspace: q4_gemv_rmsnorm_workspace_bytes (q4_gemv's suffices). */
 int q4_gemv_rmsnorm(const uint8_t* packed, const float* x, const void* norm_w, int norm_w_dtype, float eps,
                     float* y, int M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                     void* stream);
@@ -353,7 +361,7 @@ int q4_gemv_partials(const uint8_t* packed, const void* x, int x_dtype, float* p
  * (the residual stream's next value: q4_gemv_residual's bits for the GEMV that made the
  * planes). x_out must not overlap res, part or y. M = 1 with K <= 4096 and a grid of at most
  * one workgroup per CU reduces inside the GEMV's workgroups; other shapes add one reduce
- * launch first. Workspace as q4_gemv; where the GEMV itself is split (e.g. 4096 x 4096 at
+ * launch first. Workspace as q4_gemv_rmsnorm; where the GEMV itself is split (e.g. 4096 x 4096 at
  * M = 1), its partials must not overlap res, part, x_out or y (Q4MI_E_ARG): a workspace
  * shared with the planes of q4_gemv_partials is carved apart from them. */
 int q4_gemv_rmsnorm_acc(const uint8_t* packed, const float* res, const float* part, int S,

@@ -69,6 +69,7 @@ SIGNATURES = {
     "q4_gemv_q8": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_dequant": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "q4_gemv_workspace_bytes": (_sz, [_i32, _i64, _i64]),
+    "q4_gemv_rmsnorm_workspace_bytes": (_sz, [_i32, _i64, _i64]),
     "q4_gemv": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp, _sz, _vp]),
     "q4_gemv_noalloc": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "q4_gemv_grouped": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp]),

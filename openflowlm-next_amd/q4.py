@@ -760,11 +760,23 @@ def _norm_x(x, K: int, dev) -> torch.Tensor:
     return xt
 
 
+def _norm_ws_bytes(lib, M: int, w: PackedQ4, workspace) -> int:
+    """A norm GEMV's workspace: the cached one is sized for the normalise-once form of
+    vocabulary-sized matrices; a caller's needs only what gemm_q4 needs (the library picks
+    the form its size allows)."""
+    if workspace is None:
+        return int(lib.q4_gemv_rmsnorm_workspace_bytes(M, w.n, w.k))
+    return int(lib.q4_gemv_workspace_bytes(M, w.n, w.k))
+
+
 def gemm_q4_rmsnorm(w: PackedQ4, x: torch.Tensor, norm_w: torch.Tensor, eps: float = 1e-6,
                     y: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Y = bf16(RMSNorm(x) * norm_w) @ W^T with the norm formed inside the GEMV from the f32
     residual stream x [M, K] (1 <= M <= 16, K <= 16384): the bits of rmsnorm_add (bf16 out)
-    followed by gemm_q4, with no launch and no copy for the norm."""
+    followed by gemm_q4, with no launch and no copy for the norm. Vocabulary-sized matrices
+    (an lm_head: >= 1024 row groups) normalise the rows once into the workspace first (one
+    more launch, the same bits); a caller's ``workspace`` needs gemv_workspace_bytes, and
+    takes that form from q4_gemv_rmsnorm_workspace_bytes on."""
     _bf16_scales("gemm_q4_rmsnorm", w)
     dev = w.device
     xt = _norm_x(x, w.k, dev)
@@ -775,7 +787,7 @@ def gemm_q4_rmsnorm(w: PackedQ4, x: torch.Tensor, norm_w: torch.Tensor, eps: flo
     y = _buf(y, "y", torch.float32, (M, w.n), dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
-        wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        wp, wn = _ws_arg(dev, _norm_ws_bytes(lib, M, w, workspace), "gemv", workspace)
         check("q4_gemv_rmsnorm", lib.q4_gemv_rmsnorm(_ptr(w.data), _ptr(xt), _ptr(wt), wd, float(eps), _ptr(y),
                                                      M, w.n, w.k, wp, wn, _stream(dev)))
     return y
@@ -850,7 +862,7 @@ def gemm_q4_rmsnorm_acc(w: PackedQ4, res: torch.Tensor, partials: torch.Tensor |
     y = _buf(y, "y", torch.float32, (M, w.n), dev)
     lib = _lib_handle()
     with torch.cuda.device(dev):
-        wp, wn = _ws_arg(dev, lib.q4_gemv_workspace_bytes(M, w.n, w.k), "gemv", workspace)
+        wp, wn = _ws_arg(dev, _norm_ws_bytes(lib, M, w, workspace), "gemv", workspace)
         check("q4_gemv_rmsnorm_acc", lib.q4_gemv_rmsnorm_acc(_ptr(w.data), _ptr(xt), pp, S, _ptr(wt), wd, float(eps),
                                                              _ptr(x_out), _ptr(y), M, w.n, w.k, wp, wn,
                                                              _stream(dev)))

@@ -191,6 +191,14 @@ def test_gemv_workspace_query(lib):
     assert lib.q4_gemv_workspace_bytes(1, 128256, 4096) == 0     # enough row groups: no split
     assert lib.q4_gemv_workspace_bytes(16, 4096, 14336) >= 16 * 4096 * 4 * 2
     assert lib.q4_gemv_workspace_bytes(0, 64, 32) == 0
+    # the norm GEMVs: room for the bf16 rows at vocabulary size (>= 1024 row groups), after
+    # the split partials rounded up to 256 bytes; else q4_gemv's
+    assert lib.q4_gemv_rmsnorm_workspace_bytes(1, 128256, 4096) == 4096 * 2
+    assert lib.q4_gemv_rmsnorm_workspace_bytes(16, 65536, 2048) == 16 * 2048 * 2
+    assert lib.q4_gemv_rmsnorm_workspace_bytes(1, 4096, 4096) == lib.q4_gemv_workspace_bytes(1, 4096, 4096)
+    assert lib.q4_gemv_rmsnorm_workspace_bytes(3, 6144, 4096) == lib.q4_gemv_workspace_bytes(3, 6144, 4096)
+    assert lib.q4_gemv_rmsnorm_workspace_bytes(0, 64, 32) == 0
+    assert lib.q4_gemv_rmsnorm_workspace_bytes(1, 65536 + 64, 4008) == 0   # K % 32 != 0
 
 
 def test_loader_fails_loudly_without_the_library(tmp_path):

@@ -293,6 +293,37 @@ def test_gemv_rmsnorm_of_residual_plus_partials(gpu, pkg, oracle, N, K, M, S, wd
         assert oracle.maxrel(y.cpu().numpy(), ref) <= MAXREL
 
 
+@pytest.mark.parametrize("wdt", ["bf16", "f32"])
+@pytest.mark.parametrize("N,K,M,S", [(65536, 4096, 1, 0), (65536, 4096, 1, 4), (65536, 2048, 3, 1),
+                                     (131072, 1024, 16, 2)])
+def test_vocab_norm_gemv_normalises_once_with_the_same_bits(gpu, pkg, oracle, N, K, M, S, wdt):
+    """At >= 1024 row groups (an lm_head) the norm GEMVs normalise the rows once into the
+    workspace and run the plain GEMV when the workspace has q4_gemv_rmsnorm_workspace_bytes;
+    with only q4_gemv_workspace_bytes every workgroup normalises per position. Both forms, and
+    rmsnorm_add followed by gemm_q4, give the same bits; x_out too (S planes, S = 0: none)."""
+    say(f"vocab norm gemv N={N} K={K} M={M} S={S} w={wdt}")
+    rng = np.random.default_rng(2100 + N + K + M + S)
+    w = pkg.pack_q4_1(oracle.baseline_q4_1_blocks(N, K, rng), gpu)
+    res = torch.from_numpy((rng.standard_normal((M, K)) * 3).astype(np.float32)).to(gpu)
+    part = torch.from_numpy(rng.standard_normal((S, M, K)).astype(np.float32)).to(gpu) if S else None
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(gpu)
+    if wdt == "bf16":
+        nw = nw.to(torch.bfloat16)
+    lib = pkg.q4._lib_handle()
+    small, big = lib.q4_gemv_workspace_bytes(M, N, K), lib.q4_gemv_rmsnorm_workspace_bytes(M, N, K)
+    assert big >= small + M * K * 2
+    x_ref = _acc_ref(res, part)
+    _, xn = pkg.rmsnorm_add(x_ref, nw, eps=1e-5)
+    ref = pkg.gemm_q4(w, xn)
+    for nbytes in (max(small, 256), big):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+        y = pkg.gemm_q4_rmsnorm(w, x_ref, nw, eps=1e-5, workspace=ws)
+        assert torch.equal(y, ref), nbytes
+        ya, x_out = pkg.gemm_q4_rmsnorm_acc(w, res, part, nw, eps=1e-5, workspace=ws)
+        assert torch.equal(x_out, x_ref), nbytes
+        assert torch.equal(ya, ref), nbytes
+
+
 @pytest.mark.parametrize("M,S", [(1, 0), (1, 1), (1, 4), (1, 16), (2, 4)])
 def test_swiglu_rmsnorm_of_residual_plus_partials(gpu, pkg, oracle, M, S):
     say(f"swiglu rmsnorm acc M={M} S={S}")
