@@ -60,7 +60,7 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_repack(fake, 18, fake, 64, 32, 1, None) == -2          # fp16 scales: Q4_1 only
     assert lib.q4_dequant_fp16s(fake, None, 64, 32, None) == -2
     assert lib.q4_gemv_fp16s(fake, fake, 1, None, fake, 17, 64, 32, None, 0, None) == -5   # M > 16
-    assert lib.q4_gemv_fp16s(fake, fake, 1, None, fake, 1, 4096, 4096, None, 0, None) == -3   # split: workspace
+    assert lib.q4_gemv_fp16s(fake, fake, 1, None, fake, 1, 1024, 4096, None, 0, None) == -3   # split: workspace
     assert lib.q4_gemv_grouped_fp16s(None, 1, 1, 1, 1, None) == -2
     assert lib.q4_repack(None, 20, fake, 64, 32, 0, None) == -2          # NULL
     assert lib.q4_repack(fake, 20, fake, 96, 32, 0, None) == -1          # N % 64
@@ -105,10 +105,12 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.q4_gemv(fake, fake, 1, fake, 1, 100, 32, None, 0, None) == -1   # N % 64
     assert lib.q4_gemv(None, None, 1, None, 0, 64, 32, None, 0, None) == 0     # M = 0
     # a short matrix is split along K and needs the workspace the query reports
-    need = lib.q4_gemv_workspace_bytes(1, 4096, 4096)
-    assert need > 0
-    assert lib.q4_gemv(fake, fake, 1, fake, 1, 4096, 4096, None, 0, None) == -3
-    assert lib.q4_gemv(fake, fake, 1, fake, 1, 4096, 4096, fake, need - 1, None) == -3
+    for n in (1024, 4096):
+        need = lib.q4_gemv_workspace_bytes(1, n, 4096)
+        assert need > 0 and lib.q4_gemv_split_count(n, 4096) > 1
+        assert lib.q4_gemv(fake, fake, 1, fake, 1, n, 4096, None, 0, None) == -3
+        assert lib.q4_gemv(fake, fake, 1, fake, 1, n, 4096, fake, need - 1, None) == -3
+    assert lib.q4_gemv_split_count(6144, 4096) == 1     # 96 row groups: unsplit, 16 waves
     assert lib.q4_gemv_grouped(None, 1, 1, 1, 1, None) == -2
     assert lib.q4_gemv_grouped(fake, 1, 1, 17, 1, None) == -5
     # packed weights, activations, outputs and workspaces move in 16-byte vectors
@@ -288,14 +290,13 @@ def test_deferred_reduction_argument_errors(lib):
 
 
 def test_split_workspace_must_not_overlap_what_the_gemv_reads(lib):
-    """A split norm GEMV (4096 x 4096 at M = 1 plans 4 K splits and reduces the deferred
+    """A split norm GEMV (1024 x 4096 at M = 1 plans K splits and reduces the deferred
     planes inside its workgroups) stores its partials to the workspace while other
-    workgroups still read res and the planes: a workspace carved over the planes, res,
-    x_out or y is refused before any launch."""
-    K = N = 4096
-    assert lib.q4_gemv_split_count(N, K) > 1
+    workgroups still read res and the planes: a workspace carved over the planes, res, x_out
+    or y is refused before any launch."""
+    K, N = 4096, 1024
     need = lib.q4_gemv_workspace_bytes(1, N, K)
-    assert need > 0
+    assert need > 0 and lib.q4_gemv_split_count(N, K) > 1
     fake = C.c_void_p(0x1000)
     res, part, xo, y = (C.c_void_p(0x10000000 * i) for i in (1, 2, 3, 4))
     eps = C.c_float(1e-6)
