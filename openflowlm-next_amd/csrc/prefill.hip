@@ -1539,9 +1539,17 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t* __restri
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int e = tid; e < E; e += 1024) hist[e] = 0;
     __syncthreads();
-    for (int p = tid; p < P; p += 1024) {
-        const int e = ids[p];
-        if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+    constexpr int kR = 8;                           // ids per thread in flight together
+    for (int p0 = 0; p0 < P; p0 += 1024 * kR) {
+        int ev[kR];
+#pragma unroll
+        for (int j = 0; j < kR; ++j) {
+            const int p = p0 + tid + 1024 * j;
+            ev[j] = p < P ? ids[p] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < kR; ++j)
+            if (ev[j] >= 0 && ev[j] < E) atomicAdd(&hist[ev[j]], 1);
     }
     __syncthreads();
     const int per = (E + 1023) / 1024;               // experts per thread, consecutive
@@ -1575,49 +1583,65 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t* __restri
     if (tid == 1023) meta[0] = tp;
 }
 
+// A workgroup barrier for LDS only: this wave's LDS operations are complete, its global
+// stores may still be in flight (__syncthreads would also wait for those).
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Expert e's pairs, in pair order, take slots off[e], off[e] + 1, ...: slot_of_pair and the
+// slot -> token row map (padding slots -1). A batch is 4096 pairs: thread t holds the 16
+// consecutive ids [16 t, 16 t + 16) in registers (four 16-byte loads, issued together), so
+// a block-wide prefix sum of the per-thread counts orders the matches; only the waves' sums
+// go through LDS, and the slot stores are never waited for inside the loop.
 __global__ __launch_bounds__(256) void moe_slots_kernel(const int32_t* __restrict__ ids, int P, int topk,
                                                         const int* __restrict__ cnt, const int* __restrict__ off,
                                                         int* __restrict__ slot_of_pair, int* __restrict__ rowmap) {
-    constexpr int kBatch = 4096, kPer = kBatch / 256;
-    __shared__ int buf[kBatch];
-    __shared__ int wsum[4];
+    constexpr int kPer = 16, kBatch = 256 * kPer;
+    __shared__ int wsum[2][4];
     const int e = blockIdx.x, n = cnt[e];
     if (n == 0) return;
     const int o = off[e];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool vec = ((uintptr_t)ids & 15) == 0;    // 16-byte loads of ids
     int base = 0;                                   // slots given out before this batch
-    for (int b0 = 0; b0 < P && base < n; b0 += kBatch) {
-        const int nb = min(kBatch, P - b0);
-        for (int i = tid; i < nb; i += 256) buf[i] = ids[b0 + i];          // coalesced
-        __syncthreads();
-        int c = 0;                                  // this thread's pairs: kPer consecutive
+    for (int b0 = 0, par = 0; b0 < P && base < n; b0 += kBatch, par ^= 1) {
+        const int i0 = b0 + tid * kPer;
+        int iv[kPer];
+        if (vec && i0 + kPer <= P) {
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int i = tid * kPer + j;
-            c += i < nb && buf[i] == e;
+            for (int q = 0; q < kPer / 4; ++q) {
+                const int4 v = *(const int4*)(ids + i0 + 4 * q);
+                iv[4 * q] = v.x, iv[4 * q + 1] = v.y, iv[4 * q + 2] = v.z, iv[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) iv[j] = i0 + j < P ? ids[i0 + j] : -1;
         }
+        int c = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) c += iv[j] == e;
         int incl = c;
 #pragma unroll
         for (int sft = 1; sft < 64; sft <<= 1) {
             const int v = __shfl_up(incl, sft);
             if (lane >= sft) incl += v;
         }
-        if (lane == 63) wsum[wave] = incl;
-        __syncthreads();
+        if (lane == 63) wsum[par][wave] = incl;     // two sets: no barrier needed before reuse
+        lds_sync();
         int r = base + incl - c;
-        for (int w = 0; w < wave; ++w) r += wsum[w];
+        for (int w = 0; w < wave; ++w) r += wsum[par][w];
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
-            const int i = tid * kPer + j;
-            if (i < nb && buf[i] == e) {
-                const int p = b0 + i;
+            if (iv[j] == e) {
+                const int p = i0 + j;
                 slot_of_pair[p] = o + r;
                 rowmap[o + r] = p / topk;
                 ++r;
             }
         }
-        base += wsum[0] + wsum[1] + wsum[2] + wsum[3];
-        __syncthreads();                            // buf and wsum are rewritten next batch
+        base += wsum[par][0] + wsum[par][1] + wsum[par][2] + wsum[par][3];
     }
     const int pad = ((n + 255) >> 8) << 8;
     for (int i = n + tid; i < pad; i += 256) rowmap[o + i] = -1;
