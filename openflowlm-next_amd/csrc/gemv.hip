@@ -615,8 +615,16 @@ __global__ __launch_bounds__(256) void acc_reduce_kernel(const float* __restrict
     if (S == 1) {
         x = res[i] + part[i];
     } else {
+        // loads batched eight planes at a time (issued together), added in split order
         float sum = 0.f;
-        for (int q = 0; q < S; ++q) sum += part[(int64_t)q * MK + i];
+        for (int q = 0; q < S; q += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = q + u < S ? part[(int64_t)(q + u) * MK + i] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (q + u < S) sum += t[u];
+        }
         x = S == 0 ? res[i] : res[i] + sum;
     }
     x_out[i] = x;

@@ -1811,17 +1811,30 @@ __global__ __launch_bounds__(256) void moe_prefill_combine_kernel(const float* _
                                                                   int H, float* __restrict__ out) {
     const int64_t t = blockIdx.y, n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (n >= H) return;
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < topk; ++j) {
-        const int64_t p = t * topk + j;
-        const int e = ids[p];
-        if (e >= 0 && e < E) {
-            const float wp = w[p];
-            const f32x4 v = *(const f32x4*)(Y + (int64_t)slot_of_pair[p] * H + n);
+    // the token's ids, weights and slots first, then all its Y loads, then the sum in slot
+    // order j (topk <= 16): no load waits on the previous slot's
+    constexpr int kMaxK = 16;
+    int slot[kMaxK];
+    float wv[kMaxK];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) s[c] += wp * v[c];
-        }
+    for (int j = 0; j < kMaxK; ++j) {
+        const int64_t p = t * topk + j;
+        const int e = j < topk ? ids[p] : -1;
+        const bool ok = e >= 0 && e < E;
+        slot[j] = ok ? slot_of_pair[p] : -1;
+        wv[j] = ok ? w[p] : 0.f;
     }
+    f32x4 v[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+        if (slot[j] >= 0) v[j] = *(const f32x4*)(Y + (int64_t)slot[j] * H + n);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+        if (slot[j] >= 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] += wv[j] * v[j][c];
+        }
     *(f32x4*)(out + t * H + n) = s;
 }
 
