@@ -74,6 +74,26 @@ def test_moe_prefill_deterministic_and_equal_to_decode_path(gpu, pkg, oracle):
     assert oracle.maxrel(a, d) <= 1e-3
 
 
+@pytest.mark.parametrize("prec", ["bf16", "fp16"])
+def test_moe_prefill_ids_at_any_4_byte_offset(gpu, pkg, oracle, prec):
+    """The routing loads each thread's 16 ids as 16-byte vectors when the ids are 16-byte
+    aligned and one by one otherwise: ids 4 bytes past an aligned base (and a pair count
+    that is no multiple of 16) give the aligned call's bits."""
+    say(f"moe prefill unaligned ids {prec}")
+    E, H, F, T, K = 16, 512, 256, 97, 4
+    rng, gu, dn, *_ = _make(oracle, pkg, gpu, E, H, F, 47)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).to(gpu)
+    ids, w = oracle.softmax_topk(rng.standard_normal((T, E)), K)
+    a = pkg.moe_batch(gu, dn, x, ids, w, path="prefill", precision=prec).cpu()
+    buf = torch.empty(T * K + 4, dtype=torch.int32, device=gpu)
+    for shift in (1, 2, 3):
+        view = buf[shift:shift + T * K].view(T, K)
+        view.copy_(torch.from_numpy(ids.astype(np.int32)))
+        assert view.data_ptr() % 16 != 0
+        b = pkg.moe_batch(gu, dn, x, view, w, path="prefill", precision=prec).cpu()
+        assert torch.equal(a, b), shift
+
+
 @pytest.mark.parametrize("E,H,F,T,K", [(8, 256, 128, 300, 2), (16, 512, 256, 97, 4), (6, 256, 128, 700, 2),
                                        (128, 2048, 768, 512, 8)])
 def test_moe_prefill_bf16_gather_equals_tiled_image(gpu, pkg, oracle, E, H, F, T, K):
