@@ -53,10 +53,30 @@ __device__ int active_expert(const int32_t* __restrict__ ids, int P, int E, int 
     for (int i = tid; i < nw; i += 64 * WAVES) bits[i] = 0u;
     if (tid == 0) found = -1;
     __syncthreads();
-    for (int p = tid; p < P; p += 64 * WAVES) {
-        const int e = ids[p];
-        sids[p] = e;
-        if (e >= 0 && e < E) atomicOr(&bits[e >> 5], 1u << (e & 31));
+    // up to one id per thread (decode batches): one pass; more (4096 pairs at T = 512 take 16
+    // per thread): kR ids per thread issued together, not one trip to memory per id
+    constexpr int kR = 8;
+    if (P <= 64 * WAVES) {
+        if (tid < P) {
+            const int e = ids[tid];
+            sids[tid] = e;
+            if (e >= 0 && e < E) atomicOr(&bits[e >> 5], 1u << (e & 31));
+        }
+    } else {
+        for (int p0 = 0; p0 < P; p0 += 64 * WAVES * kR) {
+            int ev[kR];
+#pragma unroll
+            for (int j = 0; j < kR; ++j) {
+                const int p = p0 + tid + 64 * WAVES * j;
+                ev[j] = p < P ? ids[p] : -1;
+            }
+#pragma unroll
+            for (int j = 0; j < kR; ++j) {
+                const int p = p0 + tid + 64 * WAVES * j;
+                if (p < P) sids[p] = ev[j];
+                if (ev[j] >= 0 && ev[j] < E) atomicOr(&bits[ev[j] >> 5], 1u << (ev[j] & 31));
+            }
+        }
     }
     __syncthreads();
     const uint32_t w = tid < nw ? bits[tid] : 0u;
@@ -80,31 +100,71 @@ __device__ int active_expert(const int32_t* __restrict__ ids, int P, int E, int 
     return found;
 }
 
+// collect_pairs for P > 64 WAVES: thread t takes the kMaxPairs / (64 WAVES) consecutive
+// pairs from t times that on (read as 16-byte vectors), so a block-wide prefix sum of the
+// threads' counts orders the matches, in one pass for any P <= kMaxPairs.
+template <int WAVES>
+__device__ int collect_pairs_runs(const int* sids, int P, int e, int* list) {
+    constexpr int kPer = kMaxPairs / (64 * WAVES);
+    static_assert(kPer % 4 == 0, "whole 16-byte groups per thread");
+    __shared__ int wave_cnt[WAVES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i0 = tid * kPer;
+    int v[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer / 4; ++q) {
+        if (i0 + 4 * q < P) {               // entries from P on (inside the array) are masked below
+            const int4 g = *(const int4*)(sids + i0 + 4 * q);
+            v[4 * q] = g.x, v[4 * q + 1] = g.y, v[4 * q + 2] = g.z, v[4 * q + 3] = g.w;
+        } else {
+            v[4 * q] = v[4 * q + 1] = v[4 * q + 2] = v[4 * q + 3] = -1;
+        }
+    }
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) c += i0 + j < P && v[j] == e;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) wave_cnt[wave] = incl;
+    __syncthreads();
+    int r = incl - c, total = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+        if (w < wave) r += wave_cnt[w];
+        total += wave_cnt[w];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+        if (i0 + j < P && v[j] == e) list[r++] = i0 + j;
+    __syncthreads();                        // list complete; wave_cnt free for the next call
+    return total;
+}
+
 // The pairs p = t * topk + j with ids[p] == e, ascending, into `list`; returns their count
 // (every thread calls it; barriers inside). sids: the ids as active_expert left them in LDS.
+// Up to one pair per thread (decode batches): a ballot compaction; more: collect_pairs_runs.
 template <int WAVES>
 __device__ int collect_pairs(const int* sids, int P, int e, int* list) {
+    if (P > 64 * WAVES) return collect_pairs_runs<WAVES>(sids, P, e, list);
     __shared__ int wave_cnt[WAVES];
-    __shared__ int base;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) base = 0;
+    const bool hit = tid < P && sids[tid] == e;
+    const uint64_t mask = __ballot(hit);
+    const int within = __popcll(mask & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_cnt[wave] = __popcll(mask);
     __syncthreads();
-    for (int p0 = 0; p0 < P; p0 += 64 * WAVES) {
-        const int p = p0 + tid;
-        const bool hit = p < P && sids[p] == e;
-        const uint64_t mask = __ballot(hit);
-        const int within = __popcll(mask & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_cnt[wave] = __popcll(mask);
-        __syncthreads();
-        int off = base;
-        for (int w = 0; w < wave; ++w) off += wave_cnt[w];
-        if (hit) list[off + within] = p;
-        __syncthreads();
-        if (tid == 0)
-            for (int w = 0; w < WAVES; ++w) base += wave_cnt[w];
-        __syncthreads();
+    int off = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+        if (w < wave) off += wave_cnt[w];
+        total += wave_cnt[w];
     }
-    return base;
+    if (hit) list[off + within] = tid;
+    __syncthreads();                        // list complete; wave_cnt free for the next call
+    return total;
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -184,7 +244,7 @@ __global__ __launch_bounds__(64 * kUpWaves) void moe_up_kernel(const uint8_t* __
         return;
     }
     const int fg = F >> 6, b = (int)blockIdx.x - sh.wgs;
-    __shared__ int sids[kMaxPairs];
+    __shared__ __attribute__((aligned(16))) int sids[kMaxPairs];
     const int e = active_expert<kUpWaves>(ids, P, E, b / fg, sids);
     if (e < 0) return;
     const int rgp = b % fg;
@@ -269,7 +329,7 @@ __global__ __launch_bounds__(64 * kDnWaves) void moe_down_kernel(const uint8_t* 
         return;
     }
     const int b = (int)blockIdx.x - sh.wgs;
-    __shared__ int sids[kMaxPairs];
+    __shared__ __attribute__((aligned(16))) int sids[kMaxPairs];
     const int e = active_expert<kDnWaves>(ids, P, E, b / wg_per_e, sids);
     if (e < 0) return;
     const int rg0 = (b % wg_per_e) * NG;
