@@ -44,17 +44,17 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
                                                            int64_t MN, int S, const float* res) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= MN) return;
-    // loads batched eight splits at a time (independent of the sum), added in split order
+    // loads batched sixteen splits at a time (one trip to memory for the plans' counts),
+    // added in split order
     float s = 0.f;
-    int q = 0;
-    for (; q + 8 <= S; q += 8) {
-        float t[8];
+    for (int q = 0; q < S; q += 16) {
+        float t[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) t[u] = part[(int64_t)(q + u) * MN + i];
+        for (int u = 0; u < 16; ++u) t[u] = q + u < S ? part[(int64_t)(q + u) * MN + i] : 0.f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s += t[u];
+        for (int u = 0; u < 16; ++u)
+            if (q + u < S) s += t[u];
     }
-    for (; q < S; ++q) s += part[(int64_t)q * MN + i];
     y[i] = res ? res[i] + s : s;
 }
 
