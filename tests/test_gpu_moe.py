@@ -35,6 +35,8 @@ def _make(oracle, pkg, gpu, E, H, F, seed):
     (4, 256, 192, 40, 2, "bf16"),        # ~20 tokens per expert: more than one 16-token chunk
     (8, 256, 128, 5, 3, "f32"),
     (8, 192, 128, 5, 2, "bf16"),         # H % 256 != 0: one 64-row group per down workgroup
+    (16, 256, 128, 200, 4, "bf16"),      # 800 pairs: the routing's batched id loads and one-pass compaction
+    (32, 256, 128, 512, 8, "bf16"),      # 4096 pairs, the decode path's maximum (T = 512, top-8)
 ])
 def test_moe_matches_oracle(gpu, pkg, oracle, E, H, F, T, K, xdt):
     say(f"moe E={E} H={H} F={F} T={T} top{K} {xdt}")
