@@ -702,6 +702,24 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
             return Q4MI_E_ARG;
     }
     const bool fused = acc_fused(M, K, (N / 64) * S);
+    // the vocabulary-sized form: the bf16 rows in the workspace, past the split partials
+    uint8_t* xn_rows = nullptr;
+    if (nrm.w && !fused && !lo && !q40 && !f16s && row_norm_first(N, S) && workspace) {
+        const size_t off = row_norm_offset(M, N, K, S);
+        const int64_t rb = (int64_t)M * K * 2, xb = (int64_t)M * K * 4;
+        uint8_t* const xn = (uint8_t*)workspace + off;
+        if (workspace_bytes >= off + (size_t)rb && !overlaps(xn, rb, x, xb) && !overlaps(xn, rb, y, (int64_t)M * N * 4) &&
+            !overlaps(xn, rb, nrm.x_out, xb) && !overlaps(xn, rb, nrm.acc_part, (int64_t)nrm.acc_S * xb))
+            xn_rows = xn;
+    }
+    if (xn_rows && nrm.x_out && K <= 256 * 16) {   // reduce and normalise in one launch
+        const int rc = rmsnorm_planes((const float*)x, nrm.acc_part, nrm.acc_S, nrm.w, nrm.w_bf16 ? Q4MI_BF16 : Q4MI_F32,
+                                      nrm.x_out, xn_rows, M, K, nrm.eps, stream);
+        if (rc != Q4MI_OK) return rc;
+        x = xn_rows;
+        x_dtype = Q4MI_BF16;
+        nrm = NormSpec{};
+    }
     if (nrm.x_out && !fused) {   // deferred reduction, unfused: reduce into x_out, then the norm GEMV
         const int64_t MK = (int64_t)M * K;
         hipLaunchKernelGGL(acc_reduce_kernel, dim3((unsigned)ceil_div(MK, 256)), dim3(256), 0, (hipStream_t)stream,
@@ -712,19 +730,13 @@ int gemv_impl(const uint8_t* packed, const void* x, int x_dtype, const float* re
         nrm.acc_part = nullptr;
         nrm.acc_S = 0;
     }
-    if (nrm.w && !fused && !lo && !q40 && !f16s && row_norm_first(N, S) && workspace) {
-        const size_t off = row_norm_offset(M, N, K, S);
-        const int64_t row = (int64_t)M * K * 2;
-        uint8_t* const xn = (uint8_t*)workspace + off;
-        if (workspace_bytes >= off + (size_t)row && !overlaps(xn, row, x, (int64_t)M * K * 4) &&
-            !overlaps(xn, row, y, (int64_t)M * N * 4)) {
-            const int rc = q4_rmsnorm_add((const float*)x, nullptr, nrm.w, nrm.w_bf16 ? Q4MI_BF16 : Q4MI_F32,
-                                          nullptr, xn, Q4MI_BF16, M, K, nrm.eps, stream);
-            if (rc != Q4MI_OK) return rc;
-            x = xn;
-            x_dtype = Q4MI_BF16;
-            nrm = NormSpec{};
-        }
+    if (xn_rows && nrm.w) {
+        const int rc = q4_rmsnorm_add((const float*)x, nullptr, nrm.w, nrm.w_bf16 ? Q4MI_BF16 : Q4MI_F32, nullptr,
+                                      xn_rows, Q4MI_BF16, M, K, nrm.eps, stream);
+        if (rc != Q4MI_OK) return rc;
+        x = xn_rows;
+        x_dtype = Q4MI_BF16;
+        nrm = NormSpec{};
     }
     GemvParams P{};
     P.packed = packed;

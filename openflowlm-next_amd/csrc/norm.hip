@@ -101,6 +101,84 @@ __global__ __launch_bounds__(256) void rmsnorm_add_long_kernel(const float* __re
     }
 }
 
+// x = res + the S partial planes of a split GEMV (planes MN floats apart; acc_reduce_kernel's
+// sum: S = 1 res + p0, S > 1 res + (((0 + p0) + p1) + ...), S = 0 res), stored to x_out, then
+// rmsnorm_add_kernel's normalisation of x into xn: one launch for the reduce and the norm
+// in front of a vocabulary-sized norm GEMV. The planes' loads go out four at a time.
+template <int PER>
+__global__ __launch_bounds__(256) void rmsnorm_planes_kernel(const float* __restrict__ res, const float* __restrict__ part,
+                                                             int S, int64_t MN, const void* __restrict__ w, int w_bf16,
+                                                             float* __restrict__ x_out, void* __restrict__ xn, int xn_bf16,
+                                                             int64_t N, float eps) {
+    __shared__ double part_ss[4];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float* rr = res + row * N;
+    const float* pr = part + row * N;
+    float v[PER], wv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int64_t i = tid + 256 * j;
+        v[j] = i < N ? rr[i] : 0.0f;
+        wv[j] = i >= N ? 0.0f
+                       : (w_bf16 ? bf16_hi_to_f32((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i]);
+    }
+    if (S == 1) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int64_t i = tid + 256 * j;
+            if (i < N) v[j] = v[j] + pr[i];
+        }
+    } else if (S > 1) {
+        float sum[PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) sum[j] = 0.0f;
+        for (int q = 0; q < S; q += 4) {
+            float t[4][PER];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < PER; ++j) {
+                    const int64_t i = tid + 256 * j;
+                    t[u][j] = q + u < S && i < N ? pr[(int64_t)(q + u) * MN + i] : 0.0f;
+                }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (q + u < S) {
+#pragma unroll
+                    for (int j = 0; j < PER; ++j) sum[j] += t[u][j];
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j) v[j] = v[j] + sum[j];
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int64_t i = tid + 256 * j;
+        if (i >= N) v[j] = 0.0f;
+        ss += (double)v[j] * (double)v[j];
+    }
+    const double wsum = wave_sum_ss(ss);
+    if ((tid & 63) == 0) part_ss[tid >> 6] = wsum;
+    __syncthreads();
+    float* xo = x_out + row * N;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int64_t i = tid + 256 * j;
+        if (i < N) xo[i] = v[j];
+    }
+    const float r = inv_rms(part_ss, N, eps);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int64_t i = tid + 256 * j;
+        if (i >= N) break;
+        const float o = v[j] * r * wv[j];
+        if (xn_bf16) ((uint16_t*)xn)[row * N + i] = (uint16_t)f32_to_bf16_rne(o);
+        else ((float*)xn)[row * N + i] = o;
+    }
+}
+
 }  // namespace
 
 extern "C" int q4_rmsnorm_add(const float* x, const float* add, const void* w, int w_dtype, float* y, void* xn,
@@ -129,3 +207,22 @@ extern "C" int q4_rmsnorm_add(const float* x, const float* add, const void* w, i
         hipLaunchKernelGGL(rmsnorm_add_long_kernel, grid, block, 0, st, x, add, w, wb, y, xn, xb, N, eps);
     return launch_status();
 }
+
+namespace q4mi {
+
+int rmsnorm_planes(const float* res, const float* part, int S, const void* w, int w_dtype, float* x_out, void* xn,
+                   int M, int64_t N, float eps, void* stream) {
+    if (M <= 0 || N <= 0 || N > 256 * 16 || S < 0) return Q4MI_E_RANGE;
+    const hipStream_t st = (hipStream_t)stream;
+    const int wb = w_dtype == Q4MI_BF16;
+    const int64_t MN = (int64_t)M * N;
+    if (N <= 256 * 8)
+        hipLaunchKernelGGL(rmsnorm_planes_kernel<8>, dim3((unsigned)M), dim3(256), 0, st, res, part, S, MN, w, wb,
+                           x_out, xn, 1, N, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_planes_kernel<16>, dim3((unsigned)M), dim3(256), 0, st, res, part, S, MN, w, wb,
+                           x_out, xn, 1, N, eps);
+    return launch_status();
+}
+
+}  // namespace q4mi

@@ -25,4 +25,9 @@ inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
     return a && b && na > 0 && nb > 0 && ca < cb + nb && cb < ca + na;
 }
 
+// x_out = res + the S partial planes (split order) and xn = bf16 of its RMSNorm (q4_rmsnorm_add's
+// arithmetic) in one launch, M rows of N <= 4096 (norm.hip).
+int rmsnorm_planes(const float* res, const float* part, int S, const void* w, int w_dtype, float* x_out, void* xn,
+                   int M, int64_t N, float eps, void* stream);
+
 }  // namespace q4mi
