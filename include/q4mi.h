@@ -361,7 +361,8 @@ int q4_gemv_partials(const uint8_t* packed, const void* x, int x_dtype, float* p
  * (the residual stream's next value: q4_gemv_residual's bits for the GEMV that made the
  * planes). x_out must not overlap res, part or y. M = 1 with K <= 4096 and a grid of at most
  * one workgroup per CU reduces inside the GEMV's workgroups; other shapes add one reduce
- * launch first. Workspace as q4_gemv_rmsnorm; where the GEMV itself is split (e.g. 4096 x 4096 at
+ * launch first (vocabulary-sized matrices given q4_gemv_rmsnorm_workspace_bytes: one launch
+ * that reduces and normalises, K <= 4096). Workspace as q4_gemv_rmsnorm; where the GEMV itself is split (e.g. 4096 x 4096 at
  * M = 1), its partials must not overlap res, part, x_out or y (Q4MI_E_ARG): a workspace
  * shared with the planes of q4_gemv_partials is carved apart from them. */
 int q4_gemv_rmsnorm_acc(const uint8_t* packed, const float* res, const float* part, int S,
